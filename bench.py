@@ -1,0 +1,221 @@
+"""Benchmark: fused two-tier decode attention, µs/layer and achieved HBM GB/s.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3_7b_16k_b8]
+
+A step is one decode step over L distinct layers (each with its own device
+blob, > 1 GB in total so the 256 MB Infinity Cache cannot hold the working
+set); each layer call is one launch of the fused kernel.  The L calls are
+captured once in a HIP graph and replayed; the timed region is K replays
+bracketed by HIP events on the capture stream.  Inputs are synthetic
+(seeded Gaussian K/V with outlier channels, 2% spike tokens) and resident in
+HBM before timing starts.
+
+Prints one JSON line (rank 0).  ``value`` is the achieved algorithmic HBM
+bandwidth in GB/s (SURVEY formula for bytes per layer-call, no credit for
+gated V); ``us_per_layer`` and ``pct_peak`` are reported beside it, with a
+``roofline`` object and a ``cpu_baseline`` (the C oracle's dequant+SDPA
+formulation on a bounded sample, on the host cores).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn µs/layer + achieved HBM GB/s (% peak), 7B shapes 16K ctx, 1 GPU"
+PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec):
+    """Bytes one layer-call must move: near (valid) fp16 K+V, far fp8 K +
+    INT4 V + fp16 scale/zero, decode fp16 K+V, fp16 q in / out, flags and
+    tokens, near_valid."""
+    per_head = R * D * 4 + F * (D + D // 2 + 4) + n_dec * D * 4
+    return B * Hkv * per_head + 2 * B * Hq * D * 2 + B * Hq * 8 + Hkv * 4
+
+
+def read_traffic(path):
+    """Per-launch HBM traffic from a committed rocprofv3 --pmc summary:
+    lines 'fetch_bytes_per_launch: N' / 'write_bytes_per_launch: N'."""
+    if not path or not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            if ":" in line:
+                k, v = line.split(":", 1)
+                try:
+                    vals[k.strip()] = float(v.strip().split()[0])
+                except (ValueError, IndexError):
+                    pass
+    if "fetch_bytes_per_launch" in vals and "write_bytes_per_launch" in vals:
+        return vals["fetch_bytes_per_launch"] + vals["write_bytes_per_launch"]
+    return None
+
+
+def cpu_baseline(c, q, dk, dv, D, sample_b=1):
+    """Oracle formulation (dequant + concat + SDPA, fp64 softmax, OpenMP over
+    (b, q head)) on the first ``sample_b`` batch rows of one layer."""
+    import oracle
+
+    sl = slice(0, sample_b)
+    args = [q[sl], c["near_k"][sl], c["near_v"][sl], c["near_valid"], c["far_k"][sl], c["far_v"][sl],
+            c["far_v_scale"][sl], c["far_v_zero"][sl], dk[sl] if dk is not None else None,
+            dv[sl] if dv is not None else None]
+    oracle.attend_formulation(*args)  # warm (page-in)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.attend_formulation(*args)
+        reps += 1
+        if time.perf_counter() - t0 >= 10.0 or reps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return dt, reps
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3_7b_16k_b8")
+    ap.add_argument("--layers", type=int, default=0, help="distinct layer blobs (0: enough for > 1 GB)")
+    ap.add_argument("--spikes", type=float, default=0.02)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "attn_c3_16k_b8_traffic.txt"))
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the decode path shards by (batch, kv_head) "
+                                   "with no collective, so there is no multi-GPU figure; run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+
+    import oracle
+    from foveated_kv_amd import _lib, ext, synthetic
+
+    _lib.load()
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a ROCm GPU")
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[args.config]
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = 8
+    tb = ext.tier_boundaries_c(cfg, S)
+    R, F = tb["R_actual"], tb["far_count"]
+
+    print(f"[bench] config {args.config}: B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} "
+          f"R={R} F={F}", file=sys.stderr, flush=True)
+    k, v = synthetic.make_kv(B, Hkv, S, D, args.seed)
+    q = synthetic.make_query(B, Hq, D, args.seed)
+    synthetic.inject_spikes(k, q, tb["mid_start"], F, args.spikes, args.seed)
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, args.seed)
+    kt = torch.from_numpy(k).to(dev)
+    vt = torch.from_numpy(v).to(dev)
+    cl = ext.CompressHandle(cfg).compress_layer(kt, vt, with_archive=False)
+    del kt, vt
+    qt = torch.from_numpy(q).to(dev)[:, :, None, :]
+    dkt = torch.from_numpy(dk).to(dev) if dk is not None else None
+    dvt = torch.from_numpy(dv).to(dev) if dv is not None else None
+
+    nbytes = algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec)
+    blob_bytes = None
+    handles = []
+    L = args.layers
+    while True:
+        h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                               cl.near_valid, spike_margin=10.0)
+        handles.append(h)
+        blob_bytes = h.get_blob_info().blob_bytes
+        if (L and len(handles) >= L) or (not L and len(handles) * blob_bytes > (1 << 30) and len(handles) >= 4):
+            break
+    L = len(handles)
+    print(f"[bench] {L} layer blobs x {blob_bytes / 2**20:.1f} MiB; algorithmic {nbytes / 1e6:.2f} MB/layer",
+          file=sys.stderr, flush=True)
+
+    # eager warm-up (allocates the split workspace outside graph capture)
+    for h in handles:
+        h(qt, dkt, dvt)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.Stream(device=dev)
+    graph = torch.cuda.CUDAGraph()
+    outs = []
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for h in handles:
+                outs.append(h(qt, dkt, dvt))
+    torch.cuda.synchronize()
+
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(end)
+    ms_step = ms_total / args.steps
+    us_layer = ms_step * 1000.0 / L
+    gbs = nbytes / (us_layer * 1e-6) / 1e9
+
+    # sanity: graph output equals eager output for layer 0
+    eager = handles[0](qt, dkt, dvt)
+    torch.cuda.synchronize()
+    assert torch.equal(eager[0], outs[0][0]) and torch.equal(eager[2], outs[0][2]), "graph replay diverged"
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": args.config, "B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S,
+                   "near_valid": R, "far": F, "n_decode": n_dec, "layers_per_step": L,
+                   "spike_frac": args.spikes, "far_format": "fp8-e4m3 K + int4 per-token V"},
+        "us_per_layer": round(us_layer, 3),
+        "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
+    }
+    traffic = read_traffic(args.traffic) if args.config == "c3_7b_16k_b8" else None
+    result["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / PEAK_GBS, 4), "traffic": traffic,
+                          "algorithmic_bytes": nbytes}
+    if not args.no_cpu_baseline:
+        c = {n: getattr(cl, n).cpu().numpy() for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale",
+                                                        "far_v_zero", "near_valid")}
+        dt, reps = cpu_baseline(c, q, dk, dv, D, sample_b=1)
+        sample_bytes = algorithmic_bytes(1, Hq, Hkv, D, R, F, n_dec)
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        result["cpu_baseline"] = {
+            "value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_layer": round(dt * 1e6 * B, 1),
+            "sample": f"oracle dequant+SDPA formulation (fp64 softmax, OpenMP over (b, q head)) on batch row 0 "
+                      f"of 1 layer of {args.config}, {reps} reps; us_per_layer scaled x{B} to the full batch",
+        }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,237 @@
+"""Python mirror of the reference's native module ``foveated_ext``
+(samfurr/foveated_kv csrc/bindings.cpp:13-159), backed by the gfx950 C-ABI
+library instead of nanobind + Metal.
+
+Same class names, argument names, defaults and return shapes:
+  TierConfig, CompressedLayer, CompressHandle(cfg).compress_layer/compress_all,
+  FoveatedHandle(near_k, ..., near_valid, spike_margin=0.5)(query, dk, dv)
+  -> [out, spike_flags, spike_tokens], get_blob_info(), is_available().
+Tensors are torch tensors on a ROCm device instead of mx.array.  Every call
+is enqueued on torch's current stream of the tensors' device.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import check, dtype_code, ptr
+
+
+def is_available():
+    """bindings.cpp:158-159 -- True when the library loads and a gfx950 GPU is visible."""
+    try:
+        lib = _lib.load()
+    except _lib.FkvLibraryError:
+        return False
+    return bool(lib.fkv_is_available())
+
+
+class TierConfig:
+    """C++ TierConfig mirror (csrc/foveated_compress.h:92-98); note the C++
+    default promo_headroom_min = 4 (the Python MLXTierConfig default is 8)."""
+
+    def __init__(self):
+        self.near_pct = 0.10
+        self.n_sinks = 4
+        self.window_size = 32
+        self.promo_headroom_pct = 0.5
+        self.promo_headroom_min = 4
+
+    def to_c(self):
+        return _lib.TierConfigC(float(self.near_pct), int(self.n_sinks), int(self.window_size),
+                                float(self.promo_headroom_pct), int(self.promo_headroom_min))
+
+
+def tier_boundaries_c(cfg, S):
+    """fkv_tier_boundaries through the C ABI -> dict with the keys of
+    MLXTierConfig.tier_boundaries plus 'headroom'."""
+    lib = _lib.load()
+    out = _lib.TiersC()
+    c = cfg.to_c()
+    check(lib.fkv_tier_boundaries(ctypes.byref(c), int(S), ctypes.byref(out)), "fkv_tier_boundaries")
+    return {
+        "n_sinks": out.n_sinks, "window": out.window, "near_from_mid": out.near_from_mid,
+        "far_count": out.far_count, "R_actual": out.r_actual, "N_near_padded": out.n_near_padded,
+        "mid_start": out.mid_start, "mid_end": out.mid_end, "near_mid_start": out.near_mid_start,
+        "far_src_offset": out.mid_start, "headroom": out.headroom,
+    }
+
+
+def _require_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise TypeError("foveated_kv_amd tensors must live on a ROCm device (got a CPU tensor)")
+
+
+class CompressedLayer:
+    """csrc/foveated_compress.h:100-118 (+ the fp16 far-row archive)."""
+
+    def __init__(self, near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid,
+                 n_near_actual, archive_k=None, archive_v=None):
+        self.near_k = near_k
+        self.near_v = near_v
+        self.far_k = far_k
+        self.far_v = far_v
+        self.far_v_scale = far_v_scale
+        self.far_v_zero = far_v_zero
+        self.near_valid = near_valid
+        self.n_near_actual = n_near_actual
+        self.archive_k = archive_k
+        self.archive_v = archive_v
+
+
+class CompressHandle:
+    """CompressHandle (csrc/foveated_compress.cpp:95-227): one fused HIP kernel
+    per layer builds near / far / archive tensors.  ``metallib_path`` is
+    accepted for signature compatibility and ignored."""
+
+    def __init__(self, cfg=None, metallib_path=""):
+        self.cfg = cfg if cfg is not None else TierConfig()
+
+    def compress_layer(self, keys, values, with_archive=True):
+        _require_device(keys, values)
+        if keys.shape != values.shape or keys.dim() != 4:
+            raise ValueError(f"keys/values must be (B,H,S,D) with equal shapes, got {tuple(keys.shape)} / {tuple(values.shape)}")
+        B, H, S, D = keys.shape
+        tb = tier_boundaries_c(self.cfg, S)
+        dev = keys.device
+        k = keys.contiguous()
+        v = values.contiguous()
+        if v.dtype != k.dtype:
+            v = v.to(k.dtype)
+        if k.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            k = k.to(torch.float16)
+            v = v.to(torch.float16)
+        F = tb["far_count"]
+        npad = tb["N_near_padded"]
+        near_k = torch.empty((B, H, npad, D), dtype=torch.float16, device=dev)
+        near_v = torch.empty_like(near_k)
+        far_k = torch.empty((B, H, F, D), dtype=torch.uint8, device=dev)
+        far_v = torch.empty((B, H, F, D // 2), dtype=torch.uint8, device=dev)
+        fvs = torch.empty((B, H, F), dtype=torch.float16, device=dev)
+        fvz = torch.empty_like(fvs)
+        near_valid = torch.empty((H,), dtype=torch.int32, device=dev)
+        arc_k = torch.empty((B, H, F, D), dtype=torch.float16, device=dev) if with_archive else None
+        arc_v = torch.empty_like(arc_k) if with_archive else None
+        lib = _lib.load()
+        c = self.cfg.to_c()
+        with torch.cuda.device(dev):
+            check(lib.fkv_compress_layer(ctypes.byref(c), ptr(k), ptr(v), dtype_code(k.dtype), B, H, S, D,
+                                         ptr(near_k), ptr(near_v), ptr(far_k), ptr(far_v), ptr(fvs), ptr(fvz),
+                                         ptr(near_valid), ptr(arc_k), ptr(arc_v), _lib.stream_ptr(dev)),
+                  "fkv_compress_layer")
+        return CompressedLayer(near_k, near_v, far_k, far_v, fvs, fvz, near_valid, tb["R_actual"],
+                               arc_k, arc_v)
+
+    def compress_all(self, all_keys, all_values, with_archive=True):
+        return [self.compress_layer(k, v, with_archive) for k, v in zip(all_keys, all_values)]
+
+
+class BlobWriteInfo:
+    """csrc/promotion_pipeline.h:66-73 analogue: where promotions land in the
+    device blob (offsets in bytes from ``blob_ptr``)."""
+
+    def __init__(self, c):
+        self.blob_ptr = c.blob
+        self.blob_bytes = c.blob_bytes
+        self.near_k_offset = c.near_k_offset
+        self.near_v_offset = c.near_v_offset
+        self.near_valid_offset = c.near_valid_offset
+        self.N_near_alloc = c.n_near_alloc
+        self.N_far = c.n_far
+        self.B = c.B
+        self.H_kv = c.H_kv
+        self.D = c.D
+
+
+class FoveatedHandle:
+    """FoveatedHandle (csrc/foveated_attn.cpp:135-254): copies the static tier
+    arrays into a private device blob; calling it launches the fused kernel.
+    ``metallib_path`` is accepted for signature compatibility and ignored."""
+
+    def __init__(self, near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid,
+                 spike_margin=0.5, metallib_path=""):
+        _require_device(near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid)
+        if near_k.dim() != 4 or near_k.shape != near_v.shape:
+            raise ValueError("near_k/near_v must be (B,H,N,D) with equal shapes")
+        B, H, Na, D = near_k.shape
+        F = far_k.shape[2]
+        if tuple(far_k.shape) != (B, H, F, D) or tuple(far_v.shape) != (B, H, F, D // 2):
+            raise ValueError(f"far_k {tuple(far_k.shape)} / far_v {tuple(far_v.shape)} do not match near {tuple(near_k.shape)}")
+        if tuple(far_v_scale.shape) != (B, H, F) or tuple(far_v_zero.shape) != (B, H, F):
+            raise ValueError("far_v_scale / far_v_zero must be (B,H,F)")
+        self.device = near_k.device
+        self.B, self.H_kv, self.D, self.N_near, self.N_far = B, H, D, Na, F
+        self.spike_margin = float(spike_margin)
+        nk = near_k.contiguous()
+        nv = near_v.to(nk.dtype).contiguous()
+        if nk.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            nk, nv = nk.half(), nv.half()
+        fvs = far_v_scale.contiguous()
+        fvz = far_v_zero.to(fvs.dtype).contiguous()
+        if fvs.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            fvs, fvz = fvs.half(), fvz.half()
+        valid = near_valid.to(torch.int32).contiguous()
+        fk = far_k.to(torch.uint8).contiguous()
+        fv = far_v.to(torch.uint8).contiguous()
+        lib = _lib.load()
+        h = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            check(lib.fkv_attn_create(ctypes.byref(h), B, H, D, Na, F, ptr(nk), ptr(nv), dtype_code(nk.dtype),
+                                      ptr(fk), ptr(fv), ptr(fvs), ptr(fvz), dtype_code(fvs.dtype), ptr(valid),
+                                      self.spike_margin, _lib.stream_ptr(self.device)),
+                  "fkv_attn_create")
+        self._h = h
+        self._lib = lib
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.fkv_attn_destroy(h)
+            self._h = None
+
+    def __call__(self, query, decode_k=None, decode_v=None):
+        """-> [out (B,Hq,1,D) fp16, spike_flags (B,Hq) int32, spike_tokens (B,Hq) int32]"""
+        _require_device(query, decode_k, decode_v)
+        if query.dim() == 4:
+            if query.shape[2] != 1:
+                raise ValueError("decode attention takes one query position (B,Hq,1,D)")
+            q = query[:, :, 0, :]
+        else:
+            q = query
+        B, Hq, D = q.shape
+        if B != self.B or D != self.D:
+            raise ValueError(f"query {tuple(query.shape)} does not match the handle (B={self.B}, D={self.D})")
+        if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            q = q.half()
+        q = q.contiguous()
+        n_dec = 0
+        dk = dv = None
+        if decode_k is not None and decode_k.shape[2] > 0:
+            n_dec = decode_k.shape[2]
+            if tuple(decode_k.shape) != (B, self.H_kv, n_dec, D) or decode_v.shape != decode_k.shape:
+                raise ValueError("decode_k/decode_v must be (B,H_kv,n,D)")
+            dk = decode_k.to(torch.float16).contiguous()
+            dv = decode_v.to(torch.float16).contiguous()
+        out = torch.empty((B, Hq, 1, D), dtype=torch.float16, device=self.device)
+        flags = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
+        tokens = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
+        with torch.cuda.device(self.device):
+            check(self._lib.fkv_attn_call(self._h, ptr(q), dtype_code(q.dtype), Hq, ptr(dk), ptr(dv), n_dec,
+                                          ptr(out), ptr(flags), ptr(tokens), _lib.stream_ptr(self.device)),
+                  "fkv_attn_call")
+        return [out, flags, tokens]
+
+    def get_blob_info(self):
+        c = _lib.BlobInfoC()
+        check(self._lib.fkv_attn_blob_info(self._h, ctypes.byref(c)), "fkv_attn_blob_info")
+        return BlobWriteInfo(c)
+
+    def read_near_valid(self):
+        """Current per-KV-head near_valid of the blob (host list)."""
+        buf = (ctypes.c_uint32 * self.H_kv)()
+        with torch.cuda.device(self.device):
+            check(self._lib.fkv_attn_read_near_valid(self._h, ctypes.cast(buf, ctypes.c_void_p),
+                                                     _lib.stream_ptr(self.device)), "fkv_attn_read_near_valid")
+        return list(buf)

@@ -1,0 +1,145 @@
+/*
+ * fkv.h -- C ABI of the MI355X (gfx950) FoveatedKV decode hot path.
+ *
+ * This is the drop-in boundary that replaces the reference's nanobind module
+ * `foveated_ext` (samfurr/foveated_kv csrc/bindings.cpp:13-159).  Every
+ * entry point takes plain pointers and sizes; device pointers are borrowed
+ * (the caller owns them and keeps them alive for the call), `stream` is a
+ * hipStream_t (NULL = the legacy default stream).  All work is enqueued
+ * asynchronously on that stream unless stated otherwise.
+ *
+ * Errors: every int-returning function returns FKV_OK (0) on success and a
+ * negative FKV_E* code otherwise; fkv_last_error() gives the message of the
+ * calling thread's last failure.  No C++ exception crosses this boundary.
+ * The reference raises std::runtime_error / silently ignores bad input in
+ * the places noted per entry point; here the same conditions return codes.
+ */
+#ifndef FKV_H
+#define FKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FKV_OK 0
+#define FKV_EINVAL -1   /* bad argument / shape */
+#define FKV_EHIP -2     /* HIP runtime error */
+#define FKV_ENOMEM -3   /* device allocation failed */
+#define FKV_EDATA -4    /* input data outside what the reference can produce */
+
+/* element types accepted where noted */
+#define FKV_F16 0
+#define FKV_BF16 1
+#define FKV_F32 2
+
+/* ---------------------------------------------------------------------- */
+/* library                                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces foveated_ext.is_available (csrc/bindings.cpp:158-159): 1 when a
+ * gfx950 device is visible to the HIP runtime, else 0. */
+int fkv_is_available(void);
+/* Message of the calling thread's last failed call ("" if none). */
+const char* fkv_last_error(void);
+/* ABI version (major*100 + minor). */
+int fkv_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* tier configuration (csrc/foveated_compress.h:92-98, mlx_foveated.py:111-169) */
+/* ---------------------------------------------------------------------- */
+
+typedef struct fkv_tier_config {
+    double near_pct;           /* fraction of tokens kept in the fp16 near tier */
+    int32_t n_sinks;
+    int32_t window_size;
+    double promo_headroom_pct; /* near headroom as a fraction of R_actual */
+    int32_t promo_headroom_min;
+} fkv_tier_config;
+
+typedef struct fkv_tiers {
+    int32_t n_sinks, window, near_from_mid, far_count, r_actual, n_near_padded;
+    int32_t mid_start, mid_end, near_mid_start, headroom;
+} fkv_tiers;
+
+/* Replaces MLXTierConfig.tier_boundaries (mlx_foveated.py:128-169) and its
+ * C++ twin (csrc/foveated_compress.cpp:107-126).  Host-only, synchronous. */
+int fkv_tier_boundaries(const fkv_tier_config* cfg, int32_t S, fkv_tiers* out);
+
+/* ---------------------------------------------------------------------- */
+/* compression (CompressHandle, csrc/foveated_compress.cpp:95-227)          */
+/* ---------------------------------------------------------------------- */
+
+/* Compress one layer: keys/values (B,H,S,D) contiguous in `in_dtype`
+ * (converted to fp16 first, as astype(float16) at :129-130) into
+ *   near_k, near_v   (B,H,Npad,D) fp16, rows >= R_actual zero  (compress_foveal)
+ *   far_k            (B,H,F,D)    E4M3 codes                  (compress_fp8)
+ *   far_v            (B,H,F,D/2)  INT4, even dim in low nibble (compress_int4)
+ *   far_v_scale/zero (B,H,F)      fp16
+ *   near_valid       (H)          int32 = R_actual
+ *   archive_k/v      (B,H,F,D)    fp16 copy of the far rows (may be NULL)
+ * with Npad/F from fkv_tier_boundaries(cfg, S).  D must be 64 or 128.
+ * One fused pass over K and V. */
+int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, const void* values,
+                       int32_t in_dtype, int32_t B, int32_t H, int32_t S, int32_t D,
+                       void* near_k, void* near_v, uint8_t* far_k, uint8_t* far_v,
+                       void* far_v_scale, void* far_v_zero, int32_t* near_valid,
+                       void* archive_k, void* archive_v, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* fused attention handle (FoveatedHandle, csrc/foveated_attn.cpp:135-254)  */
+/* ---------------------------------------------------------------------- */
+
+typedef struct fkv_attn fkv_attn;
+
+/* Copies the static tier arrays into a private device blob (re-laid out
+ * for the gfx950 kernel), like FoveatedHandle's constructor (:135-162):
+ *   near_k/near_v (B,Hkv,Na,D) in near_dtype (fp16/bf16/f32)
+ *   far_k (B,Hkv,F,D) u8, far_v (B,Hkv,F,D/2) u8
+ *   far_v_scale/zero (B,Hkv,F) in sz_dtype, near_valid (Hkv) int32
+ * F may be 0.  Returns FKV_EDATA if far_k holds the E4M3 NaN codes
+ * 0x7F/0xFF, which the reference encoder never emits.  Synchronous. */
+int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
+                    const void* near_k, const void* near_v, int32_t near_dtype,
+                    const uint8_t* far_k, const uint8_t* far_v, const void* far_v_scale,
+                    const void* far_v_zero, int32_t sz_dtype, const int32_t* near_valid,
+                    float spike_margin, void* stream);
+
+/* Replaces FoveatedHandle::operator() (:164-240): query (B,Hq,1,D) in
+ * q_dtype, decode_k/v (B,Hkv,n_decode,D) fp16 (NULL when n_decode == 0).
+ * Writes out (B,Hq,D) fp16, spike_flags/spike_tokens (B,Hq) int32. */
+int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
+                  const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
+                  int32_t* spike_flags, int32_t* spike_tokens, void* stream);
+
+/* Replaces get_blob_info (:242-254): where promotions land. */
+typedef struct fkv_blob_info {
+    void* blob;               /* device base pointer */
+    uint64_t blob_bytes;
+    uint64_t near_k_offset;   /* [B*Hkv][Na_pad/64][D/8][64][8] fp16 tiles:
+                                 token t, dim d at ((t/64)*D/8 + d/8)*512 + (t%64)*8 + d%8 */
+    uint64_t near_v_offset;   /* (B,Hkv,Na_pad,D) fp16 rows */
+    uint64_t near_valid_offset; /* (Hkv) uint32 */
+    int32_t n_near_alloc;     /* Na: near slots per head incl. headroom */
+    int32_t n_far;
+    int32_t B, H_kv, D;
+} fkv_blob_info;
+int fkv_attn_blob_info(const fkv_attn* h, fkv_blob_info* out);
+
+/* Copies near_valid (Hkv uint32) to host memory (synchronous on stream). */
+int fkv_attn_read_near_valid(const fkv_attn* h, uint32_t* host_out, void* stream);
+
+void fkv_attn_destroy(fkv_attn* h);
+
+/* Decodes n (multiple of 4) E4M3 codes to fp16 with the converter the fused
+ * kernel uses (gfx950 v_cvt_scalef32_pk_f16_fp8).  Replaces the reference's
+ * decode LUT (csrc/kernels/foveated_attn.metal:237-253) for verification:
+ * equal on every code the reference encoder emits. */
+int fkv_e4m3_decode(const uint8_t* codes, void* out_f16, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FKV_H */

@@ -1,0 +1,105 @@
+"""C-ABI checks that need no GPU: the library loads, exports exactly what
+include/fkv.h declares, and its host-only entry points behave."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names |= set(re.findall(r"\b(fkv_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    # the Python binding covers every declared symbol
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    out = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
+    exported = set(re.findall(r"\bT (fkv_[a-z0-9_]+)\b", out))
+    assert declared <= exported
+
+
+def test_version_and_error_channel():
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+    assert lib.fkv_version() >= 100
+    # NULL config -> error code + message, no crash
+    rc = lib.fkv_tier_boundaries(None, 10, None)
+    assert rc == _lib.FKV_EINVAL
+    assert b"fkv_tier_boundaries" in lib.fkv_last_error()
+    # bad shapes rejected before any device work
+    h = ctypes.c_void_p()
+    rc = lib.fkv_attn_create(ctypes.byref(h), 1, 1, 96, 8, 8, None, None, 0, None, None, None, None, 0,
+                             None, 0.5, None)
+    assert rc == _lib.FKV_EINVAL and b"64 or 128" in lib.fkv_last_error()
+    rc = lib.fkv_attn_call(None, None, 0, 1, None, None, 0, None, None, None, None)
+    assert rc == _lib.FKV_EINVAL
+
+
+@pytest.mark.parametrize("S", [0, 1, 4, 36, 37, 100, 512, 1000, 4096, 16384, 32768, 65536, 100003])
+@pytest.mark.parametrize("pct,hmin", [(0.10, 8), (0.25, 4), (0.05, 0), (0.5, 8)])
+def test_tier_boundaries_c_matches_oracle_and_python(orc, S, pct, hmin):
+    from foveated_kv_amd import TierConfig, ext
+
+    c = ext.TierConfig()
+    c.near_pct = pct
+    c.promo_headroom_min = hmin
+    got = ext.tier_boundaries_c(c, S)
+    ref = orc.tier_boundaries(S, near_pct=pct, promo_headroom_min=hmin)
+    py = TierConfig(near_pct=pct, promo_headroom_min=hmin).tier_boundaries(S)
+    for key in ref:
+        assert got[key] == ref[key], key
+    for key in py:
+        assert py[key] == ref[key], key
+
+
+def test_tier_config_validation():
+    from foveated_kv_amd import MLXTierConfig, TierConfig
+
+    assert MLXTierConfig is TierConfig
+    with pytest.raises(ValueError, match="compress_method"):
+        TierConfig(compress_method="invalid")
+    assert TierConfig().compress_method == "fp8"
+    from foveated_kv_amd import ext
+
+    assert ext.TierConfig().promo_headroom_min == 4  # C++ default, foveated_compress.h:97
+
+
+def test_cpu_tensors_are_rejected():
+    import torch
+
+    from foveated_kv_amd import ext
+
+    x = torch.zeros((1, 1, 8, 64), dtype=torch.float16)
+    with pytest.raises(TypeError, match="ROCm device"):
+        ext.CompressHandle().compress_layer(x, x)
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    from foveated_kv_amd import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "_load_error", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libfkv.so"))
+    with pytest.raises(_lib.FkvLibraryError, match="not built"):
+        _lib.load()
+    from foveated_kv_amd import ext
+
+    assert ext.is_available() is False

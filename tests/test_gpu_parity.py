@@ -1,0 +1,293 @@
+"""GPU parity: the HIP library (through the C ABI) against the CPU oracle.
+
+Codes and tier partitions must be bit-exact; attention outputs within
+max-abs 2e-3 and cosine >= 0.9999 of the oracle (kernel semantics and the
+reference dequant+SDPA formulation); spike flags/tokens equal except where
+the oracle itself shows a near tie.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+COS = 0.9999
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def fkv():
+    import foveated_kv_amd
+    from foveated_kv_amd import _lib
+
+    _lib.load()
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    assert foveated_kv_amd.is_available(), "libfkv.so loaded but no gfx950 device"
+    return foveated_kv_amd
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _cfg(fkv, **kw):
+    from foveated_kv_amd import ext
+
+    c = ext.TierConfig()
+    c.promo_headroom_min = kw.get("promo_headroom_min", 8)
+    return c
+
+
+# ---------------------------------------------------------------------------
+# compression: bit-exact vs the oracle
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,H,S,D,dtype", [
+    (1, 2, 512, 64, "f16"), (1, 8, 4096, 128, "f16"), (2, 2, 300, 128, "bf16"),
+    (1, 2, 700, 64, "f32"), (1, 1, 37, 128, "f16"), (1, 2, 20, 64, "f16"), (3, 3, 1000, 128, "f16"),
+])
+def test_compress_bit_exact(fkv, orc, B, H, S, D, dtype):
+    from foveated_kv_amd import ext, synthetic
+
+    _flush(f"compress B={B} H={H} S={S} D={D} {dtype}")
+    k, v = synthetic.make_kv(B, H, S, D, seed=S + D)
+    if dtype == "bf16":
+        kt = torch.from_numpy(k.astype(np.float32)).to(torch.bfloat16)
+        vt = torch.from_numpy(v.astype(np.float32) * 3).to(torch.bfloat16)
+        k16 = kt.float().numpy().astype(np.float16)
+        v16 = vt.float().numpy().astype(np.float16)
+    elif dtype == "f32":
+        rng = np.random.default_rng(1)
+        kf = rng.standard_normal((B, H, S, D)).astype(np.float32)
+        vf = rng.standard_normal((B, H, S, D)).astype(np.float32)
+        kt, vt = torch.from_numpy(kf), torch.from_numpy(vf)
+        k16, v16 = kf.astype(np.float16), vf.astype(np.float16)
+    else:
+        kt, vt = torch.from_numpy(k), torch.from_numpy(v)
+        k16, v16 = k, v
+    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(kt.cuda(), vt.cuda())
+    torch.cuda.synchronize()
+    ref = orc.compress_layer(k16, v16)
+    assert np.array_equal(_np(cl.near_k).view(np.uint16), ref["near_k"].view(np.uint16))
+    assert np.array_equal(_np(cl.near_v).view(np.uint16), ref["near_v"].view(np.uint16))
+    assert np.array_equal(_np(cl.far_k), ref["far_k"])
+    assert np.array_equal(_np(cl.far_v), ref["far_v"])
+    assert np.array_equal(_np(cl.far_v_scale).view(np.uint16), ref["far_v_scale"].view(np.uint16))
+    assert np.array_equal(_np(cl.far_v_zero).view(np.uint16), ref["far_v_zero"].view(np.uint16))
+    assert np.array_equal(_np(cl.near_valid), ref["near_valid"])
+    assert np.array_equal(_np(cl.archive_k).view(np.uint16), ref["archive_k"].view(np.uint16))
+    assert np.array_equal(_np(cl.archive_v).view(np.uint16), ref["archive_v"].view(np.uint16))
+    assert cl.n_near_actual == ref["tb"]["R_actual"]
+
+
+def test_compress_exhaustive_fp16_patterns(fkv, orc):
+    """Every fp16 bit pattern through the GPU E4M3 encoder, plus INT4 rows
+    with exact .5 ties, constant rows and saturating magnitudes."""
+    from foveated_kv_amd import ext
+
+    D, S = 128, 1024
+    tb = orc.tier_boundaries(S)
+    F = tb["far_count"]
+    assert F * D >= 65536
+    rng = np.random.default_rng(9)
+    k = rng.standard_normal((1, 1, S, D)).astype(np.float16)
+    pats = np.arange(65536, dtype=np.uint16).view(np.float16)
+    far = k[0, 0, tb["mid_start"]:tb["mid_start"] + F].reshape(-1)
+    far[:65536] = pats
+    k[0, 0, tb["mid_start"]:tb["mid_start"] + F] = far.reshape(F, D)
+    v = rng.standard_normal((1, 1, S, D)).astype(np.float16)
+    fv = v[0, 0, tb["mid_start"]:tb["mid_start"] + F]
+    fv[0] = 0.0
+    fv[0, 1] = 15.0
+    fv[0, 2:10] = np.arange(8) + 0.5  # exact ties with scale 1
+    fv[1] = 3.0  # constant row
+    fv[2] = np.linspace(-60000, 60000, D).astype(np.float16)  # near fp16 max
+    fv[3] = np.linspace(-1e-6, 1e-6, D).astype(np.float16)  # subnormal range
+    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    torch.cuda.synchronize()
+    ref = orc.compress_layer(k, v)
+    assert np.array_equal(_np(cl.far_k), ref["far_k"])
+    assert np.array_equal(_np(cl.far_v), ref["far_v"])
+    assert np.array_equal(_np(cl.far_v_scale).view(np.uint16), ref["far_v_scale"].view(np.uint16))
+    assert np.array_equal(_np(cl.far_v_zero).view(np.uint16), ref["far_v_zero"].view(np.uint16))
+
+
+# ---------------------------------------------------------------------------
+# fused attention
+# ---------------------------------------------------------------------------
+
+def _far_scores(orc, c, q):
+    """Exact far scores per (b, q head) from the oracle's LUT decode."""
+    lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    B, Hq, D = q.shape
+    Hkv = c["far_k"].shape[1]
+    G = Hq // Hkv
+    inv = np.float32(1.0) / np.sqrt(np.float32(D))
+    out = []
+    for b in range(B):
+        row = []
+        for h in range(Hq):
+            qs = (q[b, h].astype(np.float32) * inv).astype(np.float64)
+            row.append(lut[c["far_k"][b, h // G]] @ qs)
+        out.append(row)
+    return out
+
+
+def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16, spikes=0.0,
+                  margin=10.0, near_valid_delta=0, check_formulation=True, heavy_tail=False):
+    from foveated_kv_amd import ext, synthetic
+
+    _flush(f"attention B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} seed={seed} "
+           f"q={q_dtype} spikes={spikes} nv_delta={near_valid_delta}")
+    k, v = synthetic.make_kv(B, Hkv, S, D, seed, heavy_tail=heavy_tail)
+    q = synthetic.make_query(B, Hq, D, seed)
+    tb = orc.tier_boundaries(S)
+    synthetic.inject_spikes(k, q, tb["mid_start"], tb["far_count"], spikes, seed)
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
+    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                                      with_archive=False)
+    nv = cl.near_valid.clone()
+    if near_valid_delta:
+        # promoted-looking rows: write copies of far rows into the headroom
+        npad = cl.near_k.shape[2]
+        for hh in range(Hkv):
+            add = min(near_valid_delta * (hh + 1), npad - int(nv[hh]))
+            src = torch.from_numpy(k[:, hh, tb["mid_start"]:tb["mid_start"] + add]).cuda()
+            cl.near_k[:, hh, int(nv[hh]):int(nv[hh]) + add] = src
+            cl.near_v[:, hh, int(nv[hh]):int(nv[hh]) + add] = src * 0.5
+            nv[hh] += add
+    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero, nv,
+                           spike_margin=margin)
+    qt = torch.from_numpy(q).cuda().to(q_dtype)
+    dkt = torch.from_numpy(dk).cuda() if dk is not None else None
+    dvt = torch.from_numpy(dv).cuda() if dv is not None else None
+    out, flags, tokens = h(qt[:, :, None, :], dkt, dvt)
+    torch.cuda.synchronize()
+    out = _np(out)[:, :, 0].astype(np.float64)
+    c = {n: _np(getattr(cl, n)) for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale", "far_v_zero")}
+    q16 = _np(qt.to(torch.float16))
+    ko, kf, kt, mf, mn = orc.attend_kernel(q16, c["near_k"], c["near_v"], _np(nv), c["far_k"], c["far_v"],
+                                           c["far_v_scale"], c["far_v_zero"], dk, dv, spike_margin=margin)
+    assert np.all(np.isfinite(out))
+    err = np.abs(out - ko).max()
+    cos = orc.cosine(out, ko)
+    _flush(f"  vs kernel oracle: max-abs {err:.3e} cos {cos:.8f}")
+    assert err <= ATOL and cos >= COS
+    if check_formulation and near_valid_delta == 0:
+        fo = orc.attend_formulation(q16, c["near_k"], c["near_v"], _np(nv), c["far_k"], c["far_v"],
+                                    c["far_v_scale"], c["far_v_zero"], dk, dv)
+        err_f = np.abs(out - fo).max()
+        cos_f = orc.cosine(out, fo)
+        _flush(f"  vs formulation:   max-abs {err_f:.3e} cos {cos_f:.8f}")
+        assert err_f <= ATOL and cos_f >= COS
+    flags, tokens = _np(flags), _np(tokens)
+    fs = _far_scores(orc, c, q16) if c["far_k"].shape[2] else None
+    for b in range(B):
+        for hq in range(Hq):
+            if tokens[b, hq] != kt[b, hq]:
+                # allowed only on a near tie of the two candidates' exact scores
+                s = fs[b][hq]
+                assert abs(s[tokens[b, hq]] - s[kt[b, hq]]) <= 1e-5 * (1 + abs(s.max())), (b, hq)
+            if flags[b, hq] != kf[b, hq]:
+                assert abs(mf[b, hq] - mn[b, hq] - margin) < 1e-4, (b, hq)
+    return out, flags, tokens, kf
+
+
+@pytest.mark.parametrize("args", [
+    dict(B=1, Hq=14, Hkv=2, D=64, S=512, n_dec=16, seed=1),      # config 1
+    dict(B=1, Hq=32, Hkv=8, D=128, S=4096, n_dec=64, seed=2, heavy_tail=True),  # config 2
+    dict(B=1, Hq=4, Hkv=4, D=64, S=256, n_dec=0, seed=3),        # no GQA
+    dict(B=2, Hq=8, Hkv=2, D=128, S=512, n_dec=7, seed=4),
+    dict(B=1, Hq=64, Hkv=8, D=128, S=2048, n_dec=3, seed=5),     # G = 8
+    dict(B=1, Hq=32, Hkv=2, D=64, S=700, n_dec=5, seed=6),       # G = 16: two head groups
+    dict(B=1, Hq=6, Hkv=2, D=128, S=36, n_dec=2, seed=7),        # no far tier
+    dict(B=1, Hq=8, Hkv=2, D=64, S=40, n_dec=0, seed=8),         # 4 far tokens
+    dict(B=3, Hq=12, Hkv=4, D=64, S=333, n_dec=70, seed=9),      # ragged tiles
+])
+def test_attention_parity(fkv, orc, args):
+    run_attention(fkv, orc, **args)
+
+
+def test_attention_bf16_and_f32_query(fkv, orc):
+    run_attention(fkv, orc, 1, 8, 2, 128, 600, 4, seed=11, q_dtype=torch.bfloat16, check_formulation=False)
+    run_attention(fkv, orc, 1, 8, 2, 64, 600, 4, seed=12, q_dtype=torch.float32, check_formulation=False)
+
+
+def test_attention_spikes(fkv, orc):
+    _, flags, tokens, kf = run_attention(fkv, orc, 2, 16, 4, 128, 2048, 8, seed=13, spikes=0.02)
+    assert kf.sum() > 0 and flags.sum() > 0  # the injected tokens are flagged
+
+
+def test_attention_uneven_near_valid(fkv, orc):
+    """Per-head near_valid after promotions (kernel reads near_valid[kv_head])."""
+    run_attention(fkv, orc, 1, 8, 2, 128, 1000, 3, seed=14, near_valid_delta=5)
+
+
+def test_attention_split_invariance(fkv, orc):
+    outs = []
+    for target in ("1", "64", "1024", "4096"):
+        os.environ["FKV_TARGET_WGS"] = target
+        try:
+            outs.append(run_attention(fkv, orc, 1, 8, 2, 128, 3000, 5, seed=15, check_formulation=False))
+        finally:
+            del os.environ["FKV_TARGET_WGS"]
+    for o, f, t, _ in outs[1:]:
+        assert np.abs(o - outs[0][0]).max() < 5e-4
+        assert np.array_equal(t, outs[0][2])
+
+
+def test_attention_config3_8k(fkv, orc):
+    run_attention(fkv, orc, 8, 32, 8, 128, 8192, 0, seed=16, spikes=0.02, check_formulation=False)
+
+
+def test_attention_repeat_calls_stable(fkv, orc):
+    """Split counters self-reset: back-to-back calls give identical results."""
+    from foveated_kv_amd import ext, synthetic
+
+    k, v = synthetic.make_kv(2, 4, 3000, 128, 17)
+    q = torch.from_numpy(synthetic.make_query(2, 16, 128, 17)).cuda()
+    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                           cl.near_valid, spike_margin=10.0)
+    first = [t.clone() for t in h(q[:, :, None])]
+    for _ in range(5):
+        again = h(q[:, :, None])
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)
+
+
+def test_handle_rejects_nan_codes(fkv):
+    from foveated_kv_amd import _lib, ext
+
+    B, H, Na, F, D = 1, 1, 8, 64, 64
+    nk = torch.zeros((B, H, Na, D), dtype=torch.float16, device="cuda")
+    fk = torch.zeros((B, H, F, D), dtype=torch.uint8, device="cuda")
+    fk[0, 0, 3, 5] = 0x7F
+    fv = torch.zeros((B, H, F, D // 2), dtype=torch.uint8, device="cuda")
+    sc = torch.ones((B, H, F), dtype=torch.float16, device="cuda")
+    with pytest.raises(_lib.FkvDataError):
+        ext.FoveatedHandle(nk, nk, fk, fv, sc, sc, torch.full((H,), Na, dtype=torch.int32, device="cuda"))
+
+
+def test_e4m3_converter_matches_reference_lut(fkv, orc):
+    """The fused kernel's fp8 converter against the reference decode LUT on
+    all 256 codes: equal on every code the encoder emits (228), and the blob
+    packer zeroes exponent-0 codes as the LUT does."""
+    from foveated_kv_amd import _lib
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).cuda()
+    out = torch.empty(256, dtype=torch.float16, device="cuda")
+    _lib.check(_lib.load().fkv_e4m3_decode(_lib.ptr(codes), _lib.ptr(out), 256, _lib.stream_ptr()),
+               "fkv_e4m3_decode")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).view(np.uint16)
+    reach = np.unique(orc.encode_fp8(np.arange(65536, dtype=np.uint16)))
+    assert np.array_equal(got[reach], lut[reach])
