@@ -5,29 +5,34 @@
 // (csrc/foveated_attn.cpp:83-254, csrc/kernels/foveated_attn.metal:181-432).
 //
 // Work decomposition: one workgroup of 4 waves per (batch, kv_head, split)
-// serves every query head of the GQA group, so each compressed byte is read
-// from HBM once.  A wave processes 64-token tiles:
-//   * scores are token-parallel (lane = token): K is widened to fp16 in
-//     registers (E4M3 -> fp16 with the native converter, exact) and dotted
-//     with the unscaled fp16 query via v_dot2_f32_f16 (exact products, fp32
-//     accumulation); the 1/sqrt(D) scale is applied to the fp32 score;
-//   * online softmax per head with one max reduction per tile;
-//   * P.V is d-parallel: lane = (phase, 8-dim block), token pairs are packed
-//     into half2 and accumulated with v_dot2_f32_f16 into fp32.  INT4 codes
-//     are widened exactly to fp16 (16 + c) by bit insertion; the weights are
-//     p*scale, the values re-centred to (c - 7.5), and the zero point plus
-//     the constant offsets are folded into per-head scalar terms.
-// Split partials are merged by a small second kernel (one workgroup per
-// (batch, kv_head, head group)).
+// serves up to 16 query heads of the GQA group, so each compressed byte is
+// read from HBM once.  Both contractions of one kv head run on the matrix
+// cores with v_mfma_f32_16x16x16_f16 (fp16 operands, fp32 accumulation):
+//   scores  S[t][h] = K[t][:] . q[h][:]      A = K (16 tokens x 16 dims),
+//                                             B = q (16 dims x 16 heads)
+//   output  O[d][h] += V[t][d]^T . P[t][h]    A = V^T (16 dims x 16 tokens),
+//                                             B = P (16 tokens x 16 heads)
+// The score tile comes out of the first MFMA in exactly the register layout
+// the second one takes as B, so softmax weights never leave registers.
+// E4M3 keys are widened to fp16 with the native converter (exact); INT4
+// values are widened exactly by inserting the nibble into an fp16 mantissa
+// (16 + c), weights are p*scale, and the zero point and constant offsets
+// are folded into per-head scalars.  The fp16 query is used unscaled (exact
+// products); 1/sqrt(D) is applied to the fp32 scores.
+// The blob stores every tier pre-arranged in these operand layouts so each
+// lane's operand bytes are contiguous and every wave load is a contiguous
+// 1 KB.  Split partials are merged by a small second kernel.
 #include <hip/hip_runtime.h>
 
 #include <climits>
 #include <cmath>
 #include <cstring>
-#include <vector>
 
-#include "fkv_common.h"
 #include "fkv_attn.h"
+#include "fkv_common.h"
+
+typedef _Float16 fkv_h4 __attribute__((ext_vector_type(4)));
+typedef float fkv_f4 __attribute__((ext_vector_type(4)));
 
 namespace fkv {
 
@@ -73,95 +78,104 @@ __device__ inline uint16_t load_as_f16(const void* p, int64_t i, int dtype) {
     return f2h(((const float*)p)[i]);
 }
 
-// near K -> token-parallel tiles: [tile][d/8][lane][8 halves]; near V -> rows.
-// One thread per (bkv, token, 8-dim chunk).  Rows >= Na are zero.
+// One thread per (bkv, 16-token group, lane).  Near K lane (kg, m) holds
+// token m of the group, dims 16s + 4kg + i (s = 0..D/16-1, i = 0..3); near V
+// lane (kg, m) holds dim 16j + m of tokens 4kg + i.  Slots >= Na are zero.
 __global__ void pack_near_kernel(const void* __restrict__ nk, const void* __restrict__ nv,
                                  int dtype, BlobLayout L, uint8_t* __restrict__ blob) {
-    const int D = L.D, C = D / 8;
-    const int64_t n = (int64_t)L.B * L.Hkv * L.Na_pad * C;
+    const int D = L.D, NB = D / 16;
+    const int64_t groups = L.Na_pad / 16;
+    const int64_t n = (int64_t)L.B * L.Hkv * groups * kWave;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int c = (int)(i % C);
-        const int64_t r = i / C;
-        const int t = (int)(r % L.Na_pad);
-        const int64_t bkv = r / L.Na_pad;
-        uint16_t kk[8], vv[8];
-        for (int e = 0; e < 8; e++) {
-            if (t < L.Na) {
-                const int64_t src = (bkv * L.Na + t) * D + c * 8 + e;
-                kk[e] = load_as_f16(nk, src, dtype);
-                vv[e] = load_as_f16(nv, src, dtype);
-            } else {
-                kk[e] = 0;
-                vv[e] = 0;
+        const int lane = (int)(i % kWave);
+        const int64_t r = i / kWave;
+        const int grp = (int)(r % groups);
+        const int64_t bkv = r / groups;
+        const int m = lane & 15, kg = lane >> 4;
+        uint16_t* kd = (uint16_t*)(blob + L.near_k) + bkv * (int64_t)L.Na_pad * D +
+                       (int64_t)grp * 16 * D + lane * (D / 4);
+        uint16_t* vd = (uint16_t*)(blob + L.near_v) + bkv * (int64_t)L.Na_pad * D +
+                       (int64_t)grp * 16 * D + lane * (D / 4);
+        const int tk = grp * 16 + m;
+        for (int s = 0; s < NB; s++)
+            for (int e = 0; e < 4; e++)
+                kd[s * 4 + e] = tk < L.Na ? load_as_f16(nk, (bkv * L.Na + tk) * D + 16 * s + 4 * kg + e, dtype) : 0;
+        for (int j = 0; j < NB; j++)
+            for (int e = 0; e < 4; e++) {
+                const int tv = grp * 16 + 4 * kg + e;
+                vd[j * 4 + e] = tv < L.Na ? load_as_f16(nv, (bkv * L.Na + tv) * D + 16 * j + m, dtype) : 0;
             }
-        }
-        uint16_t* kt = (uint16_t*)(blob + L.near_k) +
-                       bkv * (int64_t)L.Na_pad * D + (int64_t)(t / kTile) * kTile * D +
-                       (int64_t)c * kTile * 8 + (t % kTile) * 8;
-        uint16_t* vr = (uint16_t*)(blob + L.near_v) + (bkv * L.Na_pad + t) * D + c * 8;
-        for (int e = 0; e < 8; e++) {
-            kt[e] = kk[e];
-            vr[e] = vv[e];
-        }
     }
 }
 
-// far K codes -> [tile][d/16][lane][16 codes]; exponent-0 codes are written
-// as signed zero (the reference LUT ignores their mantissa); NaN codes are
-// reported through *bad.
+// Far K codes in the same operand layout as near K (bytes); exponent-0
+// codes are written as signed zero (the reference LUT ignores their
+// mantissa); NaN codes 0x7F/0xFF are reported through *bad.
 __global__ void pack_far_k_kernel(const uint8_t* __restrict__ fk, BlobLayout L,
                                   uint8_t* __restrict__ blob, unsigned* __restrict__ bad) {
-    const int D = L.D, C = D / 16;
-    const int64_t n = (int64_t)L.B * L.Hkv * L.F_pad * C;
+    const int D = L.D, NB = D / 16;
+    const int64_t groups = L.F_pad / 16;
+    const int64_t n = (int64_t)L.B * L.Hkv * groups * kWave;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int c = (int)(i % C);
-        const int64_t r = i / C;
-        const int t = (int)(r % L.F_pad);
-        const int64_t bkv = r / L.F_pad;
-        uint8_t* dst = blob + L.far_k + bkv * (int64_t)L.F_pad * D + (int64_t)(t / kTile) * kTile * D +
-                       (int64_t)c * kTile * 16 + (t % kTile) * 16;
-        for (int e = 0; e < 16; e++) {
-            uint8_t b = 0;
-            if (t < L.F) {
-                b = fk[(bkv * L.F + t) * D + c * 16 + e];
-                if ((b & 0x7F) == 0x7F) atomicOr(bad, 1u);
-                if ((b & 0x78) == 0) b &= 0x80;
+        const int lane = (int)(i % kWave);
+        const int64_t r = i / kWave;
+        const int grp = (int)(r % groups);
+        const int64_t bkv = r / groups;
+        const int m = lane & 15, kg = lane >> 4;
+        const int t = grp * 16 + m;
+        uint8_t* dst = blob + L.far_k + bkv * (int64_t)L.F_pad * D + (int64_t)grp * 16 * D + lane * (D / 4);
+        for (int s = 0; s < NB; s++)
+            for (int e = 0; e < 4; e++) {
+                uint8_t b = 0;
+                if (t < L.F) {
+                    b = fk[(bkv * L.F + t) * D + 16 * s + 4 * kg + e];
+                    if ((b & 0x7F) == 0x7F) atomicOr(bad, 1u);
+                    if ((b & 0x78) == 0) b &= 0x80;
+                }
+                dst[s * 4 + e] = b;
             }
-            dst[e] = b;
-        }
     }
 }
 
-// far V nibbles -> per group of GS = 4*NPH tokens: [group][lane=(ph,qb)][4 x 4 bytes]
-// where dword i holds dims 8qb..8qb+7 of token ph + NPH*i; scale/zero -> half2.
+// Far V nibbles: lane (kg, m) of a 16-token group holds D/32 dwords; dword u
+// covers blocks 2u (bits 0-7, 16-23) and 2u+1 (bits 8-15, 24-31) at dim
+// 16*block + m, with token 4kg+e at bit 16*(e&1) + 4*(e>>1) of its byte pair.
+// Scale/zero -> one u32 per token.
 __global__ void pack_far_v_kernel(const uint8_t* __restrict__ fv, const void* __restrict__ fvs,
                                   const void* __restrict__ fvz, int sz_dtype, BlobLayout L,
                                   uint8_t* __restrict__ blob) {
-    const int D = L.D, NQ = D / 8, NPH = kWave / NQ, GS = 4 * NPH;
-    const int64_t n = (int64_t)L.B * L.Hkv * L.F_pad * NQ;  // one 4-byte block per thread
+    const int D = L.D, NW = D / 32;
+    const int64_t groups = L.F_pad / 16;
+    const int64_t n = (int64_t)L.B * L.Hkv * groups * kWave;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int qb = (int)(i % NQ);
-        const int64_t r = i / NQ;
-        const int t = (int)(r % L.F_pad);
-        const int64_t bkv = r / L.F_pad;
-        uint32_t word = 0;
-        if (t < L.F) {
-            const uint8_t* src = fv + (bkv * L.F + t) * (D / 2) + qb * 4;
-            word = (uint32_t)src[0] | ((uint32_t)src[1] << 8) | ((uint32_t)src[2] << 16) |
-                   ((uint32_t)src[3] << 24);
+        const int lane = (int)(i % kWave);
+        const int64_t r = i / kWave;
+        const int grp = (int)(r % groups);
+        const int64_t bkv = r / groups;
+        const int m = lane & 15, kg = lane >> 4;
+        uint32_t* dst = (uint32_t*)(blob + L.far_v + bkv * (int64_t)L.F_pad * D / 2) +
+                        (int64_t)grp * 2 * D + lane * NW;
+        for (int u = 0; u < NW; u++) {
+            uint32_t w = 0;
+            for (int bp = 0; bp < 2; bp++)
+                for (int e = 0; e < 4; e++) {
+                    const int t = grp * 16 + 4 * kg + e;
+                    const int d = (2 * u + bp) * 16 + m;
+                    uint32_t c = 0;
+                    if (t < L.F) c = (fv[(bkv * L.F + t) * (D / 2) + d / 2] >> (4 * (d & 1))) & 15u;
+                    w |= c << (bp * 8 + (e & 1) * 16 + (e >> 1) * 4);
+                }
+            dst[u] = w;
         }
-        const int j = t / GS, rr = t % GS, ph = rr % NPH, ii = rr / NPH;
-        uint32_t* dst = (uint32_t*)(blob + L.far_v + bkv * (int64_t)L.F_pad * D / 2);
-        dst[(int64_t)j * (kWave * 4) + (ph * NQ + qb) * 4 + ii] = word;
-        if (qb == 0) {
+        if (kg == 0) {
+            const int t = grp * 16 + m;
             uint32_t sz = 0;
             if (t < L.F) {
                 const int64_t k = bkv * L.F + t;
-                sz = (uint32_t)load_as_f16(fvs, k, sz_dtype) |
-                     ((uint32_t)load_as_f16(fvz, k, sz_dtype) << 16);
+                sz = (uint32_t)load_as_f16(fvs, k, sz_dtype) | ((uint32_t)load_as_f16(fvz, k, sz_dtype) << 16);
             }
             ((uint32_t*)(blob + L.far_sz))[bkv * L.F_pad + t] = sz;
         }
@@ -202,233 +216,144 @@ __global__ void cast_to_f16_kernel(const void* __restrict__ src, int dtype, int6
 // Attention kernel
 // ---------------------------------------------------------------------------
 
+constexpr int kHeads = 16;  // query heads per workgroup row (MFMA N)
+constexpr int kHdr = 5;     // record header: m, l, min_near, max_far, first argmax
+constexpr int kMaxSplits = 64;
+
 struct AttnArgs {
     const uint8_t* blob;
     BlobLayout L;
     const uint16_t* q;      // (B, Hq, D) fp16
-    const uint16_t* dec_k;  // (B, Hkv, n_dec, D) fp16
+    const uint16_t* dec_k;  // (B, Hkv, n_dec, D) fp16 rows
     const uint16_t* dec_v;
     int n_dec;
     int Hq;
-    int G;          // query heads per kv head
-    int head_groups;  // workgroup rows per kv head (G > kMaxG)
+    int G;            // query heads per kv head
+    int head_groups;  // workgroup rows per kv head (ceil(G / 16))
     int num_splits;
     float spike_margin;
     float inv_sqrt_d;
     uint16_t* out;  // (B, Hq, D) fp16
     int32_t* flags;
     int32_t* tokens;
-    float* ws;          // split partials
+    float* ws;  // split partials: [row][split][ng][kHdr + D]
 };
 
-// Per-head partial record in LDS / workspace: m, l, min_near, max_far, arg, acc[D]
-template <int D>
-struct Rec {
-    static constexpr int kHdr = 5;
-    static constexpr int kSize = kHdr + D;
-};
-
-template <int D>
-__device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int GG_, int b, int head0, int ng);
-
-template <int D, int GG>
-struct WaveState {
-    float m[GG];
-    float lsum[GG];
-    float zsum[GG];
-    float wsum[GG];  // sum of the fp16-rounded far weights (removes the +16 decode offset)
-    float mn[GG];
-    float mx[GG];
-    int arg[GG];
-    float acc[GG][8];
-};
-
-// Tile kinds in the virtual sequence [near | far | decode].
-enum TileKind { kNear = 0, kFar = 1, kDec = 2 };
-
-template <int D, int GG>
-__device__ inline void score_tile(const AttnArgs& a, int kind, int tile, int64_t bkv,
-                                  int count, const fkv_h2* __restrict__ qs, float (&s)[GG],
-                                  uint32_t& sz) {
-    const int lane = threadIdx.x % kWave;
-    const int tok = tile * kTile + lane;
-    const bool valid = tok < count;
-#pragma unroll
-    for (int g = 0; g < GG; g++) s[g] = 0.f;
-    sz = 0;
-    if (kind == kFar) {
-        constexpr int C = D / 16;
-        const uint4* kt = (const uint4*)(a.blob + a.L.far_k) +
-                          (bkv * a.L.F_pad + (int64_t)tile * kTile) * D / 16 + lane;
-        uint4 kc[C];
-#pragma unroll
-        for (int c = 0; c < C; c++) kc[c] = kt[c * kTile];
-        sz = ((const uint32_t*)(a.blob + a.L.far_sz))[bkv * a.L.F_pad + tok];
-#pragma unroll
-        for (int c = 0; c < C; c++) {
-            fkv_h2 k2[8];
-            k2[0] = e4m3x2_to_h2(kc[c].x, false);
-            k2[1] = e4m3x2_to_h2(kc[c].x, true);
-            k2[2] = e4m3x2_to_h2(kc[c].y, false);
-            k2[3] = e4m3x2_to_h2(kc[c].y, true);
-            k2[4] = e4m3x2_to_h2(kc[c].z, false);
-            k2[5] = e4m3x2_to_h2(kc[c].z, true);
-            k2[6] = e4m3x2_to_h2(kc[c].w, false);
-            k2[7] = e4m3x2_to_h2(kc[c].w, true);
-#pragma unroll
-            for (int g = 0; g < GG; g++) {
-                uint4 q0, q1;
-                __builtin_memcpy(&q0, qs + g * (D / 2) + c * 8, 16);
-                __builtin_memcpy(&q1, qs + g * (D / 2) + c * 8 + 4, 16);
-                float acc = s[g];
-                acc = dot2(as_h2(q0.x), k2[0], acc);
-                acc = dot2(as_h2(q0.y), k2[1], acc);
-                acc = dot2(as_h2(q0.z), k2[2], acc);
-                acc = dot2(as_h2(q0.w), k2[3], acc);
-                acc = dot2(as_h2(q1.x), k2[4], acc);
-                acc = dot2(as_h2(q1.y), k2[5], acc);
-                acc = dot2(as_h2(q1.z), k2[6], acc);
-                acc = dot2(as_h2(q1.w), k2[7], acc);
-                s[g] = acc;
-            }
-        }
-    } else {
-        constexpr int C = D / 8;
-        const uint4* base;
-        int64_t stride;  // in uint4 between chunks
-        if (kind == kNear) {
-            base = (const uint4*)(a.blob + a.L.near_k) +
-                   (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D / 8 + lane;
-            stride = kTile;
-        } else {
-            base = (const uint4*)(a.dec_k + (bkv * a.n_dec + (valid ? tok : 0)) * D);
-            stride = 1;
-        }
-        if (valid || kind == kNear) {
-#pragma unroll
-            for (int half = 0; half < 2; half++) {
-                uint4 kc[C / 2];
-#pragma unroll
-                for (int c = 0; c < C / 2; c++) kc[c] = base[(half * (C / 2) + c) * stride];
-#pragma unroll
-                for (int c = 0; c < C / 2; c++) {
-                    const int cc = half * (C / 2) + c;
-#pragma unroll
-                    for (int g = 0; g < GG; g++) {
-                        uint4 q0;
-                        __builtin_memcpy(&q0, qs + g * (D / 2) + cc * 4, 16);
-                        float acc = s[g];
-                        acc = dot2(as_h2(q0.x), as_h2(kc[c].x), acc);
-                        acc = dot2(as_h2(q0.y), as_h2(kc[c].y), acc);
-                        acc = dot2(as_h2(q0.z), as_h2(kc[c].z), acc);
-                        acc = dot2(as_h2(q0.w), as_h2(kc[c].w), acc);
-                        s[g] = acc;
-                    }
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < GG; g++) s[g] = valid ? s[g] * a.inv_sqrt_d : -INFINITY;
+__device__ inline fkv_f4 mfma16(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-// d-parallel P.V over one tile.  pl: this wave's LDS weights [GG][64] (slot order).
-template <int D, int GG>
-__device__ inline void pv_tile(const AttnArgs& a, int kind, int tile, int64_t bkv, int count,
-                               const _Float16* __restrict__ pl, const uint4 (&vfar)[kTile / (4 * (kWave / (D / 8)))],
-                               WaveState<D, GG>& st) {
-    constexpr int NQ = D / 8, NPH = kWave / NQ, GS = 4 * NPH, NG = kTile / GS;
-    const int lane = threadIdx.x % kWave;
-    const int ph = lane / NQ, qb = lane % NQ;
-#pragma unroll
-    for (int j = 0; j < NG; j++) {
-        fkv_h2 v01[8], v23[8];
-        if (kind == kFar) {
-            // nibble c of tokens (A, B) -> half2 (16 + c_A, 16 + c_B): exponent-19
-            // fp16 with c in mantissa bits 6..9 (exact); the constant 16 is
-            // removed through the per-head weight sum (wsum) at the end.
-            const uint4 w = vfar[j];
-            uint32_t pr[2][2] = {{w.x, w.y}, {w.z, w.w}};
-#pragma unroll
-            for (int p = 0; p < 2; p++) {
-                const uint32_t A = pr[p][0], Bw = pr[p][1];
-                const uint32_t ulo = (A & 0xFFFFu) | (Bw << 16);
-                const uint32_t uhi = (A >> 16) | (Bw & 0xFFFF0000u);
-                fkv_h2* dst = p == 0 ? v01 : v23;
-                dst[0] = as_h2(((ulo << 6) & 0x03C003C0u) | 0x4C004C00u);
-                dst[1] = as_h2(((ulo << 2) & 0x03C003C0u) | 0x4C004C00u);
-                dst[2] = as_h2(((ulo >> 2) & 0x03C003C0u) | 0x4C004C00u);
-                dst[3] = as_h2(((ulo >> 6) & 0x03C003C0u) | 0x4C004C00u);
-                dst[4] = as_h2(((uhi << 6) & 0x03C003C0u) | 0x4C004C00u);
-                dst[5] = as_h2(((uhi << 2) & 0x03C003C0u) | 0x4C004C00u);
-                dst[6] = as_h2(((uhi >> 2) & 0x03C003C0u) | 0x4C004C00u);
-                dst[7] = as_h2(((uhi >> 6) & 0x03C003C0u) | 0x4C004C00u);
-            }
-        } else {
-            uint4 r[4];
-            const int t0 = tile * kTile + j * GS + ph;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = t0 + NPH * i;
-                if (kind == kNear) {
-                    r[i] = ((const uint4*)((const uint16_t*)(a.blob + a.L.near_v) +
-                                           (bkv * a.L.Na_pad + t) * D))[qb];
-                } else {
-                    r[i] = t < count ? ((const uint4*)(a.dec_v + (bkv * a.n_dec + t) * D))[qb]
-                                     : make_uint4(0, 0, 0, 0);
-                }
-            }
-            uint32_t ra[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
-            uint32_t rb[4] = {r[1].x, r[1].y, r[1].z, r[1].w};
-            uint32_t rc[4] = {r[2].x, r[2].y, r[2].z, r[2].w};
-            uint32_t rd[4] = {r[3].x, r[3].y, r[3].z, r[3].w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                v01[2 * k] = as_h2((ra[k] & 0xFFFFu) | (rb[k] << 16));
-                v01[2 * k + 1] = as_h2((ra[k] >> 16) | (rb[k] & 0xFFFF0000u));
-                v23[2 * k] = as_h2((rc[k] & 0xFFFFu) | (rd[k] << 16));
-                v23[2 * k + 1] = as_h2((rc[k] >> 16) | (rd[k] & 0xFFFF0000u));
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < GG; g++) {
-            uint2 pw;
-            __builtin_memcpy(&pw, pl + g * kTile + j * GS + ph * 4, 8);
-            const fkv_h2 p01 = as_h2(pw.x), p23 = as_h2(pw.y);
-#pragma unroll
-            for (int d = 0; d < 8; d++) {
-                float acc = st.acc[g][d];
-                acc = dot2(p01, v01[d], acc);
-                acc = dot2(p23, v23[d], acc);
-                st.acc[g][d] = acc;
-            }
-        }
-    }
+__device__ inline fkv_h4 h4_of(uint32_t lo, uint32_t hi) {
+    uint2 u = make_uint2(lo, hi);
+    return __builtin_bit_cast(fkv_h4, u);
 }
 
-template <int D, int GG>
+// Four E4M3 codes -> fp16 A operand (dims 4kg + 0..3 of one k-step)
+__device__ inline fkv_h4 e4m3x4(uint32_t w) {
+    return h4_of(as_u32(e4m3x2_to_h2(w, false)), as_u32(e4m3x2_to_h2(w, true)));
+}
+
+// INT4 dword -> A operand of block 2u (bp = 0) or 2u+1 (bp = 1): (16 + c)
+// for tokens 4kg + 0..3, exact.
+__device__ inline fkv_h4 int4x4(uint32_t w, int bp) {
+    const uint32_t a = bp ? ((w >> 2) & 0x03C003C0u) : ((w << 6) & 0x03C003C0u);
+    const uint32_t b = bp ? ((w >> 6) & 0x03C003C0u) : ((w << 2) & 0x03C003C0u);
+    return h4_of(a | 0x4C004C00u, b | 0x4C004C00u);
+}
+
+template <int D>
+struct Lane {
+    float m, lsum, zsum, wsum, mn, mx;
+    int arg;
+    fkv_f4 acc[D / 16];
+};
+
+template <int D>
+__device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b, int head0, int ng);
+
+// Online softmax + P.V for NG 16-token groups whose scores sc[g][e] (token
+// 4kg+e of group g, head m) are computed.  vop(g, j) yields the A operand
+// of block j of group g; far tiles pass their per-token scale/zero.
+template <int D, int NG, bool FAR, typename VOp>
+__device__ inline void softmax_pv(Lane<D>& st, const float (&sc)[NG][4], const uint32_t (&sz)[NG][4],
+                                  VOp vop) {
+    constexpr int NB = D / 16;
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) cmax = fmaxf(cmax, sc[g][e]);
+    cmax = fmaxf(cmax, wave_xor(cmax, 16));
+    cmax = fmaxf(cmax, wave_xor(cmax, 32));
+    const float m_new = fmaxf(st.m, cmax);
+    if (__builtin_amdgcn_ballot_w64(m_new > st.m)) {
+        const float alpha = m_new > st.m ? __expf(st.m - m_new) : 1.0f;
+        st.lsum *= alpha;
+        st.zsum *= alpha;
+        st.wsum *= alpha;
+#pragma unroll
+        for (int j = 0; j < NB; j++) st.acc[j] *= alpha;
+        st.m = m_new;
+    }
+    fkv_h4 bw[NG];
+    bool any = false;
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        _Float16 wh[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float s = sc[g][e];
+            float p = 0.f;
+            if (FAR) {
+                if (s >= st.m - 16.0f) p = __expf(s - st.m);  // score-gated V
+            } else if (s != -INFINITY) {
+                p = __expf(s - st.m);
+            }
+            st.lsum += p;
+            if (FAR) {
+                const float vs = h2f((uint16_t)(sz[g][e] & 0xFFFF));
+                const float vz = h2f((uint16_t)(sz[g][e] >> 16));
+                wh[e] = (_Float16)(p * vs);
+                // value = vs*(c - 7.5) + (vz + 7.5*vs); the MFMA sees wh*(16 + c)
+                st.zsum += p * (vz + 7.5f * vs);
+                st.wsum += (float)wh[e];
+            } else {
+                wh[e] = (_Float16)p;
+            }
+            any |= p > 0.f;
+        }
+        bw[g] = fkv_h4{wh[0], wh[1], wh[2], wh[3]};
+    }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole chunk gated away
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) st.acc[j] = mfma16(vop(g, j), bw[g], st.acc[j]);
+}
+
+template <int D>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-    constexpr int NQ = D / 8, NPH = kWave / NQ, GS = 4 * NPH;
-    constexpr int RS = Rec<D>::kSize;
-    __shared__ __attribute__((aligned(16))) fkv_h2 qs[GG * (D / 2)];
-    __shared__ __attribute__((aligned(16))) _Float16 pbuf[kWavesPerGroup][GG * kTile];
-    __shared__ float wrec[kWavesPerGroup][GG * RS];
+    constexpr int NB = D / 16;  // 16-dim k-steps of QK == 16-dim blocks of P.V
+    constexpr int RS = kHdr + D;
+    __shared__ float wrec[kWavesPerGroup][kHeads * RS];
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y / a.head_groups;
     const int hgrp = blockIdx.y % a.head_groups;
     const int b = blockIdx.z;
     const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
-    const int head0 = kvh * a.G + hgrp * GG;  // first q head of this workgroup
-    const int ng = min(GG, a.G - hgrp * GG);   // heads actually served
+    const int head0 = kvh * a.G + hgrp * kHeads;
+    const int ng = min(kHeads, a.G - hgrp * kHeads);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int m = lane & 15, kg = lane >> 4;
 
-    // query heads -> LDS (fp16 pairs); heads beyond ng are zero
-    for (int i = threadIdx.x; i < GG * (D / 2); i += blockDim.x) {
-        const int g = i / (D / 2), e = i % (D / 2);
-        uint32_t v = 0;
-        if (g < ng) v = ((const uint32_t*)(a.q + ((int64_t)b * a.Hq + head0 + g) * D))[e];
-        qs[i] = as_h2(v);
+    // query as the B operand of the score MFMA: head m, dims 16s + 4kg + 0..3
+    fkv_h4 qb[NB];
+#pragma unroll
+    for (int s = 0; s < NB; s++) {
+        uint2 v = make_uint2(0, 0);
+        if (m < ng) v = *(const uint2*)(a.q + ((int64_t)b * a.Hq + head0 + m) * D + 16 * s + 4 * kg);
+        qb[s] = __builtin_bit_cast(fkv_h4, v);
     }
 
     // split range over the virtual tile sequence, weighted by bytes per token
@@ -447,188 +372,208 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     };
     const int k0 = first_tile_at(W * split / a.num_splits);
     const int k1 = first_tile_at(W * (split + 1) / a.num_splits);
-    __syncthreads();
 
-    WaveState<D, GG> st;
+    Lane<D> st;
+    st.m = -INFINITY;
+    st.lsum = st.zsum = st.wsum = 0.f;
+    st.mn = INFINITY;
+    st.mx = -INFINITY;
+    st.arg = INT_MAX;
 #pragma unroll
-    for (int g = 0; g < GG; g++) {
-        st.m[g] = -INFINITY;
-        st.lsum[g] = 0.f;
-        st.zsum[g] = 0.f;
-        st.wsum[g] = 0.f;
-        st.mn[g] = INFINITY;
-        st.mx[g] = -INFINITY;
-        st.arg[g] = INT_MAX;
-#pragma unroll
-        for (int d = 0; d < 8; d++) st.acc[g][d] = 0.f;
-    }
-    _Float16* pl = pbuf[wave];
+    for (int j = 0; j < NB; j++) st.acc[j] = fkv_f4{0.f, 0.f, 0.f, 0.f};
 
     for (int k = k0 + wave; k < k1; k += kWavesPerGroup) {
-        int kind, tile, count;
-        if (k < nt_near) {
-            kind = kNear; tile = k; count = nv;
-        } else if (k < nt_near + nt_far) {
-            kind = kFar; tile = k - nt_near; count = a.L.F;
+        if (k >= nt_near && k < nt_near + nt_far) {
+            // ---------------- far tile: 4 groups of 16 tokens ----------------
+            const int tile = k - nt_near;
+            const int64_t g0 = (int64_t)tile * 4;  // first group
+            const uint8_t* kb = a.blob + a.L.far_k + bkv * (int64_t)a.L.F_pad * D + g0 * 16 * D + lane * (D / 4);
+            const uint32_t* vb = (const uint32_t*)(a.blob + a.L.far_v + bkv * (int64_t)a.L.F_pad * D / 2) +
+                                 g0 * 2 * D + lane * (D / 32);
+            const uint32_t* zb = (const uint32_t*)(a.blob + a.L.far_sz) + bkv * a.L.F_pad + g0 * 16 + 4 * kg;
+            uint32_t kw[4][NB], vw[4][NB / 2], sz[4][4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+#pragma unroll
+                for (int q4 = 0; q4 < NB / 4; q4++) {
+                    const uint4 x = *(const uint4*)(kb + g * 16 * D + q4 * 16);
+                    kw[g][4 * q4] = x.x; kw[g][4 * q4 + 1] = x.y; kw[g][4 * q4 + 2] = x.z; kw[g][4 * q4 + 3] = x.w;
+                }
+                if constexpr (NB / 2 == 4) {
+                    const uint4 x = *(const uint4*)(vb + g * 2 * D);
+                    vw[g][0] = x.x; vw[g][1] = x.y; vw[g][2] = x.z; vw[g][3] = x.w;
+                } else {
+                    const uint2 x = *(const uint2*)(vb + g * 2 * D);
+                    vw[g][0] = x.x; vw[g][1] = x.y;
+                }
+                const uint4 z = *(const uint4*)(zb + g * 16);
+                sz[g][0] = z.x; sz[g][1] = z.y; sz[g][2] = z.z; sz[g][3] = z.w;
+            }
+            float sc[4][4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                fkv_f4 acc = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < NB; s++) acc = mfma16(e4m3x4(kw[g][s]), qb[s], acc);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = tile * kTile + g * 16 + 4 * kg + e;
+                    const float s = acc[e] * a.inv_sqrt_d;
+                    const bool ok = t < a.L.F;
+                    sc[g][e] = ok ? s : -INFINITY;
+                    if (ok && s > st.mx) { st.mx = s; st.arg = t; }  // first index of the max
+                }
+            }
+            softmax_pv<D, 4, true>(st, sc, sz, [&](int g, int j) { return int4x4(vw[g][j >> 1], j & 1); });
         } else {
-            kind = kDec; tile = k - nt_near - nt_far; count = a.n_dec;
-        }
-        // far V for this tile is loaded up front so its latency hides behind QK
-        uint4 vfar[kTile / GS];
-        if (kind == kFar) {
-            const uint4* vb = (const uint4*)(a.blob + a.L.far_v) + (bkv * a.L.F_pad + (int64_t)tile * kTile) * D / 32;
+            // ---------- fp16 tile (near slots or decode rows): 2 x 2 groups ----------
+            const bool near = k < nt_near;
+            const int tile = near ? k : k - nt_near - nt_far;
+            const int count = near ? nv : a.n_dec;
+#pragma unroll 1
+            for (int half = 0; half < 2; half++) {
+                const int gbase = tile * 4 + half * 2;  // first 16-token group
+                uint32_t kw[2][2 * NB], vw[2][2 * NB];
+                if (near) {
+                    const uint16_t* kb = (const uint16_t*)(a.blob + a.L.near_k) + bkv * (int64_t)a.L.Na_pad * D +
+                                         (int64_t)gbase * 16 * D + lane * (D / 4);
+                    const uint16_t* vb = (const uint16_t*)(a.blob + a.L.near_v) + bkv * (int64_t)a.L.Na_pad * D +
+                                         (int64_t)gbase * 16 * D + lane * (D / 4);
 #pragma unroll
-            for (int j = 0; j < kTile / GS; j++) vfar[j] = vb[j * kWave + lane];
-        }
-        float s[GG];
-        uint32_t sz;
-        score_tile<D, GG>(a, kind, tile, bkv, count, qs, s, sz);
-
-        const int tok = tile * kTile + lane;
-        // spike bookkeeping (the V gate below does not affect it)
+                    for (int g = 0; g < 2; g++)
 #pragma unroll
-        for (int g = 0; g < GG; g++) {
-            if (kind == kFar) {
-                if (s[g] > st.mx[g]) { st.mx[g] = s[g]; st.arg[g] = tok; }
-            } else {
-                st.mn[g] = fminf(st.mn[g], s[g] == -INFINITY ? INFINITY : s[g]);
+                        for (int q4 = 0; q4 < NB / 2; q4++) {
+                            const uint4 x = *(const uint4*)(kb + g * 16 * D + q4 * 8);
+                            const uint4 y = *(const uint4*)(vb + g * 16 * D + q4 * 8);
+                            kw[g][4 * q4] = x.x; kw[g][4 * q4 + 1] = x.y; kw[g][4 * q4 + 2] = x.z; kw[g][4 * q4 + 3] = x.w;
+                            vw[g][4 * q4] = y.x; vw[g][4 * q4 + 1] = y.y; vw[g][4 * q4 + 2] = y.z; vw[g][4 * q4 + 3] = y.w;
+                        }
+                } else {
+                    // decode rows are row-major (B, Hkv, n_dec, D): gather operands
+#pragma unroll
+                    for (int g = 0; g < 2; g++) {
+                        const int tk = (gbase + g) * 16 + m;
+                        const uint16_t* kr = a.dec_k + (bkv * a.n_dec + (tk < count ? tk : 0)) * D;
+#pragma unroll
+                        for (int s = 0; s < NB; s++) {
+                            const uint2 x = tk < count ? *(const uint2*)(kr + 16 * s + 4 * kg) : make_uint2(0, 0);
+                            kw[g][2 * s] = x.x;
+                            kw[g][2 * s + 1] = x.y;
+                        }
+#pragma unroll
+                        for (int j = 0; j < NB; j++) {
+                            uint16_t hv[4];
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                const int tv = (gbase + g) * 16 + 4 * kg + e;
+                                hv[e] = tv < count ? a.dec_v[(bkv * a.n_dec + tv) * D + 16 * j + m] : (uint16_t)0;
+                            }
+                            vw[g][2 * j] = hv[0] | ((uint32_t)hv[1] << 16);
+                            vw[g][2 * j + 1] = hv[2] | ((uint32_t)hv[3] << 16);
+                        }
+                    }
+                }
+                float sc[2][4];
+                uint32_t szd[2][4] = {};
+#pragma unroll
+                for (int g = 0; g < 2; g++) {
+                    fkv_f4 acc = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int s = 0; s < NB; s++) acc = mfma16(h4_of(kw[g][2 * s], kw[g][2 * s + 1]), qb[s], acc);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int t = (gbase + g) * 16 + 4 * kg + e;
+                        const float s = acc[e] * a.inv_sqrt_d;
+                        const bool ok = t < count;
+                        sc[g][e] = ok ? s : -INFINITY;
+                        if (ok) st.mn = fminf(st.mn, s);
+                    }
+                }
+                softmax_pv<D, 2, false>(st, sc, szd,
+                                        [&](int g, int j) { return h4_of(vw[g][2 * j], vw[g][2 * j + 1]); });
             }
         }
-        // online softmax: one rescale per tile
-        float p[GG];
-        bool any = false;
-#pragma unroll
-        for (int g = 0; g < GG; g++) {
-            const float tmax = wave_max(s[g]);
-            const float m_new = fmaxf(st.m[g], tmax);
-            if (m_new > st.m[g]) {
-                const float alpha = __expf(st.m[g] - m_new);
-                st.lsum[g] *= alpha;
-                st.zsum[g] *= alpha;
-                st.wsum[g] *= alpha;
-#pragma unroll
-                for (int d = 0; d < 8; d++) st.acc[g][d] *= alpha;
-                st.m[g] = m_new;
-            }
-            float pg = 0.f;
-            if (kind == kFar) {
-                if (s[g] >= st.m[g] - 16.0f) pg = __expf(s[g] - st.m[g]);
-            } else if (s[g] != -INFINITY) {
-                pg = __expf(s[g] - st.m[g]);
-            }
-            p[g] = pg;
-            any |= pg > 0.f;
-        }
-        const float vs = h2f((uint16_t)(sz & 0xFFFF));
-        const float vz = h2f((uint16_t)(sz >> 16));
-        const int rr = lane % GS;
-        const int slot = (lane / GS) * GS + (rr % NPH) * 4 + rr / NPH;
-#pragma unroll
-        for (int g = 0; g < GG; g++) {
-            st.lsum[g] += p[g];
-            float w = p[g];
-            if (kind == kFar) w = p[g] * vs;
-            const _Float16 wh = (_Float16)w;
-            if (kind == kFar) {
-                // v = vs*(c - 7.5) + (vz + 7.5*vs); the accumulator receives
-                // wh*(16 + c), so subtract 23.5*wh exactly via wsum
-                st.zsum[g] += p[g] * (vz + 7.5f * vs);
-                st.wsum[g] += (float)wh;
-            }
-            __builtin_memcpy(pl + g * kTile + slot, &wh, 2);
-        }
-        // whole tile gated away -> skip its V (wave-uniform)
-        if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
-        // LDS ops of one wave complete in order: the weights just written are
-        // visible to the reads below without a workgroup barrier
-        __builtin_amdgcn_wave_barrier();
-        pv_tile<D, GG>(a, kind, tile, bkv, count, pl, vfar, st);
-        __builtin_amdgcn_wave_barrier();
     }
 
-    // ---- wave reduction ----
+    // ---- per-head reduction over the 4 lanes (kg) sharing head m ----
+    float l = st.lsum, z = st.zsum, ws = st.wsum, mn = st.mn, mx = st.mx;
+    int arg = st.arg;
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
+        l += wave_xor(l, o);
+        z += wave_xor(z, o);
+        ws += wave_xor(ws, o);
+        mn = fminf(mn, wave_xor(mn, o));
+        const float ox = wave_xor(mx, o);
+        const int oa = wave_xor(arg, o);
+        if (ox > mx || (ox == mx && oa < arg)) { mx = ox; arg = oa; }
+    }
+    z -= 23.5f * ws;  // remove the +16 INT4 decode offset and the 7.5 centring
     float* wr = wrec[wave];
-#pragma unroll
-    for (int g = 0; g < GG; g++) {
-        float l = wave_sum(st.lsum[g]);
-        float z = wave_sum(st.zsum[g]) - 23.5f * wave_sum(st.wsum[g]);
-        float mn = wave_min(st.mn[g]);
-        float mx = st.mx[g];
-        int arg = st.arg[g];
-        wave_argmax(mx, arg);
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            float v = st.acc[g][d];
-#pragma unroll
-            for (int o = NQ; o < kWave; o <<= 1) v += wave_xor(v, o);
-            st.acc[g][d] = v + z;  // fold the INT4 zero-point term
+    if (m < ng) {
+        if (kg == 0) {
+            wr[m * RS + 0] = st.m;
+            wr[m * RS + 1] = l;
+            wr[m * RS + 2] = mn;
+            wr[m * RS + 3] = mx;
+            wr[m * RS + 4] = __int_as_float(arg);
         }
-        if (lane == 0) {
-            wr[g * RS + 0] = st.m[g];
-            wr[g * RS + 1] = l;
-            wr[g * RS + 2] = mn;
-            wr[g * RS + 3] = mx;
-            wr[g * RS + 4] = __int_as_float(arg);
-        }
-        if (lane < NQ) {
 #pragma unroll
-            for (int d = 0; d < 8; d++) wr[g * RS + Rec<D>::kHdr + lane * 8 + d] = st.acc[g][d];
-        }
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) wr[m * RS + kHdr + 16 * j + 4 * kg + e] = st.acc[j][e] + z;
     }
     __syncthreads();
 
-    // ---- merge the 4 waves (wave 0) into wrec[0] ----
-    if (wave == 0) {
-        for (int g = 0; g < GG; g++) {
-            float M = -INFINITY;
-            for (int w = 0; w < kWavesPerGroup; w++) M = fmaxf(M, wrec[w][g * RS]);
-            float L = 0.f, mn = INFINITY, mx = -INFINITY;
-            int arg = INT_MAX;
-            float sc[kWavesPerGroup];
-            for (int w = 0; w < kWavesPerGroup; w++) {
-                const float mw = wrec[w][g * RS];
-                sc[w] = mw == -INFINITY ? 0.f : __expf(mw - M);
-                L += sc[w] * wrec[w][g * RS + 1];
-                mn = fminf(mn, wrec[w][g * RS + 2]);
-                const float fx = wrec[w][g * RS + 3];
-                const int fa = __float_as_int(wrec[w][g * RS + 4]);
-                if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
-            }
-            for (int d = lane; d < D; d += kWave) {
-                float v = 0.f;
-                for (int w = 0; w < kWavesPerGroup; w++) v += sc[w] * wrec[w][g * RS + Rec<D>::kHdr + d];
-                wrec[0][g * RS + Rec<D>::kHdr + d] = v;
-            }
-            if (lane == 0) {
-                wrec[0][g * RS + 0] = M;
-                wrec[0][g * RS + 1] = L;
-                wrec[0][g * RS + 2] = mn;
-                wrec[0][g * RS + 3] = mx;
-                wrec[0][g * RS + 4] = __int_as_float(arg);
-            }
+    // ---- merge the 4 waves into wrec[0] ----
+    for (int h = wave; h < ng; h += kWavesPerGroup) {
+        float M = -INFINITY;
+        for (int w = 0; w < kWavesPerGroup; w++) M = fmaxf(M, wrec[w][h * RS]);
+        float sc[kWavesPerGroup];
+        float L = 0.f, mn2 = INFINITY, mx2 = -INFINITY;
+        int arg2 = INT_MAX;
+        for (int w = 0; w < kWavesPerGroup; w++) {
+            const float mw = wrec[w][h * RS];
+            sc[w] = mw == -INFINITY ? 0.f : __expf(mw - M);
+            L += sc[w] * wrec[w][h * RS + 1];
+            mn2 = fminf(mn2, wrec[w][h * RS + 2]);
+            const float fx = wrec[w][h * RS + 3];
+            const int fa = __float_as_int(wrec[w][h * RS + 4]);
+            if (fx > mx2 || (fx == mx2 && fa < arg2)) { mx2 = fx; arg2 = fa; }
+        }
+        for (int d = lane; d < D; d += kWave) {
+            float v = 0.f;
+            for (int w = 0; w < kWavesPerGroup; w++) v += sc[w] * wrec[w][h * RS + kHdr + d];
+            wrec[0][h * RS + kHdr + d] = v;
+        }
+        if (lane == 0) {
+            wrec[0][h * RS + 0] = M;
+            wrec[0][h * RS + 1] = L;
+            wrec[0][h * RS + 2] = mn2;
+            wrec[0][h * RS + 3] = mx2;
+            wrec[0][h * RS + 4] = __int_as_float(arg2);
         }
     }
     __syncthreads();
 
     if (a.num_splits > 1) {
-        // split partial -> workspace; merge_kernel combines the splits
         const int row = (int)(bkv * a.head_groups + hgrp);  // (b, kv_head, head group)
-        float* dst = a.ws + ((int64_t)row * a.num_splits + split) * GG * RS;
-        for (int i = threadIdx.x; i < GG * RS; i += blockDim.x) dst[i] = wrec[0][i];
+        float* dst = a.ws + ((int64_t)row * a.num_splits + split) * ng * RS;
+        for (int i = threadIdx.x; i < ng * RS; i += blockDim.x) dst[i] = wrec[0][i];
         return;
     }
-    finalize_rows<D>(a, wrec[0], GG, b, head0, ng);
+    finalize_rows<D>(a, wrec[0], b, head0, ng);
 }
 
-// out = acc / l (fp16), spike flag and token for the ng heads of one record set
+// out = acc / l (fp16), spike flag and token for ng heads of one record set
 template <int D>
-__device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int GG_, int b, int head0, int ng) {
-    constexpr int RS = Rec<D>::kSize;
+__device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b, int head0, int ng) {
+    constexpr int RS = kHdr + D;
     for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
         const int g = i / D, d = i % D;
         const float L = fin[g * RS + 1];
         const float inv_l = L > 0.f ? 1.0f / L : 0.f;
-        a.out[((int64_t)b * a.Hq + head0 + g) * D + d] = f2h(fin[g * RS + Rec<D>::kHdr + d] * inv_l);
+        a.out[((int64_t)b * a.Hq + head0 + g) * D + d] = f2h(fin[g * RS + kHdr + d] * inv_l);
     }
     if ((int)threadIdx.x < ng) {
         const int g = threadIdx.x;
@@ -638,36 +583,32 @@ __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int GG
         a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
         a.tokens[o] = mx == -INFINITY ? -1 : arg;
     }
-    (void)GG_;
 }
 
 // Split-K merge (csrc/kernels/foveated_attn.metal:394-431 restated for
-// partials in memory): one workgroup per (b, kv_head, head group).  The
-// per-split maxima are rescaled to the global max; spike fields take the
-// min / first-index max.
-template <int D, int GG>
+// partials in memory): one workgroup per (b, kv_head, head group).  Split
+// maxima are rescaled to the global max; spike fields take the min and the
+// first-index max.
+template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(AttnArgs a) {
-    constexpr int RS = Rec<D>::kSize;
-    constexpr int H = Rec<D>::kHdr;
-    __shared__ float mrg[GG * RS];
-    __shared__ float hdr[256][GG][H];  // per split: m, l, min_near, max_far, arg
-    __shared__ float scl[GG][256];
+    constexpr int RS = kHdr + D;
+    __shared__ float mrg[kHeads * RS];
+    __shared__ float hdr[kMaxSplits][kHeads][kHdr];
+    __shared__ float scl[kHeads][kMaxSplits];
     const int row = blockIdx.x;
     const int hgrp = row % a.head_groups;
     const int64_t bkv = row / a.head_groups;
     const int b = (int)(bkv / a.L.Hkv), kvh = (int)(bkv % a.L.Hkv);
-    const int head0 = kvh * a.G + hgrp * GG;
-    const int ng = min(GG, a.G - hgrp * GG);
-    const float* src = a.ws + (int64_t)row * a.num_splits * GG * RS;
-    const int ns = a.num_splits;  // <= 256
-    // 1) every (split, head) header in one parallel round trip
-    for (int i = threadIdx.x; i < ns * GG * H; i += blockDim.x) {
-        const int sp = i / (GG * H), r = i % (GG * H), g = r / H, f = r % H;
-        hdr[sp][g][f] = src[(int64_t)sp * GG * RS + g * RS + f];
+    const int head0 = kvh * a.G + hgrp * kHeads;
+    const int ng = min(kHeads, a.G - hgrp * kHeads);
+    const int ns = a.num_splits;  // <= kMaxSplits
+    const float* src = a.ws + (int64_t)row * ns * ng * RS;
+    for (int i = threadIdx.x; i < ns * ng * kHdr; i += blockDim.x) {
+        const int sp = i / (ng * kHdr), r = i % (ng * kHdr), g = r / kHdr, f = r % kHdr;
+        hdr[sp][g][f] = src[(int64_t)sp * ng * RS + g * RS + f];
     }
     __syncthreads();
-    // 2) per-head global max, scales, normaliser and spike fields
-    if (threadIdx.x < GG) {
+    if ((int)threadIdx.x < ng) {
         const int g = threadIdx.x;
         float M = -INFINITY;
         for (int sp = 0; sp < ns; sp++) M = fmaxf(M, hdr[sp][g][0]);
@@ -690,17 +631,16 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnArgs a) {
         mrg[g * RS + 4] = __int_as_float(arg);
     }
     __syncthreads();
-    // 3) rescaled sum of the accumulators (independent loads per element)
-    for (int i = threadIdx.x; i < GG * D; i += blockDim.x) {
+    for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
         const int g = i / D, d = i % D;
-        const float* col = src + g * RS + H + d;
+        const float* col = src + g * RS + kHdr + d;
         float v = 0.f;
 #pragma unroll 8
-        for (int sp = 0; sp < ns; sp++) v += scl[g][sp] * col[(int64_t)sp * GG * RS];
-        mrg[g * RS + H + d] = v;
+        for (int sp = 0; sp < ns; sp++) v += scl[g][sp] * col[(int64_t)sp * ng * RS];
+        mrg[g * RS + kHdr + d] = v;
     }
     __syncthreads();
-    finalize_rows<D>(a, mrg, GG, b, head0, ng);
+    finalize_rows<D>(a, mrg, b, head0, ng);
 }
 
 }  // namespace fkv
@@ -713,46 +653,14 @@ struct fkv_attn_impl {
     fkv::BlobLayout L;
     uint8_t* blob = nullptr;
     float margin = 0.f;
-    float* ws = nullptr;          // split partials
+    float* ws = nullptr;  // split partials
     size_t ws_floats = 0;
-    uint16_t* qbuf = nullptr;     // fp16 copy of non-fp16 queries
+    uint16_t* qbuf = nullptr;  // fp16 copy of non-fp16 queries
     size_t qbuf_n = 0;
     int device = 0;
 };
 
 namespace fkv {
-
-constexpr int kMaxG = 8;  // query heads served per workgroup
-
-typedef void (*AttnKernel)(AttnArgs);
-
-template <int D>
-static AttnKernel pick_kernel(int gg) {
-    switch (gg) {
-        case 1: return attn_kernel<D, 1>;
-        case 2: return attn_kernel<D, 2>;
-        case 3: return attn_kernel<D, 3>;
-        case 4: return attn_kernel<D, 4>;
-        case 5: return attn_kernel<D, 5>;
-        case 6: return attn_kernel<D, 6>;
-        case 7: return attn_kernel<D, 7>;
-        default: return attn_kernel<D, 8>;
-    }
-}
-
-template <int D>
-static AttnKernel pick_merge(int gg) {
-    switch (gg) {
-        case 1: return merge_kernel<D, 1>;
-        case 2: return merge_kernel<D, 2>;
-        case 3: return merge_kernel<D, 3>;
-        case 4: return merge_kernel<D, 4>;
-        case 5: return merge_kernel<D, 5>;
-        case 6: return merge_kernel<D, 6>;
-        case 7: return merge_kernel<D, 7>;
-        default: return merge_kernel<D, 8>;
-    }
-}
 
 static int grid_for(int64_t n, int block) {
     int64_t g = cdiv(n, block);
@@ -774,7 +682,7 @@ int plan_splits(const BlobLayout& L, int rows, int n_dec) {
     int s = (int)cdiv(target, rows > 0 ? rows : 1);
     const int cap = tiles / (2 * kWavesPerGroup);
     if (s > cap) s = cap;
-    if (s > 256) s = 256;
+    if (s > kMaxSplits) s = kMaxSplits;
     return s < 1 ? 1 : s;
 }
 
@@ -817,12 +725,12 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
         const int blk = 256;
         const fkv::BlobLayout L = h->L;
         if (Na > 0)
-            hipLaunchKernelGGL(fkv::pack_near_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.Na_pad * (D / 8), blk)),
+            hipLaunchKernelGGL(fkv::pack_near_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * (L.Na_pad / 16) * 64, blk)),
                                dim3(blk), 0, st, near_k, near_v, near_dtype, L, h->blob);
         if (F > 0) {
-            hipLaunchKernelGGL(fkv::pack_far_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 16), blk)),
+            hipLaunchKernelGGL(fkv::pack_far_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * (L.F_pad / 16) * 64, blk)),
                                dim3(blk), 0, st, far_k, L, h->blob, bad);
-            hipLaunchKernelGGL(fkv::pack_far_v_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 8), blk)),
+            hipLaunchKernelGGL(fkv::pack_far_v_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * (L.F_pad / 16) * 64, blk)),
                                dim3(blk), 0, st, far_v, far_v_scale, far_v_zero, sz_dtype, L, h->blob);
         }
         hipLaunchKernelGGL(fkv::pack_valid_kernel, dim3(1), dim3(blk), 0, st, near_valid, Hkv, L, h->blob);
@@ -856,8 +764,8 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
     if (q_dtype < FKV_F16 || q_dtype > FKV_F32) return set_error("fkv_attn_call: unsupported query dtype");
     hipStream_t st = (hipStream_t)stream;
     const int G = Hq / L.Hkv;
-    const int gg = G < fkv::kMaxG ? G : fkv::kMaxG;
-    const int head_groups = (int)fkv::cdiv(G, gg);
+    const int head_groups = (int)fkv::cdiv(G, fkv::kHeads);
+    const int ng_max = G < fkv::kHeads ? G : fkv::kHeads;
     const int rows = L.B * L.Hkv * head_groups;
     const int splits = fkv::plan_splits(L, rows, n_decode);
     const uint16_t* q16 = (const uint16_t*)query;
@@ -874,9 +782,8 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
                            q_dtype, qn, h->qbuf);
         q16 = h->qbuf;
     }
-    const int RS = fkv::Rec<128>::kHdr + L.D;
     if (splits > 1) {
-        const size_t need = (size_t)rows * splits * gg * RS;
+        const size_t need = (size_t)rows * splits * ng_max * (fkv::kHdr + L.D);
         if (need > h->ws_floats) {
             if (h->ws) (void)hipFree(h->ws);
             h->ws = nullptr;
@@ -902,11 +809,12 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
     a.flags = spike_flags;
     a.tokens = spike_tokens;
     a.ws = h->ws;
-    fkv::AttnKernel k = L.D == 128 ? fkv::pick_kernel<128>(gg) : fkv::pick_kernel<64>(gg);
-    hipLaunchKernelGGL(k, dim3(splits, L.Hkv * head_groups, L.B), dim3(fkv::kWave * fkv::kWavesPerGroup), 0, st, a);
+    const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
+    if (L.D == 128) hipLaunchKernelGGL(fkv::attn_kernel<128>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(fkv::attn_kernel<64>, grid, block, 0, st, a);
     if (splits > 1) {
-        fkv::AttnKernel m = L.D == 128 ? fkv::pick_merge<128>(gg) : fkv::pick_merge<64>(gg);
-        hipLaunchKernelGGL(m, dim3(rows), dim3(256), 0, st, a);
+        if (L.D == 128) hipLaunchKernelGGL(fkv::merge_kernel<128>, dim3(rows), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL(fkv::merge_kernel<64>, dim3(rows), dim3(256), 0, st, a);
     }
     return check_hip(hipGetLastError(), "attn_kernel launch");
 }
