@@ -91,6 +91,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "attn_c3_16k_b8_traffic.txt"))
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches instead of a captured HIP graph (for counter collection)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -149,24 +151,32 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.Stream(device=dev)
-    graph = torch.cuda.CUDAGraph()
     outs = []
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(graph, stream=stream):
+    if args.eager:
+        def step():
             for h in handles:
-                outs.append(h(qt, dkt, dvt))
+                h(qt, dkt, dvt)
+        with torch.cuda.stream(stream):
+            outs = [h(qt, dkt, dvt) for h in handles]
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for h in handles:
+                    outs.append(h(qt, dkt, dvt))
+        step = graph.replay
     torch.cuda.synchronize()
 
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
-            graph.replay()
+            step()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         start.record(stream)
         for _ in range(args.steps):
-            graph.replay()
+            step()
         end.record(stream)
     torch.cuda.synchronize()
     ms_total = start.elapsed_time(end)
@@ -196,6 +206,7 @@ def main():
                    "near_valid": R, "far": F, "n_decode": n_dec, "layers_per_step": L,
                    "spike_frac": args.spikes, "far_format": "fp8-e4m3 K + int4 per-token V"},
         "us_per_layer": round(us_layer, 3),
+        "launch": "eager" if args.eager else "hip-graph",
         "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
     }
     traffic = read_traffic(args.traffic) if args.config == "c3_7b_16k_b8" else None

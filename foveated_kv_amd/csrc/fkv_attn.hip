@@ -5,15 +5,17 @@
 // (csrc/foveated_attn.cpp:83-254, csrc/kernels/foveated_attn.metal:181-432).
 //
 // Work decomposition: one workgroup of 4 waves per (batch, kv_head, split)
-// serves up to 16 query heads of the GQA group, so each compressed byte is
-// read from HBM once.  Both contractions of one kv head run on the matrix
-// cores with v_mfma_f32_16x16x16_f16 (fp16 operands, fp32 accumulation):
-//   scores  S[t][h] = K[t][:] . q[h][:]      A = K (16 tokens x 16 dims),
-//                                             B = q (16 dims x 16 heads)
-//   output  O[d][h] += V[t][d]^T . P[t][h]    A = V^T (16 dims x 16 tokens),
-//                                             B = P (16 tokens x 16 heads)
-// The score tile comes out of the first MFMA in exactly the register layout
-// the second one takes as B, so softmax weights never leave registers.
+// serves up to 16 query heads of the GQA group (as quads of 4), so each
+// compressed byte is read from HBM once.  A wave takes 64-token tiles; both
+// contractions run on the matrix cores with the 16-block
+// v_mfma_f32_4x4x4f16 (fp16 operands, fp32 accumulation), so a GQA group of
+// 4 heads wastes no MFMA lanes and no softmax work:
+//   scores  block b = tokens 4b..4b+3:   S[t][h] += K[t][4s..4s+3] . q[h][4s..4s+3]
+//   output  block b = dims 4b..4b+3:     O[h][d] += P[4g..4g+3][h] . V[4g..4g+3][d]
+//           with the weights of token group g broadcast to every block
+//           (cbsz = 4, abid = g).
+// The score MFMA leaves each lane the 4 weights that the P.V MFMA takes as
+// its A operand, so softmax weights never leave registers.
 // E4M3 keys are widened to fp16 with the native converter (exact); INT4
 // values are widened exactly by inserting the nibble into an fp16 mantissa
 // (16 + c), weights are p*scale, and the zero point and constant offsets
@@ -78,107 +80,96 @@ __device__ inline uint16_t load_as_f16(const void* p, int64_t i, int dtype) {
     return f2h(((const float*)p)[i]);
 }
 
-// One thread per (bkv, 16-token group, lane).  Near K lane (kg, m) holds
-// token m of the group, dims 16s + 4kg + i (s = 0..D/16-1, i = 0..3); near V
-// lane (kg, m) holds dim 16j + m of tokens 4kg + i.  Slots >= Na are zero.
+// One thread per (bkv, token, 16-dim block): near K and V into their tile
+// layouts (fkv_attn.h); slots >= Na are zero.
 __global__ void pack_near_kernel(const void* __restrict__ nk, const void* __restrict__ nv,
                                  int dtype, BlobLayout L, uint8_t* __restrict__ blob) {
     const int D = L.D, NB = D / 16;
-    const int64_t groups = L.Na_pad / 16;
-    const int64_t n = (int64_t)L.B * L.Hkv * groups * kWave;
+    const int64_t n = (int64_t)L.B * L.Hkv * L.Na_pad * NB;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int lane = (int)(i % kWave);
-        const int64_t r = i / kWave;
-        const int grp = (int)(r % groups);
-        const int64_t bkv = r / groups;
-        const int m = lane & 15, kg = lane >> 4;
-        uint16_t* kd = (uint16_t*)(blob + L.near_k) + bkv * (int64_t)L.Na_pad * D +
-                       (int64_t)grp * 16 * D + lane * (D / 4);
-        uint16_t* vd = (uint16_t*)(blob + L.near_v) + bkv * (int64_t)L.Na_pad * D +
-                       (int64_t)grp * 16 * D + lane * (D / 4);
-        const int tk = grp * 16 + m;
-        for (int s = 0; s < NB; s++)
-            for (int e = 0; e < 4; e++)
-                kd[s * 4 + e] = tk < L.Na ? load_as_f16(nk, (bkv * L.Na + tk) * D + 16 * s + 4 * kg + e, dtype) : 0;
-        for (int j = 0; j < NB; j++)
-            for (int e = 0; e < 4; e++) {
-                const int tv = grp * 16 + 4 * kg + e;
-                vd[j * 4 + e] = tv < L.Na ? load_as_f16(nv, (bkv * L.Na + tv) * D + 16 * j + m, dtype) : 0;
-            }
+        const int blk = (int)(i % NB);
+        const int64_t r = i / NB;
+        const int t = (int)(r % L.Na_pad);
+        const int64_t bkv = r / L.Na_pad;
+        uint16_t* kd = (uint16_t*)(blob + L.near_k) + bkv * (int64_t)L.Na_pad * D;
+        uint16_t* vd = (uint16_t*)(blob + L.near_v) + bkv * (int64_t)L.Na_pad * D;
+        for (int e = 0; e < 16; e++) {
+            const int d = blk * 16 + e;
+            const int64_t src = (bkv * L.Na + t) * D + d;
+            kd[near_k_index(t, d, D)] = t < L.Na ? load_as_f16(nk, src, dtype) : 0;
+            vd[near_v_index(t, d, D)] = t < L.Na ? load_as_f16(nv, src, dtype) : 0;
+        }
     }
 }
 
-// Far K codes in the same operand layout as near K (bytes); exponent-0
-// codes are written as signed zero (the reference LUT ignores their
-// mantissa); NaN codes 0x7F/0xFF are reported through *bad.
+// Far K codes into the tile layout; exponent-0 codes are written as signed
+// zero (the reference LUT ignores their mantissa); NaN codes 0x7F/0xFF are
+// reported through *bad.
 __global__ void pack_far_k_kernel(const uint8_t* __restrict__ fk, BlobLayout L,
                                   uint8_t* __restrict__ blob, unsigned* __restrict__ bad) {
     const int D = L.D, NB = D / 16;
-    const int64_t groups = L.F_pad / 16;
-    const int64_t n = (int64_t)L.B * L.Hkv * groups * kWave;
+    const int64_t n = (int64_t)L.B * L.Hkv * L.F_pad * NB;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int lane = (int)(i % kWave);
-        const int64_t r = i / kWave;
-        const int grp = (int)(r % groups);
-        const int64_t bkv = r / groups;
-        const int m = lane & 15, kg = lane >> 4;
-        const int t = grp * 16 + m;
-        uint8_t* dst = blob + L.far_k + bkv * (int64_t)L.F_pad * D + (int64_t)grp * 16 * D + lane * (D / 4);
-        for (int s = 0; s < NB; s++)
-            for (int e = 0; e < 4; e++) {
-                uint8_t b = 0;
-                if (t < L.F) {
-                    b = fk[(bkv * L.F + t) * D + 16 * s + 4 * kg + e];
-                    if ((b & 0x7F) == 0x7F) atomicOr(bad, 1u);
-                    if ((b & 0x78) == 0) b &= 0x80;
-                }
-                dst[s * 4 + e] = b;
+        const int blk = (int)(i % NB);
+        const int64_t r = i / NB;
+        const int t = (int)(r % L.F_pad);
+        const int64_t bkv = r / L.F_pad;
+        uint8_t* dst = blob + L.far_k + bkv * (int64_t)L.F_pad * D;
+        for (int e = 0; e < 16; e++) {
+            const int d = blk * 16 + e;
+            uint8_t b = 0;
+            if (t < L.F) {
+                b = fk[(bkv * L.F + t) * D + d];
+                if ((b & 0x7F) == 0x7F) atomicOr(bad, 1u);
+                if ((b & 0x78) == 0) b &= 0x80;
             }
+            dst[far_k_index(t, d, D)] = b;
+        }
     }
 }
 
-// Far V nibbles: lane (kg, m) of a 16-token group holds D/32 dwords; dword u
-// covers blocks 2u (bits 0-7, 16-23) and 2u+1 (bits 8-15, 24-31) at dim
-// 16*block + m, with token 4kg+e at bit 16*(e&1) + 4*(e>>1) of its byte pair.
-// Scale/zero -> one u32 per token.
+// Far V nibbles: one thread builds one dword of the tile layout (8 nibbles:
+// 2 four-token groups of one dim); thread (kg=0 lanes) also packs the
+// per-token scale / zero.
 __global__ void pack_far_v_kernel(const uint8_t* __restrict__ fv, const void* __restrict__ fvs,
                                   const void* __restrict__ fvz, int sz_dtype, BlobLayout L,
                                   uint8_t* __restrict__ blob) {
-    const int D = L.D, NW = D / 32;
-    const int64_t groups = L.F_pad / 16;
-    const int64_t n = (int64_t)L.B * L.Hkv * groups * kWave;
+    const int D = L.D;
+    const int64_t words_per_bkv = (int64_t)L.F_pad * D / 8;
+    const int64_t n = (int64_t)L.B * L.Hkv * words_per_bkv;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int lane = (int)(i % kWave);
-        const int64_t r = i / kWave;
-        const int grp = (int)(r % groups);
-        const int64_t bkv = r / groups;
-        const int m = lane & 15, kg = lane >> 4;
-        uint32_t* dst = (uint32_t*)(blob + L.far_v + bkv * (int64_t)L.F_pad * D / 2) +
-                        (int64_t)grp * 2 * D + lane * NW;
-        for (int u = 0; u < NW; u++) {
-            uint32_t w = 0;
-            for (int bp = 0; bp < 2; bp++)
-                for (int e = 0; e < 4; e++) {
-                    const int t = grp * 16 + 4 * kg + e;
-                    const int d = (2 * u + bp) * 16 + m;
-                    uint32_t c = 0;
-                    if (t < L.F) c = (fv[(bkv * L.F + t) * (D / 2) + d / 2] >> (4 * (d & 1))) & 15u;
-                    w |= c << (bp * 8 + (e & 1) * 16 + (e >> 1) * 4);
-                }
-            dst[u] = w;
-        }
-        if (kg == 0) {
-            const int t = grp * 16 + m;
-            uint32_t sz = 0;
-            if (t < L.F) {
-                const int64_t k = bkv * L.F + t;
-                sz = (uint32_t)load_as_f16(fvs, k, sz_dtype) | ((uint32_t)load_as_f16(fvz, k, sz_dtype) << 16);
+        const int64_t bkv = i / words_per_bkv;
+        const int64_t w = i % words_per_bkv;
+        // invert the dword position: tile, chunk, lane, word-in-chunk
+        const int tile = (int)(w / (8 * D));
+        const int rem = (int)(w % (8 * D));
+        const int c = rem / 256, lane = (rem % 256) / 4, q = rem % 4;
+        const int u = c * 4 + q, dh = u / 8, spair = u % 8;
+        const int d = dh * 64 + lane;
+        uint32_t word = 0;
+        for (int bp = 0; bp < 2; bp++)
+            for (int e = 0; e < 4; e++) {
+                const int t = tile * 64 + (2 * spair + bp) * 4 + e;
+                uint32_t code = 0;
+                if (t < L.F) code = (fv[(bkv * L.F + t) * (D / 2) + d / 2] >> (4 * (d & 1))) & 15u;
+                word |= code << (bp * 8 + (e & 1) * 16 + (e >> 1) * 4);
             }
-            ((uint32_t*)(blob + L.far_sz))[bkv * L.F_pad + t] = sz;
+        ((uint32_t*)(blob + L.far_v + bkv * (int64_t)L.F_pad * D / 2))[w] = word;
+    }
+    const int64_t nt = (int64_t)L.B * L.Hkv * L.F_pad;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nt;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int t = (int)(i % L.F_pad);
+        const int64_t bkv = i / L.F_pad;
+        uint32_t sz = 0;
+        if (t < L.F) {
+            const int64_t k = bkv * L.F + t;
+            sz = (uint32_t)load_as_f16(fvs, k, sz_dtype) | ((uint32_t)load_as_f16(fvz, k, sz_dtype) << 16);
         }
+        ((uint32_t*)(blob + L.far_sz))[bkv * L.F_pad + t] = sz;
     }
 }
 
@@ -216,7 +207,7 @@ __global__ void cast_to_f16_kernel(const void* __restrict__ src, int dtype, int6
 // Attention kernel
 // ---------------------------------------------------------------------------
 
-constexpr int kHeads = 16;  // query heads per workgroup row (MFMA N)
+constexpr int kHeads = 16;  // query heads per workgroup row: up to 4 quads of 4
 constexpr int kHdr = 5;     // record header: m, l, min_near, max_far, first argmax
 constexpr int kMaxSplits = 64;
 
@@ -239,8 +230,14 @@ struct AttnArgs {
     float* ws;  // split partials: [row][split][ng][kHdr + D]
 };
 
-__device__ inline fkv_f4 mfma16(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+// v_mfma_f32_4x4x4f16: 16 independent 4x4x4 blocks; lane l supplies row /
+// column l%4 of block l/4.  cbsz = 4, abid = s broadcasts block s's A.
+template <int ABID>
+__device__ inline fkv_f4 mfma4(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 4, ABID, 0);
+}
+__device__ inline fkv_f4 mfma4_local(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0);
 }
 
 __device__ inline fkv_h4 h4_of(uint32_t lo, uint32_t hi) {
@@ -248,93 +245,121 @@ __device__ inline fkv_h4 h4_of(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(fkv_h4, u);
 }
 
-// Four E4M3 codes -> fp16 A operand (dims 4kg + 0..3 of one k-step)
+// Four E4M3 codes -> fp16 (dims 4s..4s+3 of one token), exact.
 __device__ inline fkv_h4 e4m3x4(uint32_t w) {
     return h4_of(as_u32(e4m3x2_to_h2(w, false)), as_u32(e4m3x2_to_h2(w, true)));
 }
 
-// INT4 dword -> A operand of block 2u (bp = 0) or 2u+1 (bp = 1): (16 + c)
-// for tokens 4kg + 0..3, exact.
+// INT4 dword -> the 4 tokens of 4-token group 2u (bp = 0) or 2u+1 (bp = 1)
+// as fp16 (16 + c), exact: the nibble lands in mantissa bits 6..9 of an
+// exponent-19 half.
 __device__ inline fkv_h4 int4x4(uint32_t w, int bp) {
     const uint32_t a = bp ? ((w >> 2) & 0x03C003C0u) : ((w << 6) & 0x03C003C0u);
     const uint32_t b = bp ? ((w >> 6) & 0x03C003C0u) : ((w << 2) & 0x03C003C0u);
     return h4_of(a | 0x4C004C00u, b | 0x4C004C00u);
 }
 
-template <int D>
+// broadcast lane i of each lane quad (DPP quad_perm)
+template <int I>
+__device__ inline float quad_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), I * 0x55, 0xF, 0xF, false));
+}
+
+template <int D, int NQ>
 struct Lane {
-    float m, lsum, zsum, wsum, mn, mx;
-    int arg;
-    fkv_f4 acc[D / 16];
+    // per head quad: this lane tracks head 4*qd + (lane % 4)
+    float m[NQ], lsum[NQ], zsum[NQ], wsum[NQ], mn[NQ], mx[NQ];
+    int arg[NQ];
+    fkv_f4 acc[NQ][D / 64];  // acc[qd][dh][i] = O[head 4qd+i][dim 64dh + lane]
 };
+
+enum TileKind { kNear = 0, kFar = 1, kDec = 2 };
 
 template <int D>
 __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b, int head0, int ng);
 
-// Online softmax + P.V for NG 16-token groups whose scores sc[g][e] (token
-// 4kg+e of group g, head m) are computed.  vop(g, j) yields the A operand
-// of block j of group g; far tiles pass their per-token scale/zero.
-template <int D, int NG, bool FAR, typename VOp>
-__device__ inline void softmax_pv(Lane<D>& st, const float (&sc)[NG][4], const uint32_t (&sz)[NG][4],
+// Online softmax of one 64-token tile for head quad qd (scores s[e] of
+// tokens 4*(lane/4) + e, head 4qd + lane%4), then P.V: 16 broadcast MFMAs
+// per 64-dim half, A = the weights of 4-token group g (abid = g), B = the
+// values of that group at dim 64dh + lane.
+template <int D, int NQ, bool FAR, typename VOp>
+__device__ inline void softmax_pv(Lane<D, NQ>& st, int qd, const float (&s)[4], const uint32_t (&sz)[4],
                                   VOp vop) {
-    constexpr int NB = D / 16;
-    float cmax = -INFINITY;
+    constexpr int NH = D / 64;
+    float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
 #pragma unroll
-    for (int g = 0; g < NG; g++)
+    for (int o = 4; o <= 32; o <<= 1) cmax = fmaxf(cmax, wave_xor(cmax, o));
+    const float m_new = fmaxf(st.m[qd], cmax);
+    if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
+        const float alpha = m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f;
+        st.lsum[qd] *= alpha;
+        st.zsum[qd] *= alpha;
+        st.wsum[qd] *= alpha;
+        const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
+        const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
 #pragma unroll
-        for (int e = 0; e < 4; e++) cmax = fmaxf(cmax, sc[g][e]);
-    cmax = fmaxf(cmax, wave_xor(cmax, 16));
-    cmax = fmaxf(cmax, wave_xor(cmax, 32));
-    const float m_new = fmaxf(st.m, cmax);
-    if (__builtin_amdgcn_ballot_w64(m_new > st.m)) {
-        const float alpha = m_new > st.m ? __expf(st.m - m_new) : 1.0f;
-        st.lsum *= alpha;
-        st.zsum *= alpha;
-        st.wsum *= alpha;
-#pragma unroll
-        for (int j = 0; j < NB; j++) st.acc[j] *= alpha;
-        st.m = m_new;
+        for (int dh = 0; dh < NH; dh++) {
+            st.acc[qd][dh][0] *= a0;
+            st.acc[qd][dh][1] *= a1;
+            st.acc[qd][dh][2] *= a2;
+            st.acc[qd][dh][3] *= a3;
+        }
+        st.m[qd] = m_new;
     }
-    fkv_h4 bw[NG];
+    _Float16 wh[4];
     bool any = false;
 #pragma unroll
-    for (int g = 0; g < NG; g++) {
-        _Float16 wh[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float s = sc[g][e];
-            float p = 0.f;
-            if (FAR) {
-                if (s >= st.m - 16.0f) p = __expf(s - st.m);  // score-gated V
-            } else if (s != -INFINITY) {
-                p = __expf(s - st.m);
-            }
-            st.lsum += p;
-            if (FAR) {
-                const float vs = h2f((uint16_t)(sz[g][e] & 0xFFFF));
-                const float vz = h2f((uint16_t)(sz[g][e] >> 16));
-                wh[e] = (_Float16)(p * vs);
-                // value = vs*(c - 7.5) + (vz + 7.5*vs); the MFMA sees wh*(16 + c)
-                st.zsum += p * (vz + 7.5f * vs);
-                st.wsum += (float)wh[e];
-            } else {
-                wh[e] = (_Float16)p;
-            }
-            any |= p > 0.f;
+    for (int e = 0; e < 4; e++) {
+        float p = 0.f;
+        if (FAR) {
+            if (s[e] >= st.m[qd] - 16.0f) p = __expf(s[e] - st.m[qd]);  // score-gated V
+        } else if (s[e] != -INFINITY) {
+            p = __expf(s[e] - st.m[qd]);
         }
-        bw[g] = fkv_h4{wh[0], wh[1], wh[2], wh[3]};
+        st.lsum[qd] += p;
+        if (FAR) {
+            const float vs = h2f((uint16_t)(sz[e] & 0xFFFF));
+            const float vz = h2f((uint16_t)(sz[e] >> 16));
+            wh[e] = (_Float16)(p * vs);
+            // value = vs*(c - 7.5) + (vz + 7.5*vs); the MFMA sees wh*(16 + c)
+            st.zsum[qd] += p * (vz + 7.5f * vs);
+            st.wsum[qd] += (float)wh[e];
+        } else {
+            wh[e] = (_Float16)p;
+        }
+        any |= p > 0.f;
     }
-    if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole chunk gated away
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
+    const fkv_h4 w4 = fkv_h4{wh[0], wh[1], wh[2], wh[3]};
 #pragma unroll
-    for (int g = 0; g < NG; g++)
-#pragma unroll
-        for (int j = 0; j < NB; j++) st.acc[j] = mfma16(vop(g, j), bw[g], st.acc[j]);
+    for (int dh = 0; dh < NH; dh++) {
+        fkv_f4 acc = st.acc[qd][dh];
+        acc = mfma4<0>(w4, vop(0, dh), acc);
+        acc = mfma4<1>(w4, vop(1, dh), acc);
+        acc = mfma4<2>(w4, vop(2, dh), acc);
+        acc = mfma4<3>(w4, vop(3, dh), acc);
+        acc = mfma4<4>(w4, vop(4, dh), acc);
+        acc = mfma4<5>(w4, vop(5, dh), acc);
+        acc = mfma4<6>(w4, vop(6, dh), acc);
+        acc = mfma4<7>(w4, vop(7, dh), acc);
+        acc = mfma4<8>(w4, vop(8, dh), acc);
+        acc = mfma4<9>(w4, vop(9, dh), acc);
+        acc = mfma4<10>(w4, vop(10, dh), acc);
+        acc = mfma4<11>(w4, vop(11, dh), acc);
+        acc = mfma4<12>(w4, vop(12, dh), acc);
+        acc = mfma4<13>(w4, vop(13, dh), acc);
+        acc = mfma4<14>(w4, vop(14, dh), acc);
+        acc = mfma4<15>(w4, vop(15, dh), acc);
+        st.acc[qd][dh] = acc;
+    }
 }
 
-template <int D>
+template <int D, int NQ>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-    constexpr int NB = D / 16;  // 16-dim k-steps of QK == 16-dim blocks of P.V
+    constexpr int NS = D / 4;   // 4-dim k-steps of QK
+    constexpr int NH = D / 64;  // 64-dim halves of P.V
     constexpr int RS = kHdr + D;
+    __shared__ __attribute__((aligned(16))) uint16_t qs[NQ * NS * 4 * 4];
     __shared__ float wrec[kWavesPerGroup][kHeads * RS];
 
     const int split = blockIdx.x;
@@ -345,15 +370,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int head0 = kvh * a.G + hgrp * kHeads;
     const int ng = min(kHeads, a.G - hgrp * kHeads);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int m = lane & 15, kg = lane >> 4;
+    const int j = lane & 3, blk = lane >> 2;
 
-    // query as the B operand of the score MFMA: head m, dims 16s + 4kg + 0..3
-    fkv_h4 qb[NB];
-#pragma unroll
-    for (int s = 0; s < NB; s++) {
-        uint2 v = make_uint2(0, 0);
-        if (m < ng) v = *(const uint2*)(a.q + ((int64_t)b * a.Hq + head0 + m) * D + 16 * s + 4 * kg);
-        qb[s] = __builtin_bit_cast(fkv_h4, v);
+    // query -> LDS as the B operand of the score MFMA: [qd][s][j][4 halves]
+    for (int i = threadIdx.x; i < NQ * NS * 16; i += blockDim.x) {
+        const int e = i & 3, jj = (i >> 2) & 3, sq = i >> 4;
+        const int s = sq % NS, qd = sq / NS;
+        const int h = 4 * qd + jj;
+        qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
     }
 
     // split range over the virtual tile sequence, weighted by bytes per token
@@ -372,156 +396,173 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     };
     const int k0 = first_tile_at(W * split / a.num_splits);
     const int k1 = first_tile_at(W * (split + 1) / a.num_splits);
+    __syncthreads();
 
-    Lane<D> st;
-    st.m = -INFINITY;
-    st.lsum = st.zsum = st.wsum = 0.f;
-    st.mn = INFINITY;
-    st.mx = -INFINITY;
-    st.arg = INT_MAX;
+    Lane<D, NQ> st;
 #pragma unroll
-    for (int j = 0; j < NB; j++) st.acc[j] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+    for (int qd = 0; qd < NQ; qd++) {
+        st.m[qd] = -INFINITY;
+        st.lsum[qd] = st.zsum[qd] = st.wsum[qd] = 0.f;
+        st.mn[qd] = INFINITY;
+        st.mx[qd] = -INFINITY;
+        st.arg[qd] = INT_MAX;
+#pragma unroll
+        for (int dh = 0; dh < NH; dh++) st.acc[qd][dh] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto qop = [&](int qd, int s) {
+        uint2 v;
+        __builtin_memcpy(&v, qs + ((qd * NS + s) * 4 + j) * 4, 8);
+        return __builtin_bit_cast(fkv_h4, v);
+    };
 
     for (int k = k0 + wave; k < k1; k += kWavesPerGroup) {
         if (k >= nt_near && k < nt_near + nt_far) {
-            // ---------------- far tile: 4 groups of 16 tokens ----------------
+            // ------------------------------ far tile ------------------------------
             const int tile = k - nt_near;
-            const int64_t g0 = (int64_t)tile * 4;  // first group
-            const uint8_t* kb = a.blob + a.L.far_k + bkv * (int64_t)a.L.F_pad * D + g0 * 16 * D + lane * (D / 4);
-            const uint32_t* vb = (const uint32_t*)(a.blob + a.L.far_v + bkv * (int64_t)a.L.F_pad * D / 2) +
-                                 g0 * 2 * D + lane * (D / 32);
-            const uint32_t* zb = (const uint32_t*)(a.blob + a.L.far_sz) + bkv * a.L.F_pad + g0 * 16 + 4 * kg;
-            uint32_t kw[4][NB], vw[4][NB / 2], sz[4][4];
+            const uint8_t* kb = a.blob + a.L.far_k + (bkv * a.L.F_pad + (int64_t)tile * kTile) * D + lane * 16;
+            const uint8_t* vb = a.blob + a.L.far_v + (bkv * a.L.F_pad + (int64_t)tile * kTile) * D / 2 + lane * 16;
+            uint32_t kw[NS];     // dword s = dims 4s..4s+3 of token `lane`
+            uint32_t vw[D / 8];  // nibble dwords of dim 64dh + lane
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-#pragma unroll
-                for (int q4 = 0; q4 < NB / 4; q4++) {
-                    const uint4 x = *(const uint4*)(kb + g * 16 * D + q4 * 16);
-                    kw[g][4 * q4] = x.x; kw[g][4 * q4 + 1] = x.y; kw[g][4 * q4 + 2] = x.z; kw[g][4 * q4 + 3] = x.w;
-                }
-                if constexpr (NB / 2 == 4) {
-                    const uint4 x = *(const uint4*)(vb + g * 2 * D);
-                    vw[g][0] = x.x; vw[g][1] = x.y; vw[g][2] = x.z; vw[g][3] = x.w;
-                } else {
-                    const uint2 x = *(const uint2*)(vb + g * 2 * D);
-                    vw[g][0] = x.x; vw[g][1] = x.y;
-                }
-                const uint4 z = *(const uint4*)(zb + g * 16);
-                sz[g][0] = z.x; sz[g][1] = z.y; sz[g][2] = z.z; sz[g][3] = z.w;
+            for (int c = 0; c < D / 16; c++) {
+                const uint4 x = *(const uint4*)(kb + c * 1024);
+                kw[4 * c] = x.x; kw[4 * c + 1] = x.y; kw[4 * c + 2] = x.z; kw[4 * c + 3] = x.w;
             }
-            float sc[4][4];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
+            for (int c = 0; c < D / 32; c++) {
+                const uint4 x = *(const uint4*)(vb + c * 1024);
+                vw[4 * c] = x.x; vw[4 * c + 1] = x.y; vw[4 * c + 2] = x.z; vw[4 * c + 3] = x.w;
+            }
+            const uint4 z4 = *(const uint4*)((const uint32_t*)(a.blob + a.L.far_sz) + bkv * a.L.F_pad +
+                                             tile * kTile + 4 * blk);
+            const uint32_t sz[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) {
                 fkv_f4 acc = fkv_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int s = 0; s < NB; s++) acc = mfma16(e4m3x4(kw[g][s]), qb[s], acc);
+                for (int s = 0; s < NS; s++) acc = mfma4_local(e4m3x4(kw[s]), qop(qd, s), acc);
+                float sc[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const int t = tile * kTile + g * 16 + 4 * kg + e;
-                    const float s = acc[e] * a.inv_sqrt_d;
+                    const int t = tile * kTile + 4 * blk + e;
+                    const float sv = acc[e] * a.inv_sqrt_d;
                     const bool ok = t < a.L.F;
-                    sc[g][e] = ok ? s : -INFINITY;
-                    if (ok && s > st.mx) { st.mx = s; st.arg = t; }  // first index of the max
+                    sc[e] = ok ? sv : -INFINITY;
+                    if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
                 }
+                softmax_pv<D, NQ, true>(st, qd, sc, sz,
+                                        [&](int g, int dh) { return int4x4(vw[dh * 8 + (g >> 1)], g & 1); });
             }
-            softmax_pv<D, 4, true>(st, sc, sz, [&](int g, int j) { return int4x4(vw[g][j >> 1], j & 1); });
         } else {
-            // ---------- fp16 tile (near slots or decode rows): 2 x 2 groups ----------
+            // ------------------- fp16 tile: near slots or decode rows -------------------
             const bool near = k < nt_near;
             const int tile = near ? k : k - nt_near - nt_far;
             const int count = near ? nv : a.n_dec;
-#pragma unroll 1
-            for (int half = 0; half < 2; half++) {
-                const int gbase = tile * 4 + half * 2;  // first 16-token group
-                uint32_t kw[2][2 * NB], vw[2][2 * NB];
+            const int tk = tile * kTile + lane;  // this lane's token for the score operand
+            fkv_f4 sacc[NQ];
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+            const uint16_t* kb = (const uint16_t*)(a.blob + a.L.near_k) +
+                                 (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D + lane * 8;
+            const uint16_t* kr = a.dec_k + (bkv * a.n_dec + (tk < count ? tk : 0)) * D;
+#pragma unroll
+            for (int cg = 0; cg < D / 32; cg++) {  // 4 chunks (8 steps) per round
+                uint32_t kw[16];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    uint4 x;
+                    if (near) {
+                        x = *(const uint4*)(kb + (cg * 4 + c) * 512);
+                    } else {
+                        x = tk < count ? *(const uint4*)(kr + (cg * 4 + c) * 8) : make_uint4(0, 0, 0, 0);
+                    }
+                    kw[4 * c] = x.x; kw[4 * c + 1] = x.y; kw[4 * c + 2] = x.z; kw[4 * c + 3] = x.w;
+                }
+#pragma unroll
+                for (int qd = 0; qd < NQ; qd++)
+#pragma unroll
+                    for (int s = 0; s < 8; s++)
+                        sacc[qd] = mfma4_local(h4_of(kw[2 * s], kw[2 * s + 1]), qop(qd, cg * 8 + s), sacc[qd]);
+            }
+            // values: 8-byte units x = dh*16 + g (4-token group g, dim 64dh + lane)
+            uint32_t vw[D / 2];
+            const uint16_t* vbn = (const uint16_t*)(a.blob + a.L.near_v) +
+                                  (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D + lane * 8;
+#pragma unroll
+            for (int c = 0; c < D / 8; c++) {
+                uint4 x;
                 if (near) {
-                    const uint16_t* kb = (const uint16_t*)(a.blob + a.L.near_k) + bkv * (int64_t)a.L.Na_pad * D +
-                                         (int64_t)gbase * 16 * D + lane * (D / 4);
-                    const uint16_t* vb = (const uint16_t*)(a.blob + a.L.near_v) + bkv * (int64_t)a.L.Na_pad * D +
-                                         (int64_t)gbase * 16 * D + lane * (D / 4);
-#pragma unroll
-                    for (int g = 0; g < 2; g++)
-#pragma unroll
-                        for (int q4 = 0; q4 < NB / 2; q4++) {
-                            const uint4 x = *(const uint4*)(kb + g * 16 * D + q4 * 8);
-                            const uint4 y = *(const uint4*)(vb + g * 16 * D + q4 * 8);
-                            kw[g][4 * q4] = x.x; kw[g][4 * q4 + 1] = x.y; kw[g][4 * q4 + 2] = x.z; kw[g][4 * q4 + 3] = x.w;
-                            vw[g][4 * q4] = y.x; vw[g][4 * q4 + 1] = y.y; vw[g][4 * q4 + 2] = y.z; vw[g][4 * q4 + 3] = y.w;
-                        }
+                    x = *(const uint4*)(vbn + c * 512);
                 } else {
-                    // decode rows are row-major (B, Hkv, n_dec, D): gather operands
+                    uint16_t hv[8];
 #pragma unroll
-                    for (int g = 0; g < 2; g++) {
-                        const int tk = (gbase + g) * 16 + m;
-                        const uint16_t* kr = a.dec_k + (bkv * a.n_dec + (tk < count ? tk : 0)) * D;
+                    for (int u = 0; u < 2; u++) {
+                        const int xi = 2 * c + u, g = xi % 16, dh = xi / 16;
 #pragma unroll
-                        for (int s = 0; s < NB; s++) {
-                            const uint2 x = tk < count ? *(const uint2*)(kr + 16 * s + 4 * kg) : make_uint2(0, 0);
-                            kw[g][2 * s] = x.x;
-                            kw[g][2 * s + 1] = x.y;
-                        }
-#pragma unroll
-                        for (int j = 0; j < NB; j++) {
-                            uint16_t hv[4];
-#pragma unroll
-                            for (int e = 0; e < 4; e++) {
-                                const int tv = (gbase + g) * 16 + 4 * kg + e;
-                                hv[e] = tv < count ? a.dec_v[(bkv * a.n_dec + tv) * D + 16 * j + m] : (uint16_t)0;
-                            }
-                            vw[g][2 * j] = hv[0] | ((uint32_t)hv[1] << 16);
-                            vw[g][2 * j + 1] = hv[2] | ((uint32_t)hv[3] << 16);
+                        for (int e = 0; e < 4; e++) {
+                            const int tv = tile * kTile + 4 * g + e;
+                            hv[4 * u + e] = tv < count ? a.dec_v[(bkv * a.n_dec + tv) * D + 64 * dh + lane] : (uint16_t)0;
                         }
                     }
+                    x = make_uint4(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16),
+                                   hv[4] | ((uint32_t)hv[5] << 16), hv[6] | ((uint32_t)hv[7] << 16));
                 }
-                float sc[2][4];
-                uint32_t szd[2][4] = {};
+                vw[4 * c] = x.x; vw[4 * c + 1] = x.y; vw[4 * c + 2] = x.z; vw[4 * c + 3] = x.w;
+            }
+            const uint32_t szd[4] = {0, 0, 0, 0};
 #pragma unroll
-                for (int g = 0; g < 2; g++) {
-                    fkv_f4 acc = fkv_f4{0.f, 0.f, 0.f, 0.f};
+            for (int qd = 0; qd < NQ; qd++) {
+                float sc[4];
 #pragma unroll
-                    for (int s = 0; s < NB; s++) acc = mfma16(h4_of(kw[g][2 * s], kw[g][2 * s + 1]), qb[s], acc);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int t = (gbase + g) * 16 + 4 * kg + e;
-                        const float s = acc[e] * a.inv_sqrt_d;
-                        const bool ok = t < count;
-                        sc[g][e] = ok ? s : -INFINITY;
-                        if (ok) st.mn = fminf(st.mn, s);
-                    }
+                for (int e = 0; e < 4; e++) {
+                    const int t = tile * kTile + 4 * blk + e;
+                    const float sv = sacc[qd][e] * a.inv_sqrt_d;
+                    const bool ok = t < count;
+                    sc[e] = ok ? sv : -INFINITY;
+                    if (ok) st.mn[qd] = fminf(st.mn[qd], sv);
                 }
-                softmax_pv<D, 2, false>(st, sc, szd,
-                                        [&](int g, int j) { return h4_of(vw[g][2 * j], vw[g][2 * j + 1]); });
+                softmax_pv<D, NQ, false>(st, qd, sc, szd, [&](int g, int dh) {
+                    const int xi = dh * 16 + g;
+                    return h4_of(vw[2 * xi], vw[2 * xi + 1]);
+                });
             }
         }
     }
 
-    // ---- per-head reduction over the 4 lanes (kg) sharing head m ----
-    float l = st.lsum, z = st.zsum, ws = st.wsum, mn = st.mn, mx = st.mx;
-    int arg = st.arg;
-#pragma unroll
-    for (int o = 16; o <= 32; o <<= 1) {
-        l += wave_xor(l, o);
-        z += wave_xor(z, o);
-        ws += wave_xor(ws, o);
-        mn = fminf(mn, wave_xor(mn, o));
-        const float ox = wave_xor(mx, o);
-        const int oa = wave_xor(arg, o);
-        if (ox > mx || (ox == mx && oa < arg)) { mx = ox; arg = oa; }
-    }
-    z -= 23.5f * ws;  // remove the +16 INT4 decode offset and the 7.5 centring
+    // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
     float* wr = wrec[wave];
-    if (m < ng) {
-        if (kg == 0) {
-            wr[m * RS + 0] = st.m;
-            wr[m * RS + 1] = l;
-            wr[m * RS + 2] = mn;
-            wr[m * RS + 3] = mx;
-            wr[m * RS + 4] = __int_as_float(arg);
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        float l = st.lsum[qd], z = st.zsum[qd], ws = st.wsum[qd], mn = st.mn[qd], mx = st.mx[qd];
+        int arg = st.arg[qd];
+#pragma unroll
+        for (int o = 4; o <= 32; o <<= 1) {
+            l += wave_xor(l, o);
+            z += wave_xor(z, o);
+            ws += wave_xor(ws, o);
+            mn = fminf(mn, wave_xor(mn, o));
+            const float ox = wave_xor(mx, o);
+            const int oa = wave_xor(arg, o);
+            if (ox > mx || (ox == mx && oa < arg)) { mx = ox; arg = oa; }
         }
+        z -= 23.5f * ws;  // remove the +16 INT4 decode offset and the 7.5 centring
+        const float z0 = quad_bcast<0>(z), z1 = quad_bcast<1>(z), z2 = quad_bcast<2>(z), z3 = quad_bcast<3>(z);
+        const int h = 4 * qd + j;
+        if (lane < 4 && h < ng) {
+            wr[h * RS + 0] = st.m[qd];
+            wr[h * RS + 1] = l;
+            wr[h * RS + 2] = mn;
+            wr[h * RS + 3] = mx;
+            wr[h * RS + 4] = __int_as_float(arg);
+        }
+        const float zz[4] = {z0, z1, z2, z3};
 #pragma unroll
-        for (int j = 0; j < NB; j++)
+        for (int i = 0; i < 4; i++) {
+            if (4 * qd + i < ng) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) wr[m * RS + kHdr + 16 * j + 4 * kg + e] = st.acc[j][e] + z;
+                for (int dh = 0; dh < NH; dh++) wr[(4 * qd + i) * RS + kHdr + 64 * dh + lane] = st.acc[qd][dh][i] + zz[i];
+            }
+        }
     }
     __syncthreads();
 
@@ -662,6 +703,18 @@ struct fkv_attn_impl {
 
 namespace fkv {
 
+typedef void (*AttnKernel)(AttnArgs);
+
+template <int D>
+static AttnKernel pick_attn(int nq) {
+    switch (nq) {
+        case 1: return attn_kernel<D, 1>;
+        case 2: return attn_kernel<D, 2>;
+        case 3: return attn_kernel<D, 3>;
+        default: return attn_kernel<D, 4>;
+    }
+}
+
 static int grid_for(int64_t n, int block) {
     int64_t g = cdiv(n, block);
     if (g < 1) g = 1;
@@ -725,12 +778,12 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
         const int blk = 256;
         const fkv::BlobLayout L = h->L;
         if (Na > 0)
-            hipLaunchKernelGGL(fkv::pack_near_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * (L.Na_pad / 16) * 64, blk)),
+            hipLaunchKernelGGL(fkv::pack_near_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.Na_pad * (D / 16), blk)),
                                dim3(blk), 0, st, near_k, near_v, near_dtype, L, h->blob);
         if (F > 0) {
-            hipLaunchKernelGGL(fkv::pack_far_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * (L.F_pad / 16) * 64, blk)),
+            hipLaunchKernelGGL(fkv::pack_far_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 16), blk)),
                                dim3(blk), 0, st, far_k, L, h->blob, bad);
-            hipLaunchKernelGGL(fkv::pack_far_v_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * (L.F_pad / 16) * 64, blk)),
+            hipLaunchKernelGGL(fkv::pack_far_v_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 8), blk)),
                                dim3(blk), 0, st, far_v, far_v_scale, far_v_zero, sz_dtype, L, h->blob);
         }
         hipLaunchKernelGGL(fkv::pack_valid_kernel, dim3(1), dim3(blk), 0, st, near_valid, Hkv, L, h->blob);
@@ -810,8 +863,9 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
     a.tokens = spike_tokens;
     a.ws = h->ws;
     const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
-    if (L.D == 128) hipLaunchKernelGGL(fkv::attn_kernel<128>, grid, block, 0, st, a);
-    else hipLaunchKernelGGL(fkv::attn_kernel<64>, grid, block, 0, st, a);
+    const int nq = (ng_max + 3) / 4;
+    fkv::AttnKernel k = L.D == 128 ? fkv::pick_attn<128>(nq) : fkv::pick_attn<64>(nq);
+    hipLaunchKernelGGL(k, grid, block, 0, st, a);
     if (splits > 1) {
         if (L.D == 128) hipLaunchKernelGGL(fkv::merge_kernel<128>, dim3(rows), dim3(256), 0, st, a);
         else hipLaunchKernelGGL(fkv::merge_kernel<64>, dim3(rows), dim3(256), 0, st, a);

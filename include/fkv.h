@@ -119,7 +119,9 @@ typedef struct fkv_blob_info {
     uint64_t blob_bytes;
     uint64_t near_k_offset;   /* [B*Hkv][Na_pad/64][D/8][64][8] fp16 tiles:
                                  token t, dim d at ((t/64)*D/8 + d/8)*512 + (t%64)*8 + d%8 */
-    uint64_t near_v_offset;   /* (B,Hkv,Na_pad,D) fp16 rows */
+    uint64_t near_v_offset;   /* [B*Hkv][Na_pad/64] tiles of 64*D fp16: token t,
+                                 dim d, x = (d/64)*16 + (t%64)/4, at
+                                 (t/64)*64*D + (x/2)*512 + (d%64)*8 + (x%2)*4 + t%4 */
     uint64_t near_valid_offset; /* (Hkv) uint32 */
     int32_t n_near_alloc;     /* Na: near slots per head incl. headroom */
     int32_t n_far;
