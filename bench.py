@@ -93,6 +93,10 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured HIP graph (for counter collection)")
+    ap.add_argument("--no-read-ceiling", action="store_true", help="skip the in-run HBM read-ceiling probe")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also time a plain device copy of this many MiB (HBM calibration; reported "
+                         "as copy_gbs, read + write bytes)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -225,7 +229,68 @@ def main():
             "sample": f"oracle dequant+SDPA formulation (fp64 softmax, OpenMP over (b, q head)) on batch row 0 "
                       f"of 1 layer of {args.config}, {reps} reps; us_per_layer scaled x{B} to the full batch",
         }
+    if args.copy_mib:
+        result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)
+        result["read_ceiling_gbs"], result["read_ceiling_launch"] = read_ceiling(torch, dev, args.copy_mib)
+    elif not args.no_read_ceiling:
+        # this box's streaming-read ceiling, measured beside the kernel
+        result["read_ceiling_gbs"], _ = read_ceiling(torch, dev, 2048, sweep=False)
     print(json.dumps(result), flush=True)
+
+
+def copy_bandwidth(torch, dev, mib, reps=20):
+    """Read + write GB/s of a plain device-to-device tensor copy of ``mib`` MiB
+    (the calibration kernel for HBM counters and the practical copy ceiling)."""
+    n = mib * (1 << 20)
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    sec = start.elapsed_time(end) / 1e3 / reps
+    print(f"[bench] copy of {mib} MiB: {sec * 1e6:.1f} us -> {2 * n / sec / 1e9:.1f} GB/s (read + write)",
+          file=sys.stderr, flush=True)
+    return round(2 * n / sec / 1e9, 1)
+
+
+def read_ceiling(torch, dev, mib, reps=20, sweep=True):
+    """Best read GB/s of the library's streaming-read probe over ``mib`` MiB,
+    swept over loads in flight per lane, non-temporal hint and grid size
+    (``sweep=False``: only the best launch found on MI355X)."""
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+    n = mib * (1 << 20)
+    buf = torch.empty(n, dtype=torch.uint8, device=dev).fill_(3)
+    best = (0.0, None)
+    for blocks in ((1024, 2048, 4096, 8192) if sweep else (2048,)):
+        out = torch.empty(blocks * 4, dtype=torch.int32, device=dev)
+        for unroll in ((1, 2, 4, 8) if sweep else (1,)):
+            for nt in ((0, 1) if sweep else (1,)):
+                def run():
+                    _lib.check(lib.fkv_hbm_read_probe(_lib.ptr(buf), n, unroll, nt, blocks, _lib.ptr(out),
+                                                      _lib.stream_ptr(dev)), "fkv_hbm_read_probe")
+                run()
+                torch.cuda.synchronize()
+                start = torch.cuda.Event(enable_timing=True)
+                end = torch.cuda.Event(enable_timing=True)
+                start.record()
+                for _ in range(reps):
+                    run()
+                end.record()
+                torch.cuda.synchronize()
+                gbs = n / (start.elapsed_time(end) / 1e3 / reps) / 1e9
+                print(f"[bench] read probe blocks={blocks} unroll={unroll} nt={nt}: {gbs:.1f} GB/s",
+                      file=sys.stderr, flush=True)
+                if gbs > best[0]:
+                    best = (gbs, dict(blocks=blocks, unroll=unroll, nontemporal=nt))
+    return round(best[0], 1), best[1]
 
 
 if __name__ == "__main__":

@@ -29,6 +29,7 @@
 #include <climits>
 #include <cmath>
 #include <cstring>
+#include <vector>
 
 #include "fkv_attn.h"
 #include "fkv_common.h"
@@ -62,9 +63,8 @@ BlobLayout make_layout(int B, int Hkv, int D, int Na, int F) {
     };
     L.near_k = place(bkv * L.Na_pad * D * 2);
     L.near_v = place(bkv * L.Na_pad * D * 2);
-    L.far_k = place(bkv * L.F_pad * D);
-    L.far_v = place(bkv * L.F_pad * D / 2);
-    L.far_sz = place(bkv * L.F_pad * 4);
+    L.far_rec = (size_t)far_record_bytes(D);
+    L.far = place(bkv * (L.F_pad / kTile) * L.far_rec);
     L.near_valid = place((size_t)Hkv * 4);
     L.total = off;
     return L;
@@ -116,7 +116,7 @@ __global__ void pack_far_k_kernel(const uint8_t* __restrict__ fk, BlobLayout L,
         const int64_t r = i / NB;
         const int t = (int)(r % L.F_pad);
         const int64_t bkv = r / L.F_pad;
-        uint8_t* dst = blob + L.far_k + bkv * (int64_t)L.F_pad * D;
+        uint8_t* dst = blob + L.far + far_rec_index(L, bkv, t / kTile) * (int64_t)L.far_rec;
         for (int e = 0; e < 16; e++) {
             const int d = blk * 16 + e;
             uint8_t b = 0;
@@ -125,7 +125,7 @@ __global__ void pack_far_k_kernel(const uint8_t* __restrict__ fk, BlobLayout L,
                 if ((b & 0x7F) == 0x7F) atomicOr(bad, 1u);
                 if ((b & 0x78) == 0) b &= 0x80;
             }
-            dst[far_k_index(t, d, D)] = b;
+            dst[far_k_index(t, d)] = b;
         }
     }
 }
@@ -157,7 +157,8 @@ __global__ void pack_far_v_kernel(const uint8_t* __restrict__ fv, const void* __
                 if (t < L.F) code = (fv[(bkv * L.F + t) * (D / 2) + d / 2] >> (4 * (d & 1))) & 15u;
                 word |= code << (bp * 8 + (e & 1) * 16 + (e >> 1) * 4);
             }
-        ((uint32_t*)(blob + L.far_v + bkv * (int64_t)L.F_pad * D / 2))[w] = word;
+        ((uint32_t*)(blob + L.far + far_rec_index(L, bkv, tile) * (int64_t)L.far_rec +
+                     far_v_section(D)))[rem] = word;
     }
     const int64_t nt = (int64_t)L.B * L.Hkv * L.F_pad;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nt;
@@ -169,7 +170,8 @@ __global__ void pack_far_v_kernel(const uint8_t* __restrict__ fv, const void* __
             const int64_t k = bkv * L.F + t;
             sz = (uint32_t)load_as_f16(fvs, k, sz_dtype) | ((uint32_t)load_as_f16(fvz, k, sz_dtype) << 16);
         }
-        ((uint32_t*)(blob + L.far_sz))[bkv * L.F_pad + t] = sz;
+        ((uint32_t*)(blob + L.far + far_rec_index(L, bkv, t / kTile) * (int64_t)L.far_rec +
+                     far_sz_section(D)))[t % kTile] = sz;
     }
 }
 
@@ -227,7 +229,9 @@ struct AttnArgs {
     uint16_t* out;  // (B, Hq, D) fp16
     int32_t* flags;
     int32_t* tokens;
-    float* ws;  // split partials: [row][split][ng][kHdr + D]
+    float* ws;      // split partials: [row][split][ng][kHdr + D]
+    int* arrive;    // [row] split arrival counters (zero between calls)
+    int near_plan;  // expected near tiles per row (balances the far split)
 };
 
 // v_mfma_f32_4x4x4f16: 16 independent 4x4x4 blocks; lane l supplies row /
@@ -265,6 +269,64 @@ __device__ inline float quad_bcast(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), I * 0x55, 0xF, 0xF, false));
 }
 
+__device__ inline uint32_t word_of(const uint4& x, int i) {
+    return i == 0 ? x.x : i == 1 ? x.y : i == 2 ? x.z : x.w;
+}
+
+typedef uint32_t fkv_v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t fkv_v4u __attribute__((ext_vector_type(4)));
+#define FKV_LDS __attribute__((address_space(3)))
+
+// 32-bit LDS address of a pointer into a __shared__ array.
+__device__ inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const FKV_LDS void*)p;
+}
+
+// q as the B operand of the score MFMA, in LDS as [qd][s][j][4 halves].
+template <int NS>
+struct QOperand {
+    const uint16_t* qs;
+    int base;  // j * 4 for lane quad position j
+    __device__ QOperand fresh() const {
+        QOperand r = *this;
+        asm volatile("" : "+v"(r.base));
+        return r;
+    }
+    __device__ fkv_h4 operator()(int qd, int s) const {
+        uint2 v;
+        __builtin_memcpy(&v, qs + base + (qd * NS + s) * 16, 8);
+        return __builtin_bit_cast(fkv_h4, v);
+    }
+    // Operands of k-steps s0..s0+7 of quad qd, read by one asm block that
+    // waits for its own LDS reads (used where LDS DMA is in flight: the
+    // compiler would otherwise drain every DMA before any LDS read).
+    __device__ void read8(int qd, int s0, fkv_h4 (&o)[8]) const {
+        const uint32_t addr = lds_addr(qs + base + (qd * NS + s0) * 16);
+        fkv_v2u r0, r1, r2, r3, r4, r5, r6, r7;
+        asm volatile(
+            "ds_read_b64 %0, %8\n"
+            "ds_read_b64 %1, %8 offset:32\n"
+            "ds_read_b64 %2, %8 offset:64\n"
+            "ds_read_b64 %3, %8 offset:96\n"
+            "ds_read_b64 %4, %8 offset:128\n"
+            "ds_read_b64 %5, %8 offset:160\n"
+            "ds_read_b64 %6, %8 offset:192\n"
+            "ds_read_b64 %7, %8 offset:224\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+            : "v"(addr)
+            : "memory");
+        o[0] = __builtin_bit_cast(fkv_h4, r0);
+        o[1] = __builtin_bit_cast(fkv_h4, r1);
+        o[2] = __builtin_bit_cast(fkv_h4, r2);
+        o[3] = __builtin_bit_cast(fkv_h4, r3);
+        o[4] = __builtin_bit_cast(fkv_h4, r4);
+        o[5] = __builtin_bit_cast(fkv_h4, r5);
+        o[6] = __builtin_bit_cast(fkv_h4, r6);
+        o[7] = __builtin_bit_cast(fkv_h4, r7);
+    }
+};
+
 template <int D, int NQ>
 struct Lane {
     // per head quad: this lane tracks head 4*qd + (lane % 4)
@@ -273,18 +335,144 @@ struct Lane {
     fkv_f4 acc[NQ][D / 64];  // acc[qd][dh][i] = O[head 4qd+i][dim 64dh + lane]
 };
 
-enum TileKind { kNear = 0, kFar = 1, kDec = 2 };
+// One 64-token far tile as loaded from the blob: E4M3 keys (lane = token,
+// 16 codes per chunk), INT4 values (lane = dim), per-token scale|zero of the
+// lane's 4-token group.
+template <int D>
+struct FarTile {
+    uint4 k[D / 16];
+    uint4 v[D / 32];
+    uint4 sz;
+};
+
+// Far tile record -> an LDS slot with gfx950's direct global->LDS loads
+// (global_load_lds_dwordx4, non-temporal): the K|V sections as 1-KB chunks
+// by the whole wave, then the 256-byte SZ section by lanes 0..15.  Issues
+// far_dma_ops<D>() vector-memory instructions; completion is tracked with
+// vmcnt by the caller (the compiler does not order LDS reads after them).
+template <int D>
+constexpr int far_dma_ops() { return 3 * D / 32 + 1; }
+
+template <int D>
+__device__ inline void dma_far(const AttnArgs& a, int64_t bkv, int tile, int lane, uint8_t* slot) {
+    const uint8_t* rec = a.blob + a.L.far + far_rec_index(a.L, bkv, tile) * (int64_t)a.L.far_rec;
+#pragma unroll
+    for (int c = 0; c < 3 * D / 32; c++)
+        __builtin_amdgcn_global_load_lds((const void*)(rec + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
+                                         0, 2);
+    if (lane < 16)
+        __builtin_amdgcn_global_load_lds((const void*)(rec + far_sz_section(D) + lane * 16),
+                                         (FKV_LDS void*)(slot + far_sz_section(D)), 16, 0, 2);
+}
+
+__device__ inline uint4 u4_of(fkv_v4u v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
+// One half (K: 0 or V: 1) of a near-tier tile -> an LDS slot: D/8 1-KB
+// chunks (the tile layout is already chunk-major).
+template <int D>
+__device__ inline void dma_near(const AttnArgs& a, int64_t bkv, int tile, int half, int lane, uint8_t* slot) {
+    const uint8_t* src = a.blob + (half ? a.L.near_v : a.L.near_k) +
+                         (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D * 2;
+#pragma unroll
+    for (int c = 0; c < D / 8; c++)
+        __builtin_amdgcn_global_load_lds((const void*)(src + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
+                                         0, 2);
+}
+
+// The lane's operands of a far tile held in an LDS slot, read by one asm
+// block that waits for its own LDS reads (see QOperand::read8).
+__device__ inline void lds_far(FarTile<128>& r, const uint8_t* slot, int lane) {
+    const uint32_t a = lds_addr(slot + lane * 16), z = lds_addr(slot + far_sz_section(128) + (lane >> 2) * 16);
+    fkv_v4u c0, c1, c2, c3, c4, c5, c6, c7, c8, c9, c10, c11, sz;
+    asm volatile(
+        "ds_read_b128 %0, %13\n"
+        "ds_read_b128 %1, %13 offset:1024\n"
+        "ds_read_b128 %2, %13 offset:2048\n"
+        "ds_read_b128 %3, %13 offset:3072\n"
+        "ds_read_b128 %4, %13 offset:4096\n"
+        "ds_read_b128 %5, %13 offset:5120\n"
+        "ds_read_b128 %6, %13 offset:6144\n"
+        "ds_read_b128 %7, %13 offset:7168\n"
+        "ds_read_b128 %8, %13 offset:8192\n"
+        "ds_read_b128 %9, %13 offset:9216\n"
+        "ds_read_b128 %10, %13 offset:10240\n"
+        "ds_read_b128 %11, %13 offset:11264\n"
+        "ds_read_b128 %12, %14\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(c0), "=&v"(c1), "=&v"(c2), "=&v"(c3), "=&v"(c4), "=&v"(c5), "=&v"(c6), "=&v"(c7), "=&v"(c8),
+          "=&v"(c9), "=&v"(c10), "=&v"(c11), "=&v"(sz)
+        : "v"(a), "v"(z)
+        : "memory");
+    r.k[0] = u4_of(c0); r.k[1] = u4_of(c1); r.k[2] = u4_of(c2); r.k[3] = u4_of(c3);
+    r.k[4] = u4_of(c4); r.k[5] = u4_of(c5); r.k[6] = u4_of(c6); r.k[7] = u4_of(c7);
+    r.v[0] = u4_of(c8); r.v[1] = u4_of(c9); r.v[2] = u4_of(c10); r.v[3] = u4_of(c11);
+    r.sz = u4_of(sz);
+}
+
+__device__ inline void lds_far(FarTile<64>& r, const uint8_t* slot, int lane) {
+    const uint32_t a = lds_addr(slot + lane * 16), z = lds_addr(slot + far_sz_section(64) + (lane >> 2) * 16);
+    fkv_v4u c0, c1, c2, c3, c4, c5, sz;
+    asm volatile(
+        "ds_read_b128 %0, %7\n"
+        "ds_read_b128 %1, %7 offset:1024\n"
+        "ds_read_b128 %2, %7 offset:2048\n"
+        "ds_read_b128 %3, %7 offset:3072\n"
+        "ds_read_b128 %4, %7 offset:4096\n"
+        "ds_read_b128 %5, %7 offset:5120\n"
+        "ds_read_b128 %6, %8\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(c0), "=&v"(c1), "=&v"(c2), "=&v"(c3), "=&v"(c4), "=&v"(c5), "=&v"(sz)
+        : "v"(a), "v"(z)
+        : "memory");
+    r.k[0] = u4_of(c0); r.k[1] = u4_of(c1); r.k[2] = u4_of(c2); r.k[3] = u4_of(c3);
+    r.v[0] = u4_of(c4); r.v[1] = u4_of(c5);
+    r.sz = u4_of(sz);
+}
 
 template <int D>
 __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b, int head0, int ng);
 
-// Online softmax of one 64-token tile for head quad qd (scores s[e] of
-// tokens 4*(lane/4) + e, head 4qd + lane%4), then P.V: 16 broadcast MFMAs
-// per 64-dim half, A = the weights of 4-token group g (abid = g), B = the
-// values of that group at dim 64dh + lane.
-template <int D, int NQ, bool FAR, typename VOp>
-__device__ inline void softmax_pv(Lane<D, NQ>& st, int qd, const float (&s)[4], const uint32_t (&sz)[4],
-                                  VOp vop) {
+// P.V step of 4-token group G: the weights of the group (block G of each
+// quad's w4) broadcast to all 16 blocks, times the group's values of dims
+// 64dh + 4b..4b+3; one value operand serves every head quad.
+template <int D, int NQ, int G, typename VOp>
+__device__ inline void pv_group(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vop) {
+#pragma unroll
+    for (int dh = 0; dh < D / 64; dh++) {
+        const fkv_h4 v = vop(G, dh);
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) st.acc[qd][dh] = mfma4<G>(w4[qd], v, st.acc[qd][dh]);
+    }
+}
+
+template <int D, int NQ, typename VOp>
+__device__ inline void pv_all(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vop) {
+    pv_group<D, NQ, 0>(st, w4, vop);
+    pv_group<D, NQ, 1>(st, w4, vop);
+    pv_group<D, NQ, 2>(st, w4, vop);
+    pv_group<D, NQ, 3>(st, w4, vop);
+    pv_group<D, NQ, 4>(st, w4, vop);
+    pv_group<D, NQ, 5>(st, w4, vop);
+    pv_group<D, NQ, 6>(st, w4, vop);
+    pv_group<D, NQ, 7>(st, w4, vop);
+    pv_group<D, NQ, 8>(st, w4, vop);
+    pv_group<D, NQ, 9>(st, w4, vop);
+    pv_group<D, NQ, 10>(st, w4, vop);
+    pv_group<D, NQ, 11>(st, w4, vop);
+    pv_group<D, NQ, 12>(st, w4, vop);
+    pv_group<D, NQ, 13>(st, w4, vop);
+    pv_group<D, NQ, 14>(st, w4, vop);
+    pv_group<D, NQ, 15>(st, w4, vop);
+}
+
+// Online-softmax update of head quad qd for one 64-token tile (scores s[e]
+// of tokens 4*(lane/4) + e, head 4qd + lane%4).  Writes the fp16 P.V
+// weights of the lane (far tiles: p * per-token scale; the zero point and
+// the INT4 decode offset go to per-head scalars) and returns whether any
+// weight of the lane is non-zero.
+template <int D, int NQ, bool FAR>
+__device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], const uint32_t (&sz)[4],
+                                 fkv_h4& w4) {
     constexpr int NH = D / 64;
     float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
 #pragma unroll
@@ -329,38 +517,393 @@ __device__ inline void softmax_pv(Lane<D, NQ>& st, int qd, const float (&s)[4], 
         }
         any |= p > 0.f;
     }
-    if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
-    const fkv_h4 w4 = fkv_h4{wh[0], wh[1], wh[2], wh[3]};
+    w4 = fkv_h4{wh[0], wh[1], wh[2], wh[3]};
+    return any;
+}
+
+// Scores, spike tracking, softmax and P.V of one loaded far tile.
+template <int D, int NQ, typename QOp>
+__device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int tile, int F, int blk,
+                                   float inv_sqrt_d, const QOp& q_lds) {
+    constexpr int NS = D / 4;
+    const uint32_t sz[4] = {r.sz.x, r.sz.y, r.sz.z, r.sz.w};
+    fkv_f4 sacc[NQ];
 #pragma unroll
-    for (int dh = 0; dh < NH; dh++) {
-        fkv_f4 acc = st.acc[qd][dh];
-        acc = mfma4<0>(w4, vop(0, dh), acc);
-        acc = mfma4<1>(w4, vop(1, dh), acc);
-        acc = mfma4<2>(w4, vop(2, dh), acc);
-        acc = mfma4<3>(w4, vop(3, dh), acc);
-        acc = mfma4<4>(w4, vop(4, dh), acc);
-        acc = mfma4<5>(w4, vop(5, dh), acc);
-        acc = mfma4<6>(w4, vop(6, dh), acc);
-        acc = mfma4<7>(w4, vop(7, dh), acc);
-        acc = mfma4<8>(w4, vop(8, dh), acc);
-        acc = mfma4<9>(w4, vop(9, dh), acc);
-        acc = mfma4<10>(w4, vop(10, dh), acc);
-        acc = mfma4<11>(w4, vop(11, dh), acc);
-        acc = mfma4<12>(w4, vop(12, dh), acc);
-        acc = mfma4<13>(w4, vop(13, dh), acc);
-        acc = mfma4<14>(w4, vop(14, dh), acc);
-        acc = mfma4<15>(w4, vop(15, dh), acc);
-        st.acc[qd][dh] = acc;
+    for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s0 = 0; s0 < NS; s0 += 8) {
+        fkv_h4 q8[NQ][8];
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+#pragma unroll
+        for (int s = s0; s < s0 + 8; s++) {
+            const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k4, q8[qd][s - s0], sacc[qd]);
+        }
+    }
+    fkv_h4 w4[NQ];
+    bool any = false;
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = tile * kTile + 4 * blk + e;
+            const float sv = sacc[qd][e] * inv_sqrt_d;
+            const bool ok = t < F;
+            sc[e] = ok ? sv : -INFINITY;
+            if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
+        }
+        any |= softmax_w<D, NQ, true>(st, qd, sc, sz, w4[qd]);
+    }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
+    pv_all<D, NQ>(st, w4, [&](int g, int dh) {
+        const int u = dh * 8 + (g >> 1);
+        return int4x4(word_of(r.v[u >> 2], u & 3), g & 1);
+    });
+}
+
+// Scores, min-near tracking, softmax and P.V of one fp16 tile (near slots or
+// decode rows): key operands from kop(s) (lane = token, dims 4s..4s+3),
+// value operands from vop(g, dh).
+template <int D, int NQ, typename KOp, typename VOp, typename QOp, typename Mid>
+__device__ inline void fp16_compute(Lane<D, NQ>& st, KOp kop, VOp vop, int tile, int count, int blk,
+                                    float inv_sqrt_d, const QOp& q_lds, Mid after_scores) {
+    constexpr int NS = D / 4;
+    const QOp qop = q_lds.fresh();
+    const uint32_t szd[4] = {0, 0, 0, 0};
+    fkv_f4 sacc[NQ];
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const fkv_h4 k4 = kop(s);
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k4, qop(qd, s), sacc[qd]);
+    }
+    after_scores();
+    fkv_h4 w4[NQ];
+    bool any = false;
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = tile * kTile + 4 * blk + e;
+            const float sv = sacc[qd][e] * inv_sqrt_d;
+            const bool ok = t < count;
+            sc[e] = ok ? sv : -INFINITY;
+            if (ok) st.mn[qd] = fminf(st.mn[qd], sv);
+        }
+        any |= softmax_w<D, NQ, false>(st, qd, sc, szd, w4[qd]);
+    }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;
+    pv_all<D, NQ>(st, w4, vop);
+}
+
+// Min-near tracking, softmax and P.V of an fp16 tile whose scores are in
+// sacc (token 4*(lane/4) + e, head 4qd + lane%4), value operands from vop.
+template <int D, int NQ, typename VOp>
+__device__ inline void fp16_pv(Lane<D, NQ>& st, const fkv_f4 (&sacc)[NQ], VOp vop, int tile, int count, int blk,
+                               float inv_sqrt_d) {
+    const uint32_t szd[4] = {0, 0, 0, 0};
+    fkv_h4 w4[NQ];
+    bool any = false;
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = tile * kTile + 4 * blk + e;
+            const float sv = sacc[qd][e] * inv_sqrt_d;
+            const bool ok = t < count;
+            sc[e] = ok ? sv : -INFINITY;
+            if (ok) st.mn[qd] = fminf(st.mn[qd], sv);
+        }
+        any |= softmax_w<D, NQ, false>(st, qd, sc, szd, w4[qd]);
+    }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;
+    pv_all<D, NQ>(st, w4, vop);
+}
+
+// NC 16-byte chunks (1 KB apart) of the lane's operand bytes in an LDS
+// slot, read by one asm block that waits for its own LDS reads.
+__device__ inline void lds_chunks(fkv_v4u (&o)[16], const uint8_t* p) {
+    const uint32_t a = lds_addr(p);
+    asm volatile(
+        "ds_read_b128 %0, %16\n"
+        "ds_read_b128 %1, %16 offset:1024\n"
+        "ds_read_b128 %2, %16 offset:2048\n"
+        "ds_read_b128 %3, %16 offset:3072\n"
+        "ds_read_b128 %4, %16 offset:4096\n"
+        "ds_read_b128 %5, %16 offset:5120\n"
+        "ds_read_b128 %6, %16 offset:6144\n"
+        "ds_read_b128 %7, %16 offset:7168\n"
+        "ds_read_b128 %8, %16 offset:8192\n"
+        "ds_read_b128 %9, %16 offset:9216\n"
+        "ds_read_b128 %10, %16 offset:10240\n"
+        "ds_read_b128 %11, %16 offset:11264\n"
+        "ds_read_b128 %12, %16 offset:12288\n"
+        "ds_read_b128 %13, %16 offset:13312\n"
+        "ds_read_b128 %14, %16 offset:14336\n"
+        "ds_read_b128 %15, %16 offset:15360\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7]),
+          "=&v"(o[8]), "=&v"(o[9]), "=&v"(o[10]), "=&v"(o[11]), "=&v"(o[12]), "=&v"(o[13]), "=&v"(o[14]),
+          "=&v"(o[15])
+        : "v"(a)
+        : "memory");
+}
+
+__device__ inline void lds_chunks(fkv_v4u (&o)[8], const uint8_t* p) {
+    const uint32_t a = lds_addr(p);
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:1024\n"
+        "ds_read_b128 %2, %8 offset:2048\n"
+        "ds_read_b128 %3, %8 offset:3072\n"
+        "ds_read_b128 %4, %8 offset:4096\n"
+        "ds_read_b128 %5, %8 offset:5120\n"
+        "ds_read_b128 %6, %8 offset:6144\n"
+        "ds_read_b128 %7, %8 offset:7168\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7])
+        : "v"(a)
+        : "memory");
+}
+
+// Scores of a near-tier tile whose keys are in an LDS slot (chunk c = dims
+// 8c..8c+7 of the lane's token).
+template <int D, int NQ, typename QOp>
+__device__ inline void near_scores_lds(fkv_f4 (&sacc)[NQ], const uint8_t* slot, int lane, const QOp& q_lds) {
+    constexpr int NS = D / 4;
+    fkv_v4u kx[D / 8];
+    lds_chunks(kx, slot + lane * 16);
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s0 = 0; s0 < NS; s0 += 8) {
+        fkv_h4 q8[NQ][8];
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+#pragma unroll
+        for (int s = s0; s < s0 + 8; s++) {
+            const fkv_v4u& x = kx[s >> 1];
+            const fkv_h4 k4 = (s & 1) ? h4_of(x.z, x.w) : h4_of(x.x, x.y);
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k4, q8[qd][s - s0], sacc[qd]);
+        }
     }
 }
 
+// Softmax and P.V of a near-tier tile whose values are in an LDS slot
+// (8-byte unit x = dh*16 + g of the lane's dim 64dh + lane).
+template <int D, int NQ>
+__device__ inline void near_pv_lds(Lane<D, NQ>& st, const fkv_f4 (&sacc)[NQ], const uint8_t* slot, int lane,
+                                   int tile, int count, float inv_sqrt_d) {
+    fkv_v4u vx[D / 8];
+    lds_chunks(vx, slot + lane * 16);
+    fp16_pv<D, NQ>(
+        st, sacc,
+        [&](int g, int dh) {
+            const int xi = dh * 16 + g;
+            const fkv_v4u& x = vx[xi >> 1];
+            return (xi & 1) ? h4_of(x.z, x.w) : h4_of(x.x, x.y);
+        },
+        tile, count, lane >> 2, inv_sqrt_d);
+}
+
+// Decode-buffer tile: rows (n_dec, D) row-major fp16.  A lane reads its
+// token's key row for the score operand; the value operand (dim
+// 64dh + lane of the 4 tokens of group g) is gathered when P.V needs it.
+template <int D, int NQ, typename QOp>
+__device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int64_t bkv, int tile, int lane, const QOp& qop) {
+    const int count = a.n_dec;
+    const int tk = tile * kTile + lane;
+    uint4 kx[D / 8];
+    const uint16_t* kr = a.dec_k + (bkv * count + (tk < count ? tk : 0)) * D;
+#pragma unroll
+    for (int c = 0; c < D / 8; c++) kx[c] = tk < count ? *(const uint4*)(kr + c * 8) : make_uint4(0, 0, 0, 0);
+    const uint16_t* vr = a.dec_v + bkv * count * D + lane;
+    fp16_compute<D, NQ>(
+        st,
+        [&](int s) {
+            const uint4& x = kx[s >> 1];
+            return (s & 1) ? h4_of(x.z, x.w) : h4_of(x.x, x.y);
+        },
+        [&](int g, int dh) {
+            uint16_t hv[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int tv = tile * kTile + 4 * g + e;
+                hv[e] = tv < count ? vr[(int64_t)tv * D + 64 * dh] : (uint16_t)0;
+            }
+            return h4_of(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+        },
+        tile, count, lane >> 2, a.inv_sqrt_d, qop, []() {});
+}
+
+// Merge of the partial records of all splits of one row into `fin`
+// (csrc/kernels/foveated_attn.metal:394-431 restated for partials in
+// memory): split maxima are rescaled to the global max; spike fields take
+// the min and the first-index max.  `hdr` / `scl` are LDS scratch.
+__device__ inline float ld_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D>
+__device__ inline void merge_splits(const float* src, int ns, int ng, float* fin, float* hdr, float* scl,
+                                    float* stage, int stage_cap) {
+    constexpr int RS = kHdr + D;
+    // All records of the row in one batch of coherent loads (one memory
+    // round trip), then everything else from LDS.
+    if (ns * ng * RS <= stage_cap) {
+        const int total = ns * ng * RS;
+#pragma unroll 8
+        for (int i = threadIdx.x; i < total; i += blockDim.x) stage[i] = ld_agent(src + i);
+        __syncthreads();
+        for (int i = threadIdx.x; i < ns * ng * kHdr; i += blockDim.x) {
+            const int sp = i / (ng * kHdr), r = i % (ng * kHdr);
+            hdr[i] = stage[sp * ng * RS + (r / kHdr) * RS + r % kHdr];
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < ng) {
+            const int g = threadIdx.x;
+            float M = -INFINITY;
+            for (int sp = 0; sp < ns; sp++) M = fmaxf(M, hdr[(sp * ng + g) * kHdr]);
+            float L = 0.f, mn = INFINITY, mx = -INFINITY;
+            int arg = INT_MAX;
+            for (int sp = 0; sp < ns; sp++) {
+                const float* h = hdr + (sp * ng + g) * kHdr;
+                const float f = h[0] == -INFINITY ? 0.f : __expf(h[0] - M);
+                scl[g * kMaxSplits + sp] = f;
+                L += f * h[1];
+                mn = fminf(mn, h[2]);
+                const float fx = h[3];
+                const int fa = __float_as_int(h[4]);
+                if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
+            }
+            fin[g * RS + 0] = M;
+            fin[g * RS + 1] = L;
+            fin[g * RS + 2] = mn;
+            fin[g * RS + 3] = mx;
+            fin[g * RS + 4] = __int_as_float(arg);
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
+            const int g = i / D, d = i % D;
+            float v = 0.f;
+            for (int sp = 0; sp < ns; sp++) v += scl[g * kMaxSplits + sp] * stage[(sp * ng + g) * RS + kHdr + d];
+            fin[g * RS + kHdr + d] = v;
+        }
+        __syncthreads();
+        return;
+    }
+    for (int i = threadIdx.x; i < ns * ng * kHdr; i += blockDim.x) {
+        const int sp = i / (ng * kHdr), r = i % (ng * kHdr);
+        hdr[i] = ld_agent(src + (int64_t)sp * ng * RS + (r / kHdr) * RS + r % kHdr);
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < ng) {
+        const int g = threadIdx.x;
+        float M = -INFINITY;
+        for (int sp = 0; sp < ns; sp++) M = fmaxf(M, hdr[(sp * ng + g) * kHdr]);
+        float L = 0.f, mn = INFINITY, mx = -INFINITY;
+        int arg = INT_MAX;
+        for (int sp = 0; sp < ns; sp++) {
+            const float* h = hdr + (sp * ng + g) * kHdr;
+            const float f = h[0] == -INFINITY ? 0.f : __expf(h[0] - M);
+            scl[g * kMaxSplits + sp] = f;
+            L += f * h[1];
+            mn = fminf(mn, h[2]);
+            const float fx = h[3];
+            const int fa = __float_as_int(h[4]);
+            if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
+        }
+        fin[g * RS + 0] = M;
+        fin[g * RS + 1] = L;
+        fin[g * RS + 2] = mn;
+        fin[g * RS + 3] = mx;
+        fin[g * RS + 4] = __int_as_float(arg);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
+        const int g = i / D, d = i % D;
+        const float* col = src + g * RS + kHdr + d;
+        float v = 0.f;
+#pragma unroll 8
+        for (int sp = 0; sp < ns; sp++) v += scl[g * kMaxSplits + sp] * ld_agent(col + (int64_t)sp * ng * RS);
+        fin[g * RS + kHdr + d] = v;
+    }
+    __syncthreads();
+}
+
+// Unit u of one wave's stream: the wave's far tiles first (far tile
+// f0 + u*fs), then each of its near tiles w + j*N as two units, keys then
+// values.  w is the wave's index among the N waves of its row.
+enum UnitKind { kNone = 0, kFarUnit = 1, kNearK = 2, kNearV = 3 };
+struct Units {
+    int w, N, f0, fs, nf, nn;
+    __device__ int count() const { return nf + 2 * nn; }
+    __device__ int kind(int u) const {
+        return u >= nf + 2 * nn ? kNone : u < nf ? kFarUnit : ((u - nf) & 1) ? kNearV : kNearK;
+    }
+    __device__ int tile(int u) const { return u < nf ? f0 + u * fs : w + ((u - nf) >> 1) * N; }
+};
+
+// Far tiles of wave w of a row, byte-balanced against the row's near tiles
+// (near tile t goes to wave t mod N; `near_plan` is the host's expected near
+// tile count, so the split needs no device read).  Contiguous ranges when
+// every wave's share of far bytes covers at least one near tile (the
+// cumulative boundaries are then non-decreasing), else round-robin.
+template <int D>
+__device__ inline void plan_far(Units& un, int nt_far, int near_plan) {
+    const int64_t NB = 256 * D, FB = far_record_bytes(D), N = un.N;
+    if ((int64_t)nt_far * FB >= N * NB) {
+        const int64_t q = near_plan / N, r = near_plan % N;
+        const int64_t total = near_plan * NB + (int64_t)nt_far * FB;
+        auto bound = [&](int64_t v) -> int {  // first far tile of wave v
+            if (v >= N) return nt_far;
+            const int64_t near_before = v * q + (v < r ? v : r);
+            const int64_t num = v * total - N * near_before * NB;  // >= 0 here
+            const int64_t g = (2 * num + N * FB) / (2 * N * FB);  // round to nearest
+            return (int)(g < 0 ? 0 : g > nt_far ? nt_far : g);
+        };
+        un.f0 = bound(un.w);
+        un.nf = bound(un.w + 1) - un.f0;
+        un.fs = 1;
+    } else {
+        un.f0 = un.w;
+        un.fs = un.N;
+        un.nf = un.w < nt_far ? (int)cdiv(nt_far - un.w, un.N) : 0;
+    }
+}
+
+// One workgroup of 4 waves per (batch, kv head, split, head group); each
+// wave streams its units through a 2-slot LDS ring with gfx950's direct
+// global->LDS loads: the next unit's bytes stream in while the current one
+// is computed.  The ring takes most of the CU's LDS (one workgroup per CU).
 template <int D, int NQ>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int NS = D / 4;   // 4-dim k-steps of QK
     constexpr int NH = D / 64;  // 64-dim halves of P.V
     constexpr int RS = kHdr + D;
+    constexpr int NHW = 4 * NQ;  // head records per wave
+    constexpr int REC = (int)far_record_bytes(D);
+    constexpr int SLOT = REC > 128 * D ? REC : 128 * D;  // far record or a near K / V half
+    constexpr int FAR_OPS = far_dma_ops<D>(), NEAR_OPS = D / 8;
     __shared__ __attribute__((aligned(16))) uint16_t qs[NQ * NS * 4 * 4];
-    __shared__ float wrec[kWavesPerGroup][kHeads * RS];
+    // The rings during the tile loop; afterwards (behind a barrier) the
+    // per-wave records, then past wave 0's records the split-merge scratch
+    // of the last workgroup.
+    constexpr int kRing = kWavesPerGroup * 2 * SLOT;
+    constexpr int kRec = kWavesPerGroup * NHW * RS * 4;
+    constexpr int kMrg = (NHW * RS + kMaxSplits * NHW * kHdr + NHW * kMaxSplits) * 4;
+    constexpr int kLds = kRing > kRec ? (kRing > kMrg ? kRing : kMrg) : (kRec > kMrg ? kRec : kMrg);
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+    float* smem = (float*)lds;
+    __shared__ int s_last;
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y / a.head_groups;
@@ -371,32 +914,34 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int ng = min(kHeads, a.G - hgrp * kHeads);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int j = lane & 3, blk = lane >> 2;
+    uint8_t* ring = lds + wave * 2 * SLOT;
 
-    // query -> LDS as the B operand of the score MFMA: [qd][s][j][4 halves]
+    // ---- the wave's far tiles need no device state: start streaming ----
+    Units un;
+    un.N = kWavesPerGroup * a.num_splits;
+    un.w = kWavesPerGroup * split + wave;
+    plan_far<D>(un, (int)cdiv(a.L.F, kTile), a.near_plan);
+    un.nn = 0;
+    auto issue = [&](int u) {  // DMA of unit u into slot u % 2; returns its vector-memory op count
+        const int kd = un.kind(u);
+        uint8_t* slot = ring + (u & 1) * SLOT;
+        if (kd == kFarUnit) dma_far<D>(a, bkv, un.tile(u), lane, slot);
+        else if (kd != kNone) dma_near<D>(a, bkv, un.tile(u), kd == kNearV, lane, slot);
+        return kd == kNone ? 0 : kd == kFarUnit ? FAR_OPS : NEAR_OPS;
+    };
+    if (un.nf > 0) issue(0);
+
+    // ---- query -> LDS as the B operand of the score MFMA: [qd][s][j][4 halves]
     for (int i = threadIdx.x; i < NQ * NS * 16; i += blockDim.x) {
         const int e = i & 3, jj = (i >> 2) & 3, sq = i >> 4;
         const int s = sq % NS, qd = sq / NS;
         const int h = 4 * qd + jj;
         qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
     }
-
-    // split range over the virtual tile sequence, weighted by bytes per token
     const int nv = (int)((const uint32_t*)(a.blob + a.L.near_valid))[kvh];
     const int nt_near = (int)cdiv(nv, kTile);
-    const int nt_far = (int)cdiv(a.L.F, kTile);
-    const int nt_dec = (int)cdiv(a.n_dec, kTile);
-    const int64_t wn = 4 * D, wf = (3 * D) / 2 + 4;  // bytes per near / far token
-    const int64_t W = nt_near * wn + nt_far * wf + nt_dec * wn;
-    auto first_tile_at = [&](int64_t x) -> int {
-        if (x <= nt_near * wn) return (int)cdiv(x, wn);
-        x -= nt_near * wn;
-        if (x <= nt_far * wf) return nt_near + (int)cdiv(x, wf);
-        x -= nt_far * wf;
-        return nt_near + nt_far + (int)cdiv(x, wn);
-    };
-    const int k0 = first_tile_at(W * split / a.num_splits);
-    const int k1 = first_tile_at(W * (split + 1) / a.num_splits);
-    __syncthreads();
+    un.nn = un.w < nt_near ? (int)cdiv(nt_near - un.w, un.N) : 0;
+    if (un.nf == 0) issue(0);
 
     Lane<D, NQ> st;
 #pragma unroll
@@ -409,128 +954,45 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int dh = 0; dh < NH; dh++) st.acc[qd][dh] = fkv_f4{0.f, 0.f, 0.f, 0.f};
     }
-    auto qop = [&](int qd, int s) {
-        uint2 v;
-        __builtin_memcpy(&v, qs + ((qd * NS + s) * 4 + j) * 4, 8);
-        return __builtin_bit_cast(fkv_h4, v);
-    };
+    // q operand reads from LDS (see QOperand)
+    const QOperand<NS> qop{qs, j * 4};
+    __syncthreads();
 
-    for (int k = k0 + wave; k < k1; k += kWavesPerGroup) {
-        if (k >= nt_near && k < nt_near + nt_far) {
-            // ------------------------------ far tile ------------------------------
-            const int tile = k - nt_near;
-            const uint8_t* kb = a.blob + a.L.far_k + (bkv * a.L.F_pad + (int64_t)tile * kTile) * D + lane * 16;
-            const uint8_t* vb = a.blob + a.L.far_v + (bkv * a.L.F_pad + (int64_t)tile * kTile) * D / 2 + lane * 16;
-            uint32_t kw[NS];     // dword s = dims 4s..4s+3 of token `lane`
-            uint32_t vw[D / 8];  // nibble dwords of dim 64dh + lane
+    // ---- the stream: unit u is computed while unit u + 1 streams in ----
+    fkv_f4 sacc[NQ];  // near scores, carried from a K unit to its V unit
 #pragma unroll
-            for (int c = 0; c < D / 16; c++) {
-                const uint4 x = *(const uint4*)(kb + c * 1024);
-                kw[4 * c] = x.x; kw[4 * c + 1] = x.y; kw[4 * c + 2] = x.z; kw[4 * c + 3] = x.w;
-            }
-#pragma unroll
-            for (int c = 0; c < D / 32; c++) {
-                const uint4 x = *(const uint4*)(vb + c * 1024);
-                vw[4 * c] = x.x; vw[4 * c + 1] = x.y; vw[4 * c + 2] = x.z; vw[4 * c + 3] = x.w;
-            }
-            const uint4 z4 = *(const uint4*)((const uint32_t*)(a.blob + a.L.far_sz) + bkv * a.L.F_pad +
-                                             tile * kTile + 4 * blk);
-            const uint32_t sz[4] = {z4.x, z4.y, z4.z, z4.w};
-#pragma unroll
-            for (int qd = 0; qd < NQ; qd++) {
-                fkv_f4 acc = fkv_f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < NS; s++) acc = mfma4_local(e4m3x4(kw[s]), qop(qd, s), acc);
-                float sc[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int t = tile * kTile + 4 * blk + e;
-                    const float sv = acc[e] * a.inv_sqrt_d;
-                    const bool ok = t < a.L.F;
-                    sc[e] = ok ? sv : -INFINITY;
-                    if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
-                }
-                softmax_pv<D, NQ, true>(st, qd, sc, sz,
-                                        [&](int g, int dh) { return int4x4(vw[dh * 8 + (g >> 1)], g & 1); });
-            }
+    for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+    const int nu = un.count();
+    for (int u = 0; u < nu; u++) {
+        // the slot refilled now was read by unit u - 1, whose reads completed
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int pend = issue(u + 1);
+        // unit u's loads are complete once at most unit u + 1's are pending
+        if (pend == FAR_OPS) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FAR_OPS) : "memory");
+        else if (pend == NEAR_OPS) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NEAR_OPS) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint8_t* slot = ring + (u & 1) * SLOT;
+        const int kd = un.kind(u), tile = un.tile(u);
+        if (kd == kFarUnit) {
+            FarTile<D> r;
+            lds_far(r, slot, lane);
+            far_compute<D, NQ>(st, r, tile, a.L.F, blk, a.inv_sqrt_d, qop);
+        } else if (kd == kNearK) {
+            near_scores_lds<D, NQ>(sacc, slot, lane, qop);
         } else {
-            // ------------------- fp16 tile: near slots or decode rows -------------------
-            const bool near = k < nt_near;
-            const int tile = near ? k : k - nt_near - nt_far;
-            const int count = near ? nv : a.n_dec;
-            const int tk = tile * kTile + lane;  // this lane's token for the score operand
-            fkv_f4 sacc[NQ];
-#pragma unroll
-            for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
-            const uint16_t* kb = (const uint16_t*)(a.blob + a.L.near_k) +
-                                 (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D + lane * 8;
-            const uint16_t* kr = a.dec_k + (bkv * a.n_dec + (tk < count ? tk : 0)) * D;
-#pragma unroll
-            for (int cg = 0; cg < D / 32; cg++) {  // 4 chunks (8 steps) per round
-                uint32_t kw[16];
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    uint4 x;
-                    if (near) {
-                        x = *(const uint4*)(kb + (cg * 4 + c) * 512);
-                    } else {
-                        x = tk < count ? *(const uint4*)(kr + (cg * 4 + c) * 8) : make_uint4(0, 0, 0, 0);
-                    }
-                    kw[4 * c] = x.x; kw[4 * c + 1] = x.y; kw[4 * c + 2] = x.z; kw[4 * c + 3] = x.w;
-                }
-#pragma unroll
-                for (int qd = 0; qd < NQ; qd++)
-#pragma unroll
-                    for (int s = 0; s < 8; s++)
-                        sacc[qd] = mfma4_local(h4_of(kw[2 * s], kw[2 * s + 1]), qop(qd, cg * 8 + s), sacc[qd]);
-            }
-            // values: 8-byte units x = dh*16 + g (4-token group g, dim 64dh + lane)
-            uint32_t vw[D / 2];
-            const uint16_t* vbn = (const uint16_t*)(a.blob + a.L.near_v) +
-                                  (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D + lane * 8;
-#pragma unroll
-            for (int c = 0; c < D / 8; c++) {
-                uint4 x;
-                if (near) {
-                    x = *(const uint4*)(vbn + c * 512);
-                } else {
-                    uint16_t hv[8];
-#pragma unroll
-                    for (int u = 0; u < 2; u++) {
-                        const int xi = 2 * c + u, g = xi % 16, dh = xi / 16;
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const int tv = tile * kTile + 4 * g + e;
-                            hv[4 * u + e] = tv < count ? a.dec_v[(bkv * a.n_dec + tv) * D + 64 * dh + lane] : (uint16_t)0;
-                        }
-                    }
-                    x = make_uint4(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16),
-                                   hv[4] | ((uint32_t)hv[5] << 16), hv[6] | ((uint32_t)hv[7] << 16));
-                }
-                vw[4 * c] = x.x; vw[4 * c + 1] = x.y; vw[4 * c + 2] = x.z; vw[4 * c + 3] = x.w;
-            }
-            const uint32_t szd[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int qd = 0; qd < NQ; qd++) {
-                float sc[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int t = tile * kTile + 4 * blk + e;
-                    const float sv = sacc[qd][e] * a.inv_sqrt_d;
-                    const bool ok = t < count;
-                    sc[e] = ok ? sv : -INFINITY;
-                    if (ok) st.mn[qd] = fminf(st.mn[qd], sv);
-                }
-                softmax_pv<D, NQ, false>(st, qd, sc, szd, [&](int g, int dh) {
-                    const int xi = dh * 16 + g;
-                    return h4_of(vw[2 * xi], vw[2 * xi + 1]);
-                });
-            }
+            near_pv_lds<D, NQ>(st, sacc, slot, lane, tile, nv, a.inv_sqrt_d);
         }
     }
+    // no LDS write may land after the ring is reused or the wave ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // ---- decode buffer (row-major in global memory): tile d to wave d mod N
+    const int nt_dec = (int)cdiv(a.n_dec, kTile);
+    for (int d = un.w; d < nt_dec; d += un.N) dec_tile<D, NQ>(st, a, bkv, d, lane, qop);
 
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
-    float* wr = wrec[wave];
+    __syncthreads();  // every wave is done with its ring: the records reuse the LDS
+    float* wr = smem + wave * NHW * RS;
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         float l = st.lsum[qd], z = st.zsum[qd], ws = st.wsum[qd], mn = st.mn[qd], mx = st.mx[qd];
@@ -566,44 +1028,120 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- merge the 4 waves into wrec[0] ----
+    // ---- merge the 4 waves into wave 0's records ----
     for (int h = wave; h < ng; h += kWavesPerGroup) {
         float M = -INFINITY;
-        for (int w = 0; w < kWavesPerGroup; w++) M = fmaxf(M, wrec[w][h * RS]);
+        for (int w = 0; w < kWavesPerGroup; w++) M = fmaxf(M, smem[w * NHW * RS + h * RS]);
         float sc[kWavesPerGroup];
         float L = 0.f, mn2 = INFINITY, mx2 = -INFINITY;
         int arg2 = INT_MAX;
         for (int w = 0; w < kWavesPerGroup; w++) {
-            const float mw = wrec[w][h * RS];
-            sc[w] = mw == -INFINITY ? 0.f : __expf(mw - M);
-            L += sc[w] * wrec[w][h * RS + 1];
-            mn2 = fminf(mn2, wrec[w][h * RS + 2]);
-            const float fx = wrec[w][h * RS + 3];
-            const int fa = __float_as_int(wrec[w][h * RS + 4]);
+            const float* r = smem + w * NHW * RS + h * RS;
+            sc[w] = r[0] == -INFINITY ? 0.f : __expf(r[0] - M);
+            L += sc[w] * r[1];
+            mn2 = fminf(mn2, r[2]);
+            const float fx = r[3];
+            const int fa = __float_as_int(r[4]);
             if (fx > mx2 || (fx == mx2 && fa < arg2)) { mx2 = fx; arg2 = fa; }
         }
         for (int d = lane; d < D; d += kWave) {
             float v = 0.f;
-            for (int w = 0; w < kWavesPerGroup; w++) v += sc[w] * wrec[w][h * RS + kHdr + d];
-            wrec[0][h * RS + kHdr + d] = v;
+            for (int w = 0; w < kWavesPerGroup; w++) v += sc[w] * smem[w * NHW * RS + h * RS + kHdr + d];
+            smem[h * RS + kHdr + d] = v;
         }
         if (lane == 0) {
-            wrec[0][h * RS + 0] = M;
-            wrec[0][h * RS + 1] = L;
-            wrec[0][h * RS + 2] = mn2;
-            wrec[0][h * RS + 3] = mx2;
-            wrec[0][h * RS + 4] = __int_as_float(arg2);
+            smem[h * RS + 0] = M;
+            smem[h * RS + 1] = L;
+            smem[h * RS + 2] = mn2;
+            smem[h * RS + 3] = mx2;
+            smem[h * RS + 4] = __int_as_float(arg2);
         }
     }
     __syncthreads();
 
-    if (a.num_splits > 1) {
-        const int row = (int)(bkv * a.head_groups + hgrp);  // (b, kv_head, head group)
-        float* dst = a.ws + ((int64_t)row * a.num_splits + split) * ng * RS;
-        for (int i = threadIdx.x; i < ng * RS; i += blockDim.x) dst[i] = wrec[0][i];
+    if (a.num_splits == 1) {
+        finalize_rows<D>(a, smem, b, head0, ng);
         return;
     }
-    finalize_rows<D>(a, wrec[0], b, head0, ng);
+    // ---- split-K: publish this split's record ----
+    const int row = (int)(bkv * a.head_groups + hgrp);  // (b, kv_head, head group)
+    float* part = a.ws + (int64_t)row * a.num_splits * ng * RS;
+    if (a.arrive == nullptr) {  // merged by merge_kernel (kernel boundary orders it)
+        for (int i = threadIdx.x; i < ng * RS; i += blockDim.x) part[(int64_t)split * ng * RS + i] = smem[i];
+        return;
+    }
+    // The last split to arrive merges all records (no second launch) and
+    // re-arms the counter.  Cross-workgroup ordering without cache-wide
+    // maintenance: the records are written with agent-scope atomic stores
+    // (coherent across XCDs, nothing left dirty in a non-coherent L2), each
+    // thread waits for its stores to complete before the barrier, then one
+    // agent-scope RMW counts the arrival; the last workgroup reads the
+    // records back with agent-scope atomic loads.  (A release/acquire fence
+    // pair would write back and invalidate the whole L2 per workgroup.)
+    for (int i = threadIdx.x; i < ng * RS; i += blockDim.x)
+        __hip_atomic_store(part + (int64_t)split * ng * RS + i, smem[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(a.arrive + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == a.num_splits - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    float* hdr = smem + NHW * RS;
+    float* scl = hdr + kMaxSplits * NHW * kHdr;
+    float* stage = scl + NHW * kMaxSplits;
+    merge_splits<D>(part, a.num_splits, ng, smem, hdr, scl, stage, kLds / 4 - (int)(stage - smem));
+    finalize_rows<D>(a, smem, b, head0, ng);
+    if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split-K merge as its own launch: one wave per (row, head).  Lanes < ns
+// read the split headers; the wave reduces them (max, rescaled sum, min,
+// first-index max) and each lane merges D/64 output dims.
+template <int D>
+__global__ __launch_bounds__(64) void merge_kernel(AttnArgs a) {
+    constexpr int RS = kHdr + D;
+    const int row = blockIdx.x, g = blockIdx.y;
+    const int hgrp = row % a.head_groups;
+    const int64_t bkv = row / a.head_groups;
+    const int b = (int)(bkv / a.L.Hkv), kvh = (int)(bkv % a.L.Hkv);
+    const int head0 = kvh * a.G + hgrp * kHeads;
+    const int ng = min(kHeads, a.G - hgrp * kHeads);
+    if (g >= ng) return;
+    const int ns = a.num_splits, lane = threadIdx.x;
+    const float* src = a.ws + (int64_t)row * ns * ng * RS + g * RS;
+    float ms = -INFINITY, ls = 0.f, mn = INFINITY, mx = -INFINITY;
+    int arg = INT_MAX;
+    if (lane < ns) {
+        const float* h = src + (int64_t)lane * ng * RS;
+        ms = h[0];
+        ls = h[1];
+        mn = h[2];
+        mx = h[3];
+        arg = __float_as_int(h[4]);
+    }
+    const float M = wave_max(ms);
+    const float f = ms == -INFINITY ? 0.f : __expf(ms - M);
+    const float L = wave_sum(f * ls);
+    mn = wave_min(mn);
+    wave_argmax(mx, arg);
+    float acc[D / 64];
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) acc[i] = 0.f;
+    for (int sp = 0; sp < ns; sp++) {
+        const float fs = __shfl(f, sp, kWave);
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) acc[i] += fs * src[(int64_t)sp * ng * RS + kHdr + 64 * i + lane];
+    }
+    const float inv_l = L > 0.f ? 1.0f / L : 0.f;
+    const int64_t o = (int64_t)b * a.Hq + head0 + g;
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) a.out[o * D + 64 * i + lane] = f2h(acc[i] * inv_l);
+    if (lane == 0) {
+        a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
+        a.tokens[o] = mx == -INFINITY ? -1 : arg;
+    }
 }
 
 // out = acc / l (fp16), spike flag and token for ng heads of one record set
@@ -626,62 +1164,8 @@ __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b,
     }
 }
 
-// Split-K merge (csrc/kernels/foveated_attn.metal:394-431 restated for
-// partials in memory): one workgroup per (b, kv_head, head group).  Split
-// maxima are rescaled to the global max; spike fields take the min and the
-// first-index max.
-template <int D>
-__global__ __launch_bounds__(256) void merge_kernel(AttnArgs a) {
-    constexpr int RS = kHdr + D;
-    __shared__ float mrg[kHeads * RS];
-    __shared__ float hdr[kMaxSplits][kHeads][kHdr];
-    __shared__ float scl[kHeads][kMaxSplits];
-    const int row = blockIdx.x;
-    const int hgrp = row % a.head_groups;
-    const int64_t bkv = row / a.head_groups;
-    const int b = (int)(bkv / a.L.Hkv), kvh = (int)(bkv % a.L.Hkv);
-    const int head0 = kvh * a.G + hgrp * kHeads;
-    const int ng = min(kHeads, a.G - hgrp * kHeads);
-    const int ns = a.num_splits;  // <= kMaxSplits
-    const float* src = a.ws + (int64_t)row * ns * ng * RS;
-    for (int i = threadIdx.x; i < ns * ng * kHdr; i += blockDim.x) {
-        const int sp = i / (ng * kHdr), r = i % (ng * kHdr), g = r / kHdr, f = r % kHdr;
-        hdr[sp][g][f] = src[(int64_t)sp * ng * RS + g * RS + f];
-    }
-    __syncthreads();
-    if ((int)threadIdx.x < ng) {
-        const int g = threadIdx.x;
-        float M = -INFINITY;
-        for (int sp = 0; sp < ns; sp++) M = fmaxf(M, hdr[sp][g][0]);
-        float L = 0.f, mn = INFINITY, mx = -INFINITY;
-        int arg = INT_MAX;
-        for (int sp = 0; sp < ns; sp++) {
-            const float mw = hdr[sp][g][0];
-            const float f = mw == -INFINITY ? 0.f : __expf(mw - M);
-            scl[g][sp] = f;
-            L += f * hdr[sp][g][1];
-            mn = fminf(mn, hdr[sp][g][2]);
-            const float fx = hdr[sp][g][3];
-            const int fa = __float_as_int(hdr[sp][g][4]);
-            if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
-        }
-        mrg[g * RS + 0] = M;
-        mrg[g * RS + 1] = L;
-        mrg[g * RS + 2] = mn;
-        mrg[g * RS + 3] = mx;
-        mrg[g * RS + 4] = __int_as_float(arg);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
-        const int g = i / D, d = i % D;
-        const float* col = src + g * RS + kHdr + d;
-        float v = 0.f;
-#pragma unroll 8
-        for (int sp = 0; sp < ns; sp++) v += scl[g][sp] * col[(int64_t)sp * ng * RS];
-        mrg[g * RS + kHdr + d] = v;
-    }
-    __syncthreads();
-    finalize_rows<D>(a, mrg, b, head0, ng);
+__global__ void zero_ints_kernel(int* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
 
 }  // namespace fkv
@@ -698,6 +1182,9 @@ struct fkv_attn_impl {
     size_t ws_floats = 0;
     uint16_t* qbuf = nullptr;  // fp16 copy of non-fp16 queries
     size_t qbuf_n = 0;
+    int* arrive = nullptr;  // per-row split arrival counters (zero between calls)
+    size_t arrive_n = 0;
+    int near_plan = 0;      // expected near tiles per row: max near_valid / 64, rounded up
     int device = 0;
 };
 
@@ -731,7 +1218,7 @@ static int env_int(const char* name, int dflt) {
 // two tiles per wave.
 int plan_splits(const BlobLayout& L, int rows, int n_dec) {
     const int tiles = (int)(cdiv(L.Na, kTile) + cdiv(L.F, kTile) + cdiv(n_dec, kTile));
-    const int target = env_int("FKV_TARGET_WGS", 1024);
+    const int target = env_int("FKV_TARGET_WGS", 256);
     int s = (int)cdiv(target, rows > 0 ? rows : 1);
     const int cap = tiles / (2 * kWavesPerGroup);
     if (s > cap) s = cap;
@@ -790,8 +1277,17 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
         rc = check_hip(hipGetLastError(), "pack kernels");
     }
     unsigned bad_h = 0;
+    std::vector<uint32_t> nv_h(Hkv, 0);
     if (!rc) rc = check_hip(hipMemcpyAsync(&bad_h, bad, sizeof(unsigned), hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+    if (!rc)
+        rc = check_hip(hipMemcpyAsync(nv_h.data(), h->blob + h->L.near_valid, Hkv * sizeof(uint32_t),
+                                      hipMemcpyDeviceToHost, st), "hipMemcpyAsync(near_valid)");
     if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
+    if (!rc) {
+        uint32_t mx = 0;
+        for (uint32_t v : nv_h) mx = v > mx ? v : mx;
+        h->near_plan = (int)fkv::cdiv(mx, fkv::kTile);
+    }
     if (bad) (void)hipFree(bad);
     if (!rc && bad_h) {
         set_error("fkv_attn_create: far_k holds E4M3 NaN codes 0x7F/0xFF, which the reference encoder never emits");
@@ -844,6 +1340,16 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
             if (int rc = check_hip(hipMalloc(&h->ws, need * sizeof(float)), "hipMalloc(ws)")) return rc;
             h->ws_floats = need;
         }
+        if ((size_t)rows > h->arrive_n) {
+            if (h->arrive) (void)hipFree(h->arrive);
+            h->arrive = nullptr;
+            h->arrive_n = 0;
+            if (int rc = check_hip(hipMalloc(&h->arrive, rows * sizeof(int)), "hipMalloc(arrive)")) return rc;
+            h->arrive_n = rows;
+            // counters start at zero; the kernel's last split re-arms them
+            hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(rows, 256)), dim3(256), 0, st,
+                               h->arrive, rows);
+        }
     }
     fkv::AttnArgs a;
     a.blob = h->blob;
@@ -862,13 +1368,17 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
     a.flags = spike_flags;
     a.tokens = spike_tokens;
     a.ws = h->ws;
+    const bool fused_merge = fkv::env_int("FKV_FUSED_MERGE", 1) != 0;
+    a.arrive = fused_merge ? h->arrive : nullptr;
+    a.near_plan = h->near_plan;
     const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
     const int nq = (ng_max + 3) / 4;
     fkv::AttnKernel k = L.D == 128 ? fkv::pick_attn<128>(nq) : fkv::pick_attn<64>(nq);
     hipLaunchKernelGGL(k, grid, block, 0, st, a);
-    if (splits > 1) {
-        if (L.D == 128) hipLaunchKernelGGL(fkv::merge_kernel<128>, dim3(rows), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL(fkv::merge_kernel<64>, dim3(rows), dim3(256), 0, st, a);
+    if (splits > 1 && !fused_merge) {
+        const dim3 mgrid(rows, ng_max);
+        if (L.D == 128) hipLaunchKernelGGL(fkv::merge_kernel<128>, mgrid, dim3(fkv::kWave), 0, st, a);
+        else hipLaunchKernelGGL(fkv::merge_kernel<64>, mgrid, dim3(fkv::kWave), 0, st, a);
     }
     return check_hip(hipGetLastError(), "attn_kernel launch");
 }
@@ -911,6 +1421,7 @@ void fkv_attn_destroy(fkv_attn* h) {
     if (h->blob) (void)hipFree(h->blob);
     if (h->ws) (void)hipFree(h->ws);
     if (h->qbuf) (void)hipFree(h->qbuf);
+    if (h->arrive) (void)hipFree(h->arrive);
     delete h;
 }
 

@@ -140,6 +140,15 @@ void fkv_attn_destroy(fkv_attn* h);
  * equal on every code the reference encoder emits. */
 int fkv_e4m3_decode(const uint8_t* codes, void* out_f16, int64_t n, void* stream);
 
+/* Benchmark utility with no counterpart in the reference: streams `bytes`
+ * (a multiple of 16) from device buffer `buf` with 16-byte lane loads,
+ * `unroll` (1, 2, 4, 8) loads in flight per lane, optionally non-temporal,
+ * on `blocks` workgroups of 256 threads; writes one XOR fold per wave to
+ * `out` (blocks*4 uint32).  Measures the device's practical HBM read
+ * ceiling for the roofline of the attention kernel. */
+int fkv_hbm_read_probe(const void* buf, int64_t bytes, int32_t unroll, int32_t nontemporal, int32_t blocks,
+                       uint32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -291,3 +291,37 @@ def test_e4m3_converter_matches_reference_lut(fkv, orc):
     lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).view(np.uint16)
     reach = np.unique(orc.encode_fp8(np.arange(65536, dtype=np.uint16)))
     assert np.array_equal(got[reach], lut[reach])
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,n_dec", [(8, 32, 8, 128, 8192, 0), (2, 32, 2, 64, 3000, 9)])
+def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec):
+    """The last-arriving split merges the partial records in-kernel; its
+    arrival counters are re-armed by the kernel itself.  200 launches queued
+    back to back (no host sync between them) must all be bit-identical, and
+    must agree with the separate merge launch."""
+    from foveated_kv_amd import ext, synthetic
+
+    _flush(f"fused merge stress B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec}")
+    k, v = synthetic.make_kv(B, Hkv, S, D, 21)
+    q = torch.from_numpy(synthetic.make_query(B, Hq, D, 21)).cuda()[:, :, None]
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, 21)
+    dkt = torch.from_numpy(dk).cuda() if dk is not None else None
+    dvt = torch.from_numpy(dv).cuda() if dv is not None else None
+    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                                      with_archive=False)
+    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                           cl.near_valid, spike_margin=10.0)
+    os.environ["FKV_FUSED_MERGE"] = "0"
+    try:
+        ref = [t.clone() for t in h(q, dkt, dvt)]
+    finally:
+        del os.environ["FKV_FUSED_MERGE"]
+    outs = [h(q, dkt, dvt) for _ in range(200)]
+    torch.cuda.synchronize()
+    first = outs[0]
+    for o in outs[1:]:
+        for a, b in zip(first, o):
+            assert torch.equal(a, b)
+    assert torch.equal(first[1], ref[1]) and torch.equal(first[2], ref[2])
+    diff = (first[0].float() - ref[0].float()).abs().max().item()
+    assert diff <= 1e-3 * max(1.0, ref[0].float().abs().max().item()), diff
