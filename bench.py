@@ -1,4 +1,4 @@
-"""Benchmark: fused two-tier decode attention, µs/layer and achieved HBM GB/s.
+"""Benchmark: fused two-tier decode attention, us/layer and achieved HBM GB/s.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3_7b_16k_b8]
 
@@ -11,10 +11,14 @@ bracketed by HIP events on the capture stream.  Inputs are synthetic
 HBM before timing starts.
 
 Prints one JSON line (rank 0).  ``value`` is the achieved algorithmic HBM
-bandwidth in GB/s (SURVEY formula for bytes per layer-call, no credit for
-gated V); ``us_per_layer`` and ``pct_peak`` are reported beside it, with a
-``roofline`` object and a ``cpu_baseline`` (the C oracle's dequant+SDPA
-formulation on a bounded sample, on the host cores).
+bandwidth in GB/s: the bytes one layer-call must move (valid near rows fp16
+K+V, far E4M3 K + INT4 V + fp16 scale/zero, decode rows, q in / out, spike
+outputs, near_valid; no credit for gated-V skipping) divided by the
+per-layer time.  ``us_per_layer`` and ``pct_peak`` are reported beside it,
+with a ``roofline`` object (traffic from the committed rocprof counter
+summary), the box's streaming-read ceiling measured in-run, and a
+``cpu_baseline`` (the C oracle's dequant+SDPA formulation on a bounded
+sample, on the host cores).
 """
 
 import argparse
@@ -94,6 +98,8 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured HIP graph (for counter collection)")
     ap.add_argument("--no-read-ceiling", action="store_true", help="skip the in-run HBM read-ceiling probe")
+    ap.add_argument("--read-sweep", action="store_true",
+                    help="with --copy-mib: sweep the read probe over launch shapes (else the best known one)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also time a plain device copy of this many MiB (HBM calibration; reported "
                          "as copy_gbs, read + write bytes)")
@@ -231,7 +237,8 @@ def main():
         }
     if args.copy_mib:
         result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)
-        result["read_ceiling_gbs"], result["read_ceiling_launch"] = read_ceiling(torch, dev, args.copy_mib)
+        result["read_ceiling_gbs"], result["read_ceiling_launch"] = read_ceiling(torch, dev, args.copy_mib,
+                                                                                 sweep=args.read_sweep)
     elif not args.no_read_ceiling:
         # this box's streaming-read ceiling, measured beside the kernel
         result["read_ceiling_gbs"], _ = read_ceiling(torch, dev, 2048, sweep=False)
