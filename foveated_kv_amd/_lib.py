@@ -86,7 +86,29 @@ SIGNATURES = {
     "fkv_attn_destroy": (None, [P]),
     "fkv_e4m3_decode": (ctypes.c_int, [P, P, ctypes.c_int64, P]),
     "fkv_hbm_read_probe": (ctypes.c_int, [P, ctypes.c_int64, I32, I32, I32, P, P]),
+    "fkv_attn_promote_rows": (ctypes.c_int, [P, I32, P, P, P, I32, P]),
+    "fkv_attn_export_near": (ctypes.c_int, [P, P, P, P]),
+    "fkv_promoter_create": (ctypes.c_int, [I32, I32, I32, ctypes.POINTER(P)]),
+    "fkv_promoter_register_archive": (ctypes.c_int, [P, I32, P, P, I32, I32, I32, I32, P, I32]),
+    "fkv_promoter_register_archive_files": (ctypes.c_int, [P, I32, ctypes.c_char_p, ctypes.c_char_p, I32, I32,
+                                                           I32, P]),
+    "fkv_promoter_register_handle": (ctypes.c_int, [P, I32, P, P]),
+    "fkv_promoter_drain": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, I32, I32]),
+    "fkv_promoter_pending": (ctypes.c_int, [P, P, I32]),
+    "fkv_promoter_flush": (ctypes.c_int, [P]),
+    "fkv_promoter_order": (ctypes.c_int, [P, I32, P]),
+    "fkv_promoter_synchronize": (ctypes.c_int, [P]),
+    "fkv_promoter_get_stats": (ctypes.c_int, [P, P]),
+    "fkv_promoter_near_valid": (ctypes.c_int, [P, I32, P, I32]),
+    "fkv_promoter_destroy": (None, [P]),
 }
+
+STATS_FIELDS = ("spikes_detected", "spikes_queued", "spikes_deduplicated", "spikes_cooled_down",
+                "promotions_completed", "promotions_headroom_full")
+
+
+class PromoterStatsC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in STATS_FIELDS]
 
 _lib = None
 _load_error = None

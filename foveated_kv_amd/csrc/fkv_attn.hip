@@ -1164,6 +1164,61 @@ __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Promotion, GPU side (csrc/promotion_pipeline.cpp:192-241): exact fp16 rows
+// into near-tier headroom slots, then the near_valid bump
+// ---------------------------------------------------------------------------
+
+// One workgroup per promoted row: record i = (head, slot) = hs[2i], hs[2i+1];
+// rows_k / rows_v hold [n][nb][D] fp16 for batches 0..nb-1 (the same slot in
+// every batch: near_valid is shared across the batch; batches without an
+// archive row keep their slot as it is, as the reference's batch-0-only
+// copy does).  Records outside the blob are skipped.
+__global__ void promote_rows_kernel(const int32_t* __restrict__ hs, const uint16_t* __restrict__ rows_k,
+                                    const uint16_t* __restrict__ rows_v, int n, int nb, BlobLayout L,
+                                    uint8_t* __restrict__ blob) {
+    const int i = blockIdx.x;
+    if (i >= n) return;
+    const int h = hs[2 * i], slot = hs[2 * i + 1];
+    if (h < 0 || h >= L.Hkv || slot < 0 || slot >= L.Na) return;
+    uint16_t* nk = (uint16_t*)(blob + L.near_k);
+    uint16_t* nv = (uint16_t*)(blob + L.near_v);
+    for (int e = threadIdx.x; e < nb * L.D; e += blockDim.x) {
+        const int b = e / L.D, d = e % L.D;
+        const int64_t base = ((int64_t)b * L.Hkv + h) * L.Na_pad * L.D;
+        const int64_t src = ((int64_t)i * nb + b) * L.D + d;
+        nk[base + near_k_index(slot, d, L.D)] = rows_k[src];
+        nv[base + near_v_index(slot, d, L.D)] = rows_v[src];
+    }
+}
+
+// After the rows (stream order): near_valid[h] = max(near_valid[h], slot + 1)
+// for every record, as device-scope atomics.
+__global__ void bump_near_valid_kernel(const int32_t* __restrict__ hs, int n, BlobLayout L, uint8_t* blob) {
+    unsigned* valid = (unsigned*)(blob + L.near_valid);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int h = hs[2 * i], slot = hs[2 * i + 1];
+        if (h < 0 || h >= L.Hkv || slot < 0 || slot >= L.Na) continue;
+        atomicMax(valid + h, (unsigned)(slot + 1));
+    }
+}
+
+// Near tier of the blob back to row-major (B, Hkv, Na, D) fp16.
+__global__ void export_near_kernel(BlobLayout L, const uint8_t* __restrict__ blob, uint16_t* __restrict__ ok,
+                                   uint16_t* __restrict__ ov) {
+    const int64_t n = (int64_t)L.B * L.Hkv * L.Na * L.D;
+    const uint16_t* nk = (const uint16_t*)(blob + L.near_k);
+    const uint16_t* nv = (const uint16_t*)(blob + L.near_v);
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int d = (int)(i % L.D);
+        const int t = (int)((i / L.D) % L.Na);
+        const int64_t bkv = i / ((int64_t)L.D * L.Na);
+        const int64_t base = bkv * L.Na_pad * L.D;
+        if (ok) ok[i] = nk[base + near_k_index(t, d, L.D)];
+        if (ov) ov[i] = nv[base + near_v_index(t, d, L.D)];
+    }
+}
+
 __global__ void zero_ints_kernel(int* p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
@@ -1414,6 +1469,29 @@ int fkv_attn_read_near_valid(const fkv_attn* h, uint32_t* host_out, void* stream
                                       hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
     if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
     return rc;
+}
+
+int fkv_attn_promote_rows(fkv_attn* h, int32_t n, const int32_t* head_slot, const void* rows_k,
+                          const void* rows_v, int32_t row_batches, void* stream) {
+    if (!h || n < 0 || (n > 0 && (!head_slot || !rows_k || !rows_v)))
+        return set_error("fkv_attn_promote_rows: NULL argument or negative count");
+    if (row_batches < 1 || row_batches > h->L.B)
+        return set_error("fkv_attn_promote_rows: row_batches must be in [1, B]");
+    if (n == 0) return FKV_OK;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(fkv::promote_rows_kernel, dim3(n), dim3(256), 0, st, head_slot, (const uint16_t*)rows_k,
+                       (const uint16_t*)rows_v, n, row_batches, h->L, h->blob);
+    hipLaunchKernelGGL(fkv::bump_near_valid_kernel, dim3(1), dim3(256), 0, st, head_slot, n, h->L, h->blob);
+    return check_hip(hipGetLastError(), "promote kernels launch");
+}
+
+int fkv_attn_export_near(const fkv_attn* h, void* near_k_out, void* near_v_out, void* stream) {
+    if (!h || (!near_k_out && !near_v_out)) return set_error("fkv_attn_export_near: NULL argument");
+    const int64_t n = (int64_t)h->L.B * h->L.Hkv * h->L.Na * h->L.D;
+    if (n == 0) return FKV_OK;
+    hipLaunchKernelGGL(fkv::export_near_kernel, dim3(fkv::grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream, h->L,
+                       h->blob, (uint16_t*)near_k_out, (uint16_t*)near_v_out);
+    return check_hip(hipGetLastError(), "export_near_kernel launch");
 }
 
 void fkv_attn_destroy(fkv_attn* h) {

@@ -1,0 +1,415 @@
+// Promotion pipeline: the spike drain filter (host) and the GPU side that
+// copies exact fp16 rows from a host-pinned archive into near-tier headroom.
+//
+// Replaces the reference's PromotionPipeline (csrc/promotion_pipeline.h:75-141,
+// csrc/promotion_pipeline.cpp:99-248).  The drain filter keeps the
+// reference's semantics exactly: scan (batch, query head) in order until the
+// per-call budget is reached; the first flagged query head of each KV head is
+// the only candidate for that KV head in the call (GQA dedup); a per-(layer,
+// KV head) cooldown in steps; never promote the same (layer, KV head,
+// position) twice; far-local token -> global position -> archive-local row.
+//
+// The reference's worker thread memcpy's rows into unified memory and bumps
+// near_valid[h] with a release store.  On MI355X the same commit protocol is
+// stream-ordered device work: fkv_promoter_flush assigns headroom slots from
+// a host mirror of near_valid (the pipeline is the only writer), gathers the
+// rows into pinned staging, issues one hipMemcpyAsync on a side stream and
+// then fkv_attn_promote_rows (row scatter, then the near_valid bump ordered
+// after it).  fkv_promoter_order makes a compute stream wait for a layer's
+// last promotion, so the next dispatch sees the rows and the new count
+// together ("visible at the next dispatch", promotion_pipeline.cpp:236-237).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "fkv_common.h"
+#include "../../include/fkv.h"
+
+using fkv::check_hip;
+using fkv::set_error;
+
+namespace {
+
+struct Archive {
+    const uint16_t* k = nullptr;  // [B_arc][Hkv][S_arc][D] fp16 (host)
+    const uint16_t* v = nullptr;
+    void* owned_k = nullptr;  // pinned copies owned by the pipeline
+    void* owned_v = nullptr;
+    int B = 0, Hkv = 0, S = 0, D = 0;
+    std::vector<std::unordered_map<int32_t, int32_t>> pos_to_local;  // [Hkv]: position -> archive row
+};
+
+struct Record {
+    int32_t layer, head, arc_local, position;
+};
+
+}  // namespace
+
+struct fkv_promoter {
+    int n_layers = 0, cooldown = 5, max_per_drain = 8;
+    std::vector<Archive> arch;
+    std::vector<fkv_attn*> handles;
+    std::vector<std::vector<uint32_t>> mirror;  // host copy of each layer's near_valid
+    std::vector<int> n_alloc;                   // near slots per head, per layer
+    std::unordered_set<uint64_t> promoted;
+    std::unordered_map<uint32_t, int> last_step;
+    std::vector<Record> queue;
+    fkv_promoter_stats stats{};
+    // GPU side (created on first flush)
+    hipStream_t side = nullptr;
+    std::vector<hipEvent_t> done;      // per layer: last promotion on the side stream
+    std::vector<uint8_t> has_done;
+    hipEvent_t staged = nullptr;       // last H2D copy out of the pinned staging
+    bool staged_pending = false;
+    uint8_t* stage_h = nullptr;        // pinned host staging
+    uint8_t* stage_d = nullptr;        // device staging
+    size_t stage_cap = 0;
+};
+
+namespace {
+
+void free_archive(Archive& a) {
+    if (a.owned_k) (void)hipHostFree(a.owned_k);
+    if (a.owned_v) (void)hipHostFree(a.owned_v);
+    a = Archive();
+}
+
+int build_positions(Archive& a, const int32_t* archive_idx) {
+    a.pos_to_local.assign(a.Hkv, {});
+    if (!archive_idx) return FKV_OK;
+    for (int h = 0; h < a.Hkv; h++) {
+        auto& m = a.pos_to_local[h];
+        m.reserve((size_t)a.S);
+        for (int i = 0; i < a.S; i++) m[archive_idx[(int64_t)h * a.S + i]] = i;
+    }
+    return FKV_OK;
+}
+
+int ensure_gpu(fkv_promoter* p) {
+    if (p->side) return FKV_OK;
+    int rc = check_hip(hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    if (!rc) rc = check_hip(hipEventCreateWithFlags(&p->staged, hipEventDisableTiming), "hipEventCreate");
+    if (!rc) {
+        p->done.assign(p->n_layers, nullptr);
+        p->has_done.assign(p->n_layers, 0);
+        for (int l = 0; l < p->n_layers && !rc; l++)
+            rc = check_hip(hipEventCreateWithFlags(&p->done[l], hipEventDisableTiming), "hipEventCreate");
+    }
+    return rc;
+}
+
+int ensure_staging(fkv_promoter* p, size_t bytes) {
+    if (bytes <= p->stage_cap) return FKV_OK;
+    if (p->staged_pending) {
+        if (int rc = check_hip(hipEventSynchronize(p->staged), "hipEventSynchronize")) return rc;
+        p->staged_pending = false;
+    }
+    // the device staging may still be read by queued promote kernels
+    if (int rc = check_hip(hipStreamSynchronize(p->side), "hipStreamSynchronize")) return rc;
+    if (p->stage_h) (void)hipHostFree(p->stage_h);
+    if (p->stage_d) (void)hipFree(p->stage_d);
+    p->stage_h = nullptr;
+    p->stage_d = nullptr;
+    p->stage_cap = 0;
+    size_t cap = 64 * 1024;
+    while (cap < bytes) cap *= 2;
+    if (int rc = check_hip(hipHostMalloc((void**)&p->stage_h, cap, hipHostMallocDefault), "hipHostMalloc(staging)"))
+        return rc;
+    if (int rc = check_hip(hipMalloc((void**)&p->stage_d, cap), "hipMalloc(staging)")) return rc;
+    p->stage_cap = cap;
+    return FKV_OK;
+}
+
+inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+}  // namespace
+
+extern "C" {
+
+int fkv_promoter_create(int32_t n_layers, int32_t cooldown_steps, int32_t max_per_drain, fkv_promoter** out) {
+    if (!out) return set_error("fkv_promoter_create: out is NULL");
+    *out = nullptr;
+    if (n_layers <= 0 || n_layers > 65535 || max_per_drain < 0)
+        return set_error("fkv_promoter_create: need 0 < n_layers <= 65535 and max_per_drain >= 0");
+    fkv_promoter* p = new fkv_promoter();
+    p->n_layers = n_layers;
+    p->cooldown = cooldown_steps;
+    p->max_per_drain = max_per_drain;
+    p->arch.resize(n_layers);
+    p->handles.assign(n_layers, nullptr);
+    p->mirror.assign(n_layers, {});
+    p->n_alloc.assign(n_layers, 0);
+    *out = p;
+    return FKV_OK;
+}
+
+int fkv_promoter_register_archive(fkv_promoter* p, int32_t layer, const void* k, const void* v, int32_t B,
+                                  int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx,
+                                  int32_t copy_to_pinned) {
+    if (!p) return set_error("fkv_promoter_register_archive: NULL pipeline");
+    if (layer < 0 || layer >= p->n_layers) return set_error("fkv_promoter_register_archive: layer out of range");
+    if (B <= 0 || Hkv <= 0 || S_arc < 0 || D <= 0 || (S_arc > 0 && (!k || !v)))
+        return set_error("fkv_promoter_register_archive: bad shape or NULL rows");
+    Archive a;
+    a.B = B;
+    a.Hkv = Hkv;
+    a.S = S_arc;
+    a.D = D;
+    const size_t bytes = (size_t)B * Hkv * S_arc * D * 2;
+    if (copy_to_pinned && bytes) {
+        int rc = check_hip(hipHostMalloc(&a.owned_k, bytes, hipHostMallocDefault), "hipHostMalloc(archive)");
+        if (!rc) rc = check_hip(hipHostMalloc(&a.owned_v, bytes, hipHostMallocDefault), "hipHostMalloc(archive)");
+        if (rc) {
+            free_archive(a);
+            return rc;
+        }
+        memcpy(a.owned_k, k, bytes);
+        memcpy(a.owned_v, v, bytes);
+        a.k = (const uint16_t*)a.owned_k;
+        a.v = (const uint16_t*)a.owned_v;
+    } else {
+        a.k = (const uint16_t*)k;
+        a.v = (const uint16_t*)v;
+    }
+    build_positions(a, archive_idx);
+    free_archive(p->arch[layer]);
+    p->arch[layer] = std::move(a);
+    return FKV_OK;
+}
+
+int fkv_promoter_register_archive_files(fkv_promoter* p, int32_t layer, const char* path_k, const char* path_v,
+                                        int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx) {
+    if (!p || !path_k || !path_v) return set_error("fkv_promoter_register_archive_files: NULL argument");
+    if (layer < 0 || layer >= p->n_layers) return set_error("fkv_promoter_register_archive_files: layer out of range");
+    if (Hkv <= 0 || S_arc < 0 || D <= 0) return set_error("fkv_promoter_register_archive_files: bad shape");
+    const size_t bytes = (size_t)Hkv * S_arc * D * 2;
+    Archive a;
+    a.B = 1;
+    a.Hkv = Hkv;
+    a.S = S_arc;
+    a.D = D;
+    if (bytes) {
+        int rc = check_hip(hipHostMalloc(&a.owned_k, bytes, hipHostMallocDefault), "hipHostMalloc(archive)");
+        if (!rc) rc = check_hip(hipHostMalloc(&a.owned_v, bytes, hipHostMallocDefault), "hipHostMalloc(archive)");
+        if (rc) {
+            free_archive(a);
+            return rc;
+        }
+        const char* paths[2] = {path_k, path_v};
+        void* dst[2] = {a.owned_k, a.owned_v};
+        for (int f = 0; f < 2; f++) {
+            FILE* fp = fopen(paths[f], "rb");
+            const size_t got = fp ? fread(dst[f], 1, bytes, fp) : 0;
+            if (fp) fclose(fp);
+            if (got != bytes) {  // the layer is left without an archive, as in the reference
+                free_archive(a);
+                free_archive(p->arch[layer]);
+                return set_error(std::string("fkv_promoter_register_archive_files: cannot read ") +
+                                 std::to_string(bytes) + " bytes from " + paths[f]);
+            }
+        }
+        a.k = (const uint16_t*)a.owned_k;
+        a.v = (const uint16_t*)a.owned_v;
+    }
+    build_positions(a, archive_idx);
+    free_archive(p->arch[layer]);
+    p->arch[layer] = std::move(a);
+    return FKV_OK;
+}
+
+int fkv_promoter_register_handle(fkv_promoter* p, int32_t layer, fkv_attn* h, void* stream) {
+    if (!p || !h) return set_error("fkv_promoter_register_handle: NULL argument");
+    if (layer < 0 || layer >= p->n_layers) return set_error("fkv_promoter_register_handle: layer out of range");
+    fkv_blob_info bi;
+    if (int rc = fkv_attn_blob_info(h, &bi)) return rc;
+    std::vector<uint32_t> nv((size_t)bi.H_kv);
+    if (int rc = fkv_attn_read_near_valid(h, nv.data(), stream)) return rc;
+    p->handles[layer] = h;
+    p->mirror[layer] = std::move(nv);
+    p->n_alloc[layer] = bi.n_near_alloc;
+    return FKV_OK;
+}
+
+// promotion_pipeline.cpp:99-175
+int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* flags, const int32_t* tokens,
+                       const int32_t* far_idx, int32_t B, int32_t Hq, int32_t Hkv, int32_t N_far, int32_t step) {
+    if (!p) return set_error("fkv_promoter_drain: NULL pipeline");
+    if (layer < 0 || layer >= p->n_layers) return 0;
+    const Archive& a = p->arch[layer];
+    if (!a.k || a.S == 0) return 0;  // no archive registered for the layer
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || !flags || !tokens || !far_idx) return 0;
+    const int gqa = Hq / Hkv > 0 ? Hq / Hkv : 1;
+    std::vector<uint8_t> seen((size_t)Hkv, 0);
+    int queued = 0;
+    for (int b = 0; b < B && queued < p->max_per_drain; b++) {
+        for (int hq = 0; hq < Hq && queued < p->max_per_drain; hq++) {
+            const int flat = b * Hq + hq;
+            if (flags[flat] == 0) continue;
+            const int hkv = hq / gqa;
+            if (hkv >= Hkv || seen[hkv]) continue;
+            seen[hkv] = 1;
+            p->stats.spikes_detected++;
+            const uint32_t cd_key = ((uint32_t)layer << 16) | (uint32_t)hkv;
+            auto it = p->last_step.find(cd_key);
+            if (it != p->last_step.end() && step - it->second < p->cooldown) {
+                p->stats.spikes_cooled_down++;
+                continue;
+            }
+            p->last_step[cd_key] = step;
+            const int far_local = tokens[flat];
+            if (far_local < 0 || far_local >= N_far) continue;
+            const int32_t position = far_idx[((int64_t)b * Hkv + hkv) * N_far + far_local];
+            const uint64_t key = ((uint64_t)(layer & 0xFFFF) << 48) | ((uint64_t)(hkv & 0xFFFF) << 32) |
+                                 (uint64_t)(uint32_t)position;
+            if (!p->promoted.insert(key).second) {
+                p->stats.spikes_deduplicated++;
+                continue;
+            }
+            if (hkv >= (int)a.pos_to_local.size()) continue;
+            auto pit = a.pos_to_local[hkv].find(position);
+            if (pit == a.pos_to_local[hkv].end()) continue;
+            p->queue.push_back({layer, hkv, pit->second, position});
+            p->stats.spikes_queued++;
+            queued++;
+        }
+    }
+    return queued;
+}
+
+int fkv_promoter_pending(const fkv_promoter* p, int32_t* out_records, int32_t max_records) {
+    if (!p) return set_error("fkv_promoter_pending: NULL pipeline");
+    const int n = (int)p->queue.size();
+    for (int i = 0; i < n && i < max_records && out_records; i++) {
+        out_records[4 * i + 0] = p->queue[i].layer;
+        out_records[4 * i + 1] = p->queue[i].head;
+        out_records[4 * i + 2] = p->queue[i].arc_local;
+        out_records[4 * i + 3] = p->queue[i].position;
+    }
+    return n;
+}
+
+// promotion_pipeline.cpp:192-241, as stream-ordered device work
+int fkv_promoter_flush(fkv_promoter* p) {
+    if (!p) return set_error("fkv_promoter_flush: NULL pipeline");
+    if (p->queue.empty()) return FKV_OK;
+    if (int rc = ensure_gpu(p)) return rc;
+    // assign headroom slots per layer from the mirrors; group by layer
+    struct Item {
+        int32_t head, slot, arc_local;
+    };
+    std::vector<std::vector<Item>> per(p->n_layers);
+    for (const Record& r : p->queue) {
+        fkv_attn* h = p->handles[r.layer];
+        if (!h) continue;  // no blob registered: nothing to write into
+        uint32_t& cur = p->mirror[r.layer][r.head];
+        if ((int)cur >= p->n_alloc[r.layer]) {
+            p->stats.promotions_headroom_full++;
+            continue;
+        }
+        per[r.layer].push_back({r.head, (int32_t)cur, r.arc_local});
+        cur++;
+    }
+    p->queue.clear();
+    // staging: per layer [hs: 2n int32 | K rows: n*B*D fp16 | V rows: n*B*D fp16], 16-byte aligned
+    size_t total = 0;
+    std::vector<size_t> off(p->n_layers, 0);
+    for (int l = 0; l < p->n_layers; l++) {
+        if (per[l].empty()) continue;
+        const Archive& a = p->arch[l];
+        const size_t n = per[l].size();
+        off[l] = total;
+        total += align16(n * 8) + 2 * align16(n * (size_t)a.B * a.D * 2);
+    }
+    if (total == 0) return FKV_OK;
+    if (int rc = ensure_staging(p, total)) return rc;
+    if (p->staged_pending) {  // the previous copy out of the pinned staging has finished
+        if (int rc = check_hip(hipEventSynchronize(p->staged), "hipEventSynchronize")) return rc;
+        p->staged_pending = false;
+    }
+    for (int l = 0; l < p->n_layers; l++) {
+        if (per[l].empty()) continue;
+        const Archive& a = p->arch[l];
+        const size_t n = per[l].size(), row = (size_t)a.D;
+        int32_t* hs = (int32_t*)(p->stage_h + off[l]);
+        uint16_t* rk = (uint16_t*)(p->stage_h + off[l] + align16(n * 8));
+        uint16_t* rv = (uint16_t*)((uint8_t*)rk + align16(n * a.B * row * 2));
+        for (size_t i = 0; i < n; i++) {
+            const Item& it = per[l][i];
+            hs[2 * i] = it.head;
+            hs[2 * i + 1] = it.slot;
+            for (int b = 0; b < a.B; b++) {
+                const size_t src = (((size_t)b * a.Hkv + it.head) * a.S + it.arc_local) * row;
+                memcpy(rk + (i * a.B + b) * row, a.k + src, row * 2);
+                memcpy(rv + (i * a.B + b) * row, a.v + src, row * 2);
+            }
+        }
+    }
+    int rc = check_hip(hipMemcpyAsync(p->stage_d, p->stage_h, total, hipMemcpyHostToDevice, p->side),
+                       "hipMemcpyAsync(promotion rows)");
+    if (!rc) rc = check_hip(hipEventRecord(p->staged, p->side), "hipEventRecord");
+    if (rc) return rc;
+    p->staged_pending = true;
+    for (int l = 0; l < p->n_layers && !rc; l++) {
+        if (per[l].empty()) continue;
+        const Archive& a = p->arch[l];
+        const size_t n = per[l].size();
+        const uint8_t* base = p->stage_d + off[l];
+        const void* dk = base + align16(n * 8);
+        const void* dv = (const uint8_t*)dk + align16(n * a.B * (size_t)a.D * 2);
+        rc = fkv_attn_promote_rows(p->handles[l], (int32_t)n, (const int32_t*)base, dk, dv, a.B, p->side);
+        if (!rc) rc = check_hip(hipEventRecord(p->done[l], p->side), "hipEventRecord");
+        if (!rc) {
+            p->has_done[l] = 1;
+            p->stats.promotions_completed += n;
+        }
+    }
+    return rc;
+}
+
+int fkv_promoter_order(fkv_promoter* p, int32_t layer, void* stream) {
+    if (!p) return set_error("fkv_promoter_order: NULL pipeline");
+    if (layer < 0 || layer >= p->n_layers || !p->side || !p->has_done[layer]) return FKV_OK;
+    return check_hip(hipStreamWaitEvent((hipStream_t)stream, p->done[layer], 0), "hipStreamWaitEvent");
+}
+
+int fkv_promoter_synchronize(fkv_promoter* p) {
+    if (!p) return set_error("fkv_promoter_synchronize: NULL pipeline");
+    if (!p->side) return FKV_OK;
+    return check_hip(hipStreamSynchronize(p->side), "hipStreamSynchronize");
+}
+
+int fkv_promoter_get_stats(const fkv_promoter* p, fkv_promoter_stats* out) {
+    if (!p || !out) return set_error("fkv_promoter_get_stats: NULL argument");
+    *out = p->stats;
+    return FKV_OK;
+}
+
+int fkv_promoter_near_valid(const fkv_promoter* p, int32_t layer, uint32_t* out, int32_t n) {
+    if (!p || !out) return set_error("fkv_promoter_near_valid: NULL argument");
+    if (layer < 0 || layer >= p->n_layers) return set_error("fkv_promoter_near_valid: layer out of range");
+    const auto& m = p->mirror[layer];
+    for (int i = 0; i < n && i < (int)m.size(); i++) out[i] = m[i];
+    return (int)m.size();
+}
+
+void fkv_promoter_destroy(fkv_promoter* p) {
+    if (!p) return;
+    if (p->side) {
+        (void)hipStreamSynchronize(p->side);
+        for (hipEvent_t e : p->done)
+            if (e) (void)hipEventDestroy(e);
+        if (p->staged) (void)hipEventDestroy(p->staged);
+        (void)hipStreamDestroy(p->side);
+    }
+    if (p->stage_h) (void)hipHostFree(p->stage_h);
+    if (p->stage_d) (void)hipFree(p->stage_d);
+    for (auto& a : p->arch) free_archive(a);
+    delete p;
+}
+
+}  // extern "C"

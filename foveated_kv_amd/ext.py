@@ -226,7 +226,20 @@ class FoveatedHandle:
     def get_blob_info(self):
         c = _lib.BlobInfoC()
         check(self._lib.fkv_attn_blob_info(self._h, ctypes.byref(c)), "fkv_attn_blob_info")
-        return BlobWriteInfo(c)
+        info = BlobWriteInfo(c)
+        info.handle = self  # register_blob targets this handle
+        return info
+
+    def export_near(self):
+        """The near tier the kernel attends to (promotions included), row-major
+        (B, H_kv, N_near_alloc, D) fp16 K and V."""
+        shape = (self.B, self.H_kv, self.N_near, self.D)
+        k = torch.empty(shape, dtype=torch.float16, device=self.device)
+        v = torch.empty_like(k)
+        with torch.cuda.device(self.device):
+            check(self._lib.fkv_attn_export_near(self._h, ptr(k), ptr(v), _lib.stream_ptr(self.device)),
+                  "fkv_attn_export_near")
+        return k, v
 
     def read_near_valid(self):
         """Current per-KV-head near_valid of the blob (host list)."""

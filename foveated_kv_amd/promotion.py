@@ -1,0 +1,154 @@
+"""Promotion of far-tier tokens into near-tier headroom.
+
+Mirror of the reference's ``foveated_ext.PromotionPipeline``
+(samfurr/foveated_kv csrc/bindings.cpp:42-100, csrc/promotion_pipeline.cpp)
+on the gfx950 library: the same constructor defaults, method names and
+statistics.  ``drain_spikes`` runs the reference's filter on the host (GQA
+dedup, cooldown, position dedup, per-call budget); the copy of exact fp16
+rows from the host-pinned archive into the blob's near headroom and the
+``near_valid[h]`` bump run as stream-ordered device work on a side stream
+(``flush``), ordered before the layer's next attention launch by
+``order``.
+"""
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import check
+
+
+def _host_i32(t):
+    """int32 host copy of a tensor / array (C-contiguous numpy)."""
+    if isinstance(t, torch.Tensor):
+        t = t.detach().to("cpu", torch.int32)
+        return np.ascontiguousarray(t.numpy())
+    return np.ascontiguousarray(np.asarray(t, dtype=np.int32))
+
+
+def _np_ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None and a.size else None
+
+
+class PromotionPipeline:
+    """PromotionPipeline(n_layers, cooldown_steps=5, max_per_drain=8).
+
+    Differences from the reference kept deliberately small: there is no
+    worker thread -- ``drain_spikes`` queues records and (by default)
+    ``flush``es them as asynchronous GPU work; call ``order(layer)`` before a
+    layer's next attention launch (the fused attention path does) so the
+    promoted rows and the new ``near_valid`` are seen together.
+    """
+
+    def __init__(self, n_layers, cooldown_steps=5, max_per_drain=8):
+        self._lib = _lib.load()
+        h = ctypes.c_void_p()
+        check(self._lib.fkv_promoter_create(int(n_layers), int(cooldown_steps), int(max_per_drain), ctypes.byref(h)),
+              "fkv_promoter_create")
+        self._h = h
+        self.n_layers = int(n_layers)
+        self._keep = {}  # layer -> host arrays the C side borrows
+        self._handles = {}
+        self._stopped = False
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.fkv_promoter_destroy(h)
+            self._h = None
+
+    # ---- registration ----
+    def register_archive(self, layer_idx, path_k, path_v, H_kv, S_arc, D, archive_idx):
+        """From the reference's on-disk archive files ((H_kv, S_arc, D) fp16,
+        disk_archive.py:127-185).  Like the reference, an unusable archive is
+        not an error: the layer is left without one and its drains are no-ops."""
+        idx = _host_i32(archive_idx).reshape(-1)
+        rc = self._lib.fkv_promoter_register_archive_files(self._h, int(layer_idx), str(path_k).encode(),
+                                                           str(path_v).encode(), int(H_kv), int(S_arc), int(D),
+                                                           _np_ptr(idx))
+        return rc == _lib.FKV_OK
+
+    def register_archive_tensors(self, layer_idx, archive_k, archive_v, archive_idx):
+        """From archive rows (B, H_kv, S_arc, D) fp16 on any device (e.g. a
+        compressed layer's ``archive_k/v``) and ``archive_idx`` (B, H_kv, S_arc)
+        or (H_kv, S_arc); the rows are copied into pinned host memory."""
+        k = archive_k.detach().to("cpu", torch.float16).contiguous()
+        v = archive_v.detach().to("cpu", torch.float16).contiguous()
+        if k.dim() == 3:
+            k, v = k[None], v[None]
+        B, H, S, D = k.shape
+        idx = _host_i32(archive_idx)
+        if idx.ndim == 3:
+            idx = np.ascontiguousarray(idx[0])
+        check(self._lib.fkv_promoter_register_archive(self._h, int(layer_idx), ctypes.c_void_p(k.data_ptr()),
+                                                      ctypes.c_void_p(v.data_ptr()), B, H, S, D, _np_ptr(idx), 1),
+              "fkv_promoter_register_archive")
+
+    def register_blob(self, layer_idx, info):
+        """``info``: a FoveatedHandle or the BlobWriteInfo of one."""
+        handle = getattr(info, "handle", info)
+        with torch.cuda.device(handle.device):
+            check(self._lib.fkv_promoter_register_handle(self._h, int(layer_idx), handle._h,
+                                                         _lib.stream_ptr(handle.device)),
+                  "fkv_promoter_register_handle")
+        self._handles[int(layer_idx)] = handle
+
+    # ---- per step ----
+    def drain_spikes(self, layer_idx, spike_flags, spike_tokens, far_idx, current_step, flush=True):
+        """promotion_pipeline.cpp:99-175; spike outputs (B, H_q) and far_idx
+        (B, H_kv, N_far).  Returns the number of promotions queued."""
+        if self._stopped:
+            return 0
+        flags = _host_i32(spike_flags)
+        tokens = _host_i32(spike_tokens)
+        fidx = _host_i32(far_idx)
+        B, Hq = flags.shape[0], flags.shape[1]
+        Hkv, n_far = fidx.shape[1], fidx.shape[2]
+        n = self._lib.fkv_promoter_drain(self._h, int(layer_idx), _np_ptr(flags), _np_ptr(tokens), _np_ptr(fidx),
+                                         B, Hq, Hkv, n_far, int(current_step))
+        if n < 0:
+            check(n, "fkv_promoter_drain")
+        if flush:
+            self.flush()
+        return n
+
+    def pending(self):
+        """Queued, unflushed records: int32 (n, 4) = layer, head, archive row, position."""
+        n = self._lib.fkv_promoter_pending(self._h, None, 0)
+        out = np.zeros((max(n, 0), 4), np.int32)
+        if n > 0:
+            self._lib.fkv_promoter_pending(self._h, _np_ptr(out), n)
+        return out
+
+    def flush(self):
+        check(self._lib.fkv_promoter_flush(self._h), "fkv_promoter_flush")
+
+    def order(self, layer_idx, stream=None):
+        """Make ``stream`` (default: torch's current stream) wait for the
+        layer's last flushed promotion."""
+        s = stream if stream is not None else torch.cuda.current_stream()
+        check(self._lib.fkv_promoter_order(self._h, int(layer_idx), ctypes.c_void_p(s.cuda_stream)),
+              "fkv_promoter_order")
+
+    def synchronize(self):
+        check(self._lib.fkv_promoter_synchronize(self._h), "fkv_promoter_synchronize")
+
+    def near_valid(self, layer_idx):
+        buf = (ctypes.c_uint32 * 4096)()
+        n = self._lib.fkv_promoter_near_valid(self._h, int(layer_idx), ctypes.cast(buf, ctypes.c_void_p), 4096)
+        if n < 0:
+            check(n, "fkv_promoter_near_valid")
+        return list(buf[:n])
+
+    def get_stats(self):
+        c = _lib.PromoterStatsC()
+        check(self._lib.fkv_promoter_get_stats(self._h, ctypes.byref(c)), "fkv_promoter_get_stats")
+        return {f: int(getattr(c, f)) for f in _lib.STATS_FIELDS}
+
+    def stop(self):
+        """bindings.cpp:97-99: no further promotions; in-flight copies complete."""
+        self._stopped = True
+        if self._h is not None and self._h.value:
+            self.synchronize()

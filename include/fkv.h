@@ -140,6 +140,86 @@ void fkv_attn_destroy(fkv_attn* h);
  * equal on every code the reference encoder emits. */
 int fkv_e4m3_decode(const uint8_t* codes, void* out_f16, int64_t n, void* stream);
 
+/* GPU side of one promotion batch (csrc/promotion_pipeline.cpp:192-241):
+ * on `stream`, writes n exact fp16 rows into near-tier slots and then, after
+ * them, raises near_valid[head] to slot + 1 with device-scope atomics.
+ * head_slot: device int32 [n][2] = (kv head, slot); rows_k / rows_v: device
+ * fp16 [n][row_batches][D], the row of batches 0..row_batches-1 (batches
+ * above keep their slot unchanged, like the reference's batch-0-only copy).
+ * Records whose head or slot fall outside the blob are skipped. */
+int fkv_attn_promote_rows(fkv_attn* h, int32_t n, const int32_t* head_slot, const void* rows_k,
+                          const void* rows_v, int32_t row_batches, void* stream);
+
+/* The blob's near tier back to row-major (B, Hkv, Na, D) fp16 device
+ * buffers (either may be NULL): what the kernel attends to, promotions
+ * included. */
+int fkv_attn_export_near(const fkv_attn* h, void* near_k_out, void* near_v_out, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* promotion pipeline (PromotionPipeline, csrc/promotion_pipeline.h:75-141)  */
+/* ---------------------------------------------------------------------- */
+
+typedef struct fkv_promoter fkv_promoter;
+
+/* PromotionStats (promotion_pipeline.h:42-49). */
+typedef struct fkv_promoter_stats {
+    uint64_t spikes_detected, spikes_queued, spikes_deduplicated, spikes_cooled_down;
+    uint64_t promotions_completed, promotions_headroom_full;
+} fkv_promoter_stats;
+
+/* PromotionPipeline(n_layers, cooldown_steps=5, max_per_drain=8)
+ * (bindings.cpp:43-47).  Host only: no GPU work until the first flush. */
+int fkv_promoter_create(int32_t n_layers, int32_t cooldown_steps, int32_t max_per_drain, fkv_promoter** out);
+
+/* register_archive (promotion_pipeline.cpp:45-83) from host rows
+ * [B_arc][Hkv][S_arc][D] fp16 and archive_idx [Hkv][S_arc] int32 (global
+ * position of each archive row).  copy_to_pinned: copy the rows into
+ * pinned host memory owned by the pipeline (else the pointers are
+ * borrowed and must stay valid). */
+int fkv_promoter_register_archive(fkv_promoter* p, int32_t layer, const void* k, const void* v, int32_t B_arc,
+                                  int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx,
+                                  int32_t copy_to_pinned);
+
+/* register_archive from the reference's on-disk archive files
+ * (disk_archive.py:127-185: (Hkv, S_arc, D) fp16 raw, batch 0), read into
+ * pinned host memory.  An unreadable file leaves the layer without an
+ * archive (drain is then a no-op for it, as in the reference). */
+int fkv_promoter_register_archive_files(fkv_promoter* p, int32_t layer, const char* path_k, const char* path_v,
+                                        int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx);
+
+/* register_blob (promotion_pipeline.h:95): the layer's attention handle.
+ * Reads its near_valid once (synchronous on stream) into the pipeline's
+ * host mirror; the pipeline must then be the only writer of near_valid. */
+int fkv_promoter_register_handle(fkv_promoter* p, int32_t layer, fkv_attn* h, void* stream);
+
+/* drain_spikes (promotion_pipeline.cpp:99-175), host only: spike_flags /
+ * spike_tokens (B*Hq) and far_idx (B, Hkv, N_far) are host int32 arrays.
+ * Returns the number of records queued (>= 0); invalid layers or a layer
+ * without archive queue nothing, as in the reference. */
+int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* spike_flags, const int32_t* spike_tokens,
+                       const int32_t* far_idx, int32_t B, int32_t Hq, int32_t Hkv, int32_t N_far, int32_t step);
+
+/* Queued records (not yet flushed): returns their count and copies up to
+ * max_records of them as int32 [layer, head, archive row, position]. */
+int fkv_promoter_pending(const fkv_promoter* p, int32_t* out_records, int32_t max_records);
+
+/* The worker's job (promotion_pipeline.cpp:192-241) as stream-ordered GPU
+ * work on the pipeline's side stream: assign headroom slots (full headroom
+ * is counted and skipped), gather the rows from the pinned archive, one
+ * hipMemcpyAsync, fkv_attn_promote_rows per layer.  Returns immediately. */
+int fkv_promoter_flush(fkv_promoter* p);
+
+/* Make `stream` wait for the last flushed promotion of `layer` (call before
+ * the layer's next attention launch: the rows and the new near_valid are
+ * then visible together). */
+int fkv_promoter_order(fkv_promoter* p, int32_t layer, void* stream);
+int fkv_promoter_synchronize(fkv_promoter* p);
+int fkv_promoter_get_stats(const fkv_promoter* p, fkv_promoter_stats* out);
+/* The host mirror of a layer's near_valid (returns Hkv, copies up to n). */
+int fkv_promoter_near_valid(const fkv_promoter* p, int32_t layer, uint32_t* out, int32_t n);
+/* stop() + destructor (promotion_pipeline.cpp:30-38, 243-248). */
+void fkv_promoter_destroy(fkv_promoter* p);
+
 /* Benchmark utility with no counterpart in the reference: streams `bytes`
  * (a multiple of 16) from device buffer `buf` with 16-byte lane loads,
  * `unroll` (1, 2, 4, 8) loads in flight per lane, optionally non-temporal,

@@ -1,0 +1,284 @@
+"""Promotion pipeline: the host drain filter against its restatement and
+known answers (CPU), and the GPU side end to end (bit-exact rows, the
+near_valid bump, attention after promotion)."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import promotion as opromo
+
+# ---------------------------------------------------------------------------
+# helpers: the C-ABI drain on the host (no GPU work: borrowed archive rows)
+# ---------------------------------------------------------------------------
+
+
+class CDrain:
+    def __init__(self, n_layers, cooldown=5, budget=8):
+        from foveated_kv_amd import _lib
+
+        self.lib = _lib.load()
+        self._lib = _lib
+        self.h = ctypes.c_void_p()
+        _lib.check(self.lib.fkv_promoter_create(n_layers, cooldown, budget, ctypes.byref(self.h)),
+                   "fkv_promoter_create")
+        self.keep = []
+
+    def archive(self, layer, k, v, idx):
+        k = np.ascontiguousarray(k, np.float16)
+        v = np.ascontiguousarray(v, np.float16)
+        idx = np.ascontiguousarray(idx, np.int32)
+        self.keep += [k, v, idx]
+        B, H, S, D = k.shape
+        self._lib.check(self.lib.fkv_promoter_register_archive(
+            self.h, layer, k.ctypes.data_as(ctypes.c_void_p), v.ctypes.data_as(ctypes.c_void_p), B, H, S, D,
+            idx.ctypes.data_as(ctypes.c_void_p), 0), "register_archive")
+
+    def drain(self, layer, flags, tokens, far_idx, step):
+        flags = np.ascontiguousarray(flags, np.int32)
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        far_idx = np.ascontiguousarray(far_idx, np.int32)
+        P = ctypes.c_void_p
+        return self.lib.fkv_promoter_drain(self.h, layer, flags.ctypes.data_as(P), tokens.ctypes.data_as(P),
+                                           far_idx.ctypes.data_as(P), flags.shape[0], flags.shape[1],
+                                           far_idx.shape[1], far_idx.shape[2], step)
+
+    def pending(self):
+        n = self.lib.fkv_promoter_pending(self.h, None, 0)
+        out = np.zeros((n, 4), np.int32)
+        if n:
+            self.lib.fkv_promoter_pending(self.h, out.ctypes.data_as(ctypes.c_void_p), n)
+        return [tuple(int(x) for x in r) for r in out]
+
+    def stats(self):
+        c = self._lib.PromoterStatsC()
+        self.lib.fkv_promoter_get_stats(self.h, ctypes.byref(c))
+        return {f: int(getattr(c, f)) for f in self._lib.STATS_FIELDS}
+
+    def __del__(self):
+        if self.h.value:
+            self.lib.fkv_promoter_destroy(self.h)
+
+
+def _archive(Hkv, S, D, start=4, seed=0):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((1, Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((1, Hkv, S, D)).astype(np.float16)
+    idx = np.broadcast_to(np.arange(start, start + S, dtype=np.int32), (Hkv, S)).copy()
+    return k, v, idx
+
+
+def _both(n_layers=2, cooldown=5, budget=8):
+    return CDrain(n_layers, cooldown, budget), opromo.Pipeline(n_layers, cooldown, budget)
+
+
+def _register(c, o, layer, k, v, idx):
+    c.archive(layer, k, v, idx)
+    o.register_archive(layer, k, v, idx)
+
+
+# ---------------------------------------------------------------------------
+# known answers (each rule of promotion_pipeline.cpp:99-175), checked on both
+# the restatement and the library
+# ---------------------------------------------------------------------------
+
+def test_gqa_dedup_keeps_first_flagged_query_head():
+    c, o = _both()
+    Hq, Hkv, S = 8, 2, 40
+    k, v, idx = _archive(Hkv, S, 4)
+    _register(c, o, 0, k, v, idx)
+    far_idx = idx[None]
+    flags = np.zeros((1, Hq), np.int32)
+    tokens = np.zeros((1, Hq), np.int32)
+    flags[0, [1, 2, 5]] = 1          # heads 1, 2 -> kv 0; head 5 -> kv 1
+    tokens[0, 1], tokens[0, 2], tokens[0, 5] = 7, 9, 3
+    for impl in (c, o):
+        assert impl.drain(0, flags, tokens, far_idx, 0) == 2
+    assert c.pending() == [(0, 0, 7, 11), (0, 1, 3, 7)] == o.queue
+    assert c.stats()["spikes_detected"] == o.stats["spikes_detected"] == 2
+
+
+def test_cooldown_and_position_dedup():
+    c, o = _both(cooldown=5)
+    k, v, idx = _archive(1, 30, 4)
+    _register(c, o, 0, k, v, idx)
+    far_idx = idx[None]
+    f = np.ones((1, 1), np.int32)
+    for step, tok in [(0, 5), (3, 6), (5, 5), (11, 6)]:
+        for impl in (c, o):
+            impl.drain(0, f, np.full((1, 1), tok, np.int32), far_idx, step)
+    # step 0 queues 5; step 3 is cooled down; step 5 finds 5 already promoted;
+    # step 11 queues 6
+    assert [r[2] for r in c.pending()] == [5, 6] == [r[2] for r in o.queue]
+    s = c.stats()
+    assert s == o.stats
+    assert (s["spikes_detected"], s["spikes_cooled_down"], s["spikes_deduplicated"], s["spikes_queued"]) == (4, 1, 1, 2)
+
+
+def test_budget_out_of_range_and_missing_rows():
+    c, o = _both(budget=2)
+    Hkv, S = 4, 20
+    k, v, idx = _archive(Hkv, S, 4)
+    idx[2, 3] = 999                      # head 2, far row 3 is not in the archive under its far position
+    _register(c, o, 0, k, v, idx)
+    far_idx = np.broadcast_to(np.arange(4, 4 + S, dtype=np.int32), (1, Hkv, S)).copy()
+    flags = np.ones((1, Hkv), np.int32)
+    tokens = np.array([[-1, S, 3, 1]], np.int32)   # out of range twice, then a missing row, then ok
+    for impl in (c, o):
+        assert impl.drain(0, flags, tokens, far_idx, 0) == 1
+    assert c.pending() == o.queue == [(0, 3, 1, 5)]
+    s = c.stats()
+    assert s == o.stats and s["spikes_detected"] == 4 and s["spikes_queued"] == 1
+    # a layer without an archive and an invalid layer queue nothing
+    for impl in (c, o):
+        assert impl.drain(1, flags, tokens, far_idx, 0) == 0
+        assert impl.drain(7, flags, tokens, far_idx, 0) == 0
+
+
+def test_drain_matches_restatement_on_random_streams():
+    rng = np.random.default_rng(5)
+    c, o = _both(n_layers=3, cooldown=3, budget=5)
+    B, Hq, Hkv, S = 2, 16, 4, 50
+    for layer in range(3):
+        k, v, idx = _archive(Hkv, S, 10, seed=layer)
+        _register(c, o, layer, k, v, idx)
+    far_idx = np.broadcast_to(np.arange(10, 10 + S, dtype=np.int32), (B, Hkv, S)).copy()
+    for step in range(40):
+        for layer in range(3):
+            flags = (rng.random((B, Hq)) < 0.3).astype(np.int32)
+            tokens = rng.integers(-2, S + 2, size=(B, Hq)).astype(np.int32)
+            assert c.drain(layer, flags, tokens, far_idx, step) == o.drain(layer, flags, tokens, far_idx, step)
+    assert c.pending() == o.queue
+    assert c.stats() == o.stats
+    assert o.stats["spikes_cooled_down"] > 0 and o.stats["spikes_deduplicated"] > 0
+
+
+# ---------------------------------------------------------------------------
+# GPU side
+# ---------------------------------------------------------------------------
+
+def _layer(B, Hkv, D, S, seed, headroom_min=8):
+    import torch
+
+    from foveated_kv_amd import ext, synthetic
+
+    k, v = synthetic.make_kv(B, Hkv, S, D, seed)
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = headroom_min
+    cfg.promo_headroom_pct = 0.5
+    cl = ext.CompressHandle(cfg).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero, cl.near_valid,
+                           spike_margin=10.0)
+    return k, v, cl, h
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 2])
+def test_promotion_rows_bit_exact_and_near_valid(orc, B):
+    import torch
+
+    from foveated_kv_amd.promotion import PromotionPipeline
+    from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
+
+    Hkv, Hq, D, S = 2, 8, 128, 1000
+    print(f"promotion B={B} Hkv={Hkv} D={D} S={S}", flush=True)
+    k, v, cl, h = _layer(B, Hkv, D, S, 31)
+    tb = TierConfig(promo_headroom_min=8).tier_boundaries(S)
+    _, far_idx = tier_index_tensors(tb, S, B, Hkv, "cpu")
+    far_idx = far_idx.numpy()
+    pipe = PromotionPipeline(1, cooldown_steps=0, max_per_drain=8)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_blob(0, h.get_blob_info())
+    ref = opromo.Pipeline(1, 0, 8)
+    ref.register_archive(0, cl.archive_k.cpu().numpy(), cl.archive_v.cpu().numpy(), far_idx[0])
+    near_k = {0: cl.near_k.cpu().numpy().copy()}
+    near_v = {0: cl.near_v.cpu().numpy().copy()}
+    nv = {0: cl.near_valid.cpu().numpy().copy()}
+    rng = np.random.default_rng(3)
+    for step in range(6):
+        flags = np.ones((B, Hq), np.int32)
+        tokens = rng.integers(0, far_idx.shape[2], size=(B, Hq)).astype(np.int32)
+        pipe.drain_spikes(0, torch.from_numpy(flags), torch.from_numpy(tokens), far_idx, step)
+        ref.drain(0, flags, tokens, far_idx, step)
+        ref.commit(near_k, near_v, nv, {0: cl.near_k.shape[2]})
+    pipe.order(0)
+    torch.cuda.synchronize()
+    gk, gv = h.export_near()
+    assert h.read_near_valid() == [int(x) for x in nv[0]] == pipe.near_valid(0)
+    assert np.array_equal(gk.cpu().numpy().view(np.uint16), near_k[0].view(np.uint16))
+    assert np.array_equal(gv.cpu().numpy().view(np.uint16), near_v[0].view(np.uint16))
+    assert pipe.get_stats() == ref.stats and ref.stats["promotions_completed"] > 0
+    # the kernel attends to the promoted rows: parity with the oracle on the exported tier
+    q = torch.from_numpy(np.random.default_rng(4).standard_normal((B, Hq, D)).astype(np.float16)).cuda()
+    out, flags_o, tokens_o = h(q[:, :, None])
+    torch.cuda.synchronize()
+    o, _, _, _, _ = orc.attend_kernel(q.cpu().numpy(), near_k[0], near_v[0], nv[0], cl.far_k.cpu().numpy(),
+                                      cl.far_v.cpu().numpy(), cl.far_v_scale.cpu().numpy(),
+                                      cl.far_v_zero.cpu().numpy(), spike_margin=10.0)
+    got = out[:, :, 0].float().cpu().numpy()
+    assert np.abs(got - o).max() <= 2e-3 and orc.cosine(got, o) >= 0.9999
+
+
+@pytest.mark.gpu
+def test_promotion_headroom_full_is_counted():
+    import torch
+
+    from foveated_kv_amd.promotion import PromotionPipeline
+    from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
+
+    B, Hkv, Hq, D, S = 1, 1, 4, 64, 100   # R = 36, headroom = 18
+    _, _, cl, h = _layer(B, Hkv, D, S, 32, headroom_min=2)
+    tb = TierConfig(promo_headroom_min=2).tier_boundaries(S)
+    _, far_idx = tier_index_tensors(tb, S, B, Hkv, "cpu")
+    far_idx = far_idx.numpy()
+    cap = cl.near_k.shape[2]
+    pipe = PromotionPipeline(1, cooldown_steps=0, max_per_drain=8)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_blob(0, h)
+    n_far = far_idx.shape[2]
+    for step in range(n_far):
+        pipe.drain_spikes(0, np.ones((1, Hq), np.int32), np.full((1, Hq), step, np.int32), far_idx, step)
+    pipe.synchronize()
+    s = pipe.get_stats()
+    assert h.read_near_valid() == [cap]
+    assert s["promotions_completed"] == cap - tb["R_actual"]
+    assert s["promotions_headroom_full"] == n_far - s["promotions_completed"]
+
+
+@pytest.mark.gpu
+def test_promotion_from_archive_files(tmp_path):
+    """The reference's on-disk archive format (disk_archive.py:127-185):
+    (H_kv, S_arc, D) fp16 raw per layer, batch 0."""
+    import torch
+
+    from foveated_kv_amd.promotion import PromotionPipeline
+    from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
+
+    B, Hkv, D, S = 1, 2, 64, 512
+    _, _, cl, h = _layer(B, Hkv, D, S, 33)
+    tb = TierConfig(promo_headroom_min=8).tier_boundaries(S)
+    _, far_idx = tier_index_tensors(tb, S, B, Hkv, "cpu")
+    far_idx = far_idx.numpy()
+    ak = cl.archive_k[0].cpu().numpy()
+    av = cl.archive_v[0].cpu().numpy()
+    pk, pv = tmp_path / "archive_k_layer0.bin", tmp_path / "archive_v_layer0.bin"
+    ak.tofile(pk)
+    av.tofile(pv)
+    pipe = PromotionPipeline(1, cooldown_steps=0)
+    pipe.register_blob(0, h)
+    # an unreadable archive leaves the layer without one: drains queue nothing
+    assert not pipe.register_archive(0, tmp_path / "missing.bin", pv, Hkv, ak.shape[1], D, far_idx[0])
+    assert pipe.drain_spikes(0, np.ones((1, 8), np.int32), np.zeros((1, 8), np.int32), far_idx, 0) == 0
+    assert pipe.register_archive(0, pk, pv, Hkv, ak.shape[1], D, far_idx[0])
+    r0 = h.read_near_valid()
+    tokens = np.array([[10, 10, 10, 10, 20, 20, 20, 20]], np.int32)
+    pipe.drain_spikes(0, np.ones((1, 8), np.int32), tokens, far_idx, 1)
+    pipe.order(0)
+    torch.cuda.synchronize()
+    gk, gv = h.export_near()
+    nv = h.read_near_valid()
+    assert nv == [r0[0] + 1, r0[1] + 1]
+    for hh, tok in ((0, 10), (1, 20)):
+        assert np.array_equal(gk[0, hh, r0[hh]].cpu().numpy().view(np.uint16), ak[hh, tok].view(np.uint16))
+        assert np.array_equal(gv[0, hh, r0[hh]].cpu().numpy().view(np.uint16), av[hh, tok].view(np.uint16))
