@@ -1,0 +1,461 @@
+"""Decode-time routing of a PyTorch model's attention through the fused
+gfx950 kernel, and the prefill -> compress -> decode loop around it
+(samfurr/foveated_kv src/foveated_kv/mlx_generate.py:38-590).
+
+``install_fused_sdpa`` replaces ``torch.nn.functional.scaled_dot_product_attention``
+with a closure (mlx_generate.py:84-131):
+
+* a call whose query holds more than one position (prefill) goes to the
+  original function unchanged;
+* a one-position call (decode) is answered by the next layer's foveated
+  handle: a layer counter walks ``fov_cache.layers`` in call order, wraps
+  modulo the layer count, and is reset once per step by ``drain_spikes`` /
+  ``reset_fused_layer_counter``;
+* the handle's fp16 output is cast to the query's dtype, and its spike
+  flags / tokens are stashed on the layer's ``FusedCacheWrapper`` for the
+  promotion pipeline.
+
+The model side follows the mlx-lm conventions the reference relies on:
+``model(tokens, cache=caches)`` returns logits (B, L, vocab), each
+attention layer calls ``keys, values = cache.update_and_fetch(k, v)`` and
+then ``F.scaled_dot_product_attention`` (looked up on the module at call
+time), RoPE reads ``cache.offset``, and ``len(model.layers)`` is the layer
+count.  ``KVCache`` / ``make_prompt_cache`` are the standard fp16 cache used
+for prefill.
+
+One difference from the reference: when a ``PromotionPipeline`` is drained
+through ``drain_spikes``, each layer's decode launch is ordered after that
+layer's promotion copies (``PromotionPipeline.order``), because here the
+copies are asynchronous device work rather than CPU stores into unified
+memory.
+"""
+
+import math
+import shutil
+import tempfile
+import time
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .promotion import PromotionPipeline
+from .tier_cache import MLXFoveatedKVCache, MLXTierConfig
+
+
+def _log_softmax(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    return x - torch.logsumexp(x, dim=dim, keepdim=True)
+
+
+# ---------------------------------------------------------------------------
+# standard cache (prefill)
+# ---------------------------------------------------------------------------
+
+class KVCache:
+    """Growing fp16/bf16 K, V cache with the mlx-lm interface the models
+    use: ``update_and_fetch`` appends (B, H_kv, L, D) and returns all rows,
+    ``state`` is (keys, values), ``offset`` the number of tokens held."""
+
+    def __init__(self):
+        self.keys = None
+        self.values = None
+        self.offset = 0
+
+    def update_and_fetch(self, keys, values):
+        if self.keys is None:
+            self.keys, self.values = keys, values
+        else:
+            self.keys = torch.cat([self.keys, keys], dim=2)
+            self.values = torch.cat([self.values, values], dim=2)
+        self.offset += keys.shape[2]
+        return self.keys, self.values
+
+    @property
+    def state(self):
+        return self.keys, self.values
+
+
+def make_prompt_cache(model) -> list:
+    return [KVCache() for _ in range(len(model.layers))]
+
+
+# ---------------------------------------------------------------------------
+# fused SDPA closure
+# ---------------------------------------------------------------------------
+
+class _FusedSDPAState:
+    """mlx_generate.py:42-54."""
+
+    def __init__(self):
+        self.original_sdpa = None
+        self._installed = False
+        self._fov_cache = None
+        self._cpp_pipeline_handle = None
+        self._layer_counter = 0
+        self._n_layers = 0
+        self._decode_step = 0
+        self._fused_wrappers = None
+        self._fused_disabled = False
+        self._promotion = None  # pipeline whose flushed copies decode launches wait for
+
+
+_fused_state = _FusedSDPAState()
+
+
+class FusedCacheWrapper:
+    """mlx_generate.py:57-81: the cache object a model sees during fused
+    decode.  ``update_and_fetch`` appends the new token to the layer's
+    decode buffer and hands the same K, V back (the model needs tensors of
+    the right shape; attention itself never reads them)."""
+
+    def __init__(self, fov_layer, layer_idx: int):
+        self.fov_layer = fov_layer
+        self.layer_idx = layer_idx
+        self.offset = fov_layer.total_tokens
+        self._spike_flags = None
+        self._spike_tokens = None
+        self._far_idx_host = None
+
+    @property
+    def state(self):
+        return self.fov_layer.near_k, self.fov_layer.near_v
+
+    def update_and_fetch(self, keys, values):
+        self.fov_layer.add_token(keys, values)
+        self.offset += keys.shape[2]
+        return keys, values
+
+    def far_idx_host(self) -> np.ndarray:
+        """int32 host copy of the layer's far_idx (B, H_kv, F), made once:
+        the drain reads it every step and it never changes."""
+        if self._far_idx_host is None:
+            self._far_idx_host = np.ascontiguousarray(
+                self.fov_layer.far_idx.detach().to("cpu", torch.int32).numpy())
+        return self._far_idx_host
+
+
+def _build_fused_interceptor(state: _FusedSDPAState):
+    """mlx_generate.py:84-131.  ``scale`` is not forwarded to the kernel,
+    which (like the reference's) always uses D^-1/2."""
+    original = state.original_sdpa
+    layers = state._fov_cache.layers
+    n_layers = state._n_layers
+
+    def interceptor(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None, **kwargs):
+        if query.dim() != 4 or query.shape[2] > 1:
+            return original(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                            is_causal=is_causal, scale=scale, **kwargs)
+
+        idx = state._layer_counter
+        state._layer_counter = idx + 1
+        if idx >= n_layers:
+            idx = idx % n_layers
+
+        layer = layers[idx]
+        if layer is None or state._fused_disabled:
+            return original(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                            is_causal=is_causal, scale=scale, **kwargs)
+
+        promo = state._promotion
+        if promo is not None:
+            promo.order(idx)
+        out, flags, tokens = layer.attend_fused_with_spikes(query)
+
+        wrappers = state._fused_wrappers
+        if wrappers is not None and idx < len(wrappers):
+            w = wrappers[idx]
+            if w is not None:
+                w._spike_flags = flags
+                w._spike_tokens = tokens
+
+        if out.dtype != query.dtype:
+            out = out.to(query.dtype)
+        return out
+
+    return interceptor
+
+
+def install_fused_sdpa(fov_cache) -> None:
+    """mlx_generate.py:134-161.  Loads the gfx950 library first, so a
+    missing library raises here instead of on the first decode call."""
+    if _fused_state._installed:
+        raise RuntimeError("Fused SDPA already installed -- call uninstall_fused_sdpa() first")
+    _lib.load()
+
+    s = _fused_state
+    s.original_sdpa = F.scaled_dot_product_attention
+    s._fov_cache = fov_cache
+    s._cpp_pipeline_handle = None
+    s._layer_counter = 0
+    s._n_layers = len(fov_cache.layers)
+    s._decode_step = 0
+    s._fused_wrappers = None
+    s._fused_disabled = False
+    s._promotion = None
+    s._installed = True
+    F.scaled_dot_product_attention = _build_fused_interceptor(s)
+
+
+def uninstall_fused_sdpa() -> None:
+    """mlx_generate.py:164-178: restore the original function and clear state."""
+    s = _fused_state
+    if not s._installed:
+        return
+    F.scaled_dot_product_attention = s.original_sdpa
+    s.__init__()
+
+
+def install_fused_attention(model, fov_cache) -> list:
+    """mlx_generate.py:186-201: install the closure and return one
+    ``FusedCacheWrapper`` per layer (None for empty layers), to be passed as
+    the model's cache."""
+    wrappers = [FusedCacheWrapper(layer, i) if layer is not None else None
+                for i, layer in enumerate(fov_cache.layers)]
+    install_fused_sdpa(fov_cache)
+    _fused_state._fused_wrappers = wrappers
+    return wrappers
+
+
+def uninstall_fused_attention(model) -> None:
+    """mlx_generate.py:204-206."""
+    uninstall_fused_sdpa()
+
+
+def _drain_into(pipeline, wrappers, step: int) -> None:
+    """Hand every stashed (flags, tokens) pair to ``pipeline.drain_spikes``
+    and clear the stash.  For this package's ``PromotionPipeline`` the
+    spike arrays of all layers come to the host in one copy and the queued
+    promotions are flushed once, after the last layer."""
+    ready = [w for w in (wrappers or [])
+             if w is not None and w._spike_flags is not None and w._spike_tokens is not None]
+    if pipeline is not None and ready:
+        if isinstance(pipeline, PromotionPipeline):
+            both = torch.stack([torch.stack([w._spike_flags, w._spike_tokens]) for w in ready])
+            host = both.to("cpu", torch.int32).numpy()
+            for i, w in enumerate(ready):
+                pipeline.drain_spikes(w.layer_idx, host[i, 0], host[i, 1], w.far_idx_host(), step,
+                                      flush=False)
+            pipeline.flush()
+        else:
+            for w in ready:
+                pipeline.drain_spikes(w.layer_idx, w._spike_flags, w._spike_tokens,
+                                      w.fov_layer.far_idx, step)
+    for w in wrappers or []:
+        if w is not None:
+            w._spike_flags = None
+            w._spike_tokens = None
+
+
+def drain_spikes(wrappers: list, pipeline, decode_step: int) -> None:
+    """mlx_generate.py:209-230: reset the layer counter, then drain the
+    stashed spikes of the last step into ``pipeline`` (skipped when None)."""
+    reset_fused_layer_counter()
+    if pipeline is None:
+        return
+    if hasattr(pipeline, "order"):
+        _fused_state._promotion = pipeline
+    _drain_into(pipeline, wrappers, decode_step)
+
+
+def reset_fused_layer_counter() -> None:
+    """mlx_generate.py:233-259: start a new decode step; drains into the
+    state's own pipeline handle when one is set."""
+    s = _fused_state
+    s._layer_counter = 0
+    s._decode_step += 1
+    if s._cpp_pipeline_handle is None:
+        return
+    _drain_into(s._cpp_pipeline_handle, s._fused_wrappers, s._decode_step)
+
+
+# ---------------------------------------------------------------------------
+# generation
+# ---------------------------------------------------------------------------
+
+def _model_device(model):
+    for p in model.parameters():
+        return p.device
+    return torch.device("cuda")
+
+
+def prefill_and_compress(model, tokens: torch.Tensor, cfg: Optional[MLXTierConfig] = None):
+    """mlx_generate.py:390-416 -> (fov_cache, prefill_logits, std_caches)."""
+    cfg = cfg or MLXTierConfig()
+    std_caches = make_prompt_cache(model)
+    with torch.no_grad():
+        prefill_logits = model(tokens, cache=std_caches)
+    fov_cache = MLXFoveatedKVCache(cfg)
+    for i, c in enumerate(std_caches):
+        k, v = c.state
+        if k is not None:
+            fov_cache.update(k, v, i)
+    fov_cache.compress()
+    return fov_cache, prefill_logits, std_caches
+
+
+def _next_token(logits, temp):
+    if temp == 0:
+        return torch.argmax(logits, dim=-1)
+    return torch.multinomial(torch.softmax(logits.float() / temp, dim=-1), 1).reshape(-1)
+
+
+def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
+                   cfg: Optional[MLXTierConfig] = None, disk_archive_dir: Optional[str] = None,
+                   temp: float = 0.0, enable_promotion: bool = True):
+    """mlx_generate.py:266-387: prefill, compress, move archives to disk,
+    register them and the handles with a ``PromotionPipeline``, then decode
+    with the closure installed.  Returns (text, stats)."""
+    from .disk_archive import offload_cache_to_disk
+
+    dev = _model_device(model)
+    tokens = torch.tensor(tokenizer.encode(prompt), dtype=torch.long, device=dev).reshape(1, -1)
+
+    t0 = time.perf_counter()
+    fov_cache, prefill_logits, _ = prefill_and_compress(model, tokens, cfg)
+    t_prefill = time.perf_counter() - t0
+    mem_before = fov_cache.memory_bytes()
+
+    own_dir = disk_archive_dir is None
+    if own_dir:
+        disk_archive_dir = tempfile.mkdtemp(prefix="foveated_fused_")
+    disk_archives = offload_cache_to_disk(fov_cache, disk_archive_dir)
+    mem_after = fov_cache.memory_bytes()
+
+    pipeline = None
+    if enable_promotion:
+        pipeline = PromotionPipeline(len(fov_cache.layers))
+        for i, layer in enumerate(fov_cache.layers):
+            if layer is None:
+                continue
+            layer._ensure_kcache()
+            handle = layer._kcache.get("cpp_handle")
+            if handle is not None and hasattr(handle, "get_blob_info"):
+                pipeline.register_blob(i, handle.get_blob_info())
+            if i < len(disk_archives) and disk_archives[i] is not None:
+                a = disk_archives[i]
+                pipeline.register_archive(i, a.path_k, a.path_v, a.H_kv, a.S_arc, a.D, a.idx)
+
+    wrappers = install_fused_attention(model, fov_cache)
+    generated = []
+    next_logits = prefill_logits[:, -1, :]
+    t_dec = time.perf_counter()
+    try:
+        with torch.no_grad():
+            for step in range(max_tokens):
+                tok = _next_token(next_logits, temp)
+                token_id = int(tok.item())
+                if token_id == getattr(tokenizer, "eos_token_id", None):
+                    break
+                generated.append(token_id)
+                drain_spikes(wrappers, pipeline, step)
+                next_logits = model(tok.reshape(1, 1), cache=wrappers)[:, -1, :]
+        torch.cuda.synchronize(dev)
+    finally:
+        uninstall_fused_attention(model)
+        if pipeline is not None:
+            pipeline.stop()
+        shutil.rmtree(disk_archive_dir, ignore_errors=True)
+    t_decode = time.perf_counter() - t_dec
+
+    mb = 1024 * 1024
+    stats = {
+        "prompt_tokens": tokens.shape[1],
+        "generated_tokens": len(generated),
+        "fused_kernel": True,
+        "disk_offloaded": True,
+        "prefill_time_s": t_prefill,
+        "decode_time_s": t_decode,
+        "tokens_per_second": len(generated) / max(t_decode, 1e-6),
+        "mem_quantized_mb": mem_before["total_quantized"] / mb,
+        "mem_archive_before_mb": mem_before["archive"] / mb,
+        "mem_archive_after_mb": mem_after["archive"] / mb,
+        "mem_saved_mb": (mem_before["archive"] - mem_after["archive"]) / mb,
+    }
+    if pipeline is not None:
+        stats.update(pipeline.get_stats())
+    return tokenizer.decode(generated), stats
+
+
+def compute_perplexity(model, tokenizer, text: str, context_len: int = 4096, eval_len: int = 256,
+                       cfg: Optional[MLXTierConfig] = None):
+    """mlx_generate.py:419-496 -> (standard_ppl, foveated_ppl)."""
+    cfg = cfg or MLXTierConfig()
+    dev = _model_device(model)
+    all_tokens = torch.tensor(tokenizer.encode(text), dtype=torch.long, device=dev)
+    total = context_len + eval_len
+    if all_tokens.shape[0] < total:
+        raise ValueError(f"Text too short: {all_tokens.shape[0]} tokens, need {total}")
+    context = all_tokens[:context_len].reshape(1, -1)
+    evals = all_tokens[context_len:total]
+
+    def nll_over(cache, before_step=None):
+        nll = 0.0
+        for i in range(eval_len):
+            if before_step is not None:
+                before_step()
+            logits = model(evals[i:i + 1].reshape(1, 1), cache=cache)
+            lp = _log_softmax(logits[:, -1, :].float())
+            if i + 1 < eval_len:
+                nll -= float(lp[0, int(evals[i + 1])].item())
+        return nll
+
+    with torch.no_grad():
+        std = make_prompt_cache(model)
+        model(context, cache=std)
+        std_ppl = math.exp(nll_over(std) / max(eval_len - 1, 1))
+
+        fov_cache, _, _ = prefill_and_compress(model, context, cfg)
+        wrappers = [FusedCacheWrapper(layer, i) if layer is not None else None
+                    for i, layer in enumerate(fov_cache.layers)]
+        install_fused_sdpa(fov_cache)
+        try:
+            fov_ppl = math.exp(nll_over(wrappers, reset_fused_layer_counter) / max(eval_len - 1, 1))
+        finally:
+            uninstall_fused_sdpa()
+    return std_ppl, fov_ppl
+
+
+def _generate_short(model, tokenizer, prompt: str, max_tokens: int = 20):
+    """mlx_generate.py:568-590: greedy decode with the standard cache."""
+    dev = _model_device(model)
+    tokens = torch.tensor(tokenizer.encode(prompt), dtype=torch.long, device=dev).reshape(1, -1)
+    cache = make_prompt_cache(model)
+    generated = []
+    with torch.no_grad():
+        next_logits = model(tokens, cache=cache)[:, -1, :]
+        for _ in range(max_tokens):
+            tok = torch.argmax(next_logits, dim=-1)
+            token_id = int(tok.item())
+            if token_id == getattr(tokenizer, "eos_token_id", None):
+                break
+            generated.append(token_id)
+            next_logits = model(tok.reshape(1, 1), cache=cache)[:, -1, :]
+    return tokenizer.decode(generated), {"generated_tokens": len(generated)}
+
+
+def needle_test(model, tokenizer, context_len: int = 4096, needle_depth: float = 0.5,
+                cfg: Optional[MLXTierConfig] = None, seed: Optional[int] = None):
+    """mlx_generate.py:499-565: passkey retrieval with the standard cache and
+    with the fused foveated path -> (standard_found, foveated_found, info)."""
+    import random
+
+    cfg = cfg or MLXTierConfig()
+    passkey = str(random.Random(seed).randint(10000, 99999))
+    needle = f"The secret passkey is {passkey}. Remember it."
+    filler = "This is a document about various topics in science and technology. "
+    ask = "\nWhat is the secret passkey mentioned in the text above? The passkey is: "
+    n_fill = len(tokenizer.encode(filler))
+    avail = context_len - len(tokenizer.encode(needle)) - len(tokenizer.encode(ask)) - 10
+    before = int((avail * needle_depth) / n_fill)
+    after = int((avail * (1 - needle_depth)) / n_fill)
+    prompt_tokens = tokenizer.encode(filler * before + needle + filler * after + ask)[:context_len]
+    prompt = tokenizer.decode(prompt_tokens)
+
+    std_text, _ = _generate_short(model, tokenizer, prompt, max_tokens=20)
+    fov_text, _ = generate_fused(model, tokenizer, prompt, max_tokens=20, cfg=cfg, enable_promotion=True)
+    return passkey in std_text, passkey in fov_text, {
+        "passkey": passkey, "context_len": len(prompt_tokens), "needle_depth": needle_depth,
+        "standard_output": std_text, "foveated_output": fov_text,
+    }

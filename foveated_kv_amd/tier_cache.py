@@ -22,6 +22,11 @@ import torch.nn.functional as F
 
 from . import ext
 
+# Bound at import: the decode closure (foveated_kv_amd.generate) replaces
+# torch.nn.functional.scaled_dot_product_attention while installed, and the
+# formulation below must keep calling the real function.
+_sdpa = F.scaled_dot_product_attention
+
 
 # ---------------------------------------------------------------------------
 # codecs used by the formulation (reference semantics, device torch ops)
@@ -229,7 +234,7 @@ class FoveatedLayer:
             all_k = all_k.repeat_interleave(hq // hkv, dim=1)
             all_v = all_v.repeat_interleave(hq // hkv, dim=1)
         scale = 1.0 / math.sqrt(query.shape[-1])
-        return F.scaled_dot_product_attention(query, all_k.contiguous(), all_v.contiguous(), scale=scale)
+        return _sdpa(query, all_k.contiguous(), all_v.contiguous(), scale=scale)
 
     # ---- fused kernel ----
     def _ensure_kcache(self):
@@ -423,7 +428,7 @@ def standard_attention(query, keys, values):
     if nq != nkv:
         keys = keys.repeat_interleave(nq // nkv, dim=1)
         values = values.repeat_interleave(nq // nkv, dim=1)
-    return F.scaled_dot_product_attention(query, keys.contiguous(), values.contiguous(),
+    return _sdpa(query, keys.contiguous(), values.contiguous(),
                                           scale=1.0 / math.sqrt(query.shape[-1]))
 
 
