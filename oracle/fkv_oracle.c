@@ -25,6 +25,10 @@
  *   orc_attend_kernel       pinned: 6 legacy fixtures, fp64 brute force,
  *                           split-count invariance, spike_case fixture
  *   orc_attend_formulation  pinned: 6 legacy fixtures, brute force
+ *   orc_attend_turbo        pinned: far scores against the dequantised-key
+ *                           identities (exact reconstruction -> q.k_hat; QJL
+ *                           term = sqrt(pi/2) x the formulation's q.r_hat),
+ *                           fp64 brute force, split-count invariance
  */
 #include <math.h>
 #include <stdint.h>
@@ -547,4 +551,157 @@ ORC_API void orc_compress_foveal(const uint16_t* src, uint16_t* dst, int BH, int
             else memcpy(o, src + ((int64_t)bh * S + srct) * D, sizeof(uint16_t) * D);
         }
     }
+}
+
+/* ------------------------------------------------------------------------ */
+/* TurboQuant far tier: kernel semantics                                     */
+/* ------------------------------------------------------------------------ */
+
+/* foveated_2tier_turbo: csrc/kernels/foveated_attn.metal:559-767 with
+ * dot_turbo_k (:486-521) and load_turbo_v (:531-552); q_rot = q.Pi^T and
+ * q_sketch = q.S^T come from the host (csrc/foveated_attn.cpp:415-421) and
+ * are passed here as the caller computed them.  fp64 throughout.
+ *
+ *   q           (B,Hq,D)   fp16 bits (near / decode scores use q * rsqrt(D))
+ *   q_rot/q_sk  (B,Hq,D)   fp64
+ *   near_k/v    (B,Hkv,Npad,D) fp16 bits; near_valid (Hkv)
+ *   k_idx       (B,Hkv,F,D/4) 2-bit Lloyd-Max indices, dim 4j+i at bits 2i
+ *   k_signs     (B,Hkv,F,D/8) QJL sign bits, dim 8j+i at bit i (1 -> +1)
+ *   k_norm/k_gamma (B,Hkv,F) fp16 bits
+ *   v_packed    (B,Hkv,F,D/4) 2-bit value codes, same packing as k_idx
+ *   v_scale     (B,Hkv,F,D/32) fp16 bits, one scale per 32-dim group
+ *   centroids   (4) fp32
+ * Far score = (norm * sum q_rot*cb[idx] + (1.2533141/D) * gamma *
+ * sum(+-1)*q_sketch) * rsqrt(D); far value = level[code] * scale with
+ * levels {-1, -0.333333, 0.333333, 1}; split plan, gate, merge and spike
+ * fields as orc_attend_kernel. */
+ORC_API int orc_attend_turbo(int B, int Hq, int Hkv, int D, int Npad, int F, int n_dec,
+                             const uint16_t* q, const double* q_rot, const double* q_sk,
+                             const uint16_t* near_k, const uint16_t* near_v,
+                             const uint32_t* near_valid, const uint8_t* k_idx,
+                             const uint8_t* k_signs, const uint16_t* k_norm,
+                             const uint16_t* k_gamma, const uint8_t* v_packed,
+                             const uint16_t* v_scale, const float* centroids,
+                             const uint16_t* dec_k, const uint16_t* dec_v, float spike_margin,
+                             int split_size, int num_splits, int gate, double* out,
+                             int32_t* flags, int32_t* tokens, double* max_far_out,
+                             double* min_near_out) {
+    if (Hkv <= 0 || Hq % Hkv != 0 || D <= 0 || D % 32 != 0) return -1;
+    const int G = Hq / Hkv;
+    const int s_total = Npad + F + n_dec;
+    if (split_size <= 0 || num_splits <= 0) {
+        int plan[3];
+        orc_split_plan(s_total, plan);
+        split_size = plan[0];
+        num_splits = plan[1];
+    }
+    const float inv_sqrt_d = 1.0f / sqrtf((float)D);
+    const float qjl = 1.2533141f / (float)D;
+    const float levels[4] = {-1.0f, -0.333333f, 0.333333f, 1.0f};
+    double* qreg = (double*)malloc(sizeof(double) * D);
+    double* vv = (double*)malloc(sizeof(double) * D);
+    double* racc = (double*)malloc(sizeof(double) * D);
+    orc_state* sp = (orc_state*)malloc(sizeof(orc_state) * num_splits);
+    double* accbuf = (double*)malloc(sizeof(double) * D * num_splits);
+    if (!qreg || !vv || !racc || !sp || !accbuf) return -2;
+
+    for (int b = 0; b < B; b++) {
+        for (int hq = 0; hq < Hq; hq++) {
+            const int kvh = hq / G;
+            const int64_t bkv = (int64_t)b * Hkv + kvh;
+            const int64_t o = (int64_t)b * Hq + hq;
+            const double* qr = q_rot + o * D;
+            const double* qs = q_sk + o * D;
+            for (int d = 0; d < D; d++) qreg[d] = (double)(orc_h2f(q[o * D + d]) * inv_sqrt_d);
+            for (int s = 0; s < num_splits; s++) {
+                orc_state* st = &sp[s];
+                st->m = -INFINITY;
+                st->l = 0.0;
+                st->acc = accbuf + (int64_t)s * D;
+                for (int d = 0; d < D; d++) st->acc[d] = 0.0;
+                st->min_near = INFINITY;
+                st->max_far = -INFINITY;
+                st->far_tok = -1;
+                int g0 = s * split_size;
+                int g1 = g0 + split_size < s_total ? g0 + split_size : s_total;
+                int near0 = g0 < Npad ? g0 : Npad;
+                int near1 = g1 < Npad ? g1 : Npad;
+                int far0 = g0 > Npad ? (g0 - Npad < F ? g0 - Npad : F) : 0;
+                int far1 = g1 > Npad ? (g1 - Npad < F ? g1 - Npad : F) : 0;
+                int nf = Npad + F;
+                int dec0 = g0 > nf ? (g0 - nf < n_dec ? g0 - nf : n_dec) : 0;
+                int dec1 = g1 > nf ? (g1 - nf < n_dec ? g1 - nf : n_dec) : 0;
+                int nv = (int)near_valid[kvh];
+                int near_end = near1 < nv ? near1 : nv;
+                for (int t = near0; t < near_end; t++) {
+                    const uint16_t* kr = near_k + (bkv * Npad + t) * D;
+                    const uint16_t* vr = near_v + (bkv * Npad + t) * D;
+                    double sc = 0.0;
+                    for (int d = 0; d < D; d++) sc += qreg[d] * (double)orc_h2f(kr[d]);
+                    if (sc < st->min_near) st->min_near = sc;
+                    for (int d = 0; d < D; d++) vv[d] = orc_h2f(vr[d]);
+                    orc_accum(st, sc, vv, D);
+                }
+                for (int t = far0; t < far1; t++) {
+                    const int64_t tok = bkv * F + t;
+                    const uint8_t* ki = k_idx + tok * (D / 4);
+                    const uint8_t* ks = k_signs + tok * (D / 8);
+                    double mse = 0.0, sgn = 0.0;
+                    for (int d = 0; d < D; d++) {
+                        const int c = (ki[d >> 2] >> (2 * (d & 3))) & 3;
+                        mse += qr[d] * (double)centroids[c];
+                        sgn += ((ks[d >> 3] >> (d & 7)) & 1) ? qs[d] : -qs[d];
+                    }
+                    const double sc = ((double)orc_h2f(k_norm[tok]) * mse +
+                                       (double)qjl * (double)orc_h2f(k_gamma[tok]) * sgn) *
+                                      (double)inv_sqrt_d;
+                    if (sc > st->max_far) { st->max_far = sc; st->far_tok = t; }
+                    if (gate && sc < st->m - 16.0) continue;
+                    const uint8_t* vp = v_packed + tok * (D / 4);
+                    const uint16_t* vs = v_scale + tok * (D / 32);
+                    for (int d = 0; d < D; d++) {
+                        const int c = (vp[d >> 2] >> (2 * (d & 3))) & 3;
+                        vv[d] = (double)levels[c] * (double)orc_h2f(vs[d >> 5]);
+                    }
+                    orc_accum(st, sc, vv, D);
+                }
+                for (int t = dec0; t < dec1; t++) {
+                    const uint16_t* kr = dec_k + (bkv * n_dec + t) * D;
+                    const uint16_t* vr = dec_v + (bkv * n_dec + t) * D;
+                    double sc = 0.0;
+                    for (int d = 0; d < D; d++) sc += qreg[d] * (double)orc_h2f(kr[d]);
+                    if (sc < st->min_near) st->min_near = sc;
+                    for (int d = 0; d < D; d++) vv[d] = orc_h2f(vr[d]);
+                    orc_accum(st, sc, vv, D);
+                }
+            }
+            double mg = -INFINITY, lg = 0.0, min_near = INFINITY, max_far = -INFINITY;
+            int far_tok = -1;
+            for (int d = 0; d < D; d++) racc[d] = 0.0;
+            for (int s = 0; s < num_splits; s++) {
+                orc_state* st = &sp[s];
+                if (st->m == -INFINITY) continue;
+                double mn = mg > st->m ? mg : st->m;
+                double ag = mg > -INFINITY ? exp(mg - mn) : 0.0;
+                double as = exp(st->m - mn);
+                lg = ag * lg + as * st->l;
+                for (int d = 0; d < D; d++) racc[d] = ag * racc[d] + as * st->acc[d];
+                mg = mn;
+                if (st->min_near < min_near) min_near = st->min_near;
+                if (st->max_far > max_far) { max_far = st->max_far; far_tok = st->far_tok; }
+            }
+            double inv_l = lg > 0.0 ? 1.0 / lg : 0.0;
+            for (int d = 0; d < D; d++) out[o * D + d] = racc[d] * inv_l;
+            flags[o] = (max_far > min_near + (double)spike_margin) ? 1 : 0;
+            tokens[o] = far_tok;
+            if (max_far_out) max_far_out[o] = max_far;
+            if (min_near_out) min_near_out[o] = min_near;
+        }
+    }
+    free(qreg);
+    free(vv);
+    free(racc);
+    free(sp);
+    free(accbuf);
+    return 0;
 }
