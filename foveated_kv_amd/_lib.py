@@ -80,6 +80,10 @@ SIGNATURES = {
                                           P, P, P, P, P, P, P, P, P, P]),
     "fkv_attn_create": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P,
                                        I32, P, F32, P]),
+    "fkv_turbo_create": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P, P,
+                                        P, I32, P, P, P, P, F32, P]),
+    "fkv_turbo_compress_keys": (ctypes.c_int, [P, I32, ctypes.c_int64, I32, P, P, P, P, P, P, P, P, P]),
+    "fkv_turbo_compress_values": (ctypes.c_int, [P, I32, ctypes.c_int64, I32, P, P, P]),
     "fkv_attn_call": (ctypes.c_int, [P, P, I32, I32, P, P, I32, P, P, P, P]),
     "fkv_attn_blob_info": (ctypes.c_int, [P, ctypes.POINTER(BlobInfoC)]),
     "fkv_attn_read_near_valid": (ctypes.c_int, [P, P, P]),

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/fkv.h"
+#include "fkv_common.h"
 
 namespace fkv {
 
@@ -23,12 +24,15 @@ namespace fkv {
 //   | V: 32*D bytes of INT4 nibbles, lane l = dim 64*dh + l
 //   | SZ: 64 x u32 = fp16 scale | fp16 zero << 16 per token ]
 //   near_valid : [Hkv] u32
+// A TurboQuant blob (fmt 1) keeps the near tiers and near_valid and stores
+// the far tier as TurboQuant records instead (layout below).
 struct BlobLayout {
     int B, Hkv, D, Na, F, Na_pad, F_pad;
+    int fmt;  // 0: fp8-E4M3 K / INT4 V far records, 1: TurboQuant far records
     size_t near_k, near_v, far, far_rec, near_valid, total;
 };
 
-BlobLayout make_layout(int B, int Hkv, int D, int Na, int F);
+BlobLayout make_layout(int B, int Hkv, int D, int Na, int F, int fmt = 0);
 
 // Far records are stored tile-major across (batch, kv head) rows: record
 // (bkv, tile) sits at index tile * B*Hkv + bkv, so workgroups of different
@@ -50,6 +54,25 @@ __host__ __device__ inline int64_t near_v_index(int t, int d, int D) {
 __host__ __device__ constexpr int64_t far_v_section(int D) { return (int64_t)64 * D; }
 __host__ __device__ constexpr int64_t far_sz_section(int D) { return (int64_t)96 * D; }
 __host__ __device__ constexpr int64_t far_record_bytes(int D) { return (int64_t)96 * D + 256; }
+// TurboQuant far record (fmt 1), one per (batch, kv head, 64-token tile):
+//   [ KP: 3 bit planes x 64 tokens x D/8 bytes -- plane 0 = high bit of
+//         the 2-bit Lloyd-Max index, 1 = low bit, 2 = QJL sign; lane l =
+//         token l; dword k of a token: dims 32k+2i, 32k+2i+1 at bits
+//         15-i, 31-i
+//   | VP: per 64-dim half dh one 1 KB chunk, lane l = dim 64dh + l, four
+//         dwords [high bit own, high bit other, low bit own, low bit other]
+//         of the 2-bit value codes; "own" = the 32 tokens 32*(l/32).. of
+//         the lane's half, "other" = the other 32; tokens 2i, 2i+1 of a
+//         half at bits 15-i, 31-i
+//   | SC: [token][D/32] fp16 value-group scales
+//   | NG: [token] u32 = fp16 key norm | fp16 residual norm << 16 ]
+// Every plane bit is stored complemented (set = -1), so that
+// (w & 0x80008000) | 0x3C003C00 is the pair of +-1 fp16 operands.
+__host__ __device__ constexpr int64_t tq_vp_section(int D) { return (int64_t)24 * D; }
+__host__ __device__ constexpr int64_t tq_sc_section(int D) { return (int64_t)40 * D; }
+__host__ __device__ constexpr int64_t tq_ng_section(int D) { return (int64_t)44 * D; }
+__host__ __device__ constexpr int64_t tq_record_bytes(int D) { return (int64_t)44 * D + 256; }
+
 // Byte of the E4M3 code of (token t, dim d) inside its tile's K section.
 __host__ __device__ inline int64_t far_k_index(int t, int d) {
     return (int64_t)(d >> 4) * 1024 + (t & 63) * 16 + (d & 15);
@@ -64,5 +87,59 @@ __host__ __device__ inline void far_v_pos(int t, int d, int64_t& dword, int& bit
     dword = (int64_t)(u >> 2) * 256 + (d & 63) * 4 + (u & 3);
     bit = (sp & 1) * 8 + (e & 1) * 16 + (e >> 1) * 4;
 }
+
+// Element i of an fp16 / bf16 / fp32 array as fp16 bits (round to nearest even).
+__device__ inline uint16_t load_as_f16(const void* p, int64_t i, int dtype) {
+    if (dtype == FKV_F16) return ((const uint16_t*)p)[i];
+    if (dtype == FKV_BF16) return f2h(bf2f(((const uint16_t*)p)[i]));
+    return f2h(((const float*)p)[i]);
+}
+
+// TurboQuant constants of a handle: the 2-bit centroids written as
+// alpha + beta*sh + gamma*sl + delta*sh*sl over the +-1 index bits
+// (sh = +1 for codes 2, 3; sl = +1 for codes 1, 3), the value levels as
+// lvh*sh + lvl*sl, and the device copies of Pi^T and S^T for the query
+// rotation / sketch.
+struct TurboConsts {
+    float alpha = 0.f, beta = 0.f, gamma = 0.f, delta = 0.f, lvh = 0.f, lvl = 0.f;
+    float* PiT = nullptr;  // (D, D) fp32, PiT[j][i] = Pi[i][j]
+    float* ST = nullptr;   // (D, D) fp32, ST[j][i] = S[i][j]
+};
+
+}  // namespace fkv
+
+struct fkv_attn_impl {
+    fkv::BlobLayout L;
+    uint8_t* blob = nullptr;
+    float margin = 0.f;
+    float* ws = nullptr;  // split partials
+    size_t ws_floats = 0;
+    uint16_t* qbuf = nullptr;  // fp16 copy of non-fp16 queries
+    size_t qbuf_n = 0;
+    int* arrive = nullptr;  // per-row split arrival counters (zero between calls)
+    size_t arrive_n = 0;
+    int near_plan = 0;      // expected near tiles per row: max near_valid / 64, rounded up
+    int device = 0;
+    fkv::TurboConsts tq;    // fmt 1 only
+    uint16_t* tq_q = nullptr;  // (B, Hq, 2, D) fp16: rotated query, sketched query
+    float* tq_asum = nullptr;  // (B, Hq) alpha * sum of the rotated query
+    size_t tq_q_n = 0;
+};
+
+struct fkv_attn : fkv_attn_impl {};
+
+namespace fkv {
+
+int grid_for(int64_t n, int block);
+// Handle construction shared by the fp8 and TurboQuant formats: allocates
+// the blob (zeroed), packs the near tiers and near_valid (stream-ordered).
+int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, const void* near_k,
+               const void* near_v, int near_dtype, const int32_t* near_valid, float margin, hipStream_t st);
+// Synchronous end of construction: reads near_valid back for the split plan.
+int attn_finish(fkv_attn_impl* h, hipStream_t st);
+
+// Launches the query rotation / sketch of a TurboQuant handle for one call
+// (fkv_turbo.hip); q16 is the fp16 query (B, Hq, D).
+int tq_prepare_query(fkv_attn_impl* h, const uint16_t* q16, int Hq, hipStream_t st);
 
 }  // namespace fkv

@@ -45,8 +45,9 @@ namespace fkv {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-BlobLayout make_layout(int B, int Hkv, int D, int Na, int F) {
+BlobLayout make_layout(int B, int Hkv, int D, int Na, int F, int fmt) {
     BlobLayout L{};
+    L.fmt = fmt;
     L.B = B;
     L.Hkv = Hkv;
     L.D = D;
@@ -63,7 +64,7 @@ BlobLayout make_layout(int B, int Hkv, int D, int Na, int F) {
     };
     L.near_k = place(bkv * L.Na_pad * D * 2);
     L.near_v = place(bkv * L.Na_pad * D * 2);
-    L.far_rec = (size_t)far_record_bytes(D);
+    L.far_rec = (size_t)(fmt ? tq_record_bytes(D) : far_record_bytes(D));
     L.far = place(bkv * (L.F_pad / kTile) * L.far_rec);
     L.near_valid = place((size_t)Hkv * 4);
     L.total = off;
@@ -73,12 +74,6 @@ BlobLayout make_layout(int B, int Hkv, int D, int Na, int F) {
 // ---------------------------------------------------------------------------
 // Blob packing kernels (handle construction; csrc/foveated_attn.cpp:83-128)
 // ---------------------------------------------------------------------------
-
-__device__ inline uint16_t load_as_f16(const void* p, int64_t i, int dtype) {
-    if (dtype == FKV_F16) return ((const uint16_t*)p)[i];
-    if (dtype == FKV_BF16) return f2h(bf2f(((const uint16_t*)p)[i]));
-    return f2h(((const float*)p)[i]);
-}
 
 // One thread per (bkv, token, 16-dim block): near K and V into their tile
 // layouts (fkv_attn.h); slots >= Na are zero.
@@ -232,6 +227,12 @@ struct AttnArgs {
     float* ws;      // split partials: [row][split][ng][kHdr + D]
     int* arrive;    // [row] split arrival counters (zero between calls)
     int near_plan;  // expected near tiles per row (balances the far split)
+    // TurboQuant far tier (fmt 1)
+    const uint16_t* tq_q;   // (B, Hq, 2, D) fp16: q.Pi^T, q.S^T
+    const float* tq_asum;   // (B, Hq) alpha * sum(q.Pi^T), or null when alpha == 0
+    float tq_beta, tq_gamma, tq_delta;  // centroid coefficients (TurboConsts)
+    float tq_qjl;           // 1.2533141 / D
+    float tq_lvh, tq_lvl;   // value level coefficients
 };
 
 // v_mfma_f32_4x4x4f16: 16 independent 4x4x4 blocks; lane l supplies row /
@@ -564,6 +565,339 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
     });
 }
 
+// ---------------------------------------------------------------------------
+// TurboQuant far tiles (fmt 1): 2-bit Lloyd-Max keys + 1-bit QJL sketch,
+// 2-bit values with one fp16 scale per 32 dims
+// (csrc/kernels/foveated_attn.metal:486-767)
+// ---------------------------------------------------------------------------
+//
+// Keys: the centroid of code c is alpha + beta*sh + gamma*sl + delta*sh*sl
+// over the two +-1 index bits, so q_rot . cb[idx] is a sum of +-1 dot
+// products.  The blob holds the bits as complemented planes in which a
+// pair of tokens' bits sits at bits 15-i / 31-i of a dword: shifting by i
+// and masking with 0x80008000 | 0x3C003C00 yields the two fp16 +-1
+// operands, so each 4-dim k-step is three exact MFMAs (high bit, low bit,
+// QJL sign) against the fp16 rotated / sketched query.
+// Values: level(c) = lvh*sh + lvl*sl times the group scale.  The scale
+// differs between the two 32-dim groups of a 64-lane P.V block, so the
+// weights carry it: with cbsz = 3 the MFMA broadcasts block a's A operand
+// to blocks 0-7 and block 8+a's to blocks 8-15, i.e. lanes 0-31 (group
+// 2dh) take tokens 4a.. and lanes 32-63 (group 2dh+1) take tokens 32+4a..
+// of the lane's own half; a second pass takes the other half's tokens,
+// whose weights come across with v_permlane32_swap.  Every lane's weights
+// are therefore scaled by its own group's scale.
+
+template <int D>
+constexpr int tq_dma_ops() { return D == 128 ? 6 : 4; }
+
+// TurboQuant record -> LDS slot: the KP | VP sections (40*D bytes) as 1 KB
+// chunks (D = 64 ends with half a chunk), then SC | NG in one op.
+template <int D>
+__device__ inline void dma_tq(const AttnArgs& a, int64_t bkv, int tile, int lane, uint8_t* slot) {
+    const uint8_t* rec = a.blob + a.L.far + far_rec_index(a.L, bkv, tile) * (int64_t)a.L.far_rec;
+    constexpr int KPV = 40 * D, TAIL = 4 * D + 256;
+#pragma unroll
+    for (int c = 0; c < KPV / 1024; c++)
+        __builtin_amdgcn_global_load_lds((const void*)(rec + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
+                                         0, 2);
+    if constexpr (KPV % 1024 != 0) {
+        if (lane < (KPV % 1024) / 16)
+            __builtin_amdgcn_global_load_lds((const void*)(rec + (KPV / 1024) * 1024 + lane * 16),
+                                             (FKV_LDS void*)(slot + (KPV / 1024) * 1024), 16, 0, 2);
+    }
+    if (lane < TAIL / 16)
+        __builtin_amdgcn_global_load_lds((const void*)(rec + KPV + lane * 16), (FKV_LDS void*)(slot + KPV), 16, 0, 2);
+}
+
+// The lane's operands of a TurboQuant tile.
+template <int D>
+struct TqTile {
+    fkv_v4u kp[3];  // key planes of the lane's token (D = 64: .x/.y only)
+    fkv_v4u v[D / 64];   // value planes of dim 64dh + lane: hi own, hi other, lo own, lo other
+    fkv_v4u so[D / 64];  // group scales of the lane's 4 tokens [e][g] (fp16)
+    fkv_v4u sx[D / 64];  // ... of the other half's 4 tokens (block blk ^ 8)
+    fkv_v4u ng;          // norm | gamma << 16 of the lane's 4 tokens
+};
+
+__device__ inline void lds_tq(TqTile<128>& r, const uint8_t* slot, int lane) {
+    const int blk = lane >> 2;
+    const uint32_t a = lds_addr(slot + lane * 16);
+    const uint32_t so = lds_addr(slot + tq_sc_section(128) + blk * 32);
+    const uint32_t sx = lds_addr(slot + tq_sc_section(128) + (blk ^ 8) * 32);
+    const uint32_t ng = lds_addr(slot + tq_ng_section(128) + blk * 16);
+    asm volatile(
+        "ds_read_b128 %0, %10\n"
+        "ds_read_b128 %1, %10 offset:1024\n"
+        "ds_read_b128 %2, %10 offset:2048\n"
+        "ds_read_b128 %3, %10 offset:3072\n"
+        "ds_read_b128 %4, %10 offset:4096\n"
+        "ds_read_b128 %5, %11\n"
+        "ds_read_b128 %6, %11 offset:16\n"
+        "ds_read_b128 %7, %12\n"
+        "ds_read_b128 %8, %12 offset:16\n"
+        "ds_read_b128 %9, %13\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r.kp[0]), "=&v"(r.kp[1]), "=&v"(r.kp[2]), "=&v"(r.v[0]), "=&v"(r.v[1]), "=&v"(r.so[0]),
+          "=&v"(r.so[1]), "=&v"(r.sx[0]), "=&v"(r.sx[1]), "=&v"(r.ng)
+        : "v"(a), "v"(so), "v"(sx), "v"(ng)
+        : "memory");
+}
+
+__device__ inline void lds_tq(TqTile<64>& r, const uint8_t* slot, int lane) {
+    const int blk = lane >> 2;
+    const uint32_t a = lds_addr(slot + lane * 8);
+    const uint32_t v = lds_addr(slot + tq_vp_section(64) + lane * 16);
+    const uint32_t so = lds_addr(slot + tq_sc_section(64) + blk * 16);
+    const uint32_t sx = lds_addr(slot + tq_sc_section(64) + (blk ^ 8) * 16);
+    const uint32_t ng = lds_addr(slot + tq_ng_section(64) + blk * 16);
+    fkv_v2u k0, k1, k2;
+    asm volatile(
+        "ds_read_b64 %0, %7\n"
+        "ds_read_b64 %1, %7 offset:512\n"
+        "ds_read_b64 %2, %7 offset:1024\n"
+        "ds_read_b128 %3, %8\n"
+        "ds_read_b128 %4, %9\n"
+        "ds_read_b128 %5, %10\n"
+        "ds_read_b128 %6, %11\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k0), "=&v"(k1), "=&v"(k2), "=&v"(r.v[0]), "=&v"(r.so[0]), "=&v"(r.sx[0]), "=&v"(r.ng)
+        : "v"(a), "v"(v), "v"(so), "v"(sx), "v"(ng)
+        : "memory");
+    r.kp[0] = fkv_v4u{k0.x, k0.y, 0u, 0u};
+    r.kp[1] = fkv_v4u{k1.x, k1.y, 0u, 0u};
+    r.kp[2] = fkv_v4u{k2.x, k2.y, 0u, 0u};
+}
+
+// two +-1 fp16 values from the bits at 15 and 31 (set = -1)
+__device__ inline uint32_t pm1(uint32_t w) { return (w & 0x80008000u) | 0x3C003C00u; }
+
+// the +-1 operand of 4 consecutive dims / tokens: pairs i, i+1 of word w
+template <int I>
+__device__ inline fkv_h4 pm1x4(uint32_t w) {
+    return h4_of(pm1(w << I), pm1(w << (I + 1)));
+}
+
+// N q-operand k-steps s0.. of quad qd from an LDS operand array, one asm
+// block that waits for its own reads (see QOperand::read8).
+template <int N>
+__device__ inline void lds_q(const uint16_t* p, fkv_h4 (&o)[N]);
+template <>
+__device__ inline void lds_q<8>(const uint16_t* p, fkv_h4 (&o)[8]) {
+    const uint32_t addr = lds_addr(p);
+    fkv_v2u r0, r1, r2, r3, r4, r5, r6, r7;
+    asm volatile(
+        "ds_read_b64 %0, %8\n"
+        "ds_read_b64 %1, %8 offset:32\n"
+        "ds_read_b64 %2, %8 offset:64\n"
+        "ds_read_b64 %3, %8 offset:96\n"
+        "ds_read_b64 %4, %8 offset:128\n"
+        "ds_read_b64 %5, %8 offset:160\n"
+        "ds_read_b64 %6, %8 offset:192\n"
+        "ds_read_b64 %7, %8 offset:224\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+        : "v"(addr)
+        : "memory");
+    o[0] = __builtin_bit_cast(fkv_h4, r0); o[1] = __builtin_bit_cast(fkv_h4, r1);
+    o[2] = __builtin_bit_cast(fkv_h4, r2); o[3] = __builtin_bit_cast(fkv_h4, r3);
+    o[4] = __builtin_bit_cast(fkv_h4, r4); o[5] = __builtin_bit_cast(fkv_h4, r5);
+    o[6] = __builtin_bit_cast(fkv_h4, r6); o[7] = __builtin_bit_cast(fkv_h4, r7);
+}
+template <>
+__device__ inline void lds_q<4>(const uint16_t* p, fkv_h4 (&o)[4]) {
+    const uint32_t addr = lds_addr(p);
+    fkv_v2u r0, r1, r2, r3;
+    asm volatile(
+        "ds_read_b64 %0, %4\n"
+        "ds_read_b64 %1, %4 offset:32\n"
+        "ds_read_b64 %2, %4 offset:64\n"
+        "ds_read_b64 %3, %4 offset:96\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+        : "v"(addr)
+        : "memory");
+    o[0] = __builtin_bit_cast(fkv_h4, r0); o[1] = __builtin_bit_cast(fkv_h4, r1);
+    o[2] = __builtin_bit_cast(fkv_h4, r2); o[3] = __builtin_bit_cast(fkv_h4, r3);
+}
+template <>
+__device__ inline void lds_q<2>(const uint16_t* p, fkv_h4 (&o)[2]) {
+    const uint32_t addr = lds_addr(p);
+    fkv_v2u r0, r1;
+    asm volatile(
+        "ds_read_b64 %0, %2\n"
+        "ds_read_b64 %1, %2 offset:32\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r0), "=&v"(r1)
+        : "v"(addr)
+        : "memory");
+    o[0] = __builtin_bit_cast(fkv_h4, r0); o[1] = __builtin_bit_cast(fkv_h4, r1);
+}
+
+// Online-softmax update of head quad qd for a far tile: rescale on a new
+// maximum, then the gated weights p (the reference skips V of far tokens
+// with s < m - 16, foveated_attn.metal:713).  Returns whether any p > 0.
+template <int D, int NQ>
+__device__ inline bool tq_softmax(Lane<D, NQ>& st, int qd, const float (&s)[4], float (&p)[4]) {
+    constexpr int NH = D / 64;
+    float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+#pragma unroll
+    for (int o = 4; o <= 32; o <<= 1) cmax = fmaxf(cmax, wave_xor(cmax, o));
+    const float m_new = fmaxf(st.m[qd], cmax);
+    if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
+        const float alpha = m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f;
+        st.lsum[qd] *= alpha;
+        const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
+        const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
+#pragma unroll
+        for (int dh = 0; dh < NH; dh++) {
+            st.acc[qd][dh][0] *= a0;
+            st.acc[qd][dh][1] *= a1;
+            st.acc[qd][dh][2] *= a2;
+            st.acc[qd][dh][3] *= a3;
+        }
+        st.m[qd] = m_new;
+    }
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        p[e] = s[e] >= st.m[qd] - 16.0f ? __expf(s[e] - st.m[qd]) : 0.f;
+        st.lsum[qd] += p[e];
+        any |= p[e] > 0.f;
+    }
+    return any;
+}
+
+// v_mfma_f32_4x4x4f16 with cbsz = 3: blocks 0-7 take block A's operand,
+// blocks 8-15 take block 8+A's.
+template <int A>
+__device__ inline fkv_f4 mfma4_half(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, A, 0);
+}
+
+template <int D, int NQ, int A>
+__device__ inline void tq_pv_step(Lane<D, NQ>& st, int dh, const fkv_v4u& v, const fkv_h4 (&w)[4][NQ]) {
+    const fkv_h4 b1h = pm1x4<2 * A>(v.x), b2h = pm1x4<2 * A>(v.y);
+    const fkv_h4 b1l = pm1x4<2 * A>(v.z), b2l = pm1x4<2 * A>(v.w);
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        fkv_f4 c = st.acc[qd][dh];
+        c = mfma4_half<A>(w[0][qd], b1h, c);
+        c = mfma4_half<A>(w[1][qd], b1l, c);
+        c = mfma4_half<A>(w[2][qd], b2h, c);
+        c = mfma4_half<A>(w[3][qd], b2l, c);
+        st.acc[qd][dh] = c;
+    }
+}
+
+__device__ inline float half_of(const fkv_v4u* s, int i) {
+    const uint32_t w = s[i >> 3][(i >> 1) & 3];
+    return h2f((uint16_t)((i & 1) ? (w >> 16) : (w & 0xFFFF)));
+}
+
+// The other half's copy of v (lane l gets lane l ^ 32's value).
+__device__ inline float swap_halves(float v, int half) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(half ? r[0] : r[1]);
+}
+
+// Scores, spike tracking, softmax and P.V of one TurboQuant far tile.
+template <int D, int NQ, typename QOp>
+__device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int tile, int lane, const AttnArgs& a,
+                                      const QOp& qr, const QOp& qk, const float (&asum)[NQ]) {
+    constexpr int NS = D / 4, NH = D / 64, NG = D / 32;
+    constexpr int KS = NQ == 1 ? 8 : NQ == 2 ? 4 : 2;
+    const int blk = lane >> 2, half = lane >> 5;
+    const bool general = a.tq_delta != 0.f;
+    fkv_f4 sh[NQ], sl[NQ], sq[NQ], sx[NQ];
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) sh[qd] = sl[qd] = sq[qd] = sx[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s0 = 0; s0 < NS; s0 += KS) {
+        fkv_h4 q_r[NQ][KS], q_k[NQ][KS];
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) {
+            lds_q<KS>(qr.qs + qr.base + (qd * NS + s0) * 16, q_r[qd]);
+            lds_q<KS>(qk.qs + qk.base + (qd * NS + s0) * 16, q_k[qd]);
+        }
+#pragma unroll
+        for (int s = s0; s < s0 + KS; s++) {
+            const int k = s >> 3, i0 = 2 * (s & 7);
+            const uint32_t wh = r.kp[0][k], wl = r.kp[1][k], ws = r.kp[2][k];
+            const fkv_h4 ah = h4_of(pm1(wh << i0), pm1(wh << (i0 + 1)));
+            const fkv_h4 al = h4_of(pm1(wl << i0), pm1(wl << (i0 + 1)));
+            const fkv_h4 as = h4_of(pm1(ws << i0), pm1(ws << (i0 + 1)));
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) {
+                sh[qd] = mfma4_local(ah, q_r[qd][s - s0], sh[qd]);
+                sl[qd] = mfma4_local(al, q_r[qd][s - s0], sl[qd]);
+                sq[qd] = mfma4_local(as, q_k[qd][s - s0], sq[qd]);
+            }
+            if (general) {
+                const uint32_t wx = wh ^ wl;
+                const fkv_h4 ax = h4_of(pm1(wx << i0), pm1(wx << (i0 + 1)));
+#pragma unroll
+                for (int qd = 0; qd < NQ; qd++) sx[qd] = mfma4_local(ax, q_r[qd][s - s0], sx[qd]);
+            }
+        }
+    }
+    float p[NQ][4];
+    bool any = false;
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = tile * kTile + 4 * blk + e;
+            const uint32_t ngw = r.ng[e];
+            const float nrm = h2f((uint16_t)(ngw & 0xFFFF)), gmm = h2f((uint16_t)(ngw >> 16));
+            float mse = a.tq_beta * sh[qd][e] + a.tq_gamma * sl[qd][e] + asum[qd];
+            if (general) mse += a.tq_delta * sx[qd][e];
+            const float sv = (nrm * mse + a.tq_qjl * gmm * sq[qd][e]) * a.inv_sqrt_d;
+            const bool ok = t < a.L.F;
+            sc[e] = ok ? sv : -INFINITY;
+            if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
+        }
+        any |= tq_softmax<D, NQ>(st, qd, sc, p[qd]);
+    }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
+    float px[NQ][4];
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) px[qd][e] = swap_halves(p[qd][e], half);
+#pragma unroll
+    for (int dh = 0; dh < NH; dh++) {
+        const int g = 2 * dh + half;  // the value group of the lane's dim
+        fkv_h4 w[4][NQ];              // [hi own, lo own, hi other, lo other][qd]
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) {
+            _Float16 w0[4], w1[4], w2[4], w3[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float so = p[qd][e] * half_of(r.so, e * NG + g);
+                const float sx2 = px[qd][e] * half_of(r.sx, e * NG + g);
+                w0[e] = (_Float16)(so * a.tq_lvh);
+                w1[e] = (_Float16)(so * a.tq_lvl);
+                w2[e] = (_Float16)(sx2 * a.tq_lvh);
+                w3[e] = (_Float16)(sx2 * a.tq_lvl);
+            }
+            w[0][qd] = fkv_h4{w0[0], w0[1], w0[2], w0[3]};
+            w[1][qd] = fkv_h4{w1[0], w1[1], w1[2], w1[3]};
+            w[2][qd] = fkv_h4{w2[0], w2[1], w2[2], w2[3]};
+            w[3][qd] = fkv_h4{w3[0], w3[1], w3[2], w3[3]};
+        }
+        const fkv_v4u v = r.v[dh];
+        tq_pv_step<D, NQ, 0>(st, dh, v, w);
+        tq_pv_step<D, NQ, 1>(st, dh, v, w);
+        tq_pv_step<D, NQ, 2>(st, dh, v, w);
+        tq_pv_step<D, NQ, 3>(st, dh, v, w);
+        tq_pv_step<D, NQ, 4>(st, dh, v, w);
+        tq_pv_step<D, NQ, 5>(st, dh, v, w);
+        tq_pv_step<D, NQ, 6>(st, dh, v, w);
+        tq_pv_step<D, NQ, 7>(st, dh, v, w);
+    }
+}
+
 // Scores, min-near tracking, softmax and P.V of one fp16 tile (near slots or
 // decode rows): key operands from kop(s) (lane = token, dims 4s..4s+3),
 // value operands from vop(g, dh).
@@ -858,8 +1192,8 @@ struct Units {
 // every wave's share of far bytes covers at least one near tile (the
 // cumulative boundaries are then non-decreasing), else round-robin.
 template <int D>
-__device__ inline void plan_far(Units& un, int nt_far, int near_plan) {
-    const int64_t NB = 256 * D, FB = far_record_bytes(D), N = un.N;
+__device__ inline void plan_far(Units& un, int nt_far, int near_plan, int64_t FB) {
+    const int64_t NB = 256 * D, N = un.N;
     if ((int64_t)nt_far * FB >= N * NB) {
         const int64_t q = near_plan / N, r = near_plan % N;
         const int64_t total = near_plan * NB + (int64_t)nt_far * FB;
@@ -884,16 +1218,19 @@ __device__ inline void plan_far(Units& un, int nt_far, int near_plan) {
 // wave streams its units through a 2-slot LDS ring with gfx950's direct
 // global->LDS loads: the next unit's bytes stream in while the current one
 // is computed.  The ring takes most of the CU's LDS (one workgroup per CU).
-template <int D, int NQ>
+template <int D, int NQ, int FMT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int NS = D / 4;   // 4-dim k-steps of QK
     constexpr int NH = D / 64;  // 64-dim halves of P.V
     constexpr int RS = kHdr + D;
     constexpr int NHW = 4 * NQ;  // head records per wave
-    constexpr int REC = (int)far_record_bytes(D);
+    constexpr int REC = (int)(FMT ? tq_record_bytes(D) : far_record_bytes(D));
     constexpr int SLOT = REC > 128 * D ? REC : 128 * D;  // far record or a near K / V half
-    constexpr int FAR_OPS = far_dma_ops<D>(), NEAR_OPS = D / 8;
+    constexpr int FAR_OPS = FMT ? tq_dma_ops<D>() : far_dma_ops<D>(), NEAR_OPS = D / 8;
+    static_assert(FAR_OPS != NEAR_OPS, "the ring's vmcnt waits tell far and near units apart by op count");
     __shared__ __attribute__((aligned(16))) uint16_t qs[NQ * NS * 4 * 4];
+    // TurboQuant: rotated and sketched query operands, same layout as qs
+    __shared__ __attribute__((aligned(16))) uint16_t qt[FMT ? 2 * NQ * NS * 4 * 4 : 8];
     // The rings during the tile loop; afterwards (behind a barrier) the
     // per-wave records, then past wave 0's records the split-merge scratch
     // of the last workgroup.
@@ -920,12 +1257,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     Units un;
     un.N = kWavesPerGroup * a.num_splits;
     un.w = kWavesPerGroup * split + wave;
-    plan_far<D>(un, (int)cdiv(a.L.F, kTile), a.near_plan);
+    plan_far<D>(un, (int)cdiv(a.L.F, kTile), a.near_plan, REC);
     un.nn = 0;
     auto issue = [&](int u) {  // DMA of unit u into slot u % 2; returns its vector-memory op count
         const int kd = un.kind(u);
         uint8_t* slot = ring + (u & 1) * SLOT;
-        if (kd == kFarUnit) dma_far<D>(a, bkv, un.tile(u), lane, slot);
+        if (kd == kFarUnit) {
+            if constexpr (FMT) dma_tq<D>(a, bkv, un.tile(u), lane, slot);
+            else dma_far<D>(a, bkv, un.tile(u), lane, slot);
+        }
         else if (kd != kNone) dma_near<D>(a, bkv, un.tile(u), kd == kNearV, lane, slot);
         return kd == kNone ? 0 : kd == kFarUnit ? FAR_OPS : NEAR_OPS;
     };
@@ -937,6 +1277,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int s = sq % NS, qd = sq / NS;
         const int h = 4 * qd + jj;
         qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
+        if constexpr (FMT) {
+            const uint16_t* tq = a.tq_q + ((int64_t)b * a.Hq + head0 + h) * 2 * D + 4 * s + e;
+            qt[i] = h < ng ? tq[0] : (uint16_t)0;
+            qt[NQ * NS * 16 + i] = h < ng ? tq[D] : (uint16_t)0;
+        }
+    }
+    float asum[NQ];
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        const int h = 4 * qd + j;
+        asum[qd] = (FMT && a.tq_asum && h < ng) ? a.tq_asum[(int64_t)b * a.Hq + head0 + h] : 0.f;
     }
     const int nv = (int)((const uint32_t*)(a.blob + a.L.near_valid))[kvh];
     const int nt_near = (int)cdiv(nv, kTile);
@@ -956,6 +1307,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     // q operand reads from LDS (see QOperand)
     const QOperand<NS> qop{qs, j * 4};
+    const QOperand<NS> qrop{qt, j * 4}, qkop{qt + (FMT ? NQ * NS * 16 : 0), j * 4};
     __syncthreads();
 
     // ---- the stream: unit u is computed while unit u + 1 streams in ----
@@ -974,9 +1326,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const uint8_t* slot = ring + (u & 1) * SLOT;
         const int kd = un.kind(u), tile = un.tile(u);
         if (kd == kFarUnit) {
-            FarTile<D> r;
-            lds_far(r, slot, lane);
-            far_compute<D, NQ>(st, r, tile, a.L.F, blk, a.inv_sqrt_d, qop);
+            if constexpr (FMT) {
+                TqTile<D> r;
+                lds_tq(r, slot, lane);
+                tq_far_compute<D, NQ>(st, r, tile, lane, a, qrop, qkop, asum);
+            } else {
+                FarTile<D> r;
+                lds_far(r, slot, lane);
+                far_compute<D, NQ>(st, r, tile, a.L.F, blk, a.inv_sqrt_d, qop);
+            }
         } else if (kd == kNearK) {
             near_scores_lds<D, NQ>(sacc, slot, lane, qop);
         } else {
@@ -1229,35 +1587,21 @@ __global__ void zero_ints_kernel(int* p, int n) {
 // Host side: handle + launch
 // ---------------------------------------------------------------------------
 
-struct fkv_attn_impl {
-    fkv::BlobLayout L;
-    uint8_t* blob = nullptr;
-    float margin = 0.f;
-    float* ws = nullptr;  // split partials
-    size_t ws_floats = 0;
-    uint16_t* qbuf = nullptr;  // fp16 copy of non-fp16 queries
-    size_t qbuf_n = 0;
-    int* arrive = nullptr;  // per-row split arrival counters (zero between calls)
-    size_t arrive_n = 0;
-    int near_plan = 0;      // expected near tiles per row: max near_valid / 64, rounded up
-    int device = 0;
-};
-
 namespace fkv {
 
 typedef void (*AttnKernel)(AttnArgs);
 
-template <int D>
+template <int D, int FMT>
 static AttnKernel pick_attn(int nq) {
     switch (nq) {
-        case 1: return attn_kernel<D, 1>;
-        case 2: return attn_kernel<D, 2>;
-        case 3: return attn_kernel<D, 3>;
-        default: return attn_kernel<D, 4>;
+        case 1: return attn_kernel<D, 1, FMT>;
+        case 2: return attn_kernel<D, 2, FMT>;
+        case 3: return attn_kernel<D, 3, FMT>;
+        default: return attn_kernel<D, 4, FMT>;
     }
 }
 
-static int grid_for(int64_t n, int block) {
+int grid_for(int64_t n, int block) {
     int64_t g = cdiv(n, block);
     if (g < 1) g = 1;
     if (g > 65536) g = 65536;
@@ -1286,9 +1630,40 @@ int plan_splits(const BlobLayout& L, int rows, int n_dec) {
 using fkv::check_hip;
 using fkv::set_error;
 
-extern "C" {
+namespace fkv {
 
-struct fkv_attn : fkv_attn_impl {};
+int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, const void* near_k,
+               const void* near_v, int near_dtype, const int32_t* near_valid, float margin, hipStream_t st) {
+    h->L = make_layout(B, Hkv, D, Na, F, fmt);
+    h->margin = margin;
+    int rc = check_hip(hipGetDevice(&h->device), "hipGetDevice");
+    if (!rc) rc = check_hip(hipMalloc(&h->blob, h->L.total), "hipMalloc(blob)");
+    if (!rc) rc = check_hip(hipMemsetAsync(h->blob, 0, h->L.total, st), "hipMemsetAsync(blob)");
+    if (rc) return rc;
+    const int blk = 256;
+    const BlobLayout L = h->L;
+    if (Na > 0)
+        hipLaunchKernelGGL(pack_near_kernel, dim3(grid_for((int64_t)B * Hkv * L.Na_pad * (D / 16), blk)), dim3(blk),
+                           0, st, near_k, near_v, near_dtype, L, h->blob);
+    hipLaunchKernelGGL(pack_valid_kernel, dim3(1), dim3(blk), 0, st, near_valid, Hkv, L, h->blob);
+    return check_hip(hipGetLastError(), "pack kernels");
+}
+
+int attn_finish(fkv_attn_impl* h, hipStream_t st) {
+    std::vector<uint32_t> nv_h(h->L.Hkv, 0);
+    int rc = check_hip(hipMemcpyAsync(nv_h.data(), h->blob + h->L.near_valid, h->L.Hkv * sizeof(uint32_t),
+                                      hipMemcpyDeviceToHost, st), "hipMemcpyAsync(near_valid)");
+    if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
+    if (rc) return rc;
+    uint32_t mx = 0;
+    for (uint32_t v : nv_h) mx = v > mx ? v : mx;
+    h->near_plan = (int)cdiv(mx, kTile);
+    return FKV_OK;
+}
+
+}  // namespace fkv
+
+extern "C" {
 
 int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
                     const void* near_k, const void* near_v, int32_t near_dtype,
@@ -1308,41 +1683,22 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
         return set_error("fkv_attn_create: NULL tier array");
     hipStream_t st = (hipStream_t)stream;
     fkv_attn* h = new fkv_attn();
-    h->L = fkv::make_layout(B, Hkv, D, Na, F);
-    h->margin = spike_margin;
-    int rc = check_hip(hipGetDevice(&h->device), "hipGetDevice");
     unsigned* bad = nullptr;
-    if (!rc) rc = check_hip(hipMalloc(&h->blob, h->L.total), "hipMalloc(blob)");
+    int rc = fkv::attn_begin(h, B, Hkv, D, Na, F, 0, near_k, near_v, near_dtype, near_valid, spike_margin, st);
     if (!rc) rc = check_hip(hipMalloc(&bad, sizeof(unsigned)), "hipMalloc(flag)");
     if (!rc) rc = check_hip(hipMemsetAsync(bad, 0, sizeof(unsigned), st), "hipMemsetAsync");
-    if (!rc) rc = check_hip(hipMemsetAsync(h->blob, 0, h->L.total, st), "hipMemsetAsync(blob)");
-    if (!rc) {
+    if (!rc && F > 0) {
         const int blk = 256;
         const fkv::BlobLayout L = h->L;
-        if (Na > 0)
-            hipLaunchKernelGGL(fkv::pack_near_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.Na_pad * (D / 16), blk)),
-                               dim3(blk), 0, st, near_k, near_v, near_dtype, L, h->blob);
-        if (F > 0) {
-            hipLaunchKernelGGL(fkv::pack_far_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 16), blk)),
-                               dim3(blk), 0, st, far_k, L, h->blob, bad);
-            hipLaunchKernelGGL(fkv::pack_far_v_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 8), blk)),
-                               dim3(blk), 0, st, far_v, far_v_scale, far_v_zero, sz_dtype, L, h->blob);
-        }
-        hipLaunchKernelGGL(fkv::pack_valid_kernel, dim3(1), dim3(blk), 0, st, near_valid, Hkv, L, h->blob);
-        rc = check_hip(hipGetLastError(), "pack kernels");
+        hipLaunchKernelGGL(fkv::pack_far_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 16), blk)),
+                           dim3(blk), 0, st, far_k, L, h->blob, bad);
+        hipLaunchKernelGGL(fkv::pack_far_v_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 8), blk)),
+                           dim3(blk), 0, st, far_v, far_v_scale, far_v_zero, sz_dtype, L, h->blob);
+        rc = check_hip(hipGetLastError(), "far pack kernels");
     }
     unsigned bad_h = 0;
-    std::vector<uint32_t> nv_h(Hkv, 0);
     if (!rc) rc = check_hip(hipMemcpyAsync(&bad_h, bad, sizeof(unsigned), hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
-    if (!rc)
-        rc = check_hip(hipMemcpyAsync(nv_h.data(), h->blob + h->L.near_valid, Hkv * sizeof(uint32_t),
-                                      hipMemcpyDeviceToHost, st), "hipMemcpyAsync(near_valid)");
-    if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
-    if (!rc) {
-        uint32_t mx = 0;
-        for (uint32_t v : nv_h) mx = v > mx ? v : mx;
-        h->near_plan = (int)fkv::cdiv(mx, fkv::kTile);
-    }
+    if (!rc) rc = fkv::attn_finish(h, st);
     if (bad) (void)hipFree(bad);
     if (!rc && bad_h) {
         set_error("fkv_attn_create: far_k holds E4M3 NaN codes 0x7F/0xFF, which the reference encoder never emits");
@@ -1427,8 +1783,22 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
     a.arrive = fused_merge ? h->arrive : nullptr;
     a.near_plan = h->near_plan;
     const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
+    a.tq_q = nullptr;
+    a.tq_asum = nullptr;
+    a.tq_beta = h->tq.beta;
+    a.tq_gamma = h->tq.gamma;
+    a.tq_delta = h->tq.delta;
+    a.tq_qjl = 1.2533141f / (float)L.D;
+    a.tq_lvh = h->tq.lvh;
+    a.tq_lvl = h->tq.lvl;
+    if (L.fmt == 1) {
+        if (int rc = fkv::tq_prepare_query(h, q16, Hq, st)) return rc;
+        a.tq_q = h->tq_q;
+        a.tq_asum = h->tq.alpha != 0.f ? h->tq_asum : nullptr;
+    }
     const int nq = (ng_max + 3) / 4;
-    fkv::AttnKernel k = L.D == 128 ? fkv::pick_attn<128>(nq) : fkv::pick_attn<64>(nq);
+    fkv::AttnKernel k = L.fmt == 1 ? (L.D == 128 ? fkv::pick_attn<128, 1>(nq) : fkv::pick_attn<64, 1>(nq))
+                                   : (L.D == 128 ? fkv::pick_attn<128, 0>(nq) : fkv::pick_attn<64, 0>(nq));
     hipLaunchKernelGGL(k, grid, block, 0, st, a);
     if (splits > 1 && !fused_merge) {
         const dim3 mgrid(rows, ng_max);
@@ -1500,6 +1870,10 @@ void fkv_attn_destroy(fkv_attn* h) {
     if (h->ws) (void)hipFree(h->ws);
     if (h->qbuf) (void)hipFree(h->qbuf);
     if (h->arrive) (void)hipFree(h->arrive);
+    if (h->tq.PiT) (void)hipFree(h->tq.PiT);
+    if (h->tq.ST) (void)hipFree(h->tq.ST);
+    if (h->tq_q) (void)hipFree(h->tq_q);
+    if (h->tq_asum) (void)hipFree(h->tq_asum);
     delete h;
 }
 

@@ -106,7 +106,45 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
                     const void* far_v_zero, int32_t sz_dtype, const int32_t* near_valid,
                     float spike_margin, void* stream);
 
-/* Replaces FoveatedHandle::operator() (:164-240): query (B,Hq,1,D) in
+/* TurboQuant handle: replaces TurboFoveatedHandle's constructor
+ * (csrc/foveated_attn.cpp:365-405, blob builder :306-363).  Same near
+ * tier and near_valid as fkv_attn_create; the far tier is
+ *   k_idx   (B,Hkv,F,D/4) u8  2-bit Lloyd-Max indices, dim 4j+i at bits 2i
+ *   k_signs (B,Hkv,F,D/8) u8  QJL sign bits, dim 8j+i at bit i (1 = +1)
+ *   k_norm, k_gamma (B,Hkv,F) in nz_dtype (stored as fp16)
+ *   v_packed (B,Hkv,F,D/4) u8 2-bit value codes, packed like k_idx
+ *   v_scale (B,Hkv,F,D/32) in nz_dtype (stored as fp16)
+ * Pi, S (D,D) and centroids (4) are fp32 device arrays (the rotation, the
+ * QJL matrix and the Lloyd-Max centroids); the handle keeps its own
+ * copies.  The returned handle is called, queried and destroyed with the
+ * fkv_attn_* functions; each call first rotates and sketches the query
+ * (q.Pi^T, q.S^T, foveated_attn.cpp:415-421).  Synchronous. */
+int fkv_turbo_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
+                     const void* near_k, const void* near_v, int32_t near_dtype, const uint8_t* k_idx,
+                     const uint8_t* k_signs, const void* k_norm, const void* k_gamma, const uint8_t* v_packed,
+                     const void* v_scale, int32_t nz_dtype, const int32_t* near_valid, const float* Pi,
+                     const float* S, const float* centroids, float spike_margin, void* stream);
+
+/* TurboQuant compression on the GPU (src/foveated_kv/turbo_quantize.py:
+ * 25-91): keys (n_tokens, D) in dtype -> out_idx (n_tokens, D/4) u8,
+ * out_signs (n_tokens, D/8) u8, out_norm / out_gamma (n_tokens) fp16;
+ * Pi, S (D,D), centroids (4), boundaries (3) fp32 device arrays.  fp32
+ * arithmetic; a code whose rotated coordinate lies within fp32 rounding of
+ * a boundary (or a sign whose projection lies within rounding of 0) can
+ * differ from another fp32 evaluation order.  Synchronous (reads the
+ * centroids). */
+int fkv_turbo_compress_keys(const void* keys, int32_t dtype, int64_t n_tokens, int32_t D, const float* Pi,
+                            const float* S, const float* centroids, const float* boundaries, uint8_t* out_idx,
+                            uint8_t* out_signs, void* out_norm, void* out_gamma, void* stream);
+
+/* turbo_compress_values (turbo_quantize.py:139-178): values (n_tokens, D)
+ * -> out_packed (n_tokens, D/4) u8 2-bit codes, out_scale (n_tokens, D/32)
+ * fp16, one scale per 32 dims; codes round half to even.  Asynchronous. */
+int fkv_turbo_compress_values(const void* values, int32_t dtype, int64_t n_tokens, int32_t D, uint8_t* out_packed,
+                              void* out_scale, void* stream);
+
+/* Replaces FoveatedHandle::operator() (:164-240) and, for a TurboQuant
+ * handle, TurboFoveatedHandle::operator() (:407-491): query (B,Hq,1,D) in
  * q_dtype, decode_k/v (B,Hkv,n_decode,D) fp16 (NULL when n_decode == 0).
  * Writes out (B,Hq,D) fp16, spike_flags/spike_tokens (B,Hq) int32. */
 int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
