@@ -44,6 +44,14 @@ def algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec):
     return B * Hkv * per_head + 2 * B * Hq * D * 2 + B * Hq * 8 + Hkv * 4
 
 
+def algorithmic_bytes_turbo(B, Hq, Hkv, D, R, F, n_dec):
+    """As algorithmic_bytes with the TurboQuant far tier: 2-bit key indices,
+    1-bit QJL signs, fp16 norm + gamma, 2-bit values, one fp16 scale per 32
+    dims."""
+    per_head = R * D * 4 + F * (D // 4 + D // 8 + 4 + D // 4 + 2 * (D // 32)) + n_dec * D * 4
+    return B * Hkv * per_head + 2 * B * Hq * D * 2 + B * Hq * 8 + Hkv * 4
+
+
 def read_traffic(path):
     """Per-launch HBM traffic from a committed rocprofv3 --pmc summary:
     lines 'fetch_bytes_per_launch: N' / 'write_bytes_per_launch: N'."""
@@ -63,20 +71,28 @@ def read_traffic(path):
     return None
 
 
-def cpu_baseline(c, q, dk, dv, D, sample_b=1):
-    """Oracle formulation (dequant + concat + SDPA, fp64 softmax, OpenMP over
-    (b, q head)) on the first ``sample_b`` batch rows of one layer."""
+def cpu_baseline(c, q, dk, dv, D, sample_b=1, turbo=None):
+    """Oracle formulation (dequant + concat + SDPA, fp64 softmax; OpenMP over
+    (b, q head) for the fp8 tier, numpy for TurboQuant) on the first
+    ``sample_b`` batch rows of one layer."""
     import oracle
+    from oracle import turbo as oturbo
 
     sl = slice(0, sample_b)
-    args = [q[sl], c["near_k"][sl], c["near_v"][sl], c["near_valid"], c["far_k"][sl], c["far_v"][sl],
-            c["far_v_scale"][sl], c["far_v_zero"][sl], dk[sl] if dk is not None else None,
-            dv[sl] if dv is not None else None]
-    oracle.attend_formulation(*args)  # warm (page-in)
+    if turbo is not None:
+        args = [q[sl], c["near_k"][sl], c["near_v"][sl], c["near_valid"]] + [t[sl] for t in turbo["far"]] + [
+            turbo["C"], dk[sl] if dk is not None else None, dv[sl] if dv is not None else None]
+        fn = oturbo.attend_formulation
+    else:
+        args = [q[sl], c["near_k"][sl], c["near_v"][sl], c["near_valid"], c["far_k"][sl], c["far_v"][sl],
+                c["far_v_scale"][sl], c["far_v_zero"][sl], dk[sl] if dk is not None else None,
+                dv[sl] if dv is not None else None]
+        fn = oracle.attend_formulation
+    fn(*args)  # warm (page-in)
     reps = 0
     t0 = time.perf_counter()
     while True:
-        oracle.attend_formulation(*args)
+        fn(*args)
         reps += 1
         if time.perf_counter() - t0 >= 10.0 or reps >= 20:
             break
@@ -132,21 +148,35 @@ def main():
     q = synthetic.make_query(B, Hq, D, args.seed)
     synthetic.inject_spikes(k, q, tb["mid_start"], F, args.spikes, args.seed)
     dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, args.seed)
+    turbo = args.config.startswith("c4_turbo")
     kt = torch.from_numpy(k).to(dev)
     vt = torch.from_numpy(v).to(dev)
-    cl = ext.CompressHandle(cfg).compress_layer(kt, vt, with_archive=False)
+    cl = ext.CompressHandle(cfg).compress_layer(kt, vt, with_archive=turbo)
     del kt, vt
+    if turbo:
+        from foveated_kv_amd import turbo as tq
+
+        tc = tq.get_turbo_constants(D)
+        tfar = tq.turbo_compress_keys(cl.archive_k, tc) + tq.turbo_compress_values(cl.archive_v)
+        cl.archive_k = cl.archive_v = None
+
+        def make_handle():
+            return tq.TurboFoveatedHandle(cl.near_k, cl.near_v, *tfar, cl.near_valid, tc.Pi, tc.S, tc.centroids,
+                                          spike_margin=10.0)
+    else:
+        def make_handle():
+            return ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                                      cl.near_valid, spike_margin=10.0)
     qt = torch.from_numpy(q).to(dev)[:, :, None, :]
     dkt = torch.from_numpy(dk).to(dev) if dk is not None else None
     dvt = torch.from_numpy(dv).to(dev) if dv is not None else None
 
-    nbytes = algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec)
+    nbytes = (algorithmic_bytes_turbo if turbo else algorithmic_bytes)(B, Hq, Hkv, D, R, F, n_dec)
     blob_bytes = None
     handles = []
     L = args.layers
     while True:
-        h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
-                               cl.near_valid, spike_margin=10.0)
+        h = make_handle()
         handles.append(h)
         blob_bytes = h.get_blob_info().blob_bytes
         if (L and len(handles) >= L) or (not L and len(handles) * blob_bytes > (1 << 30) and len(handles) >= 4):
@@ -214,7 +244,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": args.config, "B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S,
                    "near_valid": R, "far": F, "n_decode": n_dec, "layers_per_step": L,
-                   "spike_frac": args.spikes, "far_format": "fp8-e4m3 K + int4 per-token V"},
+                   "spike_frac": args.spikes,
+                   "far_format": ("turboquant 2-bit K + 1-bit QJL, 2-bit V group-32" if turbo
+                                  else "fp8-e4m3 K + int4 per-token V")},
         "us_per_layer": round(us_layer, 3),
         "launch": "eager" if args.eager else "hip-graph",
         "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
@@ -226,14 +258,20 @@ def main():
     if not args.no_cpu_baseline:
         c = {n: getattr(cl, n).cpu().numpy() for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale",
                                                         "far_v_zero", "near_valid")}
-        dt, reps = cpu_baseline(c, q, dk, dv, D, sample_b=1)
-        sample_bytes = algorithmic_bytes(1, Hq, Hkv, D, R, F, n_dec)
+        tb_ = None
+        if turbo:
+            from oracle import turbo as oturbo
+
+            tb_ = {"far": [t.cpu().numpy() for t in tfar], "C": oturbo.constants(D)}
+        dt, reps = cpu_baseline(c, q, dk, dv, D, sample_b=1, turbo=tb_)
+        sample_bytes = (algorithmic_bytes_turbo if turbo else algorithmic_bytes)(1, Hq, Hkv, D, R, F, n_dec)
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         result["cpu_baseline"] = {
             "value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "us_per_layer": round(dt * 1e6 * B, 1),
-            "sample": f"oracle dequant+SDPA formulation (fp64 softmax, OpenMP over (b, q head)) on batch row 0 "
-                      f"of 1 layer of {args.config}, {reps} reps; us_per_layer scaled x{B} to the full batch",
+            "sample": f"oracle dequant+SDPA formulation (fp64 softmax{', numpy' if turbo else ', OpenMP over (b, q head)'}) "
+                      f"on batch row 0 of 1 layer of {args.config}, {reps} reps; us_per_layer scaled x{B} to the "
+                      f"full batch",
         }
     if args.copy_mib:
         result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)

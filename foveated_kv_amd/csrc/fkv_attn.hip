@@ -668,13 +668,27 @@ __device__ inline void lds_tq(TqTile<64>& r, const uint8_t* slot, int lane) {
     r.kp[2] = fkv_v4u{k2.x, k2.y, 0u, 0u};
 }
 
+// Bit-select constants held in registers: with the mask and the fp16 +1
+// pair opaque to constant folding the compiler selects one v_bfi_b32 per
+// word (gfx9 VOP3 takes no literals, so folded constants cost an AND and
+// an OR).  The empty asm emits no instruction.
+struct PmConst {
+    uint32_t m, c;
+    __device__ static PmConst make() {
+        PmConst k{0x80008000u, 0x3C003C00u};
+        asm volatile("" : "+s"(k.m));
+        asm volatile("" : "+v"(k.c));
+        return k;
+    }
+};
+
 // two +-1 fp16 values from the bits at 15 and 31 (set = -1)
-__device__ inline uint32_t pm1(uint32_t w) { return (w & 0x80008000u) | 0x3C003C00u; }
+__device__ inline uint32_t pm1(uint32_t w, const PmConst& k) { return (w & k.m) | (k.c & ~k.m); }
 
 // the +-1 operand of 4 consecutive dims / tokens: pairs i, i+1 of word w
 template <int I>
-__device__ inline fkv_h4 pm1x4(uint32_t w) {
-    return h4_of(pm1(w << I), pm1(w << (I + 1)));
+__device__ inline fkv_h4 pm1x4(uint32_t w, const PmConst& k) {
+    return h4_of(pm1(w << I, k), pm1(w << (I + 1), k));
 }
 
 // N q-operand k-steps s0.. of quad qd from an LDS operand array, one asm
@@ -774,18 +788,20 @@ __device__ inline fkv_f4 mfma4_half(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
     return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, A, 0);
 }
 
-template <int D, int NQ, int A>
-__device__ inline void tq_pv_step(Lane<D, NQ>& st, int dh, const fkv_v4u& v, const fkv_h4 (&w)[4][NQ]) {
-    const fkv_h4 b1h = pm1x4<2 * A>(v.x), b2h = pm1x4<2 * A>(v.y);
-    const fkv_h4 b1l = pm1x4<2 * A>(v.z), b2l = pm1x4<2 * A>(v.w);
+// Step A of the P.V of one tile: 4 MFMAs per head quad into two partial
+// sums (own-half and other-half tokens) so consecutive MFMAs do not wait
+// on each other.
+template <int NQ, int A>
+__device__ inline void tq_pv_step(fkv_f4 (&po)[NQ], fkv_f4 (&px)[NQ], const fkv_v4u& v, const fkv_h4 (&w)[4][NQ],
+                                  const PmConst& k) {
+    const fkv_h4 b1h = pm1x4<2 * A>(v.x, k), b2h = pm1x4<2 * A>(v.y, k);
+    const fkv_h4 b1l = pm1x4<2 * A>(v.z, k), b2l = pm1x4<2 * A>(v.w, k);
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
-        fkv_f4 c = st.acc[qd][dh];
-        c = mfma4_half<A>(w[0][qd], b1h, c);
-        c = mfma4_half<A>(w[1][qd], b1l, c);
-        c = mfma4_half<A>(w[2][qd], b2h, c);
-        c = mfma4_half<A>(w[3][qd], b2l, c);
-        st.acc[qd][dh] = c;
+        po[qd] = mfma4_half<A>(w[0][qd], b1h, po[qd]);
+        px[qd] = mfma4_half<A>(w[2][qd], b2h, px[qd]);
+        po[qd] = mfma4_half<A>(w[1][qd], b1l, po[qd]);
+        px[qd] = mfma4_half<A>(w[3][qd], b2l, px[qd]);
     }
 }
 
@@ -808,6 +824,7 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
     constexpr int KS = NQ == 1 ? 8 : NQ == 2 ? 4 : 2;
     const int blk = lane >> 2, half = lane >> 5;
     const bool general = a.tq_delta != 0.f;
+    const PmConst pk = PmConst::make();
     fkv_f4 sh[NQ], sl[NQ], sq[NQ], sx[NQ];
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) sh[qd] = sl[qd] = sq[qd] = sx[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
@@ -823,9 +840,9 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
         for (int s = s0; s < s0 + KS; s++) {
             const int k = s >> 3, i0 = 2 * (s & 7);
             const uint32_t wh = r.kp[0][k], wl = r.kp[1][k], ws = r.kp[2][k];
-            const fkv_h4 ah = h4_of(pm1(wh << i0), pm1(wh << (i0 + 1)));
-            const fkv_h4 al = h4_of(pm1(wl << i0), pm1(wl << (i0 + 1)));
-            const fkv_h4 as = h4_of(pm1(ws << i0), pm1(ws << (i0 + 1)));
+            const fkv_h4 ah = h4_of(pm1(wh << i0, pk), pm1(wh << (i0 + 1), pk));
+            const fkv_h4 al = h4_of(pm1(wl << i0, pk), pm1(wl << (i0 + 1), pk));
+            const fkv_h4 as = h4_of(pm1(ws << i0, pk), pm1(ws << (i0 + 1), pk));
 #pragma unroll
             for (int qd = 0; qd < NQ; qd++) {
                 sh[qd] = mfma4_local(ah, q_r[qd][s - s0], sh[qd]);
@@ -834,7 +851,7 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
             }
             if (general) {
                 const uint32_t wx = wh ^ wl;
-                const fkv_h4 ax = h4_of(pm1(wx << i0), pm1(wx << (i0 + 1)));
+                const fkv_h4 ax = h4_of(pm1(wx << i0, pk), pm1(wx << (i0 + 1), pk));
 #pragma unroll
                 for (int qd = 0; qd < NQ; qd++) sx[qd] = mfma4_local(ax, q_r[qd][s - s0], sx[qd]);
             }
@@ -887,14 +904,19 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
             w[3][qd] = fkv_h4{w3[0], w3[1], w3[2], w3[3]};
         }
         const fkv_v4u v = r.v[dh];
-        tq_pv_step<D, NQ, 0>(st, dh, v, w);
-        tq_pv_step<D, NQ, 1>(st, dh, v, w);
-        tq_pv_step<D, NQ, 2>(st, dh, v, w);
-        tq_pv_step<D, NQ, 3>(st, dh, v, w);
-        tq_pv_step<D, NQ, 4>(st, dh, v, w);
-        tq_pv_step<D, NQ, 5>(st, dh, v, w);
-        tq_pv_step<D, NQ, 6>(st, dh, v, w);
-        tq_pv_step<D, NQ, 7>(st, dh, v, w);
+        fkv_f4 po[NQ], pxs[NQ];
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) po[qd] = pxs[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+        tq_pv_step<NQ, 0>(po, pxs, v, w, pk);
+        tq_pv_step<NQ, 1>(po, pxs, v, w, pk);
+        tq_pv_step<NQ, 2>(po, pxs, v, w, pk);
+        tq_pv_step<NQ, 3>(po, pxs, v, w, pk);
+        tq_pv_step<NQ, 4>(po, pxs, v, w, pk);
+        tq_pv_step<NQ, 5>(po, pxs, v, w, pk);
+        tq_pv_step<NQ, 6>(po, pxs, v, w, pk);
+        tq_pv_step<NQ, 7>(po, pxs, v, w, pk);
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) st.acc[qd][dh] += po[qd] + pxs[qd];
     }
 }
 
