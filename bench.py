@@ -36,11 +36,12 @@ METRIC = "decode-attn µs/layer + achieved HBM GB/s (% peak), 7B shapes 16K ctx,
 PEAK_GBS = 8000.0
 
 
-def algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec):
+def algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec, v_group=0):
     """Bytes one layer-call must move: near (valid) fp16 K+V, far fp8 K +
-    INT4 V + fp16 scale/zero, decode fp16 K+V, fp16 q in / out, flags and
-    tokens, near_valid."""
-    per_head = R * D * 4 + F * (D + D // 2 + 4) + n_dec * D * 4
+    INT4 V + fp16 scale/zero (one pair per token, or per 32-dim group with
+    v_group = 32), decode fp16 K+V, fp16 q in / out, flags and tokens,
+    near_valid."""
+    per_head = R * D * 4 + F * (D + D // 2 + 4 * (D // v_group if v_group else 1)) + n_dec * D * 4
     return B * Hkv * per_head + 2 * B * Hq * D * 2 + B * Hq * 8 + Hkv * 4
 
 
@@ -108,6 +109,8 @@ def main():
     ap.add_argument("--config", default="c3_7b_16k_b8")
     ap.add_argument("--layers", type=int, default=0, help="distinct layer blobs (0: enough for > 1 GB)")
     ap.add_argument("--spikes", type=float, default=0.02)
+    ap.add_argument("--v-group", type=int, default=0, choices=(0, 32),
+                    help="fp8 far tier V: INT4 scale/zero per token (0) or per 32-dim group (32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "attn_c3_16k_b8_traffic.txt"))
     ap.add_argument("--seed", type=int, default=1234)
@@ -139,6 +142,8 @@ def main():
     B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[args.config]
     cfg = ext.TierConfig()
     cfg.promo_headroom_min = 8
+    turbo = args.config.startswith("c4_turbo")
+    cfg.v_group = 0 if turbo else args.v_group
     tb = ext.tier_boundaries_c(cfg, S)
     R, F = tb["R_actual"], tb["far_count"]
 
@@ -148,7 +153,6 @@ def main():
     q = synthetic.make_query(B, Hq, D, args.seed)
     synthetic.inject_spikes(k, q, tb["mid_start"], F, args.spikes, args.seed)
     dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, args.seed)
-    turbo = args.config.startswith("c4_turbo")
     kt = torch.from_numpy(k).to(dev)
     vt = torch.from_numpy(v).to(dev)
     cl = ext.CompressHandle(cfg).compress_layer(kt, vt, with_archive=turbo)
@@ -171,7 +175,8 @@ def main():
     dkt = torch.from_numpy(dk).to(dev) if dk is not None else None
     dvt = torch.from_numpy(dv).to(dev) if dv is not None else None
 
-    nbytes = (algorithmic_bytes_turbo if turbo else algorithmic_bytes)(B, Hq, Hkv, D, R, F, n_dec)
+    nbytes = (algorithmic_bytes_turbo(B, Hq, Hkv, D, R, F, n_dec) if turbo
+              else algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec, cfg.v_group))
     blob_bytes = None
     handles = []
     L = args.layers
@@ -246,12 +251,13 @@ def main():
                    "near_valid": R, "far": F, "n_decode": n_dec, "layers_per_step": L,
                    "spike_frac": args.spikes,
                    "far_format": ("turboquant 2-bit K + 1-bit QJL, 2-bit V group-32" if turbo
+                                  else "fp8-e4m3 K + int4 group-32 V" if cfg.v_group
                                   else "fp8-e4m3 K + int4 per-token V")},
         "us_per_layer": round(us_layer, 3),
         "launch": "eager" if args.eager else "hip-graph",
         "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
     }
-    traffic = read_traffic(args.traffic) if args.config == "c3_7b_16k_b8" else None
+    traffic = read_traffic(args.traffic) if args.config == "c3_7b_16k_b8" and not cfg.v_group else None
     result["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_GBS, "unit": "GB/s",
                           "frac": round(gbs / PEAK_GBS, 4), "traffic": traffic,
                           "algorithmic_bytes": nbytes}
@@ -264,7 +270,8 @@ def main():
 
             tb_ = {"far": [t.cpu().numpy() for t in tfar], "C": oturbo.constants(D)}
         dt, reps = cpu_baseline(c, q, dk, dv, D, sample_b=1, turbo=tb_)
-        sample_bytes = (algorithmic_bytes_turbo if turbo else algorithmic_bytes)(1, Hq, Hkv, D, R, F, n_dec)
+        sample_bytes = (algorithmic_bytes_turbo(1, Hq, Hkv, D, R, F, n_dec) if turbo
+                        else algorithmic_bytes(1, Hq, Hkv, D, R, F, n_dec, cfg.v_group))
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         result["cpu_baseline"] = {
             "value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",

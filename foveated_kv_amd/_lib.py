@@ -43,6 +43,7 @@ class TierConfigC(ctypes.Structure):
         ("window_size", ctypes.c_int32),
         ("promo_headroom_pct", ctypes.c_double),
         ("promo_headroom_min", ctypes.c_int32),
+        ("v_group", ctypes.c_int32),
     ]
 
 
@@ -80,6 +81,8 @@ SIGNATURES = {
                                           P, P, P, P, P, P, P, P, P, P]),
     "fkv_attn_create": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P,
                                        I32, P, F32, P]),
+    "fkv_attn_create_g32": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P,
+                                           I32, P, F32, P]),
     "fkv_turbo_create": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P, P,
                                         P, I32, P, P, P, P, F32, P]),
     "fkv_turbo_compress_keys": (ctypes.c_int, [P, I32, ctypes.c_int64, I32, P, P, P, P, P, P, P, P, P]),

@@ -28,7 +28,7 @@ namespace fkv {
 // the far tier as TurboQuant records instead (layout below).
 struct BlobLayout {
     int B, Hkv, D, Na, F, Na_pad, F_pad;
-    int fmt;  // 0: fp8-E4M3 K / INT4 V far records, 1: TurboQuant far records
+    int fmt;  // 0: fp8-E4M3 K / INT4 V far records, 1: TurboQuant, 2: fp8 K / group-32 INT4 V
     size_t near_k, near_v, far, far_rec, near_valid, total;
 };
 
@@ -72,6 +72,15 @@ __host__ __device__ constexpr int64_t tq_vp_section(int D) { return (int64_t)24 
 __host__ __device__ constexpr int64_t tq_sc_section(int D) { return (int64_t)40 * D; }
 __host__ __device__ constexpr int64_t tq_ng_section(int D) { return (int64_t)44 * D; }
 __host__ __device__ constexpr int64_t tq_record_bytes(int D) { return (int64_t)44 * D + 256; }
+
+// fp8 K + group-32 INT4 V far record (fmt 2): the fmt-0 K section, then
+//   | V: per 64-dim half dh two 1 KB chunks (own, other), lane l = dim
+//        64dh + l, 16 bytes = the nibbles of the 32 tokens of one half of
+//        the tile ("own" = tokens 32*(l/32).., "other" = the other 32) in
+//        the fmt-0 dword arrangement (dword u: 4-token groups 2u and 2u+1)
+//   | SZ: [token][D/32] u32 = fp16 scale | fp16 zero << 16 of each group ]
+__host__ __device__ constexpr int64_t g32_sz_section(int D) { return (int64_t)96 * D; }
+__host__ __device__ constexpr int64_t g32_record_bytes(int D) { return (int64_t)104 * D; }
 
 // Byte of the E4M3 code of (token t, dim d) inside its tile's K section.
 __host__ __device__ inline int64_t far_k_index(int t, int d) {

@@ -64,7 +64,7 @@ BlobLayout make_layout(int B, int Hkv, int D, int Na, int F, int fmt) {
     };
     L.near_k = place(bkv * L.Na_pad * D * 2);
     L.near_v = place(bkv * L.Na_pad * D * 2);
-    L.far_rec = (size_t)(fmt ? tq_record_bytes(D) : far_record_bytes(D));
+    L.far_rec = (size_t)(fmt == 1 ? tq_record_bytes(D) : fmt == 2 ? g32_record_bytes(D) : far_record_bytes(D));
     L.far = place(bkv * (L.F_pad / kTile) * L.far_rec);
     L.near_valid = place((size_t)Hkv * 4);
     L.total = off;
@@ -167,6 +167,55 @@ __global__ void pack_far_v_kernel(const uint8_t* __restrict__ fv, const void* __
         }
         ((uint32_t*)(blob + L.far + far_rec_index(L, bkv, t / kTile) * (int64_t)L.far_rec +
                      far_sz_section(D)))[t % kTile] = sz;
+    }
+}
+
+// Group-32 far V (fmt 2): one thread per output dword of the V section
+// (chunk c = 2*dh + half-select, lane, word u), and per token the group
+// scale | zero words.
+__global__ void pack_far_v_g32_kernel(const uint8_t* __restrict__ fv, const void* __restrict__ fvs,
+                                      const void* __restrict__ fvz, int sz_dtype, BlobLayout L,
+                                      uint8_t* __restrict__ blob) {
+    const int D = L.D, NG = D / 32;
+    const int64_t words_per_tile = (int64_t)8 * D;  // 32*D bytes of nibbles
+    const int64_t nt = L.F_pad / kTile;
+    const int64_t n = (int64_t)L.B * L.Hkv * nt * words_per_tile;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int rem = (int)(i % words_per_tile);
+        const int64_t r = i / words_per_tile;
+        const int tile = (int)(r % nt);
+        const int64_t bkv = r / nt;
+        const int c = rem / 256, lane = (rem % 256) / 4, u = rem % 4;
+        const int dh = c >> 1, other = c & 1;
+        const int d = dh * 64 + lane;
+        const int half = lane >> 5;
+        const int base = 32 * (other ? 1 - half : half);
+        uint32_t word = 0;
+        for (int bp = 0; bp < 2; bp++)
+            for (int e = 0; e < 4; e++) {
+                const int t = tile * kTile + base + (2 * u + bp) * 4 + e;
+                uint32_t code = 0;
+                if (t < L.F) code = (fv[(bkv * L.F + t) * (D / 2) + d / 2] >> (4 * (d & 1))) & 15u;
+                word |= code << (bp * 8 + (e & 1) * 16 + (e >> 1) * 4);
+            }
+        ((uint32_t*)(blob + L.far + far_rec_index(L, bkv, tile) * (int64_t)L.far_rec + far_v_section(D)))[rem] = word;
+    }
+    const int64_t ntok = (int64_t)L.B * L.Hkv * L.F_pad;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < ntok;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int t = (int)(i % L.F_pad);
+        const int64_t bkv = i / L.F_pad;
+        uint32_t* sz = (uint32_t*)(blob + L.far + far_rec_index(L, bkv, t / kTile) * (int64_t)L.far_rec +
+                                   g32_sz_section(D)) + (t % kTile) * NG;
+        for (int g = 0; g < NG; g++) {
+            uint32_t w = 0;
+            if (t < L.F) {
+                const int64_t k = (bkv * L.F + t) * NG + g;
+                w = (uint32_t)load_as_f16(fvs, k, sz_dtype) | ((uint32_t)load_as_f16(fvz, k, sz_dtype) << 16);
+            }
+            sz[g] = w;
+        }
     }
 }
 
@@ -331,10 +380,34 @@ struct QOperand {
 template <int D, int NQ>
 struct Lane {
     // per head quad: this lane tracks head 4*qd + (lane % 4)
-    float m[NQ], lsum[NQ], zsum[NQ], wsum[NQ], mn[NQ], mx[NQ];
+    float m[NQ], lsum[NQ], mn[NQ], mx[NQ];
+    // INT4 zero-point terms (per token V: index 0; group-32 V: [dh] for the
+    // group of the lane's own half, [D/64 + dh] for the other half's group)
+    float zsum[NQ][D / 32], wsum[NQ][D / 32];
     int arg[NQ];
     fkv_f4 acc[NQ][D / 64];  // acc[qd][dh][i] = O[head 4qd+i][dim 64dh + lane]
 };
+
+// Rescale head quad qd's running state by alpha (the lane's head's factor;
+// the accumulators of head i of the quad take lane i's factor).
+template <int D, int NQ>
+__device__ inline void rescale(Lane<D, NQ>& st, int qd, float alpha) {
+    st.lsum[qd] *= alpha;
+#pragma unroll
+    for (int z = 0; z < D / 32; z++) {
+        st.zsum[qd][z] *= alpha;
+        st.wsum[qd][z] *= alpha;
+    }
+    const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
+    const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
+#pragma unroll
+    for (int dh = 0; dh < D / 64; dh++) {
+        st.acc[qd][dh][0] *= a0;
+        st.acc[qd][dh][1] *= a1;
+        st.acc[qd][dh][2] *= a2;
+        st.acc[qd][dh][3] *= a3;
+    }
+}
 
 // One 64-token far tile as loaded from the blob: E4M3 keys (lane = token,
 // 16 codes per chunk), INT4 values (lane = dim), per-token scale|zero of the
@@ -474,25 +547,12 @@ __device__ inline void pv_all(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vop) 
 template <int D, int NQ, bool FAR>
 __device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], const uint32_t (&sz)[4],
                                  fkv_h4& w4) {
-    constexpr int NH = D / 64;
     float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
 #pragma unroll
     for (int o = 4; o <= 32; o <<= 1) cmax = fmaxf(cmax, wave_xor(cmax, o));
     const float m_new = fmaxf(st.m[qd], cmax);
     if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
-        const float alpha = m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f;
-        st.lsum[qd] *= alpha;
-        st.zsum[qd] *= alpha;
-        st.wsum[qd] *= alpha;
-        const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
-        const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
-#pragma unroll
-        for (int dh = 0; dh < NH; dh++) {
-            st.acc[qd][dh][0] *= a0;
-            st.acc[qd][dh][1] *= a1;
-            st.acc[qd][dh][2] *= a2;
-            st.acc[qd][dh][3] *= a3;
-        }
+        rescale<D, NQ>(st, qd, m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f);
         st.m[qd] = m_new;
     }
     _Float16 wh[4];
@@ -511,8 +571,8 @@ __device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], c
             const float vz = h2f((uint16_t)(sz[e] >> 16));
             wh[e] = (_Float16)(p * vs);
             // value = vs*(c - 7.5) + (vz + 7.5*vs); the MFMA sees wh*(16 + c)
-            st.zsum[qd] += p * (vz + 7.5f * vs);
-            st.wsum[qd] += (float)wh[e];
+            st.zsum[qd][0] += p * (vz + 7.5f * vs);
+            st.wsum[qd][0] += (float)wh[e];
         } else {
             wh[e] = (_Float16)p;
         }
@@ -752,23 +812,12 @@ __device__ inline void lds_q<2>(const uint16_t* p, fkv_h4 (&o)[2]) {
 // with s < m - 16, foveated_attn.metal:713).  Returns whether any p > 0.
 template <int D, int NQ>
 __device__ inline bool tq_softmax(Lane<D, NQ>& st, int qd, const float (&s)[4], float (&p)[4]) {
-    constexpr int NH = D / 64;
     float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
 #pragma unroll
     for (int o = 4; o <= 32; o <<= 1) cmax = fmaxf(cmax, wave_xor(cmax, o));
     const float m_new = fmaxf(st.m[qd], cmax);
     if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
-        const float alpha = m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f;
-        st.lsum[qd] *= alpha;
-        const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
-        const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
-#pragma unroll
-        for (int dh = 0; dh < NH; dh++) {
-            st.acc[qd][dh][0] *= a0;
-            st.acc[qd][dh][1] *= a1;
-            st.acc[qd][dh][2] *= a2;
-            st.acc[qd][dh][3] *= a3;
-        }
+        rescale<D, NQ>(st, qd, m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f);
         st.m[qd] = m_new;
     }
     bool any = false;
@@ -917,6 +966,203 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
         tq_pv_step<NQ, 7>(po, pxs, v, w, pk);
 #pragma unroll
         for (int qd = 0; qd < NQ; qd++) st.acc[qd][dh] += po[qd] + pxs[qd];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp8 K + group-32 INT4 V far tiles (fmt 2)
+// ---------------------------------------------------------------------------
+//
+// Scores as fmt 0.  The value scale / zero change every 32 dims, i.e.
+// between the two 32-lane halves of a P.V block, so the scale rides on the
+// weights exactly as in the TurboQuant tile: v_mfma_f32_4x4x4_16b_f16 with
+// cbsz = 3 gives lanes 0-31 block a's weights (tokens 4a.. of the lanes'
+// own half) and lanes 32-63 block 8+a's; a second MFMA takes the other
+// half's tokens, whose weights (scaled by this half's group) come across
+// with v_permlane32_swap.  The zero point and the +16 decode offset are
+// summed per (head, group) and added when the records are written.
+
+template <int D>
+constexpr int g32_dma_ops() { return D == 128 ? 13 : 7; }
+
+template <int D>
+__device__ inline void dma_g32(const AttnArgs& a, int64_t bkv, int tile, int lane, uint8_t* slot) {
+    const uint8_t* rec = a.blob + a.L.far + far_rec_index(a.L, bkv, tile) * (int64_t)a.L.far_rec;
+#pragma unroll
+    for (int c = 0; c < 3 * D / 32; c++)
+        __builtin_amdgcn_global_load_lds((const void*)(rec + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
+                                         0, 2);
+    if (lane < 8 * D / 16)
+        __builtin_amdgcn_global_load_lds((const void*)(rec + g32_sz_section(D) + lane * 16),
+                                         (FKV_LDS void*)(slot + g32_sz_section(D)), 16, 0, 2);
+}
+
+template <int D>
+struct FarTileG {
+    uint4 k[D / 16];
+    uint4 v[D / 32];   // chunk 2*dh + o: o = 0 own half's tokens, 1 the other half's
+    uint4 sz[D / 32];  // scale | zero of the lane's 4 tokens, [e][group]
+};
+
+__device__ inline void lds_g32(FarTileG<128>& r, const uint8_t* slot, int lane) {
+    const uint32_t a = lds_addr(slot + lane * 16), z = lds_addr(slot + g32_sz_section(128) + (lane >> 2) * 64);
+    fkv_v4u c[12], zz[4];
+    asm volatile(
+        "ds_read_b128 %0, %16\n"
+        "ds_read_b128 %1, %16 offset:1024\n"
+        "ds_read_b128 %2, %16 offset:2048\n"
+        "ds_read_b128 %3, %16 offset:3072\n"
+        "ds_read_b128 %4, %16 offset:4096\n"
+        "ds_read_b128 %5, %16 offset:5120\n"
+        "ds_read_b128 %6, %16 offset:6144\n"
+        "ds_read_b128 %7, %16 offset:7168\n"
+        "ds_read_b128 %8, %16 offset:8192\n"
+        "ds_read_b128 %9, %16 offset:9216\n"
+        "ds_read_b128 %10, %16 offset:10240\n"
+        "ds_read_b128 %11, %16 offset:11264\n"
+        "ds_read_b128 %12, %17\n"
+        "ds_read_b128 %13, %17 offset:16\n"
+        "ds_read_b128 %14, %17 offset:32\n"
+        "ds_read_b128 %15, %17 offset:48\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(c[4]), "=&v"(c[5]), "=&v"(c[6]), "=&v"(c[7]),
+          "=&v"(c[8]), "=&v"(c[9]), "=&v"(c[10]), "=&v"(c[11]), "=&v"(zz[0]), "=&v"(zz[1]), "=&v"(zz[2]),
+          "=&v"(zz[3])
+        : "v"(a), "v"(z)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.k[i] = u4_of(c[i]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.v[i] = u4_of(c[8 + i]);
+        r.sz[i] = u4_of(zz[i]);
+    }
+}
+
+__device__ inline void lds_g32(FarTileG<64>& r, const uint8_t* slot, int lane) {
+    const uint32_t a = lds_addr(slot + lane * 16), z = lds_addr(slot + g32_sz_section(64) + (lane >> 2) * 32);
+    fkv_v4u c[6], zz[2];
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:1024\n"
+        "ds_read_b128 %2, %8 offset:2048\n"
+        "ds_read_b128 %3, %8 offset:3072\n"
+        "ds_read_b128 %4, %8 offset:4096\n"
+        "ds_read_b128 %5, %8 offset:5120\n"
+        "ds_read_b128 %6, %9\n"
+        "ds_read_b128 %7, %9 offset:16\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(c[4]), "=&v"(c[5]), "=&v"(zz[0]), "=&v"(zz[1])
+        : "v"(a), "v"(z)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.k[i] = u4_of(c[i]);
+    r.v[0] = u4_of(c[4]);
+    r.v[1] = u4_of(c[5]);
+    r.sz[0] = u4_of(zz[0]);
+    r.sz[1] = u4_of(zz[1]);
+}
+
+// scale | zero word of group g of the lane's token e
+__device__ inline uint32_t g32_sz(const uint4* sz, int ng, int e, int g) {
+    const int i = e * ng + g;
+    return word_of(sz[i >> 2], i & 3);
+}
+
+template <int NQ, int A>
+__device__ inline void g32_pv_step(fkv_f4& acc0, fkv_f4& acc1, int qd, const uint4 (&v)[4], const fkv_h4& w1a,
+                                   const fkv_h4& w2a, const fkv_h4& w1b, const fkv_h4& w2b, bool two) {
+    // dh = 0 (chunks 0, 1) and, for D = 128, dh = 1 (chunks 2, 3)
+    acc0 = mfma4_half<A>(w1a, int4x4(word_of(v[0], A >> 1), A & 1), acc0);
+    if (two) acc1 = mfma4_half<A>(w1b, int4x4(word_of(v[2], A >> 1), A & 1), acc1);
+    acc0 = mfma4_half<A>(w2a, int4x4(word_of(v[1], A >> 1), A & 1), acc0);
+    if (two) acc1 = mfma4_half<A>(w2b, int4x4(word_of(v[3], A >> 1), A & 1), acc1);
+}
+
+// Scores, spike tracking, softmax and P.V of one group-32 far tile.
+template <int D, int NQ, typename QOp>
+__device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, int tile, int F, int lane,
+                                       float inv_sqrt_d, const QOp& q_lds) {
+    constexpr int NS = D / 4, NH = D / 64, NG = D / 32;
+    const int blk = lane >> 2, half = lane >> 5;
+    fkv_f4 sacc[NQ];
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s0 = 0; s0 < NS; s0 += 8) {
+        fkv_h4 q8[NQ][8];
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+#pragma unroll
+        for (int s = s0; s < s0 + 8; s++) {
+            const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k4, q8[qd][s - s0], sacc[qd]);
+        }
+    }
+    float p[NQ][4];
+    bool any = false;
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = tile * kTile + 4 * blk + e;
+            const float sv = sacc[qd][e] * inv_sqrt_d;
+            const bool ok = t < F;
+            sc[e] = ok ? sv : -INFINITY;
+            if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
+        }
+        any |= tq_softmax<D, NQ>(st, qd, sc, p[qd]);
+    }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
+    // weights: [dh] own-half group (w1) and other-half group before the swap (w2)
+    fkv_h4 w1[NH][NQ], w2[NH][NQ];
+#pragma unroll
+    for (int dh = 0; dh < NH; dh++) {
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) {
+            _Float16 a1[4], a2[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // group 2dh + half (own) and 2dh + 1 - half (other), selected
+                // without a dynamic register index
+                const uint32_t za = g32_sz(r.sz, NG, e, 2 * dh), zb = g32_sz(r.sz, NG, e, 2 * dh + 1);
+                const uint32_t z1 = half ? zb : za, z2 = half ? za : zb;
+                const float s1 = h2f((uint16_t)(z1 & 0xFFFF)), o1 = h2f((uint16_t)(z1 >> 16));
+                const float s2 = h2f((uint16_t)(z2 & 0xFFFF)), o2 = h2f((uint16_t)(z2 >> 16));
+                a1[e] = (_Float16)(p[qd][e] * s1);
+                a2[e] = (_Float16)(p[qd][e] * s2);
+                // value = s*(c - 7.5) + (z + 7.5*s); the MFMA sees w*(16 + c)
+                st.zsum[qd][dh] += p[qd][e] * (o1 + 7.5f * s1);
+                st.wsum[qd][dh] += (float)a1[e];
+                st.zsum[qd][NH + dh] += p[qd][e] * (o2 + 7.5f * s2);
+                st.wsum[qd][NH + dh] += (float)a2[e];
+            }
+            w1[dh][qd] = fkv_h4{a1[0], a1[1], a1[2], a1[3]};
+            const uint2 x = __builtin_bit_cast(uint2, fkv_h4{a2[0], a2[1], a2[2], a2[3]});
+            const uint2 y = make_uint2(__float_as_uint(swap_halves(__uint_as_float(x.x), half)),
+                                       __float_as_uint(swap_halves(__uint_as_float(x.y), half)));
+            w2[dh][qd] = __builtin_bit_cast(fkv_h4, y);
+        }
+    }
+    uint4 v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) v4[i] = r.v[i < NG ? i : 0];
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) {
+        fkv_f4 a0 = st.acc[qd][0], a1 = st.acc[qd][NH - 1];
+        const fkv_h4 w1b = w1[NH - 1][qd], w2b = w2[NH - 1][qd];
+        g32_pv_step<NQ, 0>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        g32_pv_step<NQ, 1>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        g32_pv_step<NQ, 2>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        g32_pv_step<NQ, 3>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        g32_pv_step<NQ, 4>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        g32_pv_step<NQ, 5>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        g32_pv_step<NQ, 6>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        g32_pv_step<NQ, 7>(a0, a1, qd, v4, w1[0][qd], w2[0][qd], w1b, w2b, NH == 2);
+        st.acc[qd][0] = a0;
+        if (NH == 2) st.acc[qd][NH - 1] = a1;
     }
 }
 
@@ -1246,13 +1492,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int NH = D / 64;  // 64-dim halves of P.V
     constexpr int RS = kHdr + D;
     constexpr int NHW = 4 * NQ;  // head records per wave
-    constexpr int REC = (int)(FMT ? tq_record_bytes(D) : far_record_bytes(D));
+    constexpr bool TQ = FMT == 1, G32 = FMT == 2;
+    constexpr int REC = (int)(TQ ? tq_record_bytes(D) : G32 ? g32_record_bytes(D) : far_record_bytes(D));
     constexpr int SLOT = REC > 128 * D ? REC : 128 * D;  // far record or a near K / V half
-    constexpr int FAR_OPS = FMT ? tq_dma_ops<D>() : far_dma_ops<D>(), NEAR_OPS = D / 8;
+    constexpr int FAR_OPS = TQ ? tq_dma_ops<D>() : G32 ? g32_dma_ops<D>() : far_dma_ops<D>(), NEAR_OPS = D / 8;
     static_assert(FAR_OPS != NEAR_OPS, "the ring's vmcnt waits tell far and near units apart by op count");
     __shared__ __attribute__((aligned(16))) uint16_t qs[NQ * NS * 4 * 4];
     // TurboQuant: rotated and sketched query operands, same layout as qs
-    __shared__ __attribute__((aligned(16))) uint16_t qt[FMT ? 2 * NQ * NS * 4 * 4 : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t qt[TQ ? 2 * NQ * NS * 4 * 4 : 8];
     // The rings during the tile loop; afterwards (behind a barrier) the
     // per-wave records, then past wave 0's records the split-merge scratch
     // of the last workgroup.
@@ -1285,7 +1532,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int kd = un.kind(u);
         uint8_t* slot = ring + (u & 1) * SLOT;
         if (kd == kFarUnit) {
-            if constexpr (FMT) dma_tq<D>(a, bkv, un.tile(u), lane, slot);
+            if constexpr (TQ) dma_tq<D>(a, bkv, un.tile(u), lane, slot);
+            else if constexpr (G32) dma_g32<D>(a, bkv, un.tile(u), lane, slot);
             else dma_far<D>(a, bkv, un.tile(u), lane, slot);
         }
         else if (kd != kNone) dma_near<D>(a, bkv, un.tile(u), kd == kNearV, lane, slot);
@@ -1299,7 +1547,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int s = sq % NS, qd = sq / NS;
         const int h = 4 * qd + jj;
         qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
-        if constexpr (FMT) {
+        if constexpr (TQ) {
             const uint16_t* tq = a.tq_q + ((int64_t)b * a.Hq + head0 + h) * 2 * D + 4 * s + e;
             qt[i] = h < ng ? tq[0] : (uint16_t)0;
             qt[NQ * NS * 16 + i] = h < ng ? tq[D] : (uint16_t)0;
@@ -1309,7 +1557,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         const int h = 4 * qd + j;
-        asum[qd] = (FMT && a.tq_asum && h < ng) ? a.tq_asum[(int64_t)b * a.Hq + head0 + h] : 0.f;
+        asum[qd] = (TQ && a.tq_asum && h < ng) ? a.tq_asum[(int64_t)b * a.Hq + head0 + h] : 0.f;
     }
     const int nv = (int)((const uint32_t*)(a.blob + a.L.near_valid))[kvh];
     const int nt_near = (int)cdiv(nv, kTile);
@@ -1320,7 +1568,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         st.m[qd] = -INFINITY;
-        st.lsum[qd] = st.zsum[qd] = st.wsum[qd] = 0.f;
+        st.lsum[qd] = 0.f;
+#pragma unroll
+        for (int z = 0; z < D / 32; z++) st.zsum[qd][z] = st.wsum[qd][z] = 0.f;
         st.mn[qd] = INFINITY;
         st.mx[qd] = -INFINITY;
         st.arg[qd] = INT_MAX;
@@ -1329,7 +1579,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     // q operand reads from LDS (see QOperand)
     const QOperand<NS> qop{qs, j * 4};
-    const QOperand<NS> qrop{qt, j * 4}, qkop{qt + (FMT ? NQ * NS * 16 : 0), j * 4};
+    const QOperand<NS> qrop{qt, j * 4}, qkop{qt + (TQ ? NQ * NS * 16 : 0), j * 4};
     __syncthreads();
 
     // ---- the stream: unit u is computed while unit u + 1 streams in ----
@@ -1348,10 +1598,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const uint8_t* slot = ring + (u & 1) * SLOT;
         const int kd = un.kind(u), tile = un.tile(u);
         if (kd == kFarUnit) {
-            if constexpr (FMT) {
+            if constexpr (TQ) {
                 TqTile<D> r;
                 lds_tq(r, slot, lane);
                 tq_far_compute<D, NQ>(st, r, tile, lane, a, qrop, qkop, asum);
+            } else if constexpr (G32) {
+                FarTileG<D> r;
+                lds_g32(r, slot, lane);
+                g32_far_compute<D, NQ>(st, r, tile, a.L.F, lane, a.inv_sqrt_d, qop);
             } else {
                 FarTile<D> r;
                 lds_far(r, slot, lane);
@@ -1375,20 +1629,47 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     float* wr = smem + wave * NHW * RS;
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
-        float l = st.lsum[qd], z = st.zsum[qd], ws = st.wsum[qd], mn = st.mn[qd], mx = st.mx[qd];
+        float l = st.lsum[qd], mn = st.mn[qd], mx = st.mx[qd];
         int arg = st.arg[qd];
 #pragma unroll
         for (int o = 4; o <= 32; o <<= 1) {
             l += wave_xor(l, o);
-            z += wave_xor(z, o);
-            ws += wave_xor(ws, o);
             mn = fminf(mn, wave_xor(mn, o));
             const float ox = wave_xor(mx, o);
             const int oa = wave_xor(arg, o);
             if (ox > mx || (ox == mx && oa < arg)) { mx = ox; arg = oa; }
         }
-        z -= 23.5f * ws;  // remove the +16 INT4 decode offset and the 7.5 centring
-        const float z0 = quad_bcast<0>(z), z1 = quad_bcast<1>(z), z2 = quad_bcast<2>(z), z3 = quad_bcast<3>(z);
+        // INT4 correction of head j (per 64-dim half dh): minus the +16
+        // decode offset and the 7.5 centring, plus the zero points.
+        // Group-32 V: the lane's dims are group 2dh + half; its own half's
+        // tokens reduce over the 16 lanes of the head in this half, the
+        // other half's tokens come across from the other half's lanes.
+        float corr[NH];
+        if constexpr (G32) {
+            const int half = lane >> 5;
+#pragma unroll
+            for (int dh = 0; dh < NH; dh++) {
+                float zo = st.zsum[qd][dh], wo = st.wsum[qd][dh];
+                float zx = st.zsum[qd][NH + dh], wx = st.wsum[qd][NH + dh];
+#pragma unroll
+                for (int o = 4; o <= 16; o <<= 1) {
+                    zo += wave_xor(zo, o);
+                    wo += wave_xor(wo, o);
+                    zx += wave_xor(zx, o);
+                    wx += wave_xor(wx, o);
+                }
+                corr[dh] = (zo - 23.5f * wo) + swap_halves(zx - 23.5f * wx, half);
+            }
+        } else {
+            float z = st.zsum[qd][0], ws = st.wsum[qd][0];
+#pragma unroll
+            for (int o = 4; o <= 32; o <<= 1) {
+                z += wave_xor(z, o);
+                ws += wave_xor(ws, o);
+            }
+#pragma unroll
+            for (int dh = 0; dh < NH; dh++) corr[dh] = z - 23.5f * ws;
+        }
         const int h = 4 * qd + j;
         if (lane < 4 && h < ng) {
             wr[h * RS + 0] = st.m[qd];
@@ -1397,13 +1678,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             wr[h * RS + 3] = mx;
             wr[h * RS + 4] = __int_as_float(arg);
         }
-        const float zz[4] = {z0, z1, z2, z3};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (4 * qd + i < ng) {
+        for (int dh = 0; dh < NH; dh++) {
+            const float zz[4] = {quad_bcast<0>(corr[dh]), quad_bcast<1>(corr[dh]), quad_bcast<2>(corr[dh]),
+                                 quad_bcast<3>(corr[dh])};
 #pragma unroll
-                for (int dh = 0; dh < NH; dh++) wr[(4 * qd + i) * RS + kHdr + 64 * dh + lane] = st.acc[qd][dh][i] + zz[i];
-            }
+            for (int i = 0; i < 4; i++)
+                if (4 * qd + i < ng) wr[(4 * qd + i) * RS + kHdr + 64 * dh + lane] = st.acc[qd][dh][i] + zz[i];
         }
     }
     __syncthreads();
@@ -1685,28 +1966,29 @@ int attn_finish(fkv_attn_impl* h, hipStream_t st) {
 
 }  // namespace fkv
 
-extern "C" {
+namespace {
 
-int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
-                    const void* near_k, const void* near_v, int32_t near_dtype,
-                    const uint8_t* far_k, const uint8_t* far_v, const void* far_v_scale,
-                    const void* far_v_zero, int32_t sz_dtype, const int32_t* near_valid,
-                    float spike_margin, void* stream) {
-    if (!out) return set_error("fkv_attn_create: out is NULL");
+// fp8 K far tier with per-token (fmt 0) or group-32 (fmt 2) INT4 V.
+int create_fp8(const char* fn, int fmt, fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
+               const void* near_k, const void* near_v, int32_t near_dtype, const uint8_t* far_k,
+               const uint8_t* far_v, const void* far_v_scale, const void* far_v_zero, int32_t sz_dtype,
+               const int32_t* near_valid, float spike_margin, void* stream) {
+    const std::string name(fn);
+    if (!out) return set_error(name + ": out is NULL");
     *out = nullptr;
     if (B <= 0 || Hkv <= 0 || Na < 0 || F < 0)
-        return set_error("fkv_attn_create: bad shape B=" + std::to_string(B) + " Hkv=" +
-                         std::to_string(Hkv) + " Na=" + std::to_string(Na) + " F=" + std::to_string(F));
-    if (D != 64 && D != 128) return set_error("fkv_attn_create: head dim must be 64 or 128, got " + std::to_string(D));
+        return set_error(name + ": bad shape B=" + std::to_string(B) + " Hkv=" + std::to_string(Hkv) +
+                         " Na=" + std::to_string(Na) + " F=" + std::to_string(F));
+    if (D != 64 && D != 128) return set_error(name + ": head dim must be 64 or 128, got " + std::to_string(D));
     if (near_dtype < FKV_F16 || near_dtype > FKV_F32 || sz_dtype < FKV_F16 || sz_dtype > FKV_F32)
-        return set_error("fkv_attn_create: unsupported dtype");
+        return set_error(name + ": unsupported dtype");
     if ((Na > 0 && (!near_k || !near_v)) || (F > 0 && (!far_k || !far_v || !far_v_scale || !far_v_zero)) ||
         !near_valid)
-        return set_error("fkv_attn_create: NULL tier array");
+        return set_error(name + ": NULL tier array");
     hipStream_t st = (hipStream_t)stream;
     fkv_attn* h = new fkv_attn();
     unsigned* bad = nullptr;
-    int rc = fkv::attn_begin(h, B, Hkv, D, Na, F, 0, near_k, near_v, near_dtype, near_valid, spike_margin, st);
+    int rc = fkv::attn_begin(h, B, Hkv, D, Na, F, fmt, near_k, near_v, near_dtype, near_valid, spike_margin, st);
     if (!rc) rc = check_hip(hipMalloc(&bad, sizeof(unsigned)), "hipMalloc(flag)");
     if (!rc) rc = check_hip(hipMemsetAsync(bad, 0, sizeof(unsigned), st), "hipMemsetAsync");
     if (!rc && F > 0) {
@@ -1714,8 +1996,14 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
         const fkv::BlobLayout L = h->L;
         hipLaunchKernelGGL(fkv::pack_far_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 16), blk)),
                            dim3(blk), 0, st, far_k, L, h->blob, bad);
-        hipLaunchKernelGGL(fkv::pack_far_v_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 8), blk)),
-                           dim3(blk), 0, st, far_v, far_v_scale, far_v_zero, sz_dtype, L, h->blob);
+        if (fmt == 2)
+            hipLaunchKernelGGL(fkv::pack_far_v_g32_kernel,
+                               dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 8), blk)), dim3(blk), 0, st,
+                               far_v, far_v_scale, far_v_zero, sz_dtype, L, h->blob);
+        else
+            hipLaunchKernelGGL(fkv::pack_far_v_kernel,
+                               dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 8), blk)), dim3(blk), 0, st,
+                               far_v, far_v_scale, far_v_zero, sz_dtype, L, h->blob);
         rc = check_hip(hipGetLastError(), "far pack kernels");
     }
     unsigned bad_h = 0;
@@ -1723,7 +2011,7 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
     if (!rc) rc = fkv::attn_finish(h, st);
     if (bad) (void)hipFree(bad);
     if (!rc && bad_h) {
-        set_error("fkv_attn_create: far_k holds E4M3 NaN codes 0x7F/0xFF, which the reference encoder never emits");
+        set_error(name + ": far_k holds E4M3 NaN codes 0x7F/0xFF, which the reference encoder never emits");
         rc = FKV_EDATA;
     }
     if (rc) {
@@ -1732,6 +2020,28 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
     }
     *out = h;
     return FKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
+                    const void* near_k, const void* near_v, int32_t near_dtype,
+                    const uint8_t* far_k, const uint8_t* far_v, const void* far_v_scale,
+                    const void* far_v_zero, int32_t sz_dtype, const int32_t* near_valid,
+                    float spike_margin, void* stream) {
+    return create_fp8("fkv_attn_create", 0, out, B, Hkv, D, Na, F, near_k, near_v, near_dtype, far_k, far_v,
+                      far_v_scale, far_v_zero, sz_dtype, near_valid, spike_margin, stream);
+}
+
+int fkv_attn_create_g32(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
+                        const void* near_k, const void* near_v, int32_t near_dtype,
+                        const uint8_t* far_k, const uint8_t* far_v, const void* far_v_scale,
+                        const void* far_v_zero, int32_t sz_dtype, const int32_t* near_valid,
+                        float spike_margin, void* stream) {
+    return create_fp8("fkv_attn_create_g32", 2, out, B, Hkv, D, Na, F, near_k, near_v, near_dtype, far_k, far_v,
+                      far_v_scale, far_v_zero, sz_dtype, near_valid, spike_margin, stream);
 }
 
 int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
@@ -1819,8 +2129,9 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
         a.tq_asum = h->tq.alpha != 0.f ? h->tq_asum : nullptr;
     }
     const int nq = (ng_max + 3) / 4;
-    fkv::AttnKernel k = L.fmt == 1 ? (L.D == 128 ? fkv::pick_attn<128, 1>(nq) : fkv::pick_attn<64, 1>(nq))
-                                   : (L.D == 128 ? fkv::pick_attn<128, 0>(nq) : fkv::pick_attn<64, 0>(nq));
+    fkv::AttnKernel k = L.fmt == 1   ? (L.D == 128 ? fkv::pick_attn<128, 1>(nq) : fkv::pick_attn<64, 1>(nq))
+                        : L.fmt == 2 ? (L.D == 128 ? fkv::pick_attn<128, 2>(nq) : fkv::pick_attn<64, 2>(nq))
+                                     : (L.D == 128 ? fkv::pick_attn<128, 0>(nq) : fkv::pick_attn<64, 0>(nq));
     hipLaunchKernelGGL(k, grid, block, 0, st, a);
     if (splits > 1 && !fused_merge) {
         const dim3 mgrid(rows, ng_max);

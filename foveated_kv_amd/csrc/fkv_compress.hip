@@ -94,7 +94,9 @@ __device__ inline uint4 pack8(const uint16_t (&x)[8]) {
                       x[4] | ((uint32_t)x[5] << 16), x[6] | ((uint32_t)x[7] << 16));
 }
 
-template <int D>
+// VG = 0: one INT4 scale / zero per token (the reference); VG = 32: one per
+// 32-dim group (4 lanes), the same quantiser applied to every group.
+template <int D, int VG>
 __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
     constexpr int LPR = D / 8;       // lanes per row
     constexpr int RPB = 256 / LPR;   // rows per block
@@ -140,7 +142,8 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
         c1 |= (uint32_t)encode_e4m3(kx[4 + i]) << (8 * i);
     }
     *(uint2*)(a.far_k + fr * D + sub * 8) = make_uint2(c0, c1);
-    // far V: per-token INT4
+    // far V: INT4 per token (VG = 0) or per 32-dim group
+    constexpr int RL = VG ? VG / 8 : LPR;  // lanes of one quantisation row
     float vf[8];
     float mn = INFINITY, mx = -INFINITY;
 #pragma unroll
@@ -150,7 +153,7 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
         mx = fmaxf(mx, vf[i]);
     }
 #pragma unroll
-    for (int o = LPR / 2; o >= 1; o >>= 1) {
+    for (int o = RL / 2; o >= 1; o >>= 1) {
         mn = fminf(mn, __shfl_xor(mn, o, LPR));
         mx = fmaxf(mx, __shfl_xor(mx, o, LPR));
     }
@@ -162,9 +165,10 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
         packed |= (uint32_t)q << (4 * i);
     }
     *(uint32_t*)(a.far_v + fr * (D / 2) + sub * 4) = packed;
-    if (sub == 0) {
-        a.fvs[fr] = f2h(scale);
-        a.fvz[fr] = f2h(mn);
+    if (sub % RL == 0) {
+        const int64_t si = VG ? fr * (D / VG) + sub / RL : fr;
+        a.fvs[si] = f2h(scale);
+        a.fvz[si] = f2h(mn);
     }
     if (a.arc_k) *(uint4*)(a.arc_k + fr * D + sub * 8) = pack8(kx);
     if (a.arc_v) *(uint4*)(a.arc_v + fr * D + sub * 8) = pack8(vx);
@@ -182,6 +186,8 @@ extern "C" int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, 
     if (B <= 0 || H <= 0 || S < 0) return set_error("fkv_compress_layer: bad shape");
     if (D != 64 && D != 128) return set_error("fkv_compress_layer: head dim must be 64 or 128, got " + std::to_string(D));
     if (in_dtype < FKV_F16 || in_dtype > FKV_F32) return set_error("fkv_compress_layer: unsupported dtype");
+    if (cfg->v_group != 0 && cfg->v_group != 32)
+        return set_error("fkv_compress_layer: v_group must be 0 (per token) or 32, got " + std::to_string(cfg->v_group));
     fkv_tiers tb;
     if (int rc = fkv_tier_boundaries(cfg, S, &tb)) return rc;
     if ((S > 0 && (!keys || !values)) || !near_k || !near_v || !near_valid ||
@@ -208,7 +214,9 @@ extern "C" int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, 
     const int rpb = 256 / (D / 8);
     dim3 grid((unsigned)fkv::cdiv(rows > 0 ? rows : 1, rpb), (unsigned)(B * H));
     hipStream_t st = (hipStream_t)stream;
-    if (D == 128) hipLaunchKernelGGL(fkv::compress_kernel<128>, grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(fkv::compress_kernel<64>, grid, dim3(256), 0, st, a);
+    const bool g32 = cfg->v_group == 32;
+    void (*kern)(fkv::CompressArgs) = D == 128 ? (g32 ? fkv::compress_kernel<128, 32> : fkv::compress_kernel<128, 0>)
+                                               : (g32 ? fkv::compress_kernel<64, 32> : fkv::compress_kernel<64, 0>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, a);
     return fkv::check_hip(hipGetLastError(), "compress_kernel launch");
 }

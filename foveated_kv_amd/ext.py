@@ -37,10 +37,14 @@ class TierConfig:
         self.window_size = 32
         self.promo_headroom_pct = 0.5
         self.promo_headroom_min = 4
+        # far V INT4 scale / zero per token (0, the reference) or per 32-dim
+        # group (32): the benchmark's group-32 packed layout
+        self.v_group = 0
 
     def to_c(self):
         return _lib.TierConfigC(float(self.near_pct), int(self.n_sinks), int(self.window_size),
-                                float(self.promo_headroom_pct), int(self.promo_headroom_min))
+                                float(self.promo_headroom_pct), int(self.promo_headroom_min),
+                                int(self.v_group))
 
 
 def tier_boundaries_c(cfg, S):
@@ -109,7 +113,8 @@ class CompressHandle:
         near_v = torch.empty_like(near_k)
         far_k = torch.empty((B, H, F, D), dtype=torch.uint8, device=dev)
         far_v = torch.empty((B, H, F, D // 2), dtype=torch.uint8, device=dev)
-        fvs = torch.empty((B, H, F), dtype=torch.float16, device=dev)
+        vg = int(self.cfg.v_group)
+        fvs = torch.empty((B, H, F, D // vg) if vg else (B, H, F), dtype=torch.float16, device=dev)
         fvz = torch.empty_like(fvs)
         near_valid = torch.empty((H,), dtype=torch.int32, device=dev)
         arc_k = torch.empty((B, H, F, D), dtype=torch.float16, device=dev) if with_archive else None
@@ -159,8 +164,14 @@ class FoveatedHandle:
         F = far_k.shape[2]
         if tuple(far_k.shape) != (B, H, F, D) or tuple(far_v.shape) != (B, H, F, D // 2):
             raise ValueError(f"far_k {tuple(far_k.shape)} / far_v {tuple(far_v.shape)} do not match near {tuple(near_k.shape)}")
-        if tuple(far_v_scale.shape) != (B, H, F) or tuple(far_v_zero.shape) != (B, H, F):
-            raise ValueError("far_v_scale / far_v_zero must be (B,H,F)")
+        # per-token V scales (B,H,F) as the reference, or one per 32-dim
+        # group (B,H,F,D/32): the group-32 packed layout
+        grouped = far_v_scale.dim() == 4
+        want = (B, H, F, D // 32) if grouped else (B, H, F)
+        if tuple(far_v_scale.shape) != want or tuple(far_v_zero.shape) != want:
+            raise ValueError(f"far_v_scale / far_v_zero must be (B,H,F) or (B,H,F,D/32), got "
+                             f"{tuple(far_v_scale.shape)} / {tuple(far_v_zero.shape)}")
+        self.v_group = 32 if grouped else 0
         self.device = near_k.device
         self.B, self.H_kv, self.D, self.N_near, self.N_far = B, H, D, Na, F
         self.spike_margin = float(spike_margin)
@@ -178,10 +189,11 @@ class FoveatedHandle:
         lib = _lib.load()
         h = ctypes.c_void_p()
         with torch.cuda.device(self.device):
-            check(lib.fkv_attn_create(ctypes.byref(h), B, H, D, Na, F, ptr(nk), ptr(nv), dtype_code(nk.dtype),
-                                      ptr(fk), ptr(fv), ptr(fvs), ptr(fvz), dtype_code(fvs.dtype), ptr(valid),
-                                      self.spike_margin, _lib.stream_ptr(self.device)),
-                  "fkv_attn_create")
+            create = lib.fkv_attn_create_g32 if grouped else lib.fkv_attn_create
+            check(create(ctypes.byref(h), B, H, D, Na, F, ptr(nk), ptr(nv), dtype_code(nk.dtype),
+                         ptr(fk), ptr(fv), ptr(fvs), ptr(fvz), dtype_code(fvs.dtype), ptr(valid),
+                         self.spike_margin, _lib.stream_ptr(self.device)),
+                  "fkv_attn_create_g32" if grouped else "fkv_attn_create")
         self._h = h
         self._lib = lib
 

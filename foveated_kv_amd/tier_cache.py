@@ -44,11 +44,16 @@ def e4m3_to_fp16(codes: torch.Tensor) -> torch.Tensor:
 
 
 def dequant_int4_per_token(packed, scale, zero):
-    """mlx_foveated.py:94-108, in fp16 arithmetic (two roundings)."""
+    """mlx_foveated.py:94-108, in fp16 arithmetic (two roundings).  Scales
+    of shape (B,H,N,D/g) (group-g V) apply to their g-dim groups."""
     lo = (packed & 0x0F).to(torch.float16)
     hi = ((packed >> 4) & 0x0F).to(torch.float16)
     B, H, N, Dh = packed.shape
     inter = torch.stack([lo, hi], dim=-1).reshape(B, H, N, Dh * 2)
+    if scale.dim() == 4:
+        g = Dh * 2 // scale.shape[-1]
+        return inter * scale.to(torch.float16).repeat_interleave(g, dim=-1) + \
+            zero.to(torch.float16).repeat_interleave(g, dim=-1)
     return inter * scale.to(torch.float16).unsqueeze(-1) + zero.to(torch.float16).unsqueeze(-1)
 
 
@@ -62,11 +67,16 @@ class TierConfig:
     promo_headroom_pct: float = 0.5
     promo_headroom_min: int = 8
     compress_method: str = "fp8"  # "fp8" (fp8 K + int4 V) or "turbo"
+    # fp8 far V: one INT4 scale / zero per token (0, the reference) or per
+    # 32-dim group (32, the group-32 packed layout)
+    v_group: int = 0
 
     def __post_init__(self):
         if self.compress_method not in ("fp8", "turbo"):
             raise ValueError(
                 f"compress_method must be 'fp8' or 'turbo', got '{self.compress_method}'")
+        if self.v_group not in (0, 32):
+            raise ValueError(f"v_group must be 0 (per token) or 32, got {self.v_group}")
 
     def tier_boundaries(self, S: int) -> dict:
         n_sinks = min(self.n_sinks, S)
@@ -103,6 +113,7 @@ class TierConfig:
         c.window_size = self.window_size
         c.promo_headroom_pct = self.promo_headroom_pct
         c.promo_headroom_min = self.promo_headroom_min
+        c.v_group = self.v_group
         return c
 
 
@@ -147,7 +158,7 @@ class FoveatedLayer:
     near_idx: torch.Tensor  # (B,H,N_near) int32, -1 for headroom
     far_k: torch.Tensor  # (B,H,F,D) uint8 E4M3
     far_v: torch.Tensor  # (B,H,F,D//2) uint8 INT4
-    far_v_scale: torch.Tensor  # (B,H,F) fp16
+    far_v_scale: torch.Tensor  # (B,H,F) fp16, or (B,H,F,D/32) with group-32 V
     far_v_zero: torch.Tensor
     far_idx: torch.Tensor  # (B,H,F) int32
     archive_k: torch.Tensor = field(repr=False)

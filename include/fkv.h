@@ -56,6 +56,8 @@ typedef struct fkv_tier_config {
     int32_t window_size;
     double promo_headroom_pct; /* near headroom as a fraction of R_actual */
     int32_t promo_headroom_min;
+    int32_t v_group;           /* far V INT4 scale / zero: 0 = one per token (the
+                                  reference), 32 = one per 32-dim group */
 } fkv_tier_config;
 
 typedef struct fkv_tiers {
@@ -76,7 +78,7 @@ int fkv_tier_boundaries(const fkv_tier_config* cfg, int32_t S, fkv_tiers* out);
  *   near_k, near_v   (B,H,Npad,D) fp16, rows >= R_actual zero  (compress_foveal)
  *   far_k            (B,H,F,D)    E4M3 codes                  (compress_fp8)
  *   far_v            (B,H,F,D/2)  INT4, even dim in low nibble (compress_int4)
- *   far_v_scale/zero (B,H,F)      fp16
+ *   far_v_scale/zero (B,H,F)      fp16; (B,H,F,D/32) when cfg->v_group = 32
  *   near_valid       (H)          int32 = R_actual
  *   archive_k/v      (B,H,F,D)    fp16 copy of the far rows (may be NULL)
  * with Npad/F from fkv_tier_boundaries(cfg, S).  D must be 64 or 128.
@@ -105,6 +107,19 @@ int fkv_attn_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t N
                     const uint8_t* far_k, const uint8_t* far_v, const void* far_v_scale,
                     const void* far_v_zero, int32_t sz_dtype, const int32_t* near_valid,
                     float spike_margin, void* stream);
+
+/* Group-32 INT4 V variant of fkv_attn_create (the benchmark's
+ * "fp8 K + INT4 V in group-32 packed layout"; the reference quantises V
+ * per token, foveated_compress.metal:153-205, and this applies the same
+ * quantiser to every 32-dim group).  Arguments as fkv_attn_create except
+ *   far_v_scale/zero (B,Hkv,F,D/32) in sz_dtype, one pair per value group.
+ * The returned handle is called, queried and destroyed with the
+ * fkv_attn_* functions.  Synchronous. */
+int fkv_attn_create_g32(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F,
+                        const void* near_k, const void* near_v, int32_t near_dtype,
+                        const uint8_t* far_k, const uint8_t* far_v, const void* far_v_scale,
+                        const void* far_v_zero, int32_t sz_dtype, const int32_t* near_valid,
+                        float spike_margin, void* stream);
 
 /* TurboQuant handle: replaces TurboFoveatedHandle's constructor
  * (csrc/foveated_attn.cpp:365-405, blob builder :306-363).  Same near

@@ -59,9 +59,9 @@ def _load():
     lib.orc_split_plan.restype = None
     lib.orc_split_plan.argtypes = [I, P]
     lib.orc_attend_kernel.restype = I
-    lib.orc_attend_kernel.argtypes = [I] * 7 + [P] * 11 + [ctypes.c_float, I, I, I] + [P] * 5
+    lib.orc_attend_kernel.argtypes = [I] * 7 + [P] * 11 + [ctypes.c_float, I, I, I, I] + [P] * 5
     lib.orc_attend_formulation.restype = I
-    lib.orc_attend_formulation.argtypes = [I] * 7 + [P, I] + [P] * 8 + [P]
+    lib.orc_attend_formulation.argtypes = [I] * 7 + [P, I] + [P] * 9 + [I, P]
     lib.orc_compress_foveal.restype = None
     lib.orc_compress_foveal.argtypes = [P, P] + [I] * 9
     _lib = lib
@@ -186,10 +186,11 @@ def compress_foveal(x, tb):
     return dst.view(np.float16)
 
 
-def compress_layer(keys, values, **cfg):
+def compress_layer(keys, values, v_group=0, **cfg):
     """The whole fp8 compress of one layer (foveated_compress.cpp:95-201):
     returns dict with near_k/near_v/far_k/far_v/far_v_scale/far_v_zero/
-    near_valid/near_idx/far_idx/archive_k/archive_v/tb."""
+    near_valid/near_idx/far_idx/archive_k/archive_v/tb.  v_group = 32
+    quantises V per 32-dim group (scales (B,H,F,D/32)) instead of per token."""
     keys = np.ascontiguousarray(keys, np.float16)
     values = np.ascontiguousarray(values, np.float16)
     B, H, S, D = keys.shape
@@ -198,7 +199,7 @@ def compress_layer(keys, values, **cfg):
     far_sl = slice(tb["mid_start"], tb["mid_start"] + F)
     fk_src = keys[:, :, far_sl]
     fv_src = values[:, :, far_sl]
-    far_v, fvs, fvz = quant_int4(fv_src)
+    far_v, fvs, fvz = quant_int4_groups(fv_src, v_group) if v_group else quant_int4(fv_src)
     return {
         "near_k": compress_foveal(keys, tb),
         "near_v": compress_foveal(values, tb),
@@ -226,6 +227,23 @@ def _dec_arrays(B, Hkv, D, dec_k, dec_v):
     return _u16(dec_k), _u16(dec_v), dec_k.shape[2]
 
 
+def _v_group(far_vs, D):
+    """0 for per-token scales (B,Hkv,F), else the group size of (B,Hkv,F,D/g) scales."""
+    fs = np.asarray(far_vs)
+    return 0 if fs.ndim == 3 else D // fs.shape[-1]
+
+
+def quant_int4_groups(x, group=32, python_semantics=False):
+    """INT4 in groups of ``group`` dims: the per-token quantiser applied to
+    every group (the group-32 extension) -> packed (..., D/2), scale and zero
+    (..., D/group) fp16."""
+    x = np.asarray(x)
+    sh = x.shape
+    rows = x.reshape(sh[:-1] + (sh[-1] // group, group))
+    p, s, z = quant_int4(rows, python_semantics=python_semantics)
+    return p.reshape(sh[:-1] + (sh[-1] // 2,)), s, z
+
+
 def attend_kernel(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_vz,
                   dec_k=None, dec_v=None, spike_margin=10.0, split_size=0,
                   num_splits=0, gate=True, far_k_f16=None):
@@ -247,6 +265,7 @@ def attend_kernel(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_vz,
     fs, fz = _u16(far_vs), _u16(far_vz)
     dk, dv, ndec = _dec_arrays(B, Hkv, D, dec_k, dec_v)
     valid = np.ascontiguousarray(near_valid, np.uint32)
+    vg = _v_group(fs, D)
     out = np.zeros((B, Hq, D), np.float64)
     flags = np.zeros((B, Hq), np.int32)
     tokens = np.zeros((B, Hq), np.int32)
@@ -255,7 +274,7 @@ def attend_kernel(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_vz,
     rc = lib.orc_attend_kernel(B, Hq, Hkv, D, Npad, F, ndec, _ptr(q), _ptr(nk), _ptr(nv_),
                                _ptr(valid), _ptr(fk), _ptr(fk16), _ptr(fv), _ptr(fs), _ptr(fz),
                                _ptr(dk), _ptr(dv), float(spike_margin), int(split_size),
-                               int(num_splits), int(bool(gate)), _ptr(out), _ptr(flags),
+                               int(num_splits), int(bool(gate)), vg, _ptr(out), _ptr(flags),
                                _ptr(tokens), _ptr(mf), _ptr(mn))
     if rc != 0:
         raise ValueError(f"orc_attend_kernel failed: {rc}")
@@ -284,7 +303,7 @@ def attend_formulation(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_
     rc = lib.orc_attend_formulation(B, Hq, Hkv, D, Npad, F, ndec, _ptr(qb),
                                     1 if q_dtype == "bfloat16" else 0, _ptr(nk), _ptr(nv_),
                                     _ptr(valid), _ptr(fk), _ptr(fv), _ptr(fs), _ptr(fz),
-                                    _ptr(dk), _ptr(dv), _ptr(out))
+                                    _ptr(dk), _ptr(dv), _v_group(fs, D), _ptr(out))
     if rc != 0:
         raise ValueError(f"orc_attend_formulation failed: {rc}")
     return out

@@ -304,7 +304,11 @@ static void orc_accum(orc_state* st, double s, const double* v, int D) {
  *                            decode of far_k (lets the legacy INT8-K fixtures
  *                            drive the INT4-V far path); NULL for fp8 keys
  *   far_v    (B,Hkv,F,D/2)   INT4 packed, low nibble = even dim
- *   far_vs/vz (B,Hkv,F)      fp16 bits
+ *   far_vs/vz (B,Hkv,F)      fp16 bits (v_group 0: one scale / zero per
+ *                            token, the reference); (B,Hkv,F,D/v_group) with
+ *                            v_group > 0: one per v_group dims (the group-32
+ *                            extension: the reference's per-token arithmetic
+ *                            applied to each group)
  *   dec_k/v  (B,Hkv,n_dec,D) fp16 bits
  *   split_size/num_splits <= 0 -> reference adaptive plan
  *   gate != 0 -> skip V of far tokens with s < m - 16 (:311-360)
@@ -317,10 +321,12 @@ ORC_API int orc_attend_kernel(int B, int Hq, int Hkv, int D, int Npad, int F, in
                               const uint8_t* far_v, const uint16_t* far_vs,
                               const uint16_t* far_vz, const uint16_t* dec_k,
                               const uint16_t* dec_v, float spike_margin, int split_size,
-                              int num_splits, int gate, double* out, int32_t* flags,
+                              int num_splits, int gate, int v_group, double* out, int32_t* flags,
                               int32_t* tokens, double* max_far_out, double* min_near_out) {
     if (Hkv <= 0 || Hq % Hkv != 0 || D <= 0) return -1;
+    if (v_group < 0 || (v_group > 0 && D % v_group != 0)) return -1;
     const int G = Hq / Hkv;
+    const int NGV = v_group > 0 ? D / v_group : 1; /* scale / zero entries per far token */
     const int s_total = Npad + F + n_dec;
     if (split_size <= 0 || num_splits <= 0) {
         int plan[3];
@@ -385,12 +391,12 @@ ORC_API int orc_attend_kernel(int B, int Hq, int Hkv, int D, int Npad, int F, in
                     }
                     if (sc > st->max_far) { st->max_far = sc; st->far_tok = t; }
                     if (gate && sc < st->m - 16.0) continue;
-                    double vs = orc_h2f(far_vs[bkv * F + t]);
-                    double vz = orc_h2f(far_vz[bkv * F + t]);
                     const uint8_t* vr = far_v + (bkv * F + t) * (D / 2);
-                    for (int p = 0; p < D / 2; p++) {
-                        vv[2 * p] = (double)(vr[p] & 15) * vs + vz;
-                        vv[2 * p + 1] = (double)(vr[p] >> 4) * vs + vz;
+                    for (int d = 0; d < D; d++) {
+                        const int64_t si = (bkv * F + t) * NGV + (v_group > 0 ? d / v_group : 0);
+                        const double vs = orc_h2f(far_vs[si]), vz = orc_h2f(far_vz[si]);
+                        const int nib = (d & 1) ? (vr[d >> 1] >> 4) : (vr[d >> 1] & 15);
+                        vv[d] = (double)nib * vs + vz;
                     }
                     orc_accum(st, sc, vv, D);
                 }
@@ -456,8 +462,11 @@ ORC_API int orc_attend_formulation(int B, int Hq, int Hkv, int D, int Npad, int 
                                    const uint16_t* near_v, const uint32_t* near_valid,
                                    const uint8_t* far_k, const uint8_t* far_v,
                                    const uint16_t* far_vs, const uint16_t* far_vz,
-                                   const uint16_t* dec_k, const uint16_t* dec_v, double* out) {
+                                   const uint16_t* dec_k, const uint16_t* dec_v, int v_group,
+                                   double* out) {
     if (Hkv <= 0 || Hq % Hkv != 0) return -1;
+    if (v_group < 0 || (v_group > 0 && D % v_group != 0)) return -1;
+    const int NGV = v_group > 0 ? D / v_group : 1;
     const int G = Hq / Hkv;
     int nv_max = 0;
     for (int h = 0; h < Hkv; h++)
@@ -514,8 +523,9 @@ ORC_API int orc_attend_formulation(int B, int Hq, int Hkv, int D, int Npad, int 
                         int64_t tf = bkv * F + (t - nv_max - n_dec);
                         uint8_t byte = far_v[tf * (D / 2) + d / 2];
                         float nib = (float)((d & 1) ? (byte >> 4) : (byte & 15));
-                        float s16 = orc_h2f(far_vs[tf]);
-                        float z16 = orc_h2f(far_vz[tf]);
+                        const int64_t si = tf * NGV + (v_group > 0 ? d / v_group : 0);
+                        float s16 = orc_h2f(far_vs[si]);
+                        float z16 = orc_h2f(far_vz[si]);
                         float prod = orc_h2f(orc_f2h(nib * s16));
                         vf = orc_h2f(orc_f2h(prod + z16));
                     }

@@ -42,6 +42,7 @@ def _cfg(fkv, **kw):
 
     c = ext.TierConfig()
     c.promo_headroom_min = kw.get("promo_headroom_min", 8)
+    c.v_group = kw.get("v_group", 0)
     return c
 
 
@@ -141,18 +142,18 @@ def _far_scores(orc, c, q):
 
 
 def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16, spikes=0.0,
-                  margin=10.0, near_valid_delta=0, check_formulation=True, heavy_tail=False):
+                  margin=10.0, near_valid_delta=0, check_formulation=True, heavy_tail=False, v_group=0):
     from foveated_kv_amd import ext, synthetic
 
     _flush(f"attention B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} seed={seed} "
-           f"q={q_dtype} spikes={spikes} nv_delta={near_valid_delta}")
+           f"q={q_dtype} spikes={spikes} nv_delta={near_valid_delta} v_group={v_group}")
     k, v = synthetic.make_kv(B, Hkv, S, D, seed, heavy_tail=heavy_tail)
     q = synthetic.make_query(B, Hq, D, seed)
     tb = orc.tier_boundaries(S)
     synthetic.inject_spikes(k, q, tb["mid_start"], tb["far_count"], spikes, seed)
     dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
-    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
-                                                      with_archive=False)
+    cl = ext.CompressHandle(_cfg(fkv, v_group=v_group)).compress_layer(
+        torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), with_archive=False)
     nv = cl.near_valid.clone()
     if near_valid_delta:
         # promoted-looking rows: write copies of far rows into the headroom
@@ -213,6 +214,40 @@ def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16
 ])
 def test_attention_parity(fkv, orc, args):
     run_attention(fkv, orc, **args)
+
+
+GROUP32 = [
+    dict(B=1, Hq=14, Hkv=2, D=64, S=512, n_dec=16, seed=31),
+    dict(B=1, Hq=32, Hkv=8, D=128, S=4096, n_dec=64, seed=32, heavy_tail=True),
+    dict(B=2, Hq=8, Hkv=2, D=128, S=700, n_dec=7, seed=33, spikes=0.02),
+    dict(B=1, Hq=32, Hkv=2, D=64, S=700, n_dec=5, seed=34),      # two head groups
+    dict(B=3, Hq=12, Hkv=4, D=64, S=333, n_dec=70, seed=35),     # ragged tiles
+    dict(B=1, Hq=8, Hkv=2, D=128, S=1000, n_dec=3, seed=36, near_valid_delta=5),
+]
+
+
+@pytest.mark.parametrize("args", GROUP32, ids=[f"B{a['B']}_Hq{a['Hq']}_D{a['D']}_S{a['S']}" for a in GROUP32])
+def test_attention_group32_parity(fkv, orc, args):
+    """fp8 K + group-32 INT4 V: compress and fused attention against the
+    oracle with one value scale / zero per 32 dims."""
+    run_attention(fkv, orc, v_group=32, **args)
+
+
+@pytest.mark.parametrize("B,H,S,D", [(1, 2, 512, 64), (2, 3, 1000, 128), (1, 1, 37, 128)])
+def test_compress_group32_bit_exact(fkv, orc, B, H, S, D):
+    from foveated_kv_amd import ext, synthetic
+
+    _flush(f"compress group-32 B={B} H={H} S={S} D={D}")
+    k, v = synthetic.make_kv(B, H, S, D, seed=S + 1)
+    v = (v * (4.0 ** np.arange(D // 32)).repeat(32)).astype(np.float16)
+    cl = ext.CompressHandle(_cfg(fkv, v_group=32)).compress_layer(torch.from_numpy(k).cuda(),
+                                                                  torch.from_numpy(v).cuda())
+    torch.cuda.synchronize()
+    ref = orc.compress_layer(k, v, v_group=32)
+    for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale", "far_v_zero", "archive_k", "archive_v"):
+        got, want = _np(getattr(cl, n)), ref[n]
+        assert got.shape == want.shape, n
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), n
 
 
 def test_attention_bf16_and_f32_query(fkv, orc):

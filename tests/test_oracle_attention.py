@@ -109,10 +109,12 @@ def test_spike_case_is_flagged(orc):
 # brute force on small random inputs
 # ---------------------------------------------------------------------------
 
-def make_case(rng, B=1, Hq=8, Hkv=2, D=64, S=200, n_dec=5, near_valid_delta=0, orc=None):
+def make_case(rng, B=1, Hq=8, Hkv=2, D=64, S=200, n_dec=5, near_valid_delta=0, orc=None, v_group=0):
     keys = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
     vals = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
-    c = orc.compress_layer(keys, vals)
+    if v_group:  # value groups of very different ranges: a group index mix-up shows
+        vals = (vals * (4.0 ** np.arange(D // v_group)).repeat(v_group)).astype(np.float16)
+    c = orc.compress_layer(keys, vals, v_group=v_group)
     nv = c["near_valid"].astype(np.uint32) + np.uint32(near_valid_delta)
     q = rng.standard_normal((B, Hq, D)).astype(np.float16)
     dk = rng.standard_normal((B, Hkv, n_dec, D)).astype(np.float16) if n_dec else None
@@ -131,10 +133,15 @@ def brute_force(q, c, nv, dk, dv, fp16_v=False):
     lo = (c["far_v"] & 15).astype(np.float64)
     hi = (c["far_v"] >> 4).astype(np.float64)
     codes = np.stack([lo, hi], -1).reshape(fk.shape)
-    s = c["far_v_scale"].astype(np.float64)[..., None]
-    zz = c["far_v_zero"].astype(np.float64)[..., None]
+    if c["far_v_scale"].ndim == 4:  # one scale / zero per D/ng-dim group
+        g = fk.shape[-1] // c["far_v_scale"].shape[-1]
+        s16, z16 = np.repeat(c["far_v_scale"], g, -1), np.repeat(c["far_v_zero"], g, -1)
+    else:
+        s16, z16 = c["far_v_scale"][..., None], c["far_v_zero"][..., None]
+    s = s16.astype(np.float64)
+    zz = z16.astype(np.float64)
     if fp16_v:
-        fvd = ((codes.astype(np.float16) * c["far_v_scale"][..., None]) + c["far_v_zero"][..., None]).astype(np.float64)
+        fvd = ((codes.astype(np.float16) * s16) + z16).astype(np.float64)
     else:
         fvd = codes * s + zz
     out = np.zeros((B, Hq, D))
@@ -171,6 +178,24 @@ def test_kernel_oracle_brute_force(orc, shape):
     outg, *_ = orc.attend_kernel(q, c["near_k"], c["near_v"], nv, c["far_k"], c["far_v"],
                                  c["far_v_scale"], c["far_v_zero"], dk, dv, gate=True)
     assert np.abs(outg - bf).max() < 1e-4  # gated tokens weigh < e^-16 each
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_kernel_and_formulation_oracle_group32_brute_force(orc, D):
+    """Group-32 V (one scale / zero per 32 dims): both C restatements against
+    the naive softmax over numpy-dequantised values."""
+    rng = np.random.default_rng(D + 1)
+    c, q, nv, dk, dv = make_case(rng, orc=orc, B=2, Hq=8, Hkv=2, D=D, S=333, n_dec=6, v_group=32)
+    assert c["far_v_scale"].shape == c["far_k"].shape[:3] + (D // 32,)
+    bf = brute_force(q, c, nv, dk, dv)
+    out, *_ = orc.attend_kernel(q, c["near_k"], c["near_v"], nv, c["far_k"], c["far_v"],
+                                c["far_v_scale"], c["far_v_zero"], dk, dv, gate=False)
+    scale = np.abs(bf).max()
+    assert np.abs(out - bf).max() < 1e-6 * scale
+    fo = orc.attend_formulation(q, c["near_k"], c["near_v"], nv, c["far_k"], c["far_v"],
+                                c["far_v_scale"], c["far_v_zero"], dk, dv)
+    bf16 = brute_force(q, c, nv, dk, dv, fp16_v=True)
+    assert np.abs(fo - bf16).max() < 1e-9 * scale
 
 
 def test_kernel_oracle_split_invariance(orc):

@@ -144,6 +144,31 @@ def test_int4_invariants(orc, D):
     assert np.all(np.abs(rec - xf) <= s32[..., None] * 0.5 * (1 + 1e-5) + 1e-6)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_int4_group32_invariants(orc, D):
+    """Group-32 INT4: every 32-dim group has its own fp32 min / range; the
+    packing keeps dim d in byte d/2 (even dim low nibble) across groups."""
+    rng = np.random.default_rng(D + 5)
+    ng = D // 32
+    mult = (3.0 ** np.arange(ng)).repeat(32)  # groups of very different ranges
+    x = (rng.standard_normal((4, 40, D)) * mult + rng.uniform(-2, 2, (4, 40, 1))).astype(np.float16)
+    packed, sc, zr = orc.quant_int4_groups(x, 32)
+    assert packed.shape == (4, 40, D // 2) and sc.shape == zr.shape == (4, 40, ng)
+    c = _unpack(packed)
+    xf = x.astype(np.float32).reshape(4, 40, ng, 32)
+    cg = c.reshape(4, 40, ng, 32)
+    mn, mx = xf.min(-1), xf.max(-1)
+    s32 = np.maximum((mx - mn) / np.float32(15), np.float32(1e-8))
+    assert np.array_equal(sc, s32.astype(np.float16)) and np.array_equal(zr, mn.astype(np.float16))
+    assert np.all(np.take_along_axis(cg, np.argmin(xf, -1)[..., None], -1) == 0)
+    assert np.all(np.take_along_axis(cg, np.argmax(xf, -1)[..., None], -1) == 15)
+    rec = cg * s32[..., None] + mn[..., None]
+    assert np.all(np.abs(rec - xf) <= s32[..., None] * 0.5 * (1 + 1e-5) + 1e-6)
+    # a group equal to a whole per-token row of 32 dims codes identically
+    p1, s1, z1 = orc.quant_int4(x[..., 32:64])
+    assert np.array_equal(p1, packed[..., 16:32]) and np.array_equal(s1, sc[..., 1])
+
+
 def test_int4_ties_and_constant_rows(orc):
     # min 0, max 15 -> scale exactly 1: 2.5 and 7.5 are exact ties
     row = np.zeros(64, np.float32)
