@@ -79,6 +79,9 @@ SIGNATURES = {
     "fkv_tier_boundaries": (ctypes.c_int, [ctypes.POINTER(TierConfigC), I32, ctypes.POINTER(TiersC)]),
     "fkv_compress_layer": (ctypes.c_int, [ctypes.POINTER(TierConfigC), P, P, I32, I32, I32, I32, I32,
                                           P, P, P, P, P, P, P, P, P, P]),
+    "fkv_partition_importance": (ctypes.c_int, [ctypes.POINTER(TierConfigC), P, I32, I32, I32, P, P, P]),
+    "fkv_compress_layer_indexed": (ctypes.c_int, [ctypes.POINTER(TierConfigC), P, P, I32, I32, I32, I32, I32,
+                                                  P, P, P, P, P, P, P, P, P, P, P, P]),
     "fkv_attn_create": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P,
                                        I32, P, F32, P]),
     "fkv_attn_create_g32": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P,

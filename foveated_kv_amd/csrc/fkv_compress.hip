@@ -94,46 +94,12 @@ __device__ inline uint4 pack8(const uint16_t (&x)[8]) {
                       x[4] | ((uint32_t)x[5] << 16), x[6] | ((uint32_t)x[7] << 16));
 }
 
-// VG = 0: one INT4 scale / zero per token (the reference); VG = 32: one per
-// 32-dim group (4 lanes), the same quantiser applied to every group.
+// One far row (fr = bh * F + f) from its fp16 K / V (8 elements per lane):
+// E4M3 keys, INT4 values per token (VG = 0) or per VG-dim group, archive.
 template <int D, int VG>
-__global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
-    constexpr int LPR = D / 8;       // lanes per row
-    constexpr int RPB = 256 / LPR;   // rows per block
-    const fkv_tiers& tb = a.tb;
-    const int bh = blockIdx.y;
-    const int r = blockIdx.x * RPB + threadIdx.x / LPR;
-    const int sub = threadIdx.x % LPR;
-    if (blockIdx.x == 0 && threadIdx.x == 0 && bh < a.H) a.near_valid[bh] = tb.r_actual;
-    const int npad = tb.n_near_padded;
-    const int F = tb.far_count;
-    if (r >= a.S + tb.headroom) return;  // whole row group leaves together
-    const uint4 zero4 = make_uint4(0, 0, 0, 0);
-    if (r >= a.S) {  // headroom slot: zeros
-        const int64_t o = ((int64_t)bh * npad + tb.r_actual + (r - a.S)) * D + sub * 8;
-        *(uint4*)(a.near_k + o) = zero4;
-        *(uint4*)(a.near_v + o) = zero4;
-        return;
-    }
-    const int t = r;
-    int slot = -1, f = -1;
-    if (t < tb.n_sinks) slot = t;
-    else if (t >= tb.near_mid_start && t < tb.mid_end) slot = tb.n_sinks + (t - tb.near_mid_start);
-    else if (tb.window > 0 && t >= a.S - tb.window) slot = tb.n_sinks + tb.near_from_mid + (t - (a.S - tb.window));
-    else if (t >= tb.mid_start && t < tb.near_mid_start) f = t - tb.mid_start;
-
-    const int64_t src = ((int64_t)bh * a.S + t) * D + sub * 8;
-    uint16_t kx[8], vx[8];
-    load8(a.k, a.dtype, src, kx);
-    load8(a.v, a.dtype, src, vx);
-    if (slot >= 0) {
-        const int64_t o = ((int64_t)bh * npad + slot) * D + sub * 8;
-        *(uint4*)(a.near_k + o) = pack8(kx);
-        *(uint4*)(a.near_v + o) = pack8(vx);
-        return;
-    }
-    if (f < 0) return;  // unreachable: every position is near or far
-    const int64_t fr = (int64_t)bh * F + f;
+__device__ inline void far_row(const CompressArgs& a, int64_t fr, int sub, const uint16_t (&kx)[8],
+                               const uint16_t (&vx)[8]) {
+    constexpr int LPR = D / 8;
     // far K: E4M3 codes
     uint32_t c0 = 0, c1 = 0;
 #pragma unroll
@@ -174,26 +140,223 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
     if (a.arc_v) *(uint4*)(a.arc_v + fr * D + sub * 8) = pack8(vx);
 }
 
+// VG = 0: one INT4 scale / zero per token (the reference); VG = 32: one per
+// 32-dim group (4 lanes), the same quantiser applied to every group.
+template <int D, int VG>
+__global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
+    constexpr int LPR = D / 8;       // lanes per row
+    constexpr int RPB = 256 / LPR;   // rows per block
+    const fkv_tiers& tb = a.tb;
+    const int bh = blockIdx.y;
+    const int r = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    if (blockIdx.x == 0 && threadIdx.x == 0 && bh < a.H) a.near_valid[bh] = tb.r_actual;
+    const int npad = tb.n_near_padded;
+    const int F = tb.far_count;
+    if (r >= a.S + tb.headroom) return;  // whole row group leaves together
+    const uint4 zero4 = make_uint4(0, 0, 0, 0);
+    if (r >= a.S) {  // headroom slot: zeros
+        const int64_t o = ((int64_t)bh * npad + tb.r_actual + (r - a.S)) * D + sub * 8;
+        *(uint4*)(a.near_k + o) = zero4;
+        *(uint4*)(a.near_v + o) = zero4;
+        return;
+    }
+    const int t = r;
+    int slot = -1, f = -1;
+    if (t < tb.n_sinks) slot = t;
+    else if (t >= tb.near_mid_start && t < tb.mid_end) slot = tb.n_sinks + (t - tb.near_mid_start);
+    else if (tb.window > 0 && t >= a.S - tb.window) slot = tb.n_sinks + tb.near_from_mid + (t - (a.S - tb.window));
+    else if (t >= tb.mid_start && t < tb.near_mid_start) f = t - tb.mid_start;
+
+    const int64_t src = ((int64_t)bh * a.S + t) * D + sub * 8;
+    uint16_t kx[8], vx[8];
+    load8(a.k, a.dtype, src, kx);
+    load8(a.v, a.dtype, src, vx);
+    if (slot >= 0) {
+        const int64_t o = ((int64_t)bh * npad + slot) * D + sub * 8;
+        *(uint4*)(a.near_k + o) = pack8(kx);
+        *(uint4*)(a.near_v + o) = pack8(vx);
+        return;
+    }
+    if (f < 0) return;  // unreachable: every position is near or far
+    far_row<D, VG>(a, (int64_t)bh * F + f, sub, kx, vx);
+}
+
+
+// ---------------------------------------------------------------------------
+// Importance partition: near = sinks + the near_from_mid middle tokens of
+// highest importance + window, per (batch, head).
+// ---------------------------------------------------------------------------
+
+// fp32 importance -> unsigned key with the same order; NaN ranks below
+// -inf, -0 equals +0.
+__device__ inline uint32_t order_key(float f) {
+    if (f != f) return 0u;
+    uint32_t b = __float_as_uint(f);
+    if (b == 0x80000000u) b = 0u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Middle token i's rank key: importance, then position (the later token
+// wins a tie, so a constant or position-valued importance gives the
+// recency partition).
+__device__ inline uint64_t rank_key(const float* row, int pos) {
+    return ((uint64_t)order_key(row[pos]) << 32) | (uint32_t)pos;
+}
+
+constexpr int kPartThreads = 1024;
+
+// One workgroup per (batch, head).  The near_from_mid-th largest rank key
+// is found by an 8-pass MSB-first radix select (256-bin LDS histograms);
+// then the middle is compacted in position order into near slots
+// n_sinks.. and far slots 0.. with a block-wide scan per 1024-token chunk.
+__global__ __launch_bounds__(kPartThreads) void partition_kernel(const float* __restrict__ imp, int S, fkv_tiers tb,
+                                                                int32_t* __restrict__ near_idx,
+                                                                int32_t* __restrict__ far_idx) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint64_t s_prefix;
+    __shared__ int s_rem;
+    __shared__ int wcount[2][kPartThreads / 64];
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const float* row = imp + (int64_t)bh * S;
+    const int npad = tb.n_near_padded, F = tb.far_count;
+    const int m0 = tb.mid_start;
+    const int mlen = tb.mid_end > tb.mid_start ? tb.mid_end - tb.mid_start : 0;
+    const int k = tb.near_from_mid;
+    int32_t* nrow = near_idx + (int64_t)bh * npad;
+    int32_t* frow = far_idx + (int64_t)bh * F;
+    // fixed slots: sinks, window, headroom
+    for (int i = tid; i < npad; i += kPartThreads) {
+        if (i < tb.n_sinks) nrow[i] = i;
+        else if (i >= tb.n_sinks + k && i < tb.r_actual) nrow[i] = S - tb.window + (i - tb.n_sinks - k);
+        else if (i >= tb.r_actual) nrow[i] = -1;
+    }
+    const bool all = k >= mlen, none = k <= 0;
+    uint64_t thr = 0;  // near <=> rank key >= thr
+    if (!all && !none) {
+        uint64_t prefix = 0, mask = 0;
+        int rem = k;
+        for (int p = 7; p >= 0; p--) {
+            for (int i = tid; i < 256; i += kPartThreads) hist[i] = 0;
+            __syncthreads();
+            for (int i = tid; i < mlen; i += kPartThreads) {
+                const uint64_t key = rank_key(row, m0 + i);
+                if ((key & mask) == prefix) atomicAdd(&hist[(key >> (8 * p)) & 255], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int cum = 0, b = 255;
+                for (; b > 0; b--) {
+                    if (cum + (int)hist[b] >= rem) break;
+                    cum += (int)hist[b];
+                }
+                s_prefix = prefix | ((uint64_t)b << (8 * p));
+                s_rem = rem - cum;
+            }
+            __syncthreads();
+            prefix = s_prefix;
+            rem = s_rem;
+            mask |= (uint64_t)255 << (8 * p);
+        }
+        thr = prefix;
+    }
+    // compaction in position order
+    const int wave = tid / 64, lane = tid % 64;
+    int near_base = 0, far_base = 0;
+    for (int c0 = 0; c0 < mlen; c0 += kPartThreads) {
+        const int i = c0 + tid;
+        const bool valid = i < mlen;
+        const bool nf = valid && (all || (!none && rank_key(row, m0 + i) >= thr));
+        const bool ff = valid && !nf;
+        const uint64_t bn = __ballot(nf), bf = __ballot(ff);
+        const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+        const int rn = __popcll(bn & below), rf = __popcll(bf & below);
+        if (lane == 0) {
+            wcount[0][wave] = __popcll(bn);
+            wcount[1][wave] = __popcll(bf);
+        }
+        __syncthreads();
+        int wn = 0, wf = 0, tn = 0, tf = 0;
+        for (int w = 0; w < kPartThreads / 64; w++) {
+            if (w < wave) {
+                wn += wcount[0][w];
+                wf += wcount[1][w];
+            }
+            tn += wcount[0][w];
+            tf += wcount[1][w];
+        }
+        if (nf) {
+            const int slot = tb.n_sinks + near_base + wn + rn;
+            if (slot < tb.n_sinks + k) nrow[slot] = m0 + i;
+        }
+        if (ff) {
+            const int f = far_base + wf + rf;
+            if (f < F) frow[f] = m0 + i;
+        }
+        near_base += tn;
+        far_base += tf;
+        __syncthreads();  // wcount is rewritten by the next chunk
+    }
+}
+
+// Compression from explicit index sets: output row r < Npad is near slot r
+// (source near_idx, zeros for headroom / -1 / out-of-range indices), row
+// Npad + f is far row f (source far_idx; an out-of-range index encodes a
+// zero row).
+template <int D, int VG>
+__global__ __launch_bounds__(256) void compress_gather_kernel(CompressArgs a, const int32_t* __restrict__ near_idx,
+                                                              const int32_t* __restrict__ far_idx) {
+    constexpr int LPR = D / 8;
+    constexpr int RPB = 256 / LPR;
+    const fkv_tiers& tb = a.tb;
+    const int bh = blockIdx.y;
+    const int r = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    if (blockIdx.x == 0 && threadIdx.x == 0 && bh < a.H) a.near_valid[bh] = tb.r_actual;
+    const int npad = tb.n_near_padded;
+    const int F = tb.far_count;
+    if (r >= npad + F) return;  // whole row group leaves together
+    uint16_t kx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, vx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const bool near = r < npad;
+    int t = -1;
+    if (near) t = r < tb.r_actual ? near_idx[(int64_t)bh * npad + r] : -1;
+    else t = far_idx[(int64_t)bh * F + (r - npad)];
+    if (t >= 0 && t < a.S) {
+        const int64_t src = ((int64_t)bh * a.S + t) * D + sub * 8;
+        load8(a.k, a.dtype, src, kx);
+        load8(a.v, a.dtype, src, vx);
+    }
+    if (near) {
+        const int64_t o = ((int64_t)bh * npad + r) * D + sub * 8;
+        *(uint4*)(a.near_k + o) = pack8(kx);
+        *(uint4*)(a.near_v + o) = pack8(vx);
+        return;
+    }
+    far_row<D, VG>(a, (int64_t)bh * F + (r - npad), sub, kx, vx);
+}
+
 }  // namespace fkv
 
-extern "C" int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, const void* values,
-                                  int32_t in_dtype, int32_t B, int32_t H, int32_t S, int32_t D,
-                                  void* near_k, void* near_v, uint8_t* far_k, uint8_t* far_v,
-                                  void* far_v_scale, void* far_v_zero, int32_t* near_valid,
-                                  void* archive_k, void* archive_v, void* stream) {
+namespace {
+
+// Shared argument checks and CompressArgs of the compress entry points.
+int compress_setup(const char* fn, const fkv_tier_config* cfg, const void* keys, const void* values,
+                   int32_t in_dtype, int32_t B, int32_t H, int32_t S, int32_t D, void* near_k, void* near_v,
+                   uint8_t* far_k, uint8_t* far_v, void* far_v_scale, void* far_v_zero, int32_t* near_valid,
+                   void* archive_k, void* archive_v, fkv::CompressArgs& a) {
     using fkv::set_error;
-    if (!cfg) return set_error("fkv_compress_layer: cfg is NULL");
-    if (B <= 0 || H <= 0 || S < 0) return set_error("fkv_compress_layer: bad shape");
-    if (D != 64 && D != 128) return set_error("fkv_compress_layer: head dim must be 64 or 128, got " + std::to_string(D));
-    if (in_dtype < FKV_F16 || in_dtype > FKV_F32) return set_error("fkv_compress_layer: unsupported dtype");
+    const std::string name(fn);
+    if (!cfg) return set_error(name + ": cfg is NULL");
+    if (B <= 0 || H <= 0 || S < 0) return set_error(name + ": bad shape");
+    if (D != 64 && D != 128) return set_error(name + ": head dim must be 64 or 128, got " + std::to_string(D));
+    if (in_dtype < FKV_F16 || in_dtype > FKV_F32) return set_error(name + ": unsupported dtype");
     if (cfg->v_group != 0 && cfg->v_group != 32)
-        return set_error("fkv_compress_layer: v_group must be 0 (per token) or 32, got " + std::to_string(cfg->v_group));
+        return set_error(name + ": v_group must be 0 (per token) or 32, got " + std::to_string(cfg->v_group));
     fkv_tiers tb;
     if (int rc = fkv_tier_boundaries(cfg, S, &tb)) return rc;
     if ((S > 0 && (!keys || !values)) || !near_k || !near_v || !near_valid ||
         (tb.far_count > 0 && (!far_k || !far_v || !far_v_scale || !far_v_zero)))
-        return set_error("fkv_compress_layer: NULL output/input");
-    fkv::CompressArgs a;
+        return set_error(name + ": NULL output/input");
     a.k = keys;
     a.v = values;
     a.dtype = in_dtype;
@@ -210,7 +373,21 @@ extern "C" int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, 
     a.near_valid = near_valid;
     a.arc_k = (uint16_t*)archive_k;
     a.arc_v = (uint16_t*)archive_v;
-    const int rows = S + tb.headroom;
+    return FKV_OK;
+}
+
+}  // namespace
+
+extern "C" int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, const void* values,
+                                  int32_t in_dtype, int32_t B, int32_t H, int32_t S, int32_t D,
+                                  void* near_k, void* near_v, uint8_t* far_k, uint8_t* far_v,
+                                  void* far_v_scale, void* far_v_zero, int32_t* near_valid,
+                                  void* archive_k, void* archive_v, void* stream) {
+    fkv::CompressArgs a;
+    if (int rc = compress_setup("fkv_compress_layer", cfg, keys, values, in_dtype, B, H, S, D, near_k, near_v, far_k,
+                                far_v, far_v_scale, far_v_zero, near_valid, archive_k, archive_v, a))
+        return rc;
+    const int rows = S + a.tb.headroom;
     const int rpb = 256 / (D / 8);
     dim3 grid((unsigned)fkv::cdiv(rows > 0 ? rows : 1, rpb), (unsigned)(B * H));
     hipStream_t st = (hipStream_t)stream;
@@ -219,4 +396,41 @@ extern "C" int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, 
                                                : (g32 ? fkv::compress_kernel<64, 32> : fkv::compress_kernel<64, 0>);
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, a);
     return fkv::check_hip(hipGetLastError(), "compress_kernel launch");
+}
+
+extern "C" int fkv_partition_importance(const fkv_tier_config* cfg, const float* importance, int32_t B, int32_t H,
+                                        int32_t S, int32_t* near_idx, int32_t* far_idx, void* stream) {
+    using fkv::set_error;
+    if (!cfg) return set_error("fkv_partition_importance: cfg is NULL");
+    if (B <= 0 || H <= 0 || S < 0) return set_error("fkv_partition_importance: bad shape");
+    fkv_tiers tb;
+    if (int rc = fkv_tier_boundaries(cfg, S, &tb)) return rc;
+    if ((S > 0 && !importance) || !near_idx || (tb.far_count > 0 && !far_idx))
+        return set_error("fkv_partition_importance: NULL argument");
+    hipLaunchKernelGGL(fkv::partition_kernel, dim3((unsigned)(B * H)), dim3(fkv::kPartThreads), 0,
+                       (hipStream_t)stream, importance, S, tb, near_idx, far_idx);
+    return fkv::check_hip(hipGetLastError(), "partition_kernel launch");
+}
+
+extern "C" int fkv_compress_layer_indexed(const fkv_tier_config* cfg, const void* keys, const void* values,
+                                          int32_t in_dtype, int32_t B, int32_t H, int32_t S, int32_t D,
+                                          const int32_t* near_idx, const int32_t* far_idx, void* near_k,
+                                          void* near_v, uint8_t* far_k, uint8_t* far_v, void* far_v_scale,
+                                          void* far_v_zero, int32_t* near_valid, void* archive_k, void* archive_v,
+                                          void* stream) {
+    fkv::CompressArgs a;
+    if (int rc = compress_setup("fkv_compress_layer_indexed", cfg, keys, values, in_dtype, B, H, S, D, near_k, near_v,
+                                far_k, far_v, far_v_scale, far_v_zero, near_valid, archive_k, archive_v, a))
+        return rc;
+    if (!near_idx || (a.tb.far_count > 0 && !far_idx))
+        return fkv::set_error("fkv_compress_layer_indexed: NULL index array");
+    const int rows = a.tb.n_near_padded + a.tb.far_count;
+    const int rpb = 256 / (D / 8);
+    dim3 grid((unsigned)fkv::cdiv(rows > 0 ? rows : 1, rpb), (unsigned)(B * H));
+    const bool g32 = cfg->v_group == 32;
+    void (*kern)(fkv::CompressArgs, const int32_t*, const int32_t*) =
+        D == 128 ? (g32 ? fkv::compress_gather_kernel<128, 32> : fkv::compress_gather_kernel<128, 0>)
+                 : (g32 ? fkv::compress_gather_kernel<64, 32> : fkv::compress_gather_kernel<64, 0>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, (hipStream_t)stream, a, near_idx, far_idx);
+    return fkv::check_hip(hipGetLastError(), "compress_gather_kernel launch");
 }

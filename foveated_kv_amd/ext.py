@@ -72,7 +72,7 @@ class CompressedLayer:
     """csrc/foveated_compress.h:100-118 (+ the fp16 far-row archive)."""
 
     def __init__(self, near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid,
-                 n_near_actual, archive_k=None, archive_v=None):
+                 n_near_actual, archive_k=None, archive_v=None, near_idx=None, far_idx=None):
         self.near_k = near_k
         self.near_v = near_v
         self.far_k = far_k
@@ -83,6 +83,10 @@ class CompressedLayer:
         self.n_near_actual = n_near_actual
         self.archive_k = archive_k
         self.archive_v = archive_v
+        # (B,H,Npad) / (B,H,F) int32 token positions of an importance
+        # partition (None: the recency partition of the tier boundaries)
+        self.near_idx = near_idx
+        self.far_idx = far_idx
 
 
 class CompressHandle:
@@ -93,8 +97,13 @@ class CompressHandle:
     def __init__(self, cfg=None, metallib_path=""):
         self.cfg = cfg if cfg is not None else TierConfig()
 
-    def compress_layer(self, keys, values, with_archive=True):
-        _require_device(keys, values)
+    def compress_layer(self, keys, values, with_archive=True, importance=None):
+        """``importance`` (optional, fp32, broadcastable to (B,H,S)): the near
+        middle becomes the near_from_mid tokens of highest importance per
+        (batch, head), ties to the later token (importance = position gives
+        the reference's recency partition); the index sets are returned as
+        ``near_idx`` / ``far_idx``."""
+        _require_device(keys, values, importance)
         if keys.shape != values.shape or keys.dim() != 4:
             raise ValueError(f"keys/values must be (B,H,S,D) with equal shapes, got {tuple(keys.shape)} / {tuple(values.shape)}")
         B, H, S, D = keys.shape
@@ -121,16 +130,43 @@ class CompressHandle:
         arc_v = torch.empty_like(arc_k) if with_archive else None
         lib = _lib.load()
         c = self.cfg.to_c()
+        near_idx = far_idx = None
         with torch.cuda.device(dev):
-            check(lib.fkv_compress_layer(ctypes.byref(c), ptr(k), ptr(v), dtype_code(k.dtype), B, H, S, D,
-                                         ptr(near_k), ptr(near_v), ptr(far_k), ptr(far_v), ptr(fvs), ptr(fvz),
-                                         ptr(near_valid), ptr(arc_k), ptr(arc_v), _lib.stream_ptr(dev)),
-                  "fkv_compress_layer")
+            if importance is None:
+                check(lib.fkv_compress_layer(ctypes.byref(c), ptr(k), ptr(v), dtype_code(k.dtype), B, H, S, D,
+                                             ptr(near_k), ptr(near_v), ptr(far_k), ptr(far_v), ptr(fvs), ptr(fvz),
+                                             ptr(near_valid), ptr(arc_k), ptr(arc_v), _lib.stream_ptr(dev)),
+                      "fkv_compress_layer")
+            else:
+                near_idx, far_idx = partition_importance(self.cfg, importance, B, H, S)
+                check(lib.fkv_compress_layer_indexed(
+                    ctypes.byref(c), ptr(k), ptr(v), dtype_code(k.dtype), B, H, S, D, ptr(near_idx), ptr(far_idx),
+                    ptr(near_k), ptr(near_v), ptr(far_k), ptr(far_v), ptr(fvs), ptr(fvz), ptr(near_valid),
+                    ptr(arc_k), ptr(arc_v), _lib.stream_ptr(dev)), "fkv_compress_layer_indexed")
         return CompressedLayer(near_k, near_v, far_k, far_v, fvs, fvz, near_valid, tb["R_actual"],
-                               arc_k, arc_v)
+                               arc_k, arc_v, near_idx, far_idx)
 
     def compress_all(self, all_keys, all_values, with_archive=True):
         return [self.compress_layer(k, v, with_archive) for k, v in zip(all_keys, all_values)]
+
+
+def partition_importance(cfg, importance, B, H, S):
+    """fkv_partition_importance: importance (fp32, broadcastable to (B,H,S),
+    on the device) -> near_idx (B,H,Npad) int32 (sinks, chosen middle,
+    window in ascending position; -1 headroom) and far_idx (B,H,F) int32
+    (the rest of the middle, ascending)."""
+    _require_device(importance)
+    tb = tier_boundaries_c(cfg, S)
+    dev = importance.device
+    imp = importance.to(torch.float32).expand(B, H, S).contiguous()
+    near_idx = torch.empty((B, H, tb["N_near_padded"]), dtype=torch.int32, device=dev)
+    far_idx = torch.empty((B, H, tb["far_count"]), dtype=torch.int32, device=dev)
+    c = cfg.to_c()
+    with torch.cuda.device(dev):
+        check(_lib.load().fkv_partition_importance(ctypes.byref(c), ptr(imp), B, H, S, ptr(near_idx),
+                                                   ptr(far_idx), _lib.stream_ptr(dev)),
+              "fkv_partition_importance")
+    return near_idx, far_idx
 
 
 class BlobWriteInfo:

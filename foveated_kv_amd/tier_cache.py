@@ -369,7 +369,11 @@ class FoveatedKVCache:
             self._prefill_keys[layer_idx] = torch.cat([self._prefill_keys[layer_idx], key_states], dim=2)
             self._prefill_values[layer_idx] = torch.cat([self._prefill_values[layer_idx], value_states], dim=2)
 
-    def compress(self, query=None) -> dict:
+    def compress(self, query=None, importance=None) -> dict:
+        """``importance`` (extension; the reference partitions by recency):
+        None, one fp32 tensor broadcastable to (B,H,S) for every layer, or a
+        list with one per layer.  The near middle of each (batch, head) is
+        then its near_from_mid tokens of highest importance."""
         if not self._prefill_keys:
             return {"compressed": False}
         total_before = total_after = 0
@@ -381,12 +385,13 @@ class FoveatedKVCache:
             B, H, S, D = keys.shape
             seq_length = S
             total_before += keys.numel() * keys.element_size() * 2
+            imp = importance[i] if isinstance(importance, (list, tuple)) else importance
             if self.cfg.compress_method == "turbo":
                 from .turbo import build_turbo_layer
 
-                layer = build_turbo_layer(self.cfg, keys, values)
+                layer = build_turbo_layer(self.cfg, keys, values, importance=imp)
             else:
-                layer = self._build_fp8_layer(handle, keys, values)
+                layer = self._build_fp8_layer(handle, keys, values, importance=imp)
             self.layers[i] = layer
             total_after += layer.memory_bytes()["total_quantized"]
         self.seq_length = seq_length
@@ -397,12 +402,14 @@ class FoveatedKVCache:
                 "before_mb": total_before / (1024 * 1024), "after_mb": total_after / (1024 * 1024),
                 "compression": total_before / max(total_after, 1)}
 
-    def _build_fp8_layer(self, handle, keys, values):
+    def _build_fp8_layer(self, handle, keys, values, importance=None):
         """_compress_cpp (mlx_foveated.py:679-797) with the fused HIP kernel."""
         B, H, S, D = keys.shape
-        cl = handle.compress_layer(keys, values)
-        tb = self.cfg.tier_boundaries(S)
-        near_idx, far_idx = tier_index_tensors(tb, S, B, H, keys.device)
+        cl = handle.compress_layer(keys, values, importance=importance)
+        if cl.near_idx is not None:
+            near_idx, far_idx = cl.near_idx, cl.far_idx
+        else:
+            near_idx, far_idx = tier_index_tensors(self.cfg.tier_boundaries(S), S, B, H, keys.device)
         return FoveatedLayer(near_k=cl.near_k, near_v=cl.near_v, near_idx=near_idx, far_k=cl.far_k,
                              far_v=cl.far_v, far_v_scale=cl.far_v_scale, far_v_zero=cl.far_v_zero,
                              far_idx=far_idx, archive_k=cl.archive_k, archive_v=cl.archive_v,

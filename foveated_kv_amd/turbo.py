@@ -290,16 +290,18 @@ class TurboFoveatedHandle(ext.FoveatedHandle):
         self._lib = lib
 
 
-def build_turbo_layer(cfg, keys, values):
+def build_turbo_layer(cfg, keys, values, importance=None):
     """The turbo branch of _assign_and_build_layer (mlx_foveated.py:799-944):
     near tier, archive and indices from the fused compress kernel, the far
     rows (fp16) compressed with TurboQuant; the fp8 far fields stay empty."""
     from .tier_cache import FoveatedLayer, tier_index_tensors
 
     B, H, S, D = keys.shape
-    cl = ext.CompressHandle(cfg.to_native()).compress_layer(keys, values)
-    tb = cfg.tier_boundaries(S)
-    near_idx, far_idx = tier_index_tensors(tb, S, B, H, keys.device)
+    cl = ext.CompressHandle(cfg.to_native()).compress_layer(keys, values, importance=importance)
+    if cl.near_idx is not None:
+        near_idx, far_idx = cl.near_idx, cl.far_idx
+    else:
+        near_idx, far_idx = tier_index_tensors(cfg.tier_boundaries(S), S, B, H, keys.device)
     tc = get_turbo_constants(D)
     dev = keys.device
     ki, ks, kn, kg = turbo_compress_keys(cl.archive_k, tc)

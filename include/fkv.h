@@ -89,6 +89,31 @@ int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, const void*
                        void* far_v_scale, void* far_v_zero, int32_t* near_valid,
                        void* archive_k, void* archive_v, void* stream);
 
+/* Importance partition.  The reference partitions by recency
+ * (mlx_foveated.py:128-169, 719-752); the benchmark configurations ask for
+ * "sinks + window + top-importance middle", which importance = position
+ * reproduces exactly.  importance (B,H,S) fp32 contiguous.  Per (b, h) the
+ * near middle is the near_from_mid middle tokens of highest importance,
+ * ties to the later token, NaN below every number, -0 == +0.  Writes
+ *   near_idx (B,H,Npad) int32: sinks, chosen middle (ascending), window,
+ *                              then -1 for the headroom slots
+ *   far_idx  (B,H,F)    int32: the rest of the middle, ascending
+ * with Npad/F from fkv_tier_boundaries(cfg, S).  One workgroup per (b, h):
+ * an 8-pass radix select of the rank key, then a stable compaction. */
+int fkv_partition_importance(const fkv_tier_config* cfg, const float* importance, int32_t B, int32_t H,
+                             int32_t S, int32_t* near_idx, int32_t* far_idx, void* stream);
+
+/* fkv_compress_layer from explicit index sets (as fkv_partition_importance
+ * writes them): near slot s < R_actual is the row near_idx[b,h,s], far row
+ * f is far_idx[b,h,f]; the archive holds the far rows in far_idx order.
+ * Indices outside [0,S) give zero rows.  Same outputs and codecs as
+ * fkv_compress_layer (which equals this with the recency index sets). */
+int fkv_compress_layer_indexed(const fkv_tier_config* cfg, const void* keys, const void* values,
+                               int32_t in_dtype, int32_t B, int32_t H, int32_t S, int32_t D,
+                               const int32_t* near_idx, const int32_t* far_idx, void* near_k, void* near_v,
+                               uint8_t* far_k, uint8_t* far_v, void* far_v_scale, void* far_v_zero,
+                               int32_t* near_valid, void* archive_k, void* archive_v, void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* fused attention handle (FoveatedHandle, csrc/foveated_attn.cpp:135-254)  */
 /* ---------------------------------------------------------------------- */

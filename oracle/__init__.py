@@ -171,6 +171,36 @@ def tier_indices(S, B, H, **cfg):
             np.broadcast_to(far, (B, H, far.size)).copy(), tb)
 
 
+def partition_importance(importance, S, B, H, **cfg):
+    """Importance partition (the BASELINE configs' "near = sinks + window +
+    top-importance middle"; the reference partitions by recency,
+    mlx_foveated.py:128-169, 719-752): per (b, h), the near_from_mid middle
+    tokens of highest importance, ties to the later token, NaN below every
+    number, -0 == +0.  -> near_idx (B,H,Npad) (sinks, chosen middle
+    ascending, window; -1 headroom), far_idx (B,H,F) (rest of the middle,
+    ascending), tb."""
+    tb = tier_boundaries(S, **cfg)
+    imp = np.broadcast_to(np.asarray(importance, np.float32), (B, H, S))
+    m0, m1, k = tb["mid_start"], tb["mid_end"], tb["near_from_mid"]
+    mid = np.arange(m0, max(m1, m0))
+    near = np.full((B, H, tb["N_near_padded"]), -1, np.int32)
+    far = np.zeros((B, H, tb["far_count"]), np.int32)
+    win = np.arange(S - tb["window"], S)
+    for b in range(B):
+        for h in range(H):
+            v = imp[b, h, mid].astype(np.float64)
+            v = np.where(np.isnan(v), -np.inf, v)
+            nan = np.isnan(imp[b, h, mid])
+            # sort by (not NaN, value, position) descending: NaN last, ties to the later token
+            order = np.lexsort((mid, v, ~nan))[::-1]
+            chosen = np.sort(mid[order[:k]])
+            rest = np.sort(mid[order[k:]])
+            seg = np.concatenate([np.arange(tb["n_sinks"]), chosen, win]).astype(np.int32)
+            near[b, h, :seg.size] = seg
+            far[b, h] = rest
+    return near, far, tb
+
+
 def compress_foveal(x, tb):
     """Near-tier gather (foveated_compress.metal:76-109): (B,H,S,D) fp16 ->
     (B,H,Npad,D) fp16 with zero headroom."""
@@ -186,23 +216,38 @@ def compress_foveal(x, tb):
     return dst.view(np.float16)
 
 
-def compress_layer(keys, values, v_group=0, **cfg):
+def _gather_rows(x, idx):
+    """x (B,H,S,D), idx (B,H,N) -> (B,H,N,D) with zero rows where idx < 0."""
+    safe = np.where(idx < 0, 0, idx)
+    out = np.take_along_axis(x, safe[..., None].astype(np.int64), axis=2)
+    out[idx < 0] = 0
+    return out
+
+
+def compress_layer(keys, values, v_group=0, importance=None, **cfg):
     """The whole fp8 compress of one layer (foveated_compress.cpp:95-201):
     returns dict with near_k/near_v/far_k/far_v/far_v_scale/far_v_zero/
     near_valid/near_idx/far_idx/archive_k/archive_v/tb.  v_group = 32
-    quantises V per 32-dim group (scales (B,H,F,D/32)) instead of per token."""
+    quantises V per 32-dim group (scales (B,H,F,D/32)) instead of per token;
+    ``importance`` selects the near middle by partition_importance."""
     keys = np.ascontiguousarray(keys, np.float16)
     values = np.ascontiguousarray(values, np.float16)
     B, H, S, D = keys.shape
-    near_idx, far_idx, tb = tier_indices(S, B, H, **cfg)
-    F = tb["far_count"]
-    far_sl = slice(tb["mid_start"], tb["mid_start"] + F)
-    fk_src = keys[:, :, far_sl]
-    fv_src = values[:, :, far_sl]
+    if importance is None:
+        near_idx, far_idx, tb = tier_indices(S, B, H, **cfg)
+        F = tb["far_count"]
+        far_sl = slice(tb["mid_start"], tb["mid_start"] + F)
+        fk_src = keys[:, :, far_sl]
+        fv_src = values[:, :, far_sl]
+        near_k, near_v = compress_foveal(keys, tb), compress_foveal(values, tb)
+    else:
+        near_idx, far_idx, tb = partition_importance(importance, S, B, H, **cfg)
+        fk_src, fv_src = _gather_rows(keys, far_idx), _gather_rows(values, far_idx)
+        near_k, near_v = _gather_rows(keys, near_idx), _gather_rows(values, near_idx)
     far_v, fvs, fvz = quant_int4_groups(fv_src, v_group) if v_group else quant_int4(fv_src)
     return {
-        "near_k": compress_foveal(keys, tb),
-        "near_v": compress_foveal(values, tb),
+        "near_k": near_k,
+        "near_v": near_v,
         "far_k": encode_fp8(fk_src),
         "far_v": far_v,
         "far_v_scale": fvs,

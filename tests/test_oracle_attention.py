@@ -260,3 +260,72 @@ def test_formulation_uses_max_near_valid(orc):
                                c["far_v_scale"], c["far_v_zero"])
     bf_max = brute_force(q, c, np.full_like(nv2, nv2.max()), None, None, fp16_v=True)
     assert np.abs(f - bf_max).max() < 1e-9
+
+
+# ---------------------------------------------------------------------------
+# importance partition (oracle.partition_importance)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("S", [0, 1, 3, 36, 37, 40, 100, 512, 1000, 4096])
+def test_importance_equal_to_position_is_the_recency_partition(orc, S):
+    n1, f1, _ = orc.tier_indices(S, 2, 3)
+    n2, f2, _ = orc.partition_importance(np.arange(S, dtype=np.float32), S, 2, 3)
+    assert np.array_equal(n1, n2) and np.array_equal(f1, f2)
+    # a constant importance ties everywhere: ties go to the later token
+    n3, f3, _ = orc.partition_importance(np.full(S, 0.5, np.float32), S, 2, 3)
+    assert np.array_equal(n1, n3) and np.array_equal(f1, f3)
+
+
+def test_importance_partition_brute_force_subsets(orc):
+    """The chosen middle maximises (sum of importance, sum of positions)
+    over every k-subset of the middle (exhaustive on small middles, integer
+    importances with many ties)."""
+    from itertools import combinations
+
+    cfg = dict(near_pct=0.5, n_sinks=2, window_size=3)
+    rng = np.random.default_rng(0)
+    for S in (12, 17, 20):
+        tb = orc.tier_boundaries(S, **cfg)
+        mid = list(range(tb["mid_start"], tb["mid_end"]))
+        k = tb["near_from_mid"]
+        for trial in range(6):
+            imp = rng.integers(0, 4, (1, 2, S)).astype(np.float32)
+            near, far, _ = orc.partition_importance(imp, S, 1, 2, **cfg)
+            for h in range(2):
+                best = max(combinations(mid, k), key=lambda c: (sum(imp[0, h, list(c)]), sum(c)))
+                got = near[0, h, tb["n_sinks"]:tb["n_sinks"] + k]
+                assert list(got) == sorted(best), (S, trial, h)
+                assert sorted(set(far[0, h]) | set(got)) == mid and len(far[0, h]) == len(mid) - k
+                assert list(near[0, h, :tb["n_sinks"]]) == list(range(tb["n_sinks"]))
+                assert list(near[0, h, tb["n_sinks"] + k:tb["R_actual"]]) == list(range(S - tb["window"], S))
+                assert np.all(near[0, h, tb["R_actual"]:] == -1)
+
+
+def test_importance_partition_special_values(orc):
+    cfg = dict(near_pct=0.5, n_sinks=1, window_size=1)
+    S = 12  # middle = positions 1..10, near_from_mid = 4
+    imp = np.zeros(S, np.float32)
+    imp[[2, 5]] = np.nan          # NaN ranks below everything, -inf included
+    imp[3] = -np.inf
+    imp[4] = np.inf
+    imp[6] = -0.0                 # -0 == +0: ties with the zeros, later token wins
+    imp[7] = 1.0
+    near, far, tb = orc.partition_importance(imp, S, 1, 1, **cfg)
+    assert tb["near_from_mid"] == 4
+    assert list(near[0, 0, 1:5]) == [4, 7, 9, 10]
+    assert list(far[0, 0]) == [1, 2, 3, 5, 6, 8]
+    imp2 = np.full(S, np.nan, np.float32)
+    imp2[1] = -np.inf
+    near2, _, _ = orc.partition_importance(imp2, S, 1, 1, **cfg)
+    assert list(near2[0, 0, 1:5]) == [1, 8, 9, 10]
+
+
+def test_compress_with_position_importance_matches_recency(orc):
+    rng = np.random.default_rng(3)
+    k = rng.standard_normal((2, 2, 300, 64)).astype(np.float16)
+    v = rng.standard_normal((2, 2, 300, 64)).astype(np.float16)
+    a = orc.compress_layer(k, v)
+    b = orc.compress_layer(k, v, importance=np.arange(300, dtype=np.float32))
+    for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale", "far_v_zero", "archive_k", "archive_v",
+              "near_idx", "far_idx"):
+        assert np.array_equal(np.asarray(a[n]).view(np.uint8), np.asarray(b[n]).view(np.uint8)), n
