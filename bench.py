@@ -109,6 +109,10 @@ def main():
     ap.add_argument("--config", default="c3_7b_16k_b8")
     ap.add_argument("--layers", type=int, default=0, help="distinct layer blobs (0: enough for > 1 GB)")
     ap.add_argument("--spikes", type=float, default=0.02)
+    ap.add_argument("--e2e", action="store_true",
+                    help="C5 end-to-end loop instead of the kernel line: importance partition + compress, then "
+                         "--e2e-steps decode steps of attention + spike drain + promotion on one 64K layer")
+    ap.add_argument("--e2e-steps", type=int, default=128)
     ap.add_argument("--v-group", type=int, default=0, choices=(0, 32),
                     help="fp8 far tier V: INT4 scale/zero per token (0) or per 32-dim group (32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -139,6 +143,9 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a ROCm GPU")
     dev = torch.device("cuda:0")
+    if args.e2e:
+        run_e2e(args, torch, dev)
+        return
     B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[args.config]
     cfg = ext.TierConfig()
     cfg.promo_headroom_min = 8
@@ -287,6 +294,97 @@ def main():
     elif not args.no_read_ceiling:
         # this box's streaming-read ceiling, measured beside the kernel
         result["read_ceiling_gbs"], _ = read_ceiling(torch, dev, 2048, sweep=False)
+    print(json.dumps(result), flush=True)
+
+
+def run_e2e(args, torch, dev):
+    """BASELINE C5: compress + decode + promote on one 70B-like layer (Hq=64,
+    Hkv=8, D=128, 64K context, B=1).  Seeded importance partition, 2 % of
+    far tokens aligned with the group query, per-step query drift, one
+    decode token appended per step, spike drain (GQA dedup, cooldown 5,
+    budget 8, the reference's filter) and promotion of exact fp16 rows from
+    the pinned host archive.  Prints one JSON line (us per decode step)."""
+    from foveated_kv_amd import ext, synthetic
+    from foveated_kv_amd.promotion import PromotionPipeline
+
+    B, Hq, Hkv, D, S, _ = synthetic.CONFIGS["c5_70b_64k"]
+    steps, seed = args.e2e_steps, args.seed
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = 8
+    cfg.v_group = args.v_group
+    k, v = synthetic.make_kv(B, Hkv, S, D, seed)
+    q0 = synthetic.make_query(B, Hq, D, seed)
+    imp = torch.from_numpy(synthetic.make_importance(B, Hkv, S, seed)).to(dev)
+    _, far_idx = ext.partition_importance(cfg, imp, B, Hkv, S)
+    far_idx = far_idx.cpu().numpy()
+    synthetic.inject_spikes_at(k, q0, far_idx, args.spikes, seed)
+    qs = torch.from_numpy(synthetic.drift_queries(q0, steps, 0.05, seed)).to(dev)[:, :, :, None, :]
+    dk, dv = synthetic.make_decode(B, Hkv, steps, D, seed)
+    dkt, dvt = torch.from_numpy(dk).to(dev), torch.from_numpy(dv).to(dev)
+    kt, vt = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+    print(f"[e2e] C5 B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps}", file=sys.stderr, flush=True)
+
+    def compress():
+        cl = ext.CompressHandle(cfg).compress_layer(kt, vt, importance=imp)
+        h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                               cl.near_valid, spike_margin=10.0)
+        return cl, h
+
+    compress()  # warm (module load, first launches)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    cl, h = compress()
+    torch.cuda.synchronize()
+    compress_ms = (time.perf_counter() - t0) * 1e3
+    pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_blob(0, h)
+    h(qs[0], dkt[:, :, :1], dvt[:, :, :1])  # allocates the call's split workspace
+    # the decode buffer as a step sees it: views of one preallocated buffer
+    torch.cuda.synchronize()
+    t_call = t_drain = 0.0
+    t0 = time.perf_counter()
+    n_flag = 0
+    for t in range(steps):
+        ta = time.perf_counter()
+        pipe.order(0)
+        out, flags, toks = h(qs[t], dkt[:, :, :t + 1], dvt[:, :, :t + 1])
+        tb_ = time.perf_counter()
+        pipe.drain_spikes(0, flags, toks, far_idx, t)  # reads the spike outputs on the host
+        n_flag += int(flags.sum().item())
+        t_call += tb_ - ta
+        t_drain += time.perf_counter() - tb_
+    pipe.synchronize()
+    torch.cuda.synchronize()
+    loop_s = time.perf_counter() - t0
+    stats = pipe.get_stats()
+    # device time of the attention call on the final state (queued back to back)
+    dk_end, dv_end = dkt.contiguous(), dvt.contiguous()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        h(qs[-1], dk_end, dv_end)
+    e1.record()
+    torch.cuda.synchronize()
+    attn_us = e0.elapsed_time(e1) * 1e3 / 20
+    result = {
+        "metric": "C5 end-to-end decode step (attention + spike drain + promotion), 70B-like layer, 64K ctx, 1 GPU",
+        "value": round(loop_s / steps * 1e6, 2), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": 0,
+        "ms_per_step": round(loop_s / steps * 1e3, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "c5_70b_64k_e2e", "B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S,
+                   "near_valid": int(cl.near_valid[0]), "far": int(cl.far_k.shape[2]),
+                   "headroom": int(cl.near_k.shape[2] - cl.near_valid[0]), "spike_frac": args.spikes,
+                   "partition": "importance (seeded N(0,1) scores)", "query_drift_eps": 0.05,
+                   "far_format": "fp8-e4m3 K + int4 group-32 V" if args.v_group else "fp8-e4m3 K + int4 per-token V"},
+        "compress_ms": round(compress_ms, 3),
+        "host_us_per_step": {"attention_call": round(t_call / steps * 1e6, 2),
+                             "spike_drain_and_promotion": round(t_drain / steps * 1e6, 2)},
+        "attn_us_device": round(attn_us, 3),
+        "flagged_heads": n_flag,
+        "promotion_stats": stats,
+        "near_valid_end": h.read_near_valid(),
+    }
     print(json.dumps(result), flush=True)
 
 

@@ -65,6 +65,51 @@ def inject_spikes(keys, q, far_start, far_count, frac, seed, score=14.0):
     return pos
 
 
+def inject_spikes_at(keys, q, far_idx, frac, seed, score=14.0):
+    """inject_spikes for a scattered far tier: ``far_idx`` (B, Hkv, F) holds
+    the far positions of each (b, kv head) (an importance partition)."""
+    if frac <= 0 or far_idx.shape[2] == 0:
+        return np.zeros(far_idx.shape[:2] + (0,), np.int64)
+    rng = np.random.default_rng(seed + 2)
+    B, Hkv, S, D = keys.shape
+    G = q.shape[1] // Hkv
+    F = far_idx.shape[2]
+    n = max(1, int(F * frac))
+    pos = np.zeros((B, Hkv, n), np.int64)
+    for b in range(B):
+        for h in range(Hkv):
+            qm = q[b, h * G:(h + 1) * G].astype(np.float32).mean(0)
+            u = qm / (np.linalg.norm(qm) + 1e-6)
+            alpha = score * np.sqrt(D) / (np.linalg.norm(qm) + 1e-6)
+            p = np.asarray(far_idx[b, h])[rng.choice(F, size=n, replace=False)]
+            noise = 0.05 * rng.standard_normal((n, D), dtype=np.float32)
+            keys[b, h, p] = (alpha * u[None] + noise).astype(np.float16)
+            pos[b, h] = np.sort(p)
+    return pos
+
+
+def make_importance(B, H, S, seed):
+    """Seeded importance scores (B, H, S) fp32 for the importance partition."""
+    rng = np.random.default_rng(seed + 4)
+    return rng.standard_normal((B, H, S), dtype=np.float32)
+
+
+def drift_queries(q0, steps, eps, seed):
+    """Per-step query drift q_t = |q_0| * unit(q_{t-1} + eps * |q_0| * u_t),
+    u_t ~ N(0, I/D) per head: (steps, B, Hq, D) fp16."""
+    rng = np.random.default_rng(seed + 5)
+    q = q0.astype(np.float32)
+    norm = np.linalg.norm(q, axis=-1, keepdims=True)
+    D = q.shape[-1]
+    out = np.empty((steps,) + q.shape, np.float16)
+    for t in range(steps):
+        u = rng.standard_normal(q.shape, dtype=np.float32) / np.sqrt(D)
+        q = q + eps * norm * u
+        q = q / (np.linalg.norm(q, axis=-1, keepdims=True) + 1e-12) * norm
+        out[t] = q.astype(np.float16)
+    return out
+
+
 def make_decode(B, Hkv, n_dec, D, seed):
     if n_dec == 0:
         return None, None

@@ -1,0 +1,83 @@
+"""End-to-end compress + decode + promote loop (the C5 workload at a
+reduced shape) on the GPU: importance partition, a growing decode buffer,
+per-step query drift that triggers spikes, and promotion of exact fp16 rows
+into the near headroom.  Every step's output and spike fields are checked
+against the oracle run on the state the CPU restatement of the promotion
+pipeline tracks; the final near tier is bit-exact."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import promotion as opromo
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,steps,vg", [(1, 16, 4, 128, 8192, 24, 0), (1, 14, 2, 64, 2048, 16, 32)])
+def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, steps, vg):
+    from foveated_kv_amd import ext, synthetic
+    from foveated_kv_amd.promotion import PromotionPipeline
+
+    seed = S + steps
+    print(f"e2e loop B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} v_group={vg}", flush=True)
+    k, v = synthetic.make_kv(B, Hkv, S, D, seed)
+    q0 = synthetic.make_query(B, Hq, D, seed)
+    imp = torch.from_numpy(synthetic.make_importance(B, Hkv, S, seed)).cuda()
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = 8
+    cfg.v_group = vg
+    _, far_idx = ext.partition_importance(cfg, imp, B, Hkv, S)
+    far_idx = _np(far_idx)
+    synthetic.inject_spikes_at(k, q0, far_idx, 0.02, seed)
+    cl = ext.CompressHandle(cfg).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                                importance=imp)
+    assert np.array_equal(_np(cl.far_idx), far_idx)
+    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                           cl.near_valid, spike_margin=10.0)
+    pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_blob(0, h)
+    ref = opromo.Pipeline(1, 5, 8)
+    ref.register_archive(0, _np(cl.archive_k), _np(cl.archive_v), far_idx[0])
+    near_k, near_v, nv = {0: _np(cl.near_k).copy()}, {0: _np(cl.near_v).copy()}, {0: _np(cl.near_valid).copy()}
+    far = [_np(getattr(cl, n)) for n in ("far_k", "far_v", "far_v_scale", "far_v_zero")]
+    qs = synthetic.drift_queries(q0, steps, 0.05, seed)
+    dk, dv = synthetic.make_decode(B, Hkv, steps, D, seed)
+    dkt, dvt = torch.from_numpy(dk).cuda(), torch.from_numpy(dv).cuda()
+    lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    flagged = 0
+    for t in range(steps):
+        pipe.order(0)
+        q = torch.from_numpy(qs[t]).cuda()
+        n = t + 1
+        out, flags, toks = h(q[:, :, None], dkt[:, :, :n].contiguous(), dvt[:, :, :n].contiguous())
+        torch.cuda.synchronize()
+        o, kf, kt, mf, mn = orc.attend_kernel(qs[t], near_k[0], near_v[0], nv[0], *far, dk[:, :, :n], dv[:, :, :n],
+                                              spike_margin=10.0)
+        got = _np(out)[:, :, 0].astype(np.float64)
+        err, cos = np.abs(got - o).max(), orc.cosine(got, o)
+        assert err <= 2e-3 and cos >= 0.9999, (t, err, cos)
+        fl, tk = _np(flags), _np(toks)
+        for b, hq in np.argwhere(fl != kf):
+            assert abs(mf[b, hq] - mn[b, hq] - 10.0) < 1e-4, (t, b, hq)
+        for b, hq in np.argwhere(tk != kt):  # only on a near tie of the exact far scores
+            qs32 = qs[t][b, hq].astype(np.float32) * np.float32(1 / np.sqrt(np.float32(D)))
+            sc = lut[far[0][b, hq // (Hq // Hkv)]] @ qs32.astype(np.float64)
+            assert abs(sc[tk[b, hq]] - sc[kt[b, hq]]) <= 1e-5 * (1 + abs(sc.max())), (t, b, hq)
+        flagged += int(fl.sum())
+        # both pipelines see the GPU's spike outputs, so their states stay comparable
+        pipe.drain_spikes(0, flags, toks, far_idx, t)
+        ref.drain(0, fl, tk, far_idx, t)
+        ref.commit(near_k, near_v, nv, {0: cl.near_k.shape[2]})
+    pipe.synchronize()
+    gk, gv = h.export_near()
+    assert flagged > 0 and ref.stats["promotions_completed"] > 0
+    assert h.read_near_valid() == [int(x) for x in nv[0]]
+    assert np.array_equal(_np(gk).view(np.uint16), near_k[0].view(np.uint16))
+    assert np.array_equal(_np(gv).view(np.uint16), near_v[0].view(np.uint16))
+    assert pipe.get_stats() == ref.stats
