@@ -319,6 +319,76 @@ __device__ inline float quad_bcast(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), I * 0x55, 0xF, 0xF, false));
 }
 
+// Cross-lane reductions over the 16 lanes that share lane % 4 (one head of
+// a quad) without LDS permutes: DPP row rotations by 4 and 8 lanes cover a
+// row of 16, v_permlane16_swap / v_permlane32_swap the other rows.  A swap
+// returns (this lane's new vdst, new vsrc); with vdst = vsrc = v the pair is
+// {v[l], v[l ^ 16]} (or ^ 32) in an order that depends on the lane, so only
+// symmetric combinations of the two are taken.
+template <int N>
+__device__ inline uint32_t row_ror(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x120 + N, 0xF, 0xF, false);
+}
+struct LanePair {
+    uint32_t a, b;
+};
+__device__ inline LanePair swap16(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return {r[0], r[1]};
+}
+__device__ inline LanePair swap32(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return {r[0], r[1]};
+}
+// max over the lanes l' = l (mod 4) of the wave
+__device__ inline float head_max(float v) {
+    v = fmaxf(v, __uint_as_float(row_ror<4>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(row_ror<8>(__float_as_uint(v))));
+    LanePair p = swap16(__float_as_uint(v));
+    v = fmaxf(__uint_as_float(p.a), __uint_as_float(p.b));
+    p = swap32(__float_as_uint(v));
+    return fmaxf(__uint_as_float(p.a), __uint_as_float(p.b));
+}
+__device__ inline float head_min(float v) {
+    v = fminf(v, __uint_as_float(row_ror<4>(__float_as_uint(v))));
+    v = fminf(v, __uint_as_float(row_ror<8>(__float_as_uint(v))));
+    LanePair p = swap16(__float_as_uint(v));
+    v = fminf(__uint_as_float(p.a), __uint_as_float(p.b));
+    p = swap32(__float_as_uint(v));
+    return fminf(__uint_as_float(p.a), __uint_as_float(p.b));
+}
+// sum over the lanes l' = l (mod 4) of this lane's 32-lane half (WHOLE = false)
+// or of the whole wave
+template <bool WHOLE>
+__device__ inline float head_sum(float v) {
+    v += __uint_as_float(row_ror<4>(__float_as_uint(v)));
+    v += __uint_as_float(row_ror<8>(__float_as_uint(v)));
+    LanePair p = swap16(__float_as_uint(v));
+    v = __uint_as_float(p.a) + __uint_as_float(p.b);
+    if (WHOLE) {
+        p = swap32(__float_as_uint(v));
+        v = __uint_as_float(p.a) + __uint_as_float(p.b);
+    }
+    return v;
+}
+// (max, first index of the max) over the lanes l' = l (mod 4)
+__device__ inline void pick_max(float& mx, int& arg, float ox, int oa) {
+    if (ox > mx || (ox == mx && oa < arg)) { mx = ox; arg = oa; }
+}
+__device__ inline void head_argmax(float& mx, int& arg) {
+    pick_max(mx, arg, __uint_as_float(row_ror<4>(__float_as_uint(mx))), (int)row_ror<4>((uint32_t)arg));
+    pick_max(mx, arg, __uint_as_float(row_ror<8>(__float_as_uint(mx))), (int)row_ror<8>((uint32_t)arg));
+    LanePair pm = swap16(__float_as_uint(mx)), pa = swap16((uint32_t)arg);
+    mx = __uint_as_float(pm.a);
+    arg = (int)pa.a;
+    pick_max(mx, arg, __uint_as_float(pm.b), (int)pa.b);
+    pm = swap32(__float_as_uint(mx));
+    pa = swap32((uint32_t)arg);
+    mx = __uint_as_float(pm.a);
+    arg = (int)pa.a;
+    pick_max(mx, arg, __uint_as_float(pm.b), (int)pa.b);
+}
+
 __device__ inline uint32_t word_of(const uint4& x, int i) {
     return i == 0 ? x.x : i == 1 ? x.y : i == 2 ? x.z : x.w;
 }
@@ -548,8 +618,7 @@ template <int D, int NQ, bool FAR>
 __device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], const uint32_t (&sz)[4],
                                  fkv_h4& w4) {
     float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-#pragma unroll
-    for (int o = 4; o <= 32; o <<= 1) cmax = fmaxf(cmax, wave_xor(cmax, o));
+    cmax = head_max(cmax);
     const float m_new = fmaxf(st.m[qd], cmax);
     if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
         rescale<D, NQ>(st, qd, m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f);
@@ -813,8 +882,7 @@ __device__ inline void lds_q<2>(const uint16_t* p, fkv_h4 (&o)[2]) {
 template <int D, int NQ>
 __device__ inline bool tq_softmax(Lane<D, NQ>& st, int qd, const float (&s)[4], float (&p)[4]) {
     float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-#pragma unroll
-    for (int o = 4; o <= 32; o <<= 1) cmax = fmaxf(cmax, wave_xor(cmax, o));
+    cmax = head_max(cmax);
     const float m_new = fmaxf(st.m[qd], cmax);
     if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
         rescale<D, NQ>(st, qd, m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f);
@@ -1354,6 +1422,62 @@ __device__ inline float ld_agent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The last split of a row when all records fit in LDS: one batch of
+// coherent loads (every load issued before the first wait), then each
+// thread merges its output elements straight into the outputs -- the same
+// arithmetic, in the same order, as merge_splits + finalize_rows.
+template <int D>
+__device__ inline void merge_finalize_staged(const AttnArgs& a, const float* src, int ns, int ng, float* stage,
+                                             int b, int head0) {
+    constexpr int RS = kHdr + D;
+    constexpr int kBatch = 16;
+    const int total = ns * ng * RS;
+    const int nt = (int)blockDim.x, t = (int)threadIdx.x;
+    for (int base = 0; base < total; base += kBatch * nt) {
+        float r[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; k++) {
+            const int i = base + k * nt + t;
+            r[k] = ld_agent(src + (i < total ? i : total - 1));
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; k++) {
+            const int i = base + k * nt + t;
+            if (i < total) stage[i] = r[k];
+        }
+    }
+    __syncthreads();
+    for (int i = t; i < ng * D; i += nt) {
+        const int g = i / D, d = i % D;
+        float M = -INFINITY;
+        for (int sp = 0; sp < ns; sp++) M = fmaxf(M, stage[(sp * ng + g) * RS]);
+        float L = 0.f, v = 0.f;
+        for (int sp = 0; sp < ns; sp++) {
+            const float* h = stage + (sp * ng + g) * RS;
+            const float f = h[0] == -INFINITY ? 0.f : __expf(h[0] - M);
+            L += f * h[1];
+            v += f * h[kHdr + d];
+        }
+        const float inv_l = L > 0.f ? 1.0f / L : 0.f;
+        a.out[((int64_t)b * a.Hq + head0 + g) * D + d] = f2h(v * inv_l);
+    }
+    if (t < ng) {
+        const int g = t;
+        float mn = INFINITY, mx = -INFINITY;
+        int arg = INT_MAX;
+        for (int sp = 0; sp < ns; sp++) {
+            const float* h = stage + (sp * ng + g) * RS;
+            mn = fminf(mn, h[2]);
+            const float fx = h[3];
+            const int fa = __float_as_int(h[4]);
+            if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
+        }
+        const int64_t o = (int64_t)b * a.Hq + head0 + g;
+        a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
+        a.tokens[o] = mx == -INFINITY ? -1 : arg;
+    }
+}
+
 template <int D>
 __device__ inline void merge_splits(const float* src, int ns, int ng, float* fin, float* hdr, float* scl,
                                     float* stage, int stage_cap) {
@@ -1629,16 +1753,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     float* wr = smem + wave * NHW * RS;
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
-        float l = st.lsum[qd], mn = st.mn[qd], mx = st.mx[qd];
+        const float l = head_sum<true>(st.lsum[qd]), mn = head_min(st.mn[qd]);
+        float mx = st.mx[qd];
         int arg = st.arg[qd];
-#pragma unroll
-        for (int o = 4; o <= 32; o <<= 1) {
-            l += wave_xor(l, o);
-            mn = fminf(mn, wave_xor(mn, o));
-            const float ox = wave_xor(mx, o);
-            const int oa = wave_xor(arg, o);
-            if (ox > mx || (ox == mx && oa < arg)) { mx = ox; arg = oa; }
-        }
+        head_argmax(mx, arg);
         // INT4 correction of head j (per 64-dim half dh): minus the +16
         // decode offset and the 7.5 centring, plus the zero points.
         // Group-32 V: the lane's dims are group 2dh + half; its own half's
@@ -1649,24 +1767,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             const int half = lane >> 5;
 #pragma unroll
             for (int dh = 0; dh < NH; dh++) {
-                float zo = st.zsum[qd][dh], wo = st.wsum[qd][dh];
-                float zx = st.zsum[qd][NH + dh], wx = st.wsum[qd][NH + dh];
-#pragma unroll
-                for (int o = 4; o <= 16; o <<= 1) {
-                    zo += wave_xor(zo, o);
-                    wo += wave_xor(wo, o);
-                    zx += wave_xor(zx, o);
-                    wx += wave_xor(wx, o);
-                }
+                const float zo = head_sum<false>(st.zsum[qd][dh]), wo = head_sum<false>(st.wsum[qd][dh]);
+                const float zx = head_sum<false>(st.zsum[qd][NH + dh]), wx = head_sum<false>(st.wsum[qd][NH + dh]);
                 corr[dh] = (zo - 23.5f * wo) + swap_halves(zx - 23.5f * wx, half);
             }
         } else {
-            float z = st.zsum[qd][0], ws = st.wsum[qd][0];
-#pragma unroll
-            for (int o = 4; o <= 32; o <<= 1) {
-                z += wave_xor(z, o);
-                ws += wave_xor(ws, o);
-            }
+            const float z = head_sum<true>(st.zsum[qd][0]), ws = head_sum<true>(st.wsum[qd][0]);
 #pragma unroll
             for (int dh = 0; dh < NH; dh++) corr[dh] = z - 23.5f * ws;
         }
@@ -1749,11 +1855,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
-    float* hdr = smem + NHW * RS;
-    float* scl = hdr + kMaxSplits * NHW * kHdr;
-    float* stage = scl + NHW * kMaxSplits;
-    merge_splits<D>(part, a.num_splits, ng, smem, hdr, scl, stage, kLds / 4 - (int)(stage - smem));
-    finalize_rows<D>(a, smem, b, head0, ng);
+    if (a.num_splits * ng * RS <= kLds / 4) {
+        // every record (this split's included) is in global memory now: the
+        // whole LDS can stage them
+        merge_finalize_staged<D>(a, part, a.num_splits, ng, smem, b, head0);
+    } else {
+        float* hdr = smem + NHW * RS;
+        float* scl = hdr + kMaxSplits * NHW * kHdr;
+        float* stage = scl + NHW * kMaxSplits;
+        merge_splits<D>(part, a.num_splits, ng, smem, hdr, scl, stage, kLds / 4 - (int)(stage - smem));
+        finalize_rows<D>(a, smem, b, head0, ng);
+    }
     if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
