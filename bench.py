@@ -113,6 +113,8 @@ def main():
                     help="C5 end-to-end loop instead of the kernel line: importance partition + compress, then "
                          "--e2e-steps decode steps of attention + spike drain + promotion on one 64K layer")
     ap.add_argument("--e2e-steps", type=int, default=128)
+    ap.add_argument("--no-group32", action="store_true",
+                    help="C3 configs: skip the group-32 V layout measured beside the per-token headline")
     ap.add_argument("--v-group", type=int, default=0, choices=(0, 32),
                     help="fp8 far tier V: INT4 scale/zero per token (0) or per 32-dim group (32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -163,6 +165,14 @@ def main():
     kt = torch.from_numpy(k).to(dev)
     vt = torch.from_numpy(v).to(dev)
     cl = ext.CompressHandle(cfg).compress_layer(kt, vt, with_archive=turbo)
+    # BASELINE's C3 names the group-32 V layout: measured beside the
+    # reference's per-token layout in the same run (not the headline value)
+    g32_side = args.config.startswith("c3_") and cfg.v_group == 0 and not args.no_group32
+    if g32_side:
+        cfg32 = ext.TierConfig()
+        cfg32.promo_headroom_min = 8
+        cfg32.v_group = 32
+        cl32 = ext.CompressHandle(cfg32).compress_layer(kt, vt, with_archive=False)
     del kt, vt
     if turbo:
         from foveated_kv_amd import turbo as tq
@@ -184,62 +194,12 @@ def main():
 
     nbytes = (algorithmic_bytes_turbo(B, Hq, Hkv, D, R, F, n_dec) if turbo
               else algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec, cfg.v_group))
-    blob_bytes = None
-    handles = []
-    L = args.layers
-    while True:
-        h = make_handle()
-        handles.append(h)
-        blob_bytes = h.get_blob_info().blob_bytes
-        if (L and len(handles) >= L) or (not L and len(handles) * blob_bytes > (1 << 30) and len(handles) >= 4):
-            break
-    L = len(handles)
-    print(f"[bench] {L} layer blobs x {blob_bytes / 2**20:.1f} MiB; algorithmic {nbytes / 1e6:.2f} MB/layer",
-          file=sys.stderr, flush=True)
-
-    # eager warm-up (allocates the split workspace outside graph capture)
-    for h in handles:
-        h(qt, dkt, dvt)
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.Stream(device=dev)
-    outs = []
-    if args.eager:
-        def step():
-            for h in handles:
-                h(qt, dkt, dvt)
-        with torch.cuda.stream(stream):
-            outs = [h(qt, dkt, dvt) for h in handles]
-    else:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(graph, stream=stream):
-                for h in handles:
-                    outs.append(h(qt, dkt, dvt))
-        step = graph.replay
-    torch.cuda.synchronize()
-
-    with torch.cuda.stream(stream):
-        for _ in range(args.warmup):
-            step()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        for _ in range(args.steps):
-            step()
-        end.record(stream)
-    torch.cuda.synchronize()
-    ms_total = start.elapsed_time(end)
-    ms_step = ms_total / args.steps
+    L, blob_bytes, ms_step = time_layers(torch, dev, make_handle, args.layers, qt, dkt, dvt, args.steps,
+                                         args.warmup, args.eager)
     us_layer = ms_step * 1000.0 / L
     gbs = nbytes / (us_layer * 1e-6) / 1e9
-
-    # sanity: graph output equals eager output for layer 0
-    eager = handles[0](qt, dkt, dvt)
-    torch.cuda.synchronize()
-    assert torch.equal(eager[0], outs[0][0]) and torch.equal(eager[2], outs[0][2]), "graph replay diverged"
+    print(f"[bench] {L} layer blobs x {blob_bytes / 2**20:.1f} MiB; algorithmic {nbytes / 1e6:.2f} MB/layer; "
+          f"{us_layer:.3f} us/layer", file=sys.stderr, flush=True)
 
     result = {
         "metric": METRIC,
@@ -264,6 +224,19 @@ def main():
         "launch": "eager" if args.eager else "hip-graph",
         "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
     }
+    if g32_side:
+        def make32():
+            return ext.FoveatedHandle(cl.near_k, cl.near_v, cl32.far_k, cl32.far_v, cl32.far_v_scale,
+                                      cl32.far_v_zero, cl.near_valid, spike_margin=10.0)
+        L32, _, ms32 = time_layers(torch, dev, make32, args.layers, qt, dkt, dvt, args.steps, args.warmup,
+                                   args.eager)
+        b32 = algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec, 32)
+        us32 = ms32 * 1000.0 / L32
+        result["group32_v"] = {"far_format": "fp8-e4m3 K + int4 group-32 V", "us_per_layer": round(us32, 3),
+                               "gbs": round(b32 / (us32 * 1e-6) / 1e9, 2),
+                               "pct_peak": round(100.0 * b32 / (us32 * 1e-6) / 1e9 / PEAK_GBS, 2),
+                               "algorithmic_bytes": b32, "layers_per_step": L32}
+        del cl32
     traffic = read_traffic(args.traffic) if args.config == "c3_7b_16k_b8" and not cfg.v_group else None
     result["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_GBS, "unit": "GB/s",
                           "frac": round(gbs / PEAK_GBS, 4), "traffic": traffic,
@@ -295,6 +268,60 @@ def main():
         # this box's streaming-read ceiling, measured beside the kernel
         result["read_ceiling_gbs"], _ = read_ceiling(torch, dev, 2048, sweep=False)
     print(json.dumps(result), flush=True)
+
+
+def time_layers(torch, dev, make_handle, layers, qt, dkt, dvt, steps, warmup, eager):
+    """Build distinct layer handles (> 1 GiB of blobs unless ``layers``), run
+    one decode step over all of them as a HIP graph (or eagerly), time
+    ``steps`` steps with HIP events on the replay stream.  Returns (layers,
+    blob bytes, ms per step); checks that a replay equals an eager call."""
+    handles = []
+    blob_bytes = None
+    while True:
+        h = make_handle()
+        handles.append(h)
+        blob_bytes = h.get_blob_info().blob_bytes
+        if (layers and len(handles) >= layers) or (not layers and len(handles) * blob_bytes > (1 << 30)
+                                                   and len(handles) >= 4):
+            break
+    # eager warm-up (allocates the split workspace outside graph capture)
+    for h in handles:
+        h(qt, dkt, dvt)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    outs = []
+    if eager:
+        def step():
+            for h in handles:
+                h(qt, dkt, dvt)
+        with torch.cuda.stream(stream):
+            outs = [h(qt, dkt, dvt) for h in handles]
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for h in handles:
+                    outs.append(h(qt, dkt, dvt))
+        step = graph.replay
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(steps):
+            step()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / steps
+    # sanity: graph output equals eager output for layer 0
+    ref = handles[0](qt, dkt, dvt)
+    torch.cuda.synchronize()
+    assert torch.equal(ref[0], outs[0][0]) and torch.equal(ref[2], outs[0][2]), "graph replay diverged"
+    return len(handles), blob_bytes, ms_step
 
 
 def run_e2e(args, torch, dev):
@@ -350,8 +377,10 @@ def run_e2e(args, torch, dev):
         pipe.order(0)
         out, flags, toks = h(qs[t], dkt[:, :, :t + 1], dvt[:, :, :t + 1])
         tb_ = time.perf_counter()
-        pipe.drain_spikes(0, flags, toks, far_idx, t)  # reads the spike outputs on the host
-        n_flag += int(flags.sum().item())
+        # the drain reads the spike outputs on the host (one copy, as the reference's drain does)
+        both = torch.stack([flags, toks]).cpu().numpy()
+        pipe.drain_spikes(0, both[0], both[1], far_idx, t)
+        n_flag += int(both[0].sum())
         t_call += tb_ - ta
         t_drain += time.perf_counter() - tb_
     pipe.synchronize()

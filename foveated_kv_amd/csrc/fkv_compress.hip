@@ -213,11 +213,13 @@ constexpr int kPartThreads = 1024;
 __global__ __launch_bounds__(kPartThreads) void partition_kernel(const float* __restrict__ imp, int S, fkv_tiers tb,
                                                                 int32_t* __restrict__ near_idx,
                                                                 int32_t* __restrict__ far_idx) {
-    __shared__ uint32_t hist[256];
+    constexpr int NW = kPartThreads / 64;
+    __shared__ uint32_t hist[NW][256];  // one histogram per wave (less atomic contention)
     __shared__ uint64_t s_prefix;
     __shared__ int s_rem;
-    __shared__ int wcount[2][kPartThreads / 64];
+    __shared__ int wcount[2][NW];
     const int bh = blockIdx.x, tid = threadIdx.x;
+    const int wave = tid / 64, lane = tid % 64;
     const float* row = imp + (int64_t)bh * S;
     const int npad = tb.n_near_padded, F = tb.far_count;
     const int m0 = tb.mid_start;
@@ -237,21 +239,36 @@ __global__ __launch_bounds__(kPartThreads) void partition_kernel(const float* __
         uint64_t prefix = 0, mask = 0;
         int rem = k;
         for (int p = 7; p >= 0; p--) {
-            for (int i = tid; i < 256; i += kPartThreads) hist[i] = 0;
+            for (int i = tid; i < NW * 256; i += kPartThreads) (&hist[0][0])[i] = 0;
             __syncthreads();
             for (int i = tid; i < mlen; i += kPartThreads) {
                 const uint64_t key = rank_key(row, m0 + i);
-                if ((key & mask) == prefix) atomicAdd(&hist[(key >> (8 * p)) & 255], 1u);
+                if ((key & mask) == prefix) atomicAdd(&hist[wave][(key >> (8 * p)) & 255], 1u);
             }
             __syncthreads();
-            if (tid == 0) {
-                int cum = 0, b = 255;
-                for (; b > 0; b--) {
-                    if (cum + (int)hist[b] >= rem) break;
-                    cum += (int)hist[b];
+            if (wave == 0) {
+                // lane l holds bins 4l..4l+3; the bin holding the rem-th largest
+                // key is the one where the count of larger keys crosses rem
+                uint32_t c[4] = {0, 0, 0, 0};
+                for (int w = 0; w < NW; w++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) c[e] += hist[w][4 * lane + e];
+                const uint32_t tot = c[0] + c[1] + c[2] + c[3];
+                uint32_t suf = tot;  // inclusive suffix sum over lanes >= l
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const uint32_t t = __shfl_down(suf, d, 64);
+                    if (lane + d < 64) suf += t;
                 }
-                s_prefix = prefix | ((uint64_t)b << (8 * p));
-                s_rem = rem - cum;
+                uint32_t cum = suf - tot;  // keys in bins above this lane's
+#pragma unroll
+                for (int e = 3; e >= 0; e--) {
+                    if (cum < (uint32_t)rem && cum + c[e] >= (uint32_t)rem) {
+                        s_prefix = prefix | ((uint64_t)(4 * lane + e) << (8 * p));
+                        s_rem = rem - (int)cum;
+                    }
+                    cum += c[e];
+                }
             }
             __syncthreads();
             prefix = s_prefix;
@@ -261,7 +278,6 @@ __global__ __launch_bounds__(kPartThreads) void partition_kernel(const float* __
         thr = prefix;
     }
     // compaction in position order
-    const int wave = tid / 64, lane = tid % 64;
     int near_base = 0, far_base = 0;
     for (int c0 = 0; c0 < mlen; c0 += kPartThreads) {
         const int i = c0 + tid;
@@ -277,7 +293,7 @@ __global__ __launch_bounds__(kPartThreads) void partition_kernel(const float* __
         }
         __syncthreads();
         int wn = 0, wf = 0, tn = 0, tf = 0;
-        for (int w = 0; w < kPartThreads / 64; w++) {
+        for (int w = 0; w < NW; w++) {
             if (w < wave) {
                 wn += wcount[0][w];
                 wf += wcount[1][w];

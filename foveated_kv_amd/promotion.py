@@ -101,8 +101,14 @@ class PromotionPipeline:
         (B, H_kv, N_far).  Returns the number of promotions queued."""
         if self._stopped:
             return 0
-        flags = _host_i32(spike_flags)
-        tokens = _host_i32(spike_tokens)
+        if isinstance(spike_flags, torch.Tensor) and isinstance(spike_tokens, torch.Tensor) and \
+                spike_flags.is_cuda and spike_flags.shape == spike_tokens.shape:
+            # one device-to-host copy (one synchronisation) for both outputs
+            both = torch.stack([spike_flags.to(torch.int32), spike_tokens.to(torch.int32)]).cpu().numpy()
+            flags, tokens = np.ascontiguousarray(both[0]), np.ascontiguousarray(both[1])
+        else:
+            flags = _host_i32(spike_flags)
+            tokens = _host_i32(spike_tokens)
         fidx = _host_i32(far_idx)
         B, Hq = flags.shape[0], flags.shape[1]
         Hkv, n_far = fidx.shape[1], fidx.shape[2]
