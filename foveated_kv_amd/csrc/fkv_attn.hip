@@ -451,9 +451,11 @@ template <int D, int NQ>
 struct Lane {
     // per head quad: this lane tracks head 4*qd + (lane % 4)
     float m[NQ], lsum[NQ], mn[NQ], mx[NQ];
-    // INT4 zero-point terms (per token V: index 0; group-32 V: [dh] for the
-    // group of the lane's own half, [D/64 + dh] for the other half's group)
-    float zsum[NQ][D / 32], wsum[NQ][D / 32];
+    // INT4 correction terms, sum of p*(zero + 7.5*scale) - 23.5*w over the
+    // lane's tokens (w: the fp16 P.V weight; removes the +16 decode offset
+    // and the 7.5 centring).  Per token V: index 0; group-32 V: [dh] for the
+    // group of the lane's own half, [D/64 + dh] for the other half's group.
+    float zsum[NQ][D / 32];
     int arg[NQ];
     fkv_f4 acc[NQ][D / 64];  // acc[qd][dh][i] = O[head 4qd+i][dim 64dh + lane]
 };
@@ -466,7 +468,6 @@ __device__ inline void rescale(Lane<D, NQ>& st, int qd, float alpha) {
 #pragma unroll
     for (int z = 0; z < D / 32; z++) {
         st.zsum[qd][z] *= alpha;
-        st.wsum[qd][z] *= alpha;
     }
     const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
     const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
@@ -625,6 +626,7 @@ __device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], c
         st.m[qd] = m_new;
     }
     _Float16 wh[4];
+    float pe[4], ce[4];
     bool any = false;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -634,19 +636,21 @@ __device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], c
         } else if (s[e] != -INFINITY) {
             p = __expf(s[e] - st.m[qd]);
         }
-        st.lsum[qd] += p;
+        pe[e] = p;
         if (FAR) {
             const float vs = h2f((uint16_t)(sz[e] & 0xFFFF));
             const float vz = h2f((uint16_t)(sz[e] >> 16));
             wh[e] = (_Float16)(p * vs);
-            // value = vs*(c - 7.5) + (vz + 7.5*vs); the MFMA sees wh*(16 + c)
-            st.zsum[qd][0] += p * (vz + 7.5f * vs);
-            st.wsum[qd][0] += (float)wh[e];
+            // value = vs*(c - 7.5) + (vz + 7.5*vs) and the MFMA sees wh*(16 + c):
+            // the token adds p*(vz + 7.5*vs) - 23.5*wh
+            ce[e] = fmaf(-23.5f, (float)wh[e], p * (vz + 7.5f * vs));
         } else {
             wh[e] = (_Float16)p;
         }
         any |= p > 0.f;
     }
+    st.lsum[qd] += (pe[0] + pe[1]) + (pe[2] + pe[3]);
+    if (FAR) st.zsum[qd][0] += (ce[0] + ce[1]) + (ce[2] + ce[3]);
     w4 = fkv_h4{wh[0], wh[1], wh[2], wh[3]};
     return any;
 }
@@ -1191,6 +1195,7 @@ __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, in
 #pragma unroll
         for (int qd = 0; qd < NQ; qd++) {
             _Float16 a1[4], a2[4];
+            float c1[4], c2[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 // group 2dh + half (own) and 2dh + 1 - half (other), selected
@@ -1201,12 +1206,13 @@ __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, in
                 const float s2 = h2f((uint16_t)(z2 & 0xFFFF)), o2 = h2f((uint16_t)(z2 >> 16));
                 a1[e] = (_Float16)(p[qd][e] * s1);
                 a2[e] = (_Float16)(p[qd][e] * s2);
-                // value = s*(c - 7.5) + (z + 7.5*s); the MFMA sees w*(16 + c)
-                st.zsum[qd][dh] += p[qd][e] * (o1 + 7.5f * s1);
-                st.wsum[qd][dh] += (float)a1[e];
-                st.zsum[qd][NH + dh] += p[qd][e] * (o2 + 7.5f * s2);
-                st.wsum[qd][NH + dh] += (float)a2[e];
+                // value = s*(c - 7.5) + (z + 7.5*s) and the MFMA sees w*(16 + c)
+                // with w the fp16 weight: the token adds p*(z + 7.5*s) - 23.5*w
+                c1[e] = fmaf(-23.5f, (float)a1[e], p[qd][e] * (o1 + 7.5f * s1));
+                c2[e] = fmaf(-23.5f, (float)a2[e], p[qd][e] * (o2 + 7.5f * s2));
             }
+            st.zsum[qd][dh] += (c1[0] + c1[1]) + (c1[2] + c1[3]);
+            st.zsum[qd][NH + dh] += (c2[0] + c2[1]) + (c2[2] + c2[3]);
             w1[dh][qd] = fkv_h4{a1[0], a1[1], a1[2], a1[3]};
             const uint2 x = __builtin_bit_cast(uint2, fkv_h4{a2[0], a2[1], a2[2], a2[3]});
             const uint2 y = make_uint2(__float_as_uint(swap_halves(__uint_as_float(x.x), half)),
@@ -1694,7 +1700,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         st.m[qd] = -INFINITY;
         st.lsum[qd] = 0.f;
 #pragma unroll
-        for (int z = 0; z < D / 32; z++) st.zsum[qd][z] = st.wsum[qd][z] = 0.f;
+        for (int z = 0; z < D / 32; z++) st.zsum[qd][z] = 0.f;
         st.mn[qd] = INFINITY;
         st.mx[qd] = -INFINITY;
         st.arg[qd] = INT_MAX;
@@ -1767,14 +1773,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             const int half = lane >> 5;
 #pragma unroll
             for (int dh = 0; dh < NH; dh++) {
-                const float zo = head_sum<false>(st.zsum[qd][dh]), wo = head_sum<false>(st.wsum[qd][dh]);
-                const float zx = head_sum<false>(st.zsum[qd][NH + dh]), wx = head_sum<false>(st.wsum[qd][NH + dh]);
-                corr[dh] = (zo - 23.5f * wo) + swap_halves(zx - 23.5f * wx, half);
+                const float zo = head_sum<false>(st.zsum[qd][dh]);
+                const float zx = head_sum<false>(st.zsum[qd][NH + dh]);
+                corr[dh] = zo + swap_halves(zx, half);
             }
         } else {
-            const float z = head_sum<true>(st.zsum[qd][0]), ws = head_sum<true>(st.wsum[qd][0]);
+            const float z = head_sum<true>(st.zsum[qd][0]);
 #pragma unroll
-            for (int dh = 0; dh < NH; dh++) corr[dh] = z - 23.5f * ws;
+            for (int dh = 0; dh < NH; dh++) corr[dh] = z;
         }
         const int h = 4 * qd + j;
         if (lane < 4 && h < ng) {
