@@ -130,9 +130,6 @@ struct fkv_attn_impl {
     int near_plan = 0;      // expected near tiles per row: max near_valid / 64, rounded up
     int device = 0;
     fkv::TurboConsts tq;    // fmt 1 only
-    uint16_t* tq_q = nullptr;  // (B, Hq, 2, D) fp16: rotated query, sketched query
-    float* tq_asum = nullptr;  // (B, Hq) alpha * sum of the rotated query
-    size_t tq_q_n = 0;
 };
 
 struct fkv_attn : fkv_attn_impl {};
@@ -146,9 +143,5 @@ int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, 
                const void* near_v, int near_dtype, const int32_t* near_valid, float margin, hipStream_t st);
 // Synchronous end of construction: reads near_valid back for the split plan.
 int attn_finish(fkv_attn_impl* h, hipStream_t st);
-
-// Launches the query rotation / sketch of a TurboQuant handle for one call
-// (fkv_turbo.hip); q16 is the fp16 query (B, Hq, D).
-int tq_prepare_query(fkv_attn_impl* h, const uint16_t* q16, int Hq, hipStream_t st);
 
 }  // namespace fkv

@@ -277,8 +277,9 @@ struct AttnArgs {
     int* arrive;    // [row] split arrival counters (zero between calls)
     int near_plan;  // expected near tiles per row (balances the far split)
     // TurboQuant far tier (fmt 1)
-    const uint16_t* tq_q;   // (B, Hq, 2, D) fp16: q.Pi^T, q.S^T
-    const float* tq_asum;   // (B, Hq) alpha * sum(q.Pi^T), or null when alpha == 0
+    const float* tq_PiT;    // (D, D) fp32, PiT[j][i] = Pi[i][j]
+    const float* tq_ST;     // (D, D) fp32, ST[j][i] = S[i][j]
+    float tq_alpha;         // centroid constant term (0 for a symmetric codebook)
     float tq_beta, tq_gamma, tq_delta;  // centroid coefficients (TurboConsts)
     float tq_qjl;           // 1.2533141 / D
     float tq_lvh, tq_lvl;   // value level coefficients
@@ -1612,6 +1613,76 @@ __device__ inline void plan_far(Units& un, int nt_far, int near_plan, int64_t FB
     }
 }
 
+// TurboQuant query rotation and sketch inside the attention kernel:
+// q.Pi^T and q.S^T (foveated_attn.cpp:415-421) for the workgroup's heads, in
+// fp32 from the fp16 query, rounded to fp16 into the qt operand layout.
+// Thread = (matrix, 4-column block cb, j-slice js of D/4 rows); the matrix rows are read once per workgroup
+// (coalesced float4 per thread), the slices' partial sums meet in `part`
+// (a free ring slot, 4 * 4 * D * 2 floats); the quad's fp32 q.Pi^T then
+// replaces its query in `qf` and alpha * sum(q.Pi^T) per head goes to
+// `rsum`.  Must be entered by every thread of the workgroup.
+template <int D, int NQ>
+__device__ inline void tq_rotate_query(const AttnArgs& a, float* qf, uint16_t* qt, float* part, float* rsum) {
+    constexpr int NS = D / 4, CB = D / 4, SL = 4, JL = D / SL, TPM = CB * SL;
+    const int t = threadIdx.x;
+    const bool active = t < 2 * TPM;
+    const int mat = t / TPM, cb = t % CB, js = (t % TPM) / CB;
+    const float* M = mat ? a.tq_ST : a.tq_PiT;
+    float4 m[JL];
+    if (active) {
+#pragma unroll
+        for (int jj = 0; jj < JL; jj++) m[jj] = *(const float4*)(M + (js * JL + jj) * D + 4 * cb);
+    }
+#pragma unroll 1
+    for (int qd = 0; qd < NQ; qd++) {
+        if (active) {
+            float acc[4][4];
+#pragma unroll
+            for (int h = 0; h < 4; h++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[h][c] = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < JL; jj++) {
+                const int jx = js * JL + jj;
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const float x = qf[(4 * qd + h) * D + jx];
+                    acc[h][0] = fmaf(x, m[jj].x, acc[h][0]);
+                    acc[h][1] = fmaf(x, m[jj].y, acc[h][1]);
+                    acc[h][2] = fmaf(x, m[jj].z, acc[h][2]);
+                    acc[h][3] = fmaf(x, m[jj].w, acc[h][3]);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < 4; h++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) part[((js * 2 + mat) * 4 + h) * D + 4 * cb + c] = acc[h][c];
+        }
+        __syncthreads();
+        for (int o = t; o < 2 * 4 * D; o += blockDim.x) {
+            const int mo = o / (4 * D), h = (o / D) % 4, col = o % D;
+            float v = 0.f;
+#pragma unroll
+            for (int k = 0; k < SL; k++) v += part[((k * 2 + mo) * 4 + h) * D + col];
+            const int idx = ((qd * NS + col / 4) * 4 + h) * 4 + col % 4;
+            qt[mo * NQ * NS * 16 + idx] = f2h(v);
+            if (mo == 0) qf[(4 * qd + h) * D + col] = v;  // q.Pi^T in fp32 (the quad's q is consumed)
+        }
+        if (a.tq_alpha != 0.f) {
+            __syncthreads();
+            // wave w sums head w's rotated query
+            const int w = t / kWave, ln = t % kWave;
+            if (w < 4) {
+                float v = 0.f;
+                for (int col = ln; col < D; col += kWave) v += qf[(4 * qd + w) * D + col];
+                v = wave_sum(v);
+                if (ln == 0) rsum[4 * qd + w] = a.tq_alpha * v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // One workgroup of 4 waves per (batch, kv head, split, head group); each
 // wave streams its units through a 2-slot LDS ring with gfx950's direct
 // global->LDS loads: the next unit's bytes stream in while the current one
@@ -1628,8 +1699,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int FAR_OPS = TQ ? tq_dma_ops<D>() : G32 ? g32_dma_ops<D>() : far_dma_ops<D>(), NEAR_OPS = D / 8;
     static_assert(FAR_OPS != NEAR_OPS, "the ring's vmcnt waits tell far and near units apart by op count");
     __shared__ __attribute__((aligned(16))) uint16_t qs[NQ * NS * 4 * 4];
-    // TurboQuant: rotated and sketched query operands, same layout as qs
+    // TurboQuant: rotated and sketched query operands, same layout as qs;
+    // the fp32 query and the per-head alpha * sum(q.Pi^T)
     __shared__ __attribute__((aligned(16))) uint16_t qt[TQ ? 2 * NQ * NS * 4 * 4 : 8];
+    __shared__ __attribute__((aligned(16))) float qf[TQ ? 4 * NQ * D : 4];
+    __shared__ float rsum[TQ ? 4 * NQ : 4];
     // The rings during the tile loop; afterwards (behind a barrier) the
     // per-wave records, then past wave 0's records the split-merge scratch
     // of the last workgroup.
@@ -1677,17 +1751,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int s = sq % NS, qd = sq / NS;
         const int h = 4 * qd + jj;
         qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
-        if constexpr (TQ) {
-            const uint16_t* tq = a.tq_q + ((int64_t)b * a.Hq + head0 + h) * 2 * D + 4 * s + e;
-            qt[i] = h < ng ? tq[0] : (uint16_t)0;
-            qt[NQ * NS * 16 + i] = h < ng ? tq[D] : (uint16_t)0;
-        }
     }
     float asum[NQ];
 #pragma unroll
-    for (int qd = 0; qd < NQ; qd++) {
-        const int h = 4 * qd + j;
-        asum[qd] = (TQ && a.tq_asum && h < ng) ? a.tq_asum[(int64_t)b * a.Hq + head0 + h] : 0.f;
+    for (int qd = 0; qd < NQ; qd++) asum[qd] = 0.f;
+    if constexpr (TQ) {
+        for (int i = threadIdx.x; i < 4 * NQ * D; i += blockDim.x) {
+            const int h = i / D;
+            qf[i] = h < ng ? h2f(a.q[((int64_t)b * a.Hq + head0 + h) * D + i % D]) : 0.f;
+        }
+        __syncthreads();
+        // slot 1 of wave 0 is free until the stream starts
+        tq_rotate_query<D, NQ>(a, qf, qt, (float*)(lds + SLOT), rsum);
+        if (a.tq_alpha != 0.f) {
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) asum[qd] = rsum[4 * qd + j];
+        }
     }
     const int nv = (int)((const uint32_t*)(a.blob + a.L.near_valid))[kvh];
     const int nt_near = (int)cdiv(nv, kTile);
@@ -2233,19 +2312,15 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
     a.arrive = fused_merge ? h->arrive : nullptr;
     a.near_plan = h->near_plan;
     const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
-    a.tq_q = nullptr;
-    a.tq_asum = nullptr;
+    a.tq_PiT = h->tq.PiT;
+    a.tq_ST = h->tq.ST;
+    a.tq_alpha = h->tq.alpha;
     a.tq_beta = h->tq.beta;
     a.tq_gamma = h->tq.gamma;
     a.tq_delta = h->tq.delta;
     a.tq_qjl = 1.2533141f / (float)L.D;
     a.tq_lvh = h->tq.lvh;
     a.tq_lvl = h->tq.lvl;
-    if (L.fmt == 1) {
-        if (int rc = fkv::tq_prepare_query(h, q16, Hq, st)) return rc;
-        a.tq_q = h->tq_q;
-        a.tq_asum = h->tq.alpha != 0.f ? h->tq_asum : nullptr;
-    }
     const int nq = (ng_max + 3) / 4;
     fkv::AttnKernel k = L.fmt == 1   ? (L.D == 128 ? fkv::pick_attn<128, 1>(nq) : fkv::pick_attn<64, 1>(nq))
                         : L.fmt == 2 ? (L.D == 128 ? fkv::pick_attn<128, 2>(nq) : fkv::pick_attn<64, 2>(nq))
@@ -2323,8 +2398,6 @@ void fkv_attn_destroy(fkv_attn* h) {
     if (h->arrive) (void)hipFree(h->arrive);
     if (h->tq.PiT) (void)hipFree(h->tq.PiT);
     if (h->tq.ST) (void)hipFree(h->tq.ST);
-    if (h->tq_q) (void)hipFree(h->tq_q);
-    if (h->tq_asum) (void)hipFree(h->tq_asum);
     delete h;
 }
 

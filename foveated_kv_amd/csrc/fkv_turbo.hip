@@ -126,76 +126,6 @@ __global__ void transpose_kernel(const float* __restrict__ in, float* __restrict
 // per-call query preparation (csrc/foveated_attn.cpp:415-421)
 // ---------------------------------------------------------------------------
 
-// One workgroup of 512 threads per (b, q head): thread (i, part) sums the
-// D/4 products j = part*D/4 .. of output dim i for q.Pi^T and q.S^T (fp32
-// from the fp16 query; the four partial sums are added in a fixed order),
-// stored as fp16 operands; alpha * sum(q.Pi^T) when the centroids need the
-// constant term.
-template <int D>
-__global__ __launch_bounds__(512) void tq_qprep_kernel(const uint16_t* __restrict__ q16, const float* __restrict__ PiT,
-                                                       const float* __restrict__ ST, float alpha,
-                                                       uint16_t* __restrict__ out, float* __restrict__ asum) {
-    constexpr int NP = 512 / D, JP = D / NP;
-    __shared__ float qv[D];
-    __shared__ float part[2][NP][D];
-    const int64_t bh = blockIdx.x;
-    const int i = threadIdx.x % D, pi = threadIdx.x / D;
-    if (threadIdx.x < D) qv[threadIdx.x] = h2f(q16[bh * D + threadIdx.x]);
-    __syncthreads();
-    float r = 0.f, k = 0.f;
-#pragma unroll 8
-    for (int j = pi * JP; j < (pi + 1) * JP; j++) {
-        const float x = qv[j];
-        r = fmaf(x, PiT[j * D + i], r);
-        k = fmaf(x, ST[j * D + i], k);
-    }
-    part[0][pi][i] = r;
-    part[1][pi][i] = k;
-    __syncthreads();
-    if (threadIdx.x < D) {
-        float rr = 0.f, kk = 0.f;
-#pragma unroll
-        for (int p = 0; p < NP; p++) {
-            rr += part[0][p][i];
-            kk += part[1][p][i];
-        }
-        out[(bh * 2 + 0) * D + i] = f2h(rr);
-        out[(bh * 2 + 1) * D + i] = f2h(kk);
-        part[0][0][i] = rr;
-    }
-    if (asum != nullptr) {
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float s = 0.f;
-            for (int d = 0; d < D; d++) s += part[0][0][d];
-            asum[bh] = alpha * s;
-        }
-    }
-}
-
-int tq_prepare_query(fkv_attn_impl* h, const uint16_t* q16, int Hq, hipStream_t st) {
-    const int D = h->L.D;
-    const size_t rows = (size_t)h->L.B * Hq;
-    if (rows > h->tq_q_n) {
-        if (h->tq_q) (void)hipFree(h->tq_q);
-        if (h->tq_asum) (void)hipFree(h->tq_asum);
-        h->tq_q = nullptr;
-        h->tq_asum = nullptr;
-        h->tq_q_n = 0;
-        if (int rc = check_hip(hipMalloc(&h->tq_q, rows * 2 * D * sizeof(uint16_t)), "hipMalloc(tq_q)")) return rc;
-        if (int rc = check_hip(hipMalloc(&h->tq_asum, rows * sizeof(float)), "hipMalloc(tq_asum)")) return rc;
-        h->tq_q_n = rows;
-    }
-    float* asum = h->tq.alpha != 0.f ? h->tq_asum : nullptr;
-    if (D == 128)
-        hipLaunchKernelGGL(tq_qprep_kernel<128>, dim3((unsigned)rows), dim3(512), 0, st, q16, h->tq.PiT, h->tq.ST,
-                           h->tq.alpha, h->tq_q, asum);
-    else
-        hipLaunchKernelGGL(tq_qprep_kernel<64>, dim3((unsigned)rows), dim3(512), 0, st, q16, h->tq.PiT, h->tq.ST,
-                           h->tq.alpha, h->tq_q, asum);
-    return check_hip(hipGetLastError(), "tq_qprep_kernel launch");
-}
-
 // ---------------------------------------------------------------------------
 // compression (src/foveated_kv/turbo_quantize.py:25-91, 139-178), fp32
 // ---------------------------------------------------------------------------
