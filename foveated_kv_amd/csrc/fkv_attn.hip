@@ -506,6 +506,8 @@ __device__ inline void dma_far(const AttnArgs& a, int64_t bkv, int tile, int lan
     for (int c = 0; c < 3 * D / 32; c++)
         __builtin_amdgcn_global_load_lds((const void*)(rec + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
                                          0, 2);
+    // the 256-byte SZ section by lanes 0..15 (a single lane-conditional
+    // instruction: the branch cannot be merged with another one, see dma_tq)
     if (lane < 16)
         __builtin_amdgcn_global_load_lds((const void*)(rec + far_sz_section(D) + lane * 16),
                                          (FKV_LDS void*)(slot + far_sz_section(D)), 16, 0, 2);
@@ -734,13 +736,19 @@ __device__ inline void dma_tq(const AttnArgs& a, int64_t bkv, int tile, int lane
     for (int c = 0; c < KPV / 1024; c++)
         __builtin_amdgcn_global_load_lds((const void*)(rec + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
                                          0, 2);
-    if constexpr (KPV % 1024 != 0) {
-        if (lane < (KPV % 1024) / 16)
-            __builtin_amdgcn_global_load_lds((const void*)(rec + (KPV / 1024) * 1024 + lane * 16),
-                                             (FKV_LDS void*)(slot + (KPV / 1024) * 1024), 16, 0, 2);
-    }
-    if (lane < TAIL / 16)
-        __builtin_amdgcn_global_load_lds((const void*)(rec + KPV + lane * 16), (FKV_LDS void*)(slot + KPV), 16, 0, 2);
+    // Whole-wave instructions: the LDS address operand (M0) must be
+    // wave-uniform, and lane-divergent branches around consecutive LDS-DMA
+    // builtins can be tail-merged by the compiler into one instruction whose
+    // M0 comes from the first active lane.  The partial chunk's upper lanes
+    // read the first TAIL bytes, which the next instruction writes to the
+    // same LDS bytes; the TAIL's upper lanes repeat lower addresses (same
+    // cache lines) and land past the record in the slot.
+    if constexpr (KPV % 1024 != 0)
+        __builtin_amdgcn_global_load_lds((const void*)(rec + (KPV / 1024) * 1024 + lane * 16),
+                                         (FKV_LDS void*)(slot + (KPV / 1024) * 1024), 16, 0, 2);
+    constexpr int TL = TAIL / 16;  // lanes of the tail
+    __builtin_amdgcn_global_load_lds((const void*)(rec + KPV + (lane < TL ? lane : lane - (64 - TL)) * 16),
+                                     (FKV_LDS void*)(slot + KPV), 16, 0, 2);
 }
 
 // The lane's operands of a TurboQuant tile.
@@ -1065,9 +1073,11 @@ __device__ inline void dma_g32(const AttnArgs& a, int64_t bkv, int tile, int lan
     for (int c = 0; c < 3 * D / 32; c++)
         __builtin_amdgcn_global_load_lds((const void*)(rec + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
                                          0, 2);
-    if (lane < 8 * D / 16)
-        __builtin_amdgcn_global_load_lds((const void*)(rec + g32_sz_section(D) + lane * 16),
-                                         (FKV_LDS void*)(slot + g32_sz_section(D)), 16, 0, 2);
+    // SZ: 8*D bytes = 8*D/16 lanes; for D = 64 the upper lanes repeat the
+    // lower lanes' addresses and land past the record in the slot (whole-wave
+    // instruction, see dma_tq)
+    __builtin_amdgcn_global_load_lds((const void*)(rec + g32_sz_section(D) + (lane & (8 * D / 16 - 1)) * 16),
+                                     (FKV_LDS void*)(slot + g32_sz_section(D)), 16, 0, 2);
 }
 
 template <int D>
