@@ -328,22 +328,23 @@ def test_e4m3_converter_matches_reference_lut(fkv, orc):
     assert np.array_equal(got[reach], lut[reach])
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,S,n_dec", [(8, 32, 8, 128, 8192, 0), (2, 32, 2, 64, 3000, 9)])
-def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec):
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,n_dec,vg", [(8, 32, 8, 128, 8192, 0, 0), (2, 32, 2, 64, 3000, 9, 0),
+                                                   (8, 32, 8, 128, 8192, 0, 32)])
+def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
     """The last-arriving split merges the partial records in-kernel; its
     arrival counters are re-armed by the kernel itself.  200 launches queued
     back to back (no host sync between them) must all be bit-identical, and
     must agree with the separate merge launch."""
     from foveated_kv_amd import ext, synthetic
 
-    _flush(f"fused merge stress B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec}")
+    _flush(f"fused merge stress B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} v_group={vg}")
     k, v = synthetic.make_kv(B, Hkv, S, D, 21)
     q = torch.from_numpy(synthetic.make_query(B, Hq, D, 21)).cuda()[:, :, None]
     dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, 21)
     dkt = torch.from_numpy(dk).cuda() if dk is not None else None
     dvt = torch.from_numpy(dv).cuda() if dv is not None else None
-    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
-                                                      with_archive=False)
+    cl = ext.CompressHandle(_cfg(fkv, v_group=vg)).compress_layer(
+        torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), with_archive=False)
     h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
                            cl.near_valid, spike_margin=10.0)
     os.environ["FKV_FUSED_MERGE"] = "0"
