@@ -27,6 +27,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "fkv_attn.h"
 #include "fkv_common.h"
 #include "../../include/fkv.h"
 
@@ -47,6 +48,19 @@ struct Archive {
 struct Record {
     int32_t layer, head, arc_local, position;
 };
+
+// Device-side drain state of one layer (fkv_promoter_drain_device)
+struct DevDrain {
+    int32_t* last_step = nullptr;     // [Hkv], kNoStep until the first candidate
+    uint32_t* promoted = nullptr;     // [Hkv][words]: positions already promoted
+    int32_t* pos_to_local = nullptr;  // [Hkv][P]: position -> archive row, -1 if none
+    int P = 0, words = 0;
+    const uint16_t* ark = nullptr;    // device views of the pinned archive rows
+    const uint16_t* arv = nullptr;
+};
+
+constexpr int32_t kNoStep = INT32_MIN;
+constexpr int kMaxDrainHeads = 256;
 
 }  // namespace
 
@@ -69,9 +83,23 @@ struct fkv_promoter {
     uint8_t* stage_h = nullptr;        // pinned host staging
     uint8_t* stage_d = nullptr;        // device staging
     size_t stage_cap = 0;
+    // device drain
+    std::vector<DevDrain> dev;
+    unsigned long long* dstats = nullptr;  // 6 counters, fkv_promoter_stats order
 };
 
 namespace {
+
+// Forget a layer's device-drain state (its archive is being replaced).
+void free_dev_drain(fkv_promoter* p, int layer) {
+    if (p->dev.empty() || !p->dev[layer].last_step) return;
+    (void)hipDeviceSynchronize();  // a queued drain may still read it
+    DevDrain& d = p->dev[layer];
+    (void)hipFree(d.last_step);
+    (void)hipFree(d.promoted);
+    (void)hipFree(d.pos_to_local);
+    d = DevDrain();
+}
 
 void free_archive(Archive& a) {
     if (a.owned_k) (void)hipHostFree(a.owned_k);
@@ -129,6 +157,160 @@ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
 
 }  // namespace
 
+
+namespace {
+
+struct DrainArgs {
+    const int32_t* flags;
+    const int32_t* tokens;
+    const int32_t* far_idx;
+    int B, Hq, Hkv, N_far, step, cooldown, budget;
+    int32_t* last_step;
+    uint32_t* promoted;
+    const int32_t* pos_to_local;
+    int P, words;
+    const uint16_t* ark;
+    const uint16_t* arv;
+    int arc_B, arc_S;
+    fkv::BlobLayout L;
+    uint8_t* blob;
+    unsigned long long* stats;
+};
+
+// The drain filter (promotion_pipeline.cpp:99-175) and the promotion
+// (:192-241) of one layer as one workgroup: thread 0 scans (batch, query
+// head) in order exactly as fkv_promoter_drain does and assigns headroom
+// slots from the blob's near_valid; all threads then copy the exact fp16
+// rows of every archive batch from pinned host memory into the slots; the
+// near_valid bumps are written last (the next launch on the stream sees
+// rows and counts together).
+__global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
+    __shared__ uint8_t seen[kMaxDrainHeads];
+    __shared__ int n_rec;
+    __shared__ int rec_h[kMaxDrainHeads], rec_slot[kMaxDrainHeads], rec_arc[kMaxDrainHeads];
+    for (int i = threadIdx.x; i < kMaxDrainHeads; i += blockDim.x) seen[i] = 0;
+    __syncthreads();
+    uint32_t* near_valid = (uint32_t*)(a.blob + a.L.near_valid);
+    if (threadIdx.x == 0) {
+        unsigned long long det = 0, que = 0, dup = 0, cool = 0, full = 0;
+        const int gqa = a.Hq / a.Hkv > 0 ? a.Hq / a.Hkv : 1;
+        int queued = 0, n = 0;
+        for (int b = 0; b < a.B && queued < a.budget; b++) {
+            for (int hq = 0; hq < a.Hq && queued < a.budget; hq++) {
+                const int flat = b * a.Hq + hq;
+                if (a.flags[flat] == 0) continue;
+                const int hkv = hq / gqa;
+                if (hkv >= a.Hkv || seen[hkv]) continue;
+                seen[hkv] = 1;
+                det++;
+                const int32_t last = a.last_step[hkv];
+                if (last != kNoStep && a.step - last < a.cooldown) {
+                    cool++;
+                    continue;
+                }
+                a.last_step[hkv] = a.step;
+                const int fl = a.tokens[flat];
+                if (fl < 0 || fl >= a.N_far) continue;
+                const int32_t pos = a.far_idx[((int64_t)b * a.Hkv + hkv) * a.N_far + fl];
+                if (pos < 0 || pos >= a.P) continue;  // not an archived position
+                uint32_t* w = a.promoted + (int64_t)hkv * a.words + (pos >> 5);
+                const uint32_t bit = 1u << (pos & 31);
+                if (*w & bit) {
+                    dup++;
+                    continue;
+                }
+                *w |= bit;
+                const int32_t arc = a.pos_to_local[(int64_t)hkv * a.P + pos];
+                if (arc < 0) continue;
+                que++;
+                queued++;
+                const uint32_t cur = near_valid[hkv];  // one record per KV head per drain
+                if ((int)cur >= a.L.Na) {
+                    full++;
+                    continue;
+                }
+                rec_h[n] = hkv;
+                rec_slot[n] = (int)cur;
+                rec_arc[n] = arc;
+                n++;
+            }
+        }
+        n_rec = n;
+        a.stats[0] += det;
+        a.stats[1] += que;
+        a.stats[2] += dup;
+        a.stats[3] += cool;
+        a.stats[4] += (unsigned long long)n;
+        a.stats[5] += full;
+    }
+    __syncthreads();
+    const int n = n_rec, D = a.L.D;
+    const int nb = a.arc_B < a.L.B ? a.arc_B : a.L.B;
+    uint16_t* nk = (uint16_t*)(a.blob + a.L.near_k);
+    uint16_t* nv = (uint16_t*)(a.blob + a.L.near_v);
+    for (int e = threadIdx.x; e < n * nb * D; e += blockDim.x) {
+        const int d = e % D, b = (e / D) % nb, i = e / (D * nb);
+        const int h = rec_h[i], slot = rec_slot[i];
+        const int64_t base = ((int64_t)b * a.L.Hkv + h) * a.L.Na_pad * D;
+        const int64_t src = (((int64_t)b * a.Hkv + h) * a.arc_S + rec_arc[i]) * D + d;
+        nk[base + fkv::near_k_index(slot, d, D)] = a.ark[src];
+        nv[base + fkv::near_v_index(slot, d, D)] = a.arv[src];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int i = 0; i < n; i++) near_valid[rec_h[i]] = (uint32_t)(rec_slot[i] + 1);
+}
+
+// Device state of a layer for the device drain, made on its first use.
+int ensure_dev_drain(fkv_promoter* p, int layer, hipStream_t st) {
+    if (p->dev.empty()) p->dev.resize(p->n_layers);
+    if (!p->dstats) {
+        if (int rc = check_hip(hipMalloc((void**)&p->dstats, 6 * sizeof(unsigned long long)), "hipMalloc(stats)"))
+            return rc;
+        const unsigned long long zero[6] = {0, 0, 0, 0, 0, 0};
+        if (int rc = check_hip(hipMemcpy(p->dstats, zero, sizeof(zero), hipMemcpyHostToDevice), "hipMemcpy(stats)"))
+            return rc;
+    }
+    DevDrain& d = p->dev[layer];
+    if (d.last_step) return FKV_OK;
+    const Archive& a = p->arch[layer];
+    if (!a.owned_k || !a.owned_v)
+        return set_error("fkv_promoter_drain_device: the layer's archive is not in pipeline-owned pinned memory");
+    int maxpos = -1;
+    for (const auto& m : a.pos_to_local)
+        for (const auto& kv : m) maxpos = kv.first > maxpos ? kv.first : maxpos;
+    d.P = maxpos + 1;
+    d.words = (d.P + 31) / 32;
+    std::vector<int32_t> p2l((size_t)a.Hkv * (d.P > 0 ? d.P : 1), -1);
+    for (int h = 0; h < a.Hkv; h++)
+        for (const auto& kv : a.pos_to_local[h])
+            if (kv.first >= 0) p2l[(size_t)h * d.P + kv.first] = kv.second;
+    std::vector<int32_t> ls((size_t)a.Hkv, kNoStep);
+    int rc = check_hip(hipMalloc((void**)&d.last_step, a.Hkv * sizeof(int32_t)), "hipMalloc(last_step)");
+    if (!rc) rc = check_hip(hipMalloc((void**)&d.promoted, (size_t)a.Hkv * (d.words > 0 ? d.words : 1) * 4),
+                            "hipMalloc(promoted)");
+    if (!rc) rc = check_hip(hipMalloc((void**)&d.pos_to_local, p2l.size() * 4), "hipMalloc(pos_to_local)");
+    if (!rc) rc = check_hip(hipMemcpy(d.last_step, ls.data(), ls.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    if (!rc) rc = check_hip(hipMemset(d.promoted, 0, (size_t)a.Hkv * (d.words > 0 ? d.words : 1) * 4), "hipMemset");
+    if (!rc) rc = check_hip(hipMemcpy(d.pos_to_local, p2l.data(), p2l.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    void* dk = nullptr;
+    void* dv = nullptr;
+    if (!rc) rc = check_hip(hipHostGetDevicePointer(&dk, a.owned_k, 0), "hipHostGetDevicePointer");
+    if (!rc) rc = check_hip(hipHostGetDevicePointer(&dv, a.owned_v, 0), "hipHostGetDevicePointer");
+    if (rc) {
+        if (d.last_step) (void)hipFree(d.last_step);
+        if (d.promoted) (void)hipFree(d.promoted);
+        if (d.pos_to_local) (void)hipFree(d.pos_to_local);
+        d = DevDrain();
+        return rc;
+    }
+    d.ark = (const uint16_t*)dk;
+    d.arv = (const uint16_t*)dv;
+    return FKV_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int fkv_promoter_create(int32_t n_layers, int32_t cooldown_steps, int32_t max_per_drain, fkv_promoter** out) {
@@ -177,6 +359,7 @@ int fkv_promoter_register_archive(fkv_promoter* p, int32_t layer, const void* k,
         a.v = (const uint16_t*)v;
     }
     build_positions(a, archive_idx);
+    free_dev_drain(p, layer);
     free_archive(p->arch[layer]);
     p->arch[layer] = std::move(a);
     return FKV_OK;
@@ -217,6 +400,7 @@ int fkv_promoter_register_archive_files(fkv_promoter* p, int32_t layer, const ch
         a.v = (const uint16_t*)a.owned_v;
     }
     build_positions(a, archive_idx);
+    free_dev_drain(p, layer);
     free_archive(p->arch[layer]);
     p->arch[layer] = std::move(a);
     return FKV_OK;
@@ -291,6 +475,48 @@ int fkv_promoter_pending(const fkv_promoter* p, int32_t* out_records, int32_t ma
         out_records[4 * i + 3] = p->queue[i].position;
     }
     return n;
+}
+
+
+int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* flags, const int32_t* tokens,
+                              const int32_t* far_idx, int32_t B, int32_t Hq, int32_t Hkv, int32_t N_far, int32_t step,
+                              void* stream) {
+    if (!p) return set_error("fkv_promoter_drain_device: NULL pipeline");
+    if (layer < 0 || layer >= p->n_layers) return 0;
+    const Archive& arc = p->arch[layer];
+    fkv_attn* h = p->handles[layer];
+    if (!arc.k || arc.S == 0 || !h) return 0;  // nothing to promote from or into (as the host drain)
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || !flags || !tokens || !far_idx) return 0;
+    if (Hkv > kMaxDrainHeads || Hkv != arc.Hkv || Hkv != h->L.Hkv || arc.D != h->L.D)
+        return set_error("fkv_promoter_drain_device: archive, handle and spike shapes disagree (or H_kv > 256)");
+    hipStream_t st = (hipStream_t)stream;
+    if (int rc = ensure_dev_drain(p, layer, st)) return rc;
+    const DevDrain& d = p->dev[layer];
+    DrainArgs a;
+    a.flags = flags;
+    a.tokens = tokens;
+    a.far_idx = far_idx;
+    a.B = B;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.N_far = N_far;
+    a.step = step;
+    a.cooldown = p->cooldown;
+    a.budget = p->max_per_drain;
+    a.last_step = d.last_step;
+    a.promoted = d.promoted;
+    a.pos_to_local = d.pos_to_local;
+    a.P = d.P;
+    a.words = d.words;
+    a.ark = d.ark;
+    a.arv = d.arv;
+    a.arc_B = arc.B;
+    a.arc_S = arc.S;
+    a.L = h->L;
+    a.blob = h->blob;
+    a.stats = p->dstats;
+    hipLaunchKernelGGL(drain_promote_kernel, dim3(1), dim3(256), 0, st, a);
+    return check_hip(hipGetLastError(), "drain_promote_kernel launch");
 }
 
 // promotion_pipeline.cpp:192-241, as stream-ordered device work
@@ -386,6 +612,18 @@ int fkv_promoter_synchronize(fkv_promoter* p) {
 int fkv_promoter_get_stats(const fkv_promoter* p, fkv_promoter_stats* out) {
     if (!p || !out) return set_error("fkv_promoter_get_stats: NULL argument");
     *out = p->stats;
+    if (p->dstats) {  // device-drain counters (waits for the device)
+        unsigned long long c[6];
+        if (int rc = check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize")) return rc;
+        if (int rc = check_hip(hipMemcpy(c, p->dstats, sizeof(c), hipMemcpyDeviceToHost), "hipMemcpy(stats)"))
+            return rc;
+        out->spikes_detected += c[0];
+        out->spikes_queued += c[1];
+        out->spikes_deduplicated += c[2];
+        out->spikes_cooled_down += c[3];
+        out->promotions_completed += c[4];
+        out->promotions_headroom_full += c[5];
+    }
     return FKV_OK;
 }
 
@@ -408,6 +646,13 @@ void fkv_promoter_destroy(fkv_promoter* p) {
     }
     if (p->stage_h) (void)hipHostFree(p->stage_h);
     if (p->stage_d) (void)hipFree(p->stage_d);
+    if (p->dstats || !p->dev.empty()) (void)hipDeviceSynchronize();  // device drains may still run
+    for (auto& d : p->dev) {
+        if (d.last_step) (void)hipFree(d.last_step);
+        if (d.promoted) (void)hipFree(d.promoted);
+        if (d.pos_to_local) (void)hipFree(d.pos_to_local);
+    }
+    if (p->dstats) (void)hipFree(p->dstats);
     for (auto& a : p->arch) free_archive(a);
     delete p;
 }

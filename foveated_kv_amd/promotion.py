@@ -120,6 +120,29 @@ class PromotionPipeline:
             self.flush()
         return n
 
+    def drain_spikes_device(self, layer_idx, spike_flags, spike_tokens, far_idx, current_step):
+        """The same drain and promotion as ``drain_spikes`` + ``flush``, as one
+        kernel on torch's current stream of the tensors' device: spike outputs
+        (B, H_q) and far_idx (B, H_kv, N_far) int32 stay in device memory and
+        nothing waits for the host; the layer's next attention launch on that
+        stream sees the promoted rows.  Needs the archive registered with
+        ``register_archive_tensors`` (pinned copy) or from files; do not mix
+        with ``drain_spikes`` on one pipeline."""
+        if self._stopped:
+            return
+        for t in (spike_flags, spike_tokens, far_idx):
+            if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.int32 and t.is_contiguous()):
+                raise TypeError("drain_spikes_device takes contiguous int32 device tensors")
+        B, Hq = spike_flags.shape[0], spike_flags.shape[1]
+        Hkv, n_far = far_idx.shape[1], far_idx.shape[2]
+        dev = spike_flags.device
+        with torch.cuda.device(dev):
+            check(self._lib.fkv_promoter_drain_device(self._h, int(layer_idx), _lib.ptr(spike_flags),
+                                                      _lib.ptr(spike_tokens), _lib.ptr(far_idx), B, Hq, Hkv, n_far,
+                                                      int(current_step), _lib.stream_ptr(dev)),
+                  "fkv_promoter_drain_device")
+        self._keep[("dev", int(layer_idx))] = (spike_flags, spike_tokens, far_idx)
+
     def pending(self):
         """Queued, unflushed records: int32 (n, 4) = layer, head, archive row, position."""
         n = self._lib.fkv_promoter_pending(self._h, None, 0)

@@ -277,6 +277,24 @@ int fkv_promoter_register_handle(fkv_promoter* p, int32_t layer, fkv_attn* h, vo
 int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* spike_flags, const int32_t* spike_tokens,
                        const int32_t* far_idx, int32_t B, int32_t Hq, int32_t Hkv, int32_t N_far, int32_t step);
 
+/* Device-side drain + promotion.  No counterpart in the reference, whose
+ * drain runs on the host after reading the spike outputs back: the same
+ * filter as fkv_promoter_drain (scan order, GQA dedup, cooldown, position
+ * dedup, budget) and the same commit as the flush (rows of every archive
+ * batch into the next headroom slot, then the near_valid bump), as one
+ * kernel on `stream` reading spike_flags / spike_tokens (B*Hq) and far_idx
+ * (B, Hkv, N_far) int32 in device memory and the archive rows from the
+ * pipeline's pinned host copy.  No host synchronisation: the next launch on
+ * `stream` sees the promoted rows.  For callers that keep a decode step on
+ * the GPU.  Needs a registered handle and an archive registered with
+ * copy_to_pinned (or from files); the first call per layer allocates (not
+ * capturable).  A pipeline uses either this or the host drain + flush (the
+ * host mirror of near_valid is not updated here); statistics accumulate on
+ * the device and fkv_promoter_get_stats adds them (synchronising). */
+int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* spike_flags,
+                              const int32_t* spike_tokens, const int32_t* far_idx, int32_t B, int32_t Hq,
+                              int32_t Hkv, int32_t N_far, int32_t step, void* stream);
+
 /* Queued records (not yet flushed): returns their count and copies up to
  * max_records of them as int32 [layer, head, archive row, position]. */
 int fkv_promoter_pending(const fkv_promoter* p, int32_t* out_records, int32_t max_records);

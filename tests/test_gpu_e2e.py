@@ -18,13 +18,17 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,S,steps,vg", [(1, 16, 4, 128, 8192, 24, 0), (1, 14, 2, 64, 2048, 16, 32)])
-def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, steps, vg):
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,steps,vg,dev_drain", [(1, 16, 4, 128, 8192, 24, 0, False),
+                                                             (1, 14, 2, 64, 2048, 16, 32, False),
+                                                             (1, 16, 4, 128, 8192, 24, 0, True),
+                                                             (2, 16, 2, 64, 3000, 20, 32, True)])
+def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, steps, vg, dev_drain):
     from foveated_kv_amd import ext, synthetic
     from foveated_kv_amd.promotion import PromotionPipeline
 
     seed = S + steps
-    print(f"e2e loop B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} v_group={vg}", flush=True)
+    print(f"e2e loop B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} v_group={vg} device_drain={dev_drain}",
+          flush=True)
     k, v = synthetic.make_kv(B, Hkv, S, D, seed)
     q0 = synthetic.make_query(B, Hq, D, seed)
     imp = torch.from_numpy(synthetic.make_importance(B, Hkv, S, seed)).cuda()
@@ -46,13 +50,15 @@ def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, st
     ref.register_archive(0, _np(cl.archive_k), _np(cl.archive_v), far_idx[0])
     near_k, near_v, nv = {0: _np(cl.near_k).copy()}, {0: _np(cl.near_v).copy()}, {0: _np(cl.near_valid).copy()}
     far = [_np(getattr(cl, n)) for n in ("far_k", "far_v", "far_v_scale", "far_v_zero")]
+    fdev = cl.far_idx.to(torch.int32).contiguous()
     qs = synthetic.drift_queries(q0, steps, 0.05, seed)
     dk, dv = synthetic.make_decode(B, Hkv, steps, D, seed)
     dkt, dvt = torch.from_numpy(dk).cuda(), torch.from_numpy(dv).cuda()
     lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).astype(np.float64)
     flagged = 0
     for t in range(steps):
-        pipe.order(0)
+        if not dev_drain:
+            pipe.order(0)
         q = torch.from_numpy(qs[t]).cuda()
         n = t + 1
         out, flags, toks = h(q[:, :, None], dkt[:, :, :n].contiguous(), dvt[:, :, :n].contiguous())
@@ -71,7 +77,10 @@ def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, st
             assert abs(sc[tk[b, hq]] - sc[kt[b, hq]]) <= 1e-5 * (1 + abs(sc.max())), (t, b, hq)
         flagged += int(fl.sum())
         # both pipelines see the GPU's spike outputs, so their states stay comparable
-        pipe.drain_spikes(0, flags, toks, far_idx, t)
+        if dev_drain:
+            pipe.drain_spikes_device(0, flags, toks, fdev, t)
+        else:
+            pipe.drain_spikes(0, flags, toks, far_idx, t)
         ref.drain(0, fl, tk, far_idx, t)
         ref.commit(near_k, near_v, nv, {0: cl.near_k.shape[2]})
     pipe.synchronize()

@@ -282,3 +282,47 @@ def test_promotion_from_archive_files(tmp_path):
     for hh, tok in ((0, 10), (1, 20)):
         assert np.array_equal(gk[0, hh, r0[hh]].cpu().numpy().view(np.uint16), ak[hh, tok].view(np.uint16))
         assert np.array_equal(gv[0, hh, r0[hh]].cpu().numpy().view(np.uint16), av[hh, tok].view(np.uint16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,cooldown,budget,headroom_min", [(1, 0, 8, 8), (2, 3, 2, 8), (1, 1, 8, 2)])
+def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroom_min):
+    """drain_spikes_device (filter + promotion in one kernel, spike outputs
+    and far_idx in device memory) against the CPU restatement of the host
+    drain + flush on random flag streams: same near tiers, near_valid and
+    statistics."""
+    import torch
+
+    from foveated_kv_amd.promotion import PromotionPipeline
+    from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
+
+    Hkv, Hq, D, S = 4, 16, 128, 900
+    print(f"device drain B={B} cooldown={cooldown} budget={budget} headroom_min={headroom_min}", flush=True)
+    k, v, cl, h = _layer(B, Hkv, D, S, 41, headroom_min=headroom_min)
+    tb = TierConfig(promo_headroom_min=headroom_min).tier_boundaries(S)
+    _, far_idx = tier_index_tensors(tb, S, B, Hkv, "cpu")
+    far_idx = far_idx.numpy()
+    fdev = torch.from_numpy(far_idx).cuda().contiguous()
+    pipe = PromotionPipeline(1, cooldown_steps=cooldown, max_per_drain=budget)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_blob(0, h)
+    ref = opromo.Pipeline(1, cooldown, budget)
+    ref.register_archive(0, cl.archive_k.cpu().numpy(), cl.archive_v.cpu().numpy(), far_idx[0])
+    near_k = {0: cl.near_k.cpu().numpy().copy()}
+    near_v = {0: cl.near_v.cpu().numpy().copy()}
+    nv = {0: cl.near_valid.cpu().numpy().copy()}
+    rng = np.random.default_rng(B * 10 + budget)
+    n_far = far_idx.shape[2]
+    for step in range(30):
+        flags = (rng.random((B, Hq)) < 0.4).astype(np.int32)
+        tokens = rng.integers(0, min(n_far, 40), size=(B, Hq)).astype(np.int32)  # repeats exercise dedup
+        tokens[rng.random((B, Hq)) < 0.05] = -1
+        pipe.drain_spikes_device(0, torch.from_numpy(flags).cuda(), torch.from_numpy(tokens).cuda(), fdev, step)
+        ref.drain(0, flags, tokens, far_idx, step)
+        ref.commit(near_k, near_v, nv, {0: cl.near_k.shape[2]})
+    torch.cuda.synchronize()
+    gk, gv = h.export_near()
+    assert h.read_near_valid() == [int(x) for x in nv[0]]
+    assert np.array_equal(gk.cpu().numpy().view(np.uint16), near_k[0].view(np.uint16))
+    assert np.array_equal(gv.cpu().numpy().view(np.uint16), near_v[0].view(np.uint16))
+    assert pipe.get_stats() == ref.stats and ref.stats["promotions_completed"] > 0
