@@ -127,6 +127,12 @@ class FusedCacheWrapper:
         self.offset += keys.shape[2]
         return keys, values
 
+    def far_idx_device(self) -> torch.Tensor:
+        """The layer's far_idx as a contiguous int32 device tensor (made once)."""
+        if getattr(self, "_far_idx_dev", None) is None:
+            self._far_idx_dev = self.fov_layer.far_idx.to(torch.int32).contiguous()
+        return self._far_idx_dev
+
     def far_idx_host(self) -> np.ndarray:
         """int32 host copy of the layer's far_idx (B, H_kv, F), made once:
         the drain reads it every step and it never changes."""
@@ -227,11 +233,18 @@ def _drain_into(pipeline, wrappers, step: int) -> None:
     """Hand every stashed (flags, tokens) pair to ``pipeline.drain_spikes``
     and clear the stash.  For this package's ``PromotionPipeline`` the
     spike arrays of all layers come to the host in one copy and the queued
-    promotions are flushed once, after the last layer."""
+    promotions are flushed once, after the last layer; with
+    ``pipeline.device_drain`` set the drain and the row copies stay on the
+    GPU (``drain_spikes_device``, no host round trip)."""
     ready = [w for w in (wrappers or [])
              if w is not None and w._spike_flags is not None and w._spike_tokens is not None]
     if pipeline is not None and ready:
-        if isinstance(pipeline, PromotionPipeline):
+        if isinstance(pipeline, PromotionPipeline) and getattr(pipeline, "device_drain", False):
+            for w in ready:
+                pipeline.drain_spikes_device(w.layer_idx, w._spike_flags.to(torch.int32).contiguous(),
+                                             w._spike_tokens.to(torch.int32).contiguous(), w.far_idx_device(),
+                                             step)
+        elif isinstance(pipeline, PromotionPipeline):
             both = torch.stack([torch.stack([w._spike_flags, w._spike_tokens]) for w in ready])
             host = both.to("cpu", torch.int32).numpy()
             for i, w in enumerate(ready):
@@ -303,10 +316,12 @@ def _next_token(logits, temp):
 
 def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
                    cfg: Optional[MLXTierConfig] = None, disk_archive_dir: Optional[str] = None,
-                   temp: float = 0.0, enable_promotion: bool = True):
+                   temp: float = 0.0, enable_promotion: bool = True, device_drain: bool = False):
     """mlx_generate.py:266-387: prefill, compress, move archives to disk,
     register them and the handles with a ``PromotionPipeline``, then decode
-    with the closure installed.  Returns (text, stats)."""
+    with the closure installed.  Returns (text, stats).  ``device_drain``
+    (extension): drain and promote on the GPU after each step instead of
+    reading the spike outputs back (same promotions)."""
     from .disk_archive import offload_cache_to_disk
 
     dev = _model_device(model)
@@ -326,6 +341,7 @@ def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
     pipeline = None
     if enable_promotion:
         pipeline = PromotionPipeline(len(fov_cache.layers))
+        pipeline.device_drain = bool(device_drain)
         for i, layer in enumerate(fov_cache.layers):
             if layer is None:
                 continue

@@ -308,3 +308,11 @@ def test_generate_fused_promotes_spiking_far_tokens(closure, tmp_path):
     assert stats["promotions_completed"] > 0
     assert stats["promotions_completed"] + stats["promotions_headroom_full"] <= stats["spikes_queued"]
     assert not (tmp_path / "arc").exists()
+    # the drain on the device promotes the same tokens and generates the same text
+    text_d, stats_d = gen.generate_fused(model, tok, _prompt(700, 3), max_tokens=12,
+                                         disk_archive_dir=str(tmp_path / "arc2"), enable_promotion=True,
+                                         device_drain=True)
+    assert text_d == text
+    for key in ("spikes_detected", "spikes_queued", "spikes_deduplicated", "spikes_cooled_down",
+                "promotions_completed", "promotions_headroom_full"):
+        assert stats_d[key] == stats[key], key
