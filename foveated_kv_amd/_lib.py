@@ -91,6 +91,7 @@ SIGNATURES = {
     "fkv_turbo_compress_keys": (ctypes.c_int, [P, I32, ctypes.c_int64, I32, P, P, P, P, P, P, P, P, P]),
     "fkv_turbo_compress_values": (ctypes.c_int, [P, I32, ctypes.c_int64, I32, P, P, P]),
     "fkv_attn_call": (ctypes.c_int, [P, P, I32, I32, P, P, I32, P, P, P, P]),
+    "fkv_attn_call_dev": (ctypes.c_int, [P, P, I32, I32, P, P, P, I32, P, P, P, P]),
     "fkv_attn_blob_info": (ctypes.c_int, [P, ctypes.POINTER(BlobInfoC)]),
     "fkv_attn_read_near_valid": (ctypes.c_int, [P, P, P]),
     "fkv_attn_destroy": (None, [P]),
@@ -103,7 +104,7 @@ SIGNATURES = {
     "fkv_promoter_register_archive_files": (ctypes.c_int, [P, I32, ctypes.c_char_p, ctypes.c_char_p, I32, I32,
                                                            I32, P]),
     "fkv_promoter_register_handle": (ctypes.c_int, [P, I32, P, P]),
-    "fkv_promoter_drain_device": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, I32, I32, P]),
+    "fkv_promoter_drain_device": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, I32, I32, P, P]),
     "fkv_promoter_drain": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, I32, I32]),
     "fkv_promoter_pending": (ctypes.c_int, [P, P, I32]),
     "fkv_promoter_flush": (ctypes.c_int, [P]),

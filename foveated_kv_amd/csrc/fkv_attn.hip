@@ -261,9 +261,11 @@ struct AttnArgs {
     const uint8_t* blob;
     BlobLayout L;
     const uint16_t* q;      // (B, Hq, D) fp16
-    const uint16_t* dec_k;  // (B, Hkv, n_dec, D) fp16 rows
+    const uint16_t* dec_k;  // (B, Hkv, dec_stride, D) fp16 rows, the first n_dec valid
     const uint16_t* dec_v;
     int n_dec;
+    int dec_stride;
+    const int32_t* n_dec_dev;  // when set, n_dec is read here (clamped to [0, dec_stride])
     int Hq;
     int G;            // query heads per kv head
     int head_groups;  // workgroup rows per kv head (ceil(G / 16))
@@ -1405,14 +1407,14 @@ __device__ inline void near_pv_lds(Lane<D, NQ>& st, const fkv_f4 (&sacc)[NQ], co
 // token's key row for the score operand; the value operand (dim
 // 64dh + lane of the 4 tokens of group g) is gathered when P.V needs it.
 template <int D, int NQ, typename QOp>
-__device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int64_t bkv, int tile, int lane, const QOp& qop) {
-    const int count = a.n_dec;
+__device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, int64_t bkv, int tile, int lane,
+                                const QOp& qop) {
     const int tk = tile * kTile + lane;
     uint4 kx[D / 8];
-    const uint16_t* kr = a.dec_k + (bkv * count + (tk < count ? tk : 0)) * D;
+    const uint16_t* kr = a.dec_k + (bkv * a.dec_stride + (tk < count ? tk : 0)) * D;
 #pragma unroll
     for (int c = 0; c < D / 8; c++) kx[c] = tk < count ? *(const uint4*)(kr + c * 8) : make_uint4(0, 0, 0, 0);
-    const uint16_t* vr = a.dec_v + bkv * count * D + lane;
+    const uint16_t* vr = a.dec_v + bkv * a.dec_stride * D + lane;
     fp16_compute<D, NQ>(
         st,
         [&](int s) {
@@ -1779,6 +1781,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
     }
     const int nv = (int)((const uint32_t*)(a.blob + a.L.near_valid))[kvh];
+    int n_dec = a.n_dec;
+    if (a.n_dec_dev) {  // a length kept on the device (graph-captured callers)
+        const int nd = *a.n_dec_dev;
+        n_dec = nd < 0 ? 0 : nd > a.dec_stride ? a.dec_stride : nd;
+    }
     const int nt_near = (int)cdiv(nv, kTile);
     un.nn = un.w < nt_near ? (int)cdiv(nt_near - un.w, un.N) : 0;
     if (un.nf == 0) issue(0);
@@ -1840,8 +1847,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // ---- decode buffer (row-major in global memory): tile d to wave d mod N
-    const int nt_dec = (int)cdiv(a.n_dec, kTile);
-    for (int d = un.w; d < nt_dec; d += un.N) dec_tile<D, NQ>(st, a, bkv, d, lane, qop);
+    const int nt_dec = (int)cdiv(n_dec, kTile);
+    for (int d = un.w; d < nt_dec; d += un.N) dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop);
 
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
     __syncthreads();  // every wave is done with its ring: the records reuse the LDS
@@ -2251,16 +2258,23 @@ int fkv_attn_create_g32(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32
                       far_v_scale, far_v_zero, sz_dtype, near_valid, spike_margin, stream);
 }
 
-int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
-                  const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
-                  int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
-    if (!h || !query || !out || !spike_flags || !spike_tokens) return set_error("fkv_attn_call: NULL argument");
+}  // extern "C"
+
+namespace {
+
+// n_decode: decode rows (host count) or, with n_dec_dev, the buffers' row
+// capacity (the count is then read by the kernel).
+int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
+              const void* decode_v, int32_t n_decode, const int32_t* n_dec_dev, void* out, int32_t* spike_flags,
+              int32_t* spike_tokens, void* stream) {
+    const std::string name(fn);
+    if (!h || !query || !out || !spike_flags || !spike_tokens) return set_error(name + ": NULL argument");
     const fkv::BlobLayout& L = h->L;
     if (Hq <= 0 || Hq % L.Hkv != 0)
-        return set_error("fkv_attn_call: Hq=" + std::to_string(Hq) + " is not a multiple of H_kv=" + std::to_string(L.Hkv));
+        return set_error(name + ": Hq=" + std::to_string(Hq) + " is not a multiple of H_kv=" + std::to_string(L.Hkv));
     if (n_decode < 0 || (n_decode > 0 && (!decode_k || !decode_v)))
-        return set_error("fkv_attn_call: bad decode buffer");
-    if (q_dtype < FKV_F16 || q_dtype > FKV_F32) return set_error("fkv_attn_call: unsupported query dtype");
+        return set_error(name + ": bad decode buffer");
+    if (q_dtype < FKV_F16 || q_dtype > FKV_F32) return set_error(name + ": unsupported query dtype");
     hipStream_t st = (hipStream_t)stream;
     const int G = Hq / L.Hkv;
     const int head_groups = (int)fkv::cdiv(G, fkv::kHeads);
@@ -2307,7 +2321,9 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
     a.q = q16;
     a.dec_k = (const uint16_t*)decode_k;
     a.dec_v = (const uint16_t*)decode_v;
-    a.n_dec = n_decode;
+    a.n_dec = n_dec_dev ? 0 : n_decode;
+    a.dec_stride = n_decode;
+    a.n_dec_dev = n_dec_dev;
     a.Hq = Hq;
     a.G = G;
     a.head_groups = head_groups;
@@ -2342,6 +2358,25 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
         else hipLaunchKernelGGL(fkv::merge_kernel<64>, mgrid, dim3(fkv::kWave), 0, st, a);
     }
     return check_hip(hipGetLastError(), "attn_kernel launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
+                  const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
+                  int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
+    return attn_call("fkv_attn_call", h, query, q_dtype, Hq, decode_k, decode_v, n_decode, nullptr, out, spike_flags,
+                     spike_tokens, stream);
+}
+
+int fkv_attn_call_dev(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
+                      const void* decode_v, const int32_t* n_decode_dev, int32_t capacity, void* out,
+                      int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
+    if (!n_decode_dev) return set_error("fkv_attn_call_dev: NULL n_decode_dev");
+    return attn_call("fkv_attn_call_dev", h, query, q_dtype, Hq, decode_k, decode_v, capacity, n_decode_dev, out,
+                     spike_flags, spike_tokens, stream);
 }
 
 int fkv_e4m3_decode(const uint8_t* codes, void* out_f16, int64_t n, void* stream) {

@@ -165,6 +165,7 @@ struct DrainArgs {
     const int32_t* tokens;
     const int32_t* far_idx;
     int B, Hq, Hkv, N_far, step, cooldown, budget;
+    const int32_t* step_dev;  // when set, the step is read here
     int32_t* last_step;
     uint32_t* promoted;
     const int32_t* pos_to_local;
@@ -194,6 +195,7 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
     if (threadIdx.x == 0) {
         unsigned long long det = 0, que = 0, dup = 0, cool = 0, full = 0;
         const int gqa = a.Hq / a.Hkv > 0 ? a.Hq / a.Hkv : 1;
+        const int step = a.step_dev ? *a.step_dev : a.step;
         int queued = 0, n = 0;
         for (int b = 0; b < a.B && queued < a.budget; b++) {
             for (int hq = 0; hq < a.Hq && queued < a.budget; hq++) {
@@ -204,11 +206,11 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
                 seen[hkv] = 1;
                 det++;
                 const int32_t last = a.last_step[hkv];
-                if (last != kNoStep && a.step - last < a.cooldown) {
+                if (last != kNoStep && step - last < a.cooldown) {
                     cool++;
                     continue;
                 }
-                a.last_step[hkv] = a.step;
+                a.last_step[hkv] = step;
                 const int fl = a.tokens[flat];
                 if (fl < 0 || fl >= a.N_far) continue;
                 const int32_t pos = a.far_idx[((int64_t)b * a.Hkv + hkv) * a.N_far + fl];
@@ -480,7 +482,7 @@ int fkv_promoter_pending(const fkv_promoter* p, int32_t* out_records, int32_t ma
 
 int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* flags, const int32_t* tokens,
                               const int32_t* far_idx, int32_t B, int32_t Hq, int32_t Hkv, int32_t N_far, int32_t step,
-                              void* stream) {
+                              const int32_t* step_dev, void* stream) {
     if (!p) return set_error("fkv_promoter_drain_device: NULL pipeline");
     if (layer < 0 || layer >= p->n_layers) return 0;
     const Archive& arc = p->arch[layer];
@@ -501,6 +503,7 @@ int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* fla
     a.Hkv = Hkv;
     a.N_far = N_far;
     a.step = step;
+    a.step_dev = step_dev;
     a.cooldown = p->cooldown;
     a.budget = p->max_per_drain;
     a.last_step = d.last_step;

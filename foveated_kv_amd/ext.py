@@ -239,9 +239,14 @@ class FoveatedHandle:
             self._lib.fkv_attn_destroy(h)
             self._h = None
 
-    def __call__(self, query, decode_k=None, decode_v=None):
-        """-> [out (B,Hq,1,D) fp16, spike_flags (B,Hq) int32, spike_tokens (B,Hq) int32]"""
-        _require_device(query, decode_k, decode_v)
+    def __call__(self, query, decode_k=None, decode_v=None, n_decode=None):
+        """-> [out (B,Hq,1,D) fp16, spike_flags (B,Hq) int32, spike_tokens (B,Hq) int32]
+
+        n_decode (optional): a one-element int32 device tensor holding how many
+        rows of decode_k/decode_v (then a fixed-capacity buffer) are valid.
+        The kernel reads it on the device, so a decode step can be captured
+        in a HIP graph once and replayed while the buffer fills."""
+        _require_device(query, decode_k, decode_v, n_decode)
         if query.dim() == 4:
             if query.shape[2] != 1:
                 raise ValueError("decode attention takes one query position (B,Hq,1,D)")
@@ -262,13 +267,24 @@ class FoveatedHandle:
                 raise ValueError("decode_k/decode_v must be (B,H_kv,n,D)")
             dk = decode_k.to(torch.float16).contiguous()
             dv = decode_v.to(torch.float16).contiguous()
+        if n_decode is not None:
+            if n_decode.dtype != torch.int32 or n_decode.numel() != 1:
+                raise TypeError("n_decode must be a one-element int32 device tensor")
+            if dk is None:
+                raise ValueError("a device n_decode needs a decode buffer of nonzero capacity")
         out = torch.empty((B, Hq, 1, D), dtype=torch.float16, device=self.device)
         flags = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
         tokens = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
         with torch.cuda.device(self.device):
-            check(self._lib.fkv_attn_call(self._h, ptr(q), dtype_code(q.dtype), Hq, ptr(dk), ptr(dv), n_dec,
-                                          ptr(out), ptr(flags), ptr(tokens), _lib.stream_ptr(self.device)),
-                  "fkv_attn_call")
+            if n_decode is None:
+                check(self._lib.fkv_attn_call(self._h, ptr(q), dtype_code(q.dtype), Hq, ptr(dk), ptr(dv), n_dec,
+                                              ptr(out), ptr(flags), ptr(tokens), _lib.stream_ptr(self.device)),
+                      "fkv_attn_call")
+            else:
+                check(self._lib.fkv_attn_call_dev(self._h, ptr(q), dtype_code(q.dtype), Hq, ptr(dk), ptr(dv),
+                                                  ptr(n_decode), n_dec, ptr(out), ptr(flags), ptr(tokens),
+                                                  _lib.stream_ptr(self.device)),
+                      "fkv_attn_call_dev")
         return [out, flags, tokens]
 
     def get_blob_info(self):

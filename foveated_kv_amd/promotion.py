@@ -136,10 +136,15 @@ class PromotionPipeline:
         B, Hq = spike_flags.shape[0], spike_flags.shape[1]
         Hkv, n_far = far_idx.shape[1], far_idx.shape[2]
         dev = spike_flags.device
+        # the step: a host int, or a device int32 tensor (read by the kernel)
+        step_dev = current_step if isinstance(current_step, torch.Tensor) else None
+        if step_dev is not None and not (step_dev.is_cuda and step_dev.dtype == torch.int32):
+            raise TypeError("a device step must be an int32 device tensor")
         with torch.cuda.device(dev):
             check(self._lib.fkv_promoter_drain_device(self._h, int(layer_idx), _lib.ptr(spike_flags),
                                                       _lib.ptr(spike_tokens), _lib.ptr(far_idx), B, Hq, Hkv, n_far,
-                                                      int(current_step), _lib.stream_ptr(dev)),
+                                                      0 if step_dev is not None else int(current_step),
+                                                      _lib.ptr(step_dev), _lib.stream_ptr(dev)),
                   "fkv_promoter_drain_device")
         self._keep[("dev", int(layer_idx))] = (spike_flags, spike_tokens, far_idx)
 

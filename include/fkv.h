@@ -191,6 +191,14 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
                   const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
                   int32_t* spike_flags, int32_t* spike_tokens, void* stream);
 
+/* fkv_attn_call with the decode-buffer length in device memory, for callers
+ * that capture decode steps in a HIP graph (no counterpart in the
+ * reference): decode_k/v (B,Hkv,capacity,D) fp16, rows [0, *n_decode_dev)
+ * valid; the kernel reads *n_decode_dev (clamped to [0, capacity]). */
+int fkv_attn_call_dev(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
+                      const void* decode_v, const int32_t* n_decode_dev, int32_t capacity, void* out,
+                      int32_t* spike_flags, int32_t* spike_tokens, void* stream);
+
 /* Replaces get_blob_info (:242-254): where promotions land. */
 typedef struct fkv_blob_info {
     void* blob;               /* device base pointer */
@@ -290,10 +298,12 @@ int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* spike_flag
  * copy_to_pinned (or from files); the first call per layer allocates (not
  * capturable).  A pipeline uses either this or the host drain + flush (the
  * host mirror of near_valid is not updated here); statistics accumulate on
- * the device and fkv_promoter_get_stats adds them (synchronising). */
+ * the device and fkv_promoter_get_stats adds them (synchronising).
+ * step_dev (may be NULL): the decode step is read from this device int32
+ * instead of `step` (a graph-captured step keeps its counter on the GPU). */
 int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* spike_flags,
                               const int32_t* spike_tokens, const int32_t* far_idx, int32_t B, int32_t Hq,
-                              int32_t Hkv, int32_t N_far, int32_t step, void* stream);
+                              int32_t Hkv, int32_t N_far, int32_t step, const int32_t* step_dev, void* stream);
 
 /* Queued records (not yet flushed): returns their count and copies up to
  * max_records of them as int32 [layer, head, archive row, position]. */
