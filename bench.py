@@ -165,7 +165,7 @@ def main():
     kt = torch.from_numpy(k).to(dev)
     vt = torch.from_numpy(v).to(dev)
     cl = ext.CompressHandle(cfg).compress_layer(kt, vt, with_archive=turbo)
-    # BASELINE's C3 names the group-32 V layout: measured beside the
+    # the published C3 configuration names the group-32 V layout: measured beside the
     # reference's per-token layout in the same run (not the headline value)
     g32_side = args.config.startswith("c3_") and cfg.v_group == 0 and not args.no_group32
     if g32_side:
@@ -325,14 +325,15 @@ def time_layers(torch, dev, make_handle, layers, qt, dkt, dvt, steps, warmup, ea
 
 
 def run_e2e(args, torch, dev):
-    """BASELINE C5: compress + decode + promote on one 70B-like layer (Hq=64,
+    """Workload C5: compress + decode + promote on one 70B-like layer (Hq=64,
     Hkv=8, D=128, 64K context, B=1).  Seeded importance partition, 2 % of
     far tokens aligned with the group query, per-step query drift, one
     decode token appended per step, spike drain (GQA dedup, cooldown 5,
     budget 8, the reference's filter) and promotion of exact fp16 rows from
     the pinned host archive -- on the device, and again with the reference's
-    host-side drain for comparison.  Prints one JSON line (us per decode
-    step of the device-drain loop)."""
+    host-side drain for comparison.  Prints one JSON line: us per decode
+    step of the graph-replayed device-drain loop, with the eager device-drain
+    loop and the host-drain loop beside it."""
     from foveated_kv_amd import ext, synthetic
     from foveated_kv_amd.promotion import PromotionPipeline
 
@@ -401,8 +402,49 @@ def run_e2e(args, torch, dev):
                 "host_call_us": t_call / steps * 1e6, "host_drain_us": t_drain / steps * 1e6,
                 "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
 
+    def loop_graph():
+        """The device-drain loop with the decode step captured once in a HIP
+        graph: gather step t's query, set the decode-row count from a device
+        step counter, attention over the fixed-capacity decode buffer, the
+        drain kernel, advance the counter.  Step 0 runs eagerly (it sizes the
+        workspaces), steps 1.. are graph replays with nothing read back."""
+        t0 = time.perf_counter()
+        cl, h = compress()
+        torch.cuda.synchronize()
+        compress_ms = (time.perf_counter() - t0) * 1e3
+        pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
+        pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+        pipe.register_blob(0, h)
+        step_d = torch.zeros(1, dtype=torch.int32, device=dev)
+        n_d = torch.ones(1, dtype=torch.int32, device=dev)
+        q_d = torch.empty((1,) + tuple(qs.shape[1:]), dtype=qs.dtype, device=dev)
+
+        def one():
+            torch.index_select(qs, 0, step_d, out=q_d)
+            torch.add(step_d, 1, out=n_d)
+            out, flags, toks = h(q_d[0], dkt, dvt, n_decode=n_d)
+            pipe.drain_spikes_device(0, flags, toks, fdev, step_d)
+            step_d.add_(1)
+            return out
+
+        one()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            one()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(1, steps):
+            g.replay()
+        torch.cuda.synchronize()
+        loop_s = time.perf_counter() - t0
+        assert int(step_d.item()) == steps, "graph replays did not advance the step counter"
+        return {"us_per_step": loop_s / max(steps - 1, 1) * 1e6, "compress_ms": compress_ms,
+                "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
+
     dres = loop(True)
     hres = loop(False)
+    gres = loop_graph()
     cl, h = dres["cl"], dres["h"]
     # device time of the attention call on the final state (queued back to back)
     dk_end, dv_end = dkt.contiguous(), dvt.contiguous()
@@ -415,26 +457,31 @@ def run_e2e(args, torch, dev):
     attn_us = e0.elapsed_time(e1) * 1e3 / 20
     result = {
         "metric": "C5 end-to-end decode step (attention + spike drain + promotion), 70B-like layer, 64K ctx, 1 GPU",
-        "value": round(dres["us_per_step"], 2), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": 0,
-        "ms_per_step": round(dres["us_per_step"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+        "value": round(gres["us_per_step"], 2), "unit": "us/step", "n_gpus": 1, "steps": steps - 1, "warmup": 1,
+        "ms_per_step": round(gres["us_per_step"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "c5_70b_64k_e2e", "B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S,
                    "near_valid": int(cl.near_valid[0]), "far": int(cl.far_k.shape[2]),
                    "headroom": int(cl.near_k.shape[2] - cl.near_valid[0]), "spike_frac": args.spikes,
                    "partition": "importance (seeded N(0,1) scores)", "query_drift_eps": 0.05,
                    "drain": "device (filter + row copies in one kernel after each attention launch)",
+                   "launch": "one HIP graph replay per step (query gather, counters, attention, drain); "
+                             "step 0 eager",
                    "far_format": "fp8-e4m3 K + int4 group-32 V" if args.v_group else "fp8-e4m3 K + int4 per-token V"},
-        "compress_ms": round(dres["compress_ms"], 3),
-        "host_us_per_step": {"attention_call": round(dres["host_call_us"], 2),
-                             "drain_launch": round(dres["host_drain_us"], 2)},
+        "compress_ms": round(gres["compress_ms"], 3),
         "attn_us_device": round(attn_us, 3),
-        "promotion_stats": dres["stats"],
-        "near_valid_end": dres["near_valid_end"],
+        "promotion_stats": gres["stats"],
+        "near_valid_end": gres["near_valid_end"],
+        "eager_device_drain": {"us_per_step": round(dres["us_per_step"], 2),
+                               "host_us_per_step": {"attention_call": round(dres["host_call_us"], 2),
+                                                    "drain_launch": round(dres["host_drain_us"], 2)},
+                               "same_promotions": gres["stats"] == dres["stats"]
+                               and gres["near_valid_end"] == dres["near_valid_end"]},
         "host_drain": {"us_per_step": round(hres["us_per_step"], 2),
                        "host_us_per_step": {"attention_call": round(hres["host_call_us"], 2),
                                             "spike_readback_drain_and_flush": round(hres["host_drain_us"], 2)},
-                       "same_promotions": hres["stats"] == dres["stats"]
-                       and hres["near_valid_end"] == dres["near_valid_end"]},
+                       "same_promotions": hres["stats"] == gres["stats"]
+                       and hres["near_valid_end"] == gres["near_valid_end"]},
     }
     print(json.dumps(result), flush=True)
 

@@ -179,78 +179,102 @@ struct DrainArgs {
 };
 
 // The drain filter (promotion_pipeline.cpp:99-175) and the promotion
-// (:192-241) of one layer as one workgroup: thread 0 scans (batch, query
-// head) in order exactly as fkv_promoter_drain does and assigns headroom
-// slots from the blob's near_valid; all threads then copy the exact fp16
-// rows of every archive batch from pinned host memory into the slots; the
-// near_valid bumps are written last (the next launch on the stream sees
-// rows and counts together).
+// (:192-241) of one layer as one workgroup, with the sequential scan
+// restated in parallel.  The scan visits (batch, query head) in order, keeps
+// only the first spike of each KV head (its GQA dedup), and stops once
+// `budget` spikes are queued.  Each KV head's state (last promotion step,
+// promoted bitmap, near_valid) is touched only by its own first spike, so
+// every head's outcome -- cooled down, no archived position, duplicate, or
+// queued -- is independent of the others; the scan's budget stop then means:
+// a head's first spike is processed iff fewer than `budget` queued first
+// spikes precede it in scan order.  Threads: one per (batch, query head) to
+// find each head's first spike, one per KV head for its outcome and the
+// budget rank, then all threads copy the exact fp16 rows of every archive
+// batch from pinned host memory into the assigned headroom slots; the
+// near_valid bumps are written last (the next launch on the stream sees rows
+// and counts together).  Records carry no order: each KV head has at most
+// one per drain and gets the slot at its own near_valid.
+enum : int { kNoSpike = 0, kCooled, kStamped, kDuplicate, kMarked, kQueued };
+
 __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
-    __shared__ uint8_t seen[kMaxDrainHeads];
+    __shared__ int first[kMaxDrainHeads];
+    __shared__ uint8_t queues[kMaxDrainHeads];
+    __shared__ unsigned cnt[6];  // detected, queued, deduplicated, cooled down, records, headroom full
     __shared__ int n_rec;
     __shared__ int rec_h[kMaxDrainHeads], rec_slot[kMaxDrainHeads], rec_arc[kMaxDrainHeads];
-    for (int i = threadIdx.x; i < kMaxDrainHeads; i += blockDim.x) seen[i] = 0;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kMaxDrainHeads; i += blockDim.x) first[i] = INT_MAX;
+    if (tid < 6) cnt[tid] = 0;
+    if (tid == 0) n_rec = 0;
     __syncthreads();
-    uint32_t* near_valid = (uint32_t*)(a.blob + a.L.near_valid);
-    if (threadIdx.x == 0) {
-        unsigned long long det = 0, que = 0, dup = 0, cool = 0, full = 0;
-        const int gqa = a.Hq / a.Hkv > 0 ? a.Hq / a.Hkv : 1;
-        const int step = a.step_dev ? *a.step_dev : a.step;
-        int queued = 0, n = 0;
-        for (int b = 0; b < a.B && queued < a.budget; b++) {
-            for (int hq = 0; hq < a.Hq && queued < a.budget; hq++) {
-                const int flat = b * a.Hq + hq;
-                if (a.flags[flat] == 0) continue;
-                const int hkv = hq / gqa;
-                if (hkv >= a.Hkv || seen[hkv]) continue;
-                seen[hkv] = 1;
-                det++;
-                const int32_t last = a.last_step[hkv];
-                if (last != kNoStep && step - last < a.cooldown) {
-                    cool++;
-                    continue;
+    const int gqa = a.Hq / a.Hkv > 0 ? a.Hq / a.Hkv : 1;
+    const int total = a.B * a.Hq;
+    for (int f = tid; f < total; f += blockDim.x) {
+        if (a.flags[f] != 0) {
+            const int hkv = (f % a.Hq) / gqa;
+            if (hkv < a.Hkv) atomicMin(&first[hkv], f);
+        }
+    }
+    __syncthreads();
+    // thread hkv: the outcome of the KV head's first spike
+    const int hkv = tid;
+    const int f = hkv < a.Hkv ? first[hkv] : INT_MAX;
+    const int step = a.step_dev ? *a.step_dev : a.step;
+    int kind = kNoSpike, pos = 0, arc = -1;
+    uint32_t word = 0;
+    if (f != INT_MAX) {
+        const int32_t last = a.last_step[hkv];
+        kind = (last != kNoStep && step - last < a.cooldown) ? kCooled : kStamped;
+        const int fl = a.tokens[f];
+        if (kind == kStamped && fl >= 0 && fl < a.N_far) {
+            const int32_t p = a.far_idx[((int64_t)(f / a.Hq) * a.Hkv + hkv) * a.N_far + fl];
+            if (p >= 0 && p < a.P) {
+                pos = p;
+                word = a.promoted[(int64_t)hkv * a.words + (p >> 5)];
+                if (word & (1u << (p & 31))) {
+                    kind = kDuplicate;
+                } else {
+                    arc = a.pos_to_local[(int64_t)hkv * a.P + p];
+                    kind = arc >= 0 ? kQueued : kMarked;
                 }
-                a.last_step[hkv] = step;
-                const int fl = a.tokens[flat];
-                if (fl < 0 || fl >= a.N_far) continue;
-                const int32_t pos = a.far_idx[((int64_t)b * a.Hkv + hkv) * a.N_far + fl];
-                if (pos < 0 || pos >= a.P) continue;  // not an archived position
-                uint32_t* w = a.promoted + (int64_t)hkv * a.words + (pos >> 5);
-                const uint32_t bit = 1u << (pos & 31);
-                if (*w & bit) {
-                    dup++;
-                    continue;
-                }
-                *w |= bit;
-                const int32_t arc = a.pos_to_local[(int64_t)hkv * a.P + pos];
-                if (arc < 0) continue;
-                que++;
-                queued++;
-                const uint32_t cur = near_valid[hkv];  // one record per KV head per drain
-                if ((int)cur >= a.L.Na) {
-                    full++;
-                    continue;
-                }
-                rec_h[n] = hkv;
-                rec_slot[n] = (int)cur;
-                rec_arc[n] = arc;
-                n++;
             }
         }
-        n_rec = n;
-        a.stats[0] += det;
-        a.stats[1] += que;
-        a.stats[2] += dup;
-        a.stats[3] += cool;
-        a.stats[4] += (unsigned long long)n;
-        a.stats[5] += full;
+    }
+    if (hkv < kMaxDrainHeads) queues[hkv] = kind == kQueued;
+    __syncthreads();
+    if (kind != kNoSpike) {
+        int before = 0;  // queued first spikes earlier in scan order
+        for (int j = 0; j < a.Hkv; j++) before += (queues[j] && first[j] < f) ? 1 : 0;
+        if (before < a.budget) {
+            atomicAdd(&cnt[0], 1u);
+            if (kind == kCooled) {
+                atomicAdd(&cnt[3], 1u);
+            } else {
+                a.last_step[hkv] = step;
+                if (kind == kDuplicate) atomicAdd(&cnt[2], 1u);
+                if (kind >= kMarked) a.promoted[(int64_t)hkv * a.words + (pos >> 5)] = word | (1u << (pos & 31));
+                if (kind == kQueued) {
+                    atomicAdd(&cnt[1], 1u);
+                    const uint32_t cur = ((const uint32_t*)(a.blob + a.L.near_valid))[hkv];
+                    if ((int)cur >= a.L.Na) {
+                        atomicAdd(&cnt[5], 1u);
+                    } else {
+                        const int r = atomicAdd(&n_rec, 1);
+                        rec_h[r] = hkv;
+                        rec_slot[r] = (int)cur;
+                        rec_arc[r] = arc;
+                    }
+                }
+            }
+        }
     }
     __syncthreads();
     const int n = n_rec, D = a.L.D;
+    if (tid < 6) a.stats[tid] += tid == 4 ? (unsigned long long)n : (unsigned long long)cnt[tid];
     const int nb = a.arc_B < a.L.B ? a.arc_B : a.L.B;
     uint16_t* nk = (uint16_t*)(a.blob + a.L.near_k);
     uint16_t* nv = (uint16_t*)(a.blob + a.L.near_v);
-    for (int e = threadIdx.x; e < n * nb * D; e += blockDim.x) {
+    for (int e = tid; e < n * nb * D; e += blockDim.x) {
         const int d = e % D, b = (e / D) % nb, i = e / (D * nb);
         const int h = rec_h[i], slot = rec_slot[i];
         const int64_t base = ((int64_t)b * a.L.Hkv + h) * a.L.Na_pad * D;
@@ -259,8 +283,7 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
         nv[base + fkv::near_v_index(slot, d, D)] = a.arv[src];
     }
     __syncthreads();
-    if (threadIdx.x == 0)
-        for (int i = 0; i < n; i++) near_valid[rec_h[i]] = (uint32_t)(rec_slot[i] + 1);
+    if (tid < n) ((uint32_t*)(a.blob + a.L.near_valid))[rec_h[tid]] = (uint32_t)(rec_slot[tid] + 1);
 }
 
 // Device state of a layer for the device drain, made on its first use.

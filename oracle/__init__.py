@@ -172,7 +172,7 @@ def tier_indices(S, B, H, **cfg):
 
 
 def partition_importance(importance, S, B, H, **cfg):
-    """Importance partition (the BASELINE configs' "near = sinks + window +
+    """Importance partition (the published benchmark configs' "near = sinks + window +
     top-importance middle"; the reference partitions by recency,
     mlx_foveated.py:128-169, 719-752): per (b, h), the near_from_mid middle
     tokens of highest importance, ties to the later token, NaN below every

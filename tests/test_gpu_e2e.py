@@ -18,17 +18,22 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,S,steps,vg,dev_drain", [(1, 16, 4, 128, 8192, 24, 0, False),
-                                                             (1, 14, 2, 64, 2048, 16, 32, False),
-                                                             (1, 16, 4, 128, 8192, 24, 0, True),
-                                                             (2, 16, 2, 64, 3000, 20, 32, True)])
-def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, steps, vg, dev_drain):
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,steps,vg,mode", [(1, 16, 4, 128, 8192, 24, 0, "host"),
+                                                        (1, 14, 2, 64, 2048, 16, 32, "host"),
+                                                        (1, 16, 4, 128, 8192, 24, 0, "device"),
+                                                        (2, 16, 2, 64, 3000, 20, 32, "device"),
+                                                        (1, 16, 4, 128, 8192, 24, 0, "graph"),
+                                                        (2, 16, 2, 64, 3000, 20, 32, "graph")])
+def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, steps, vg, mode):
+    """mode: "host" drains the read-back spike outputs on the host; "device"
+    drains with the device kernel; "graph" captures step 1's attention (decode
+    count on the device) and device drain (step on the device) in a HIP graph
+    and replays it for every later step."""
     from foveated_kv_amd import ext, synthetic
     from foveated_kv_amd.promotion import PromotionPipeline
 
     seed = S + steps
-    print(f"e2e loop B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} v_group={vg} device_drain={dev_drain}",
-          flush=True)
+    print(f"e2e loop B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} v_group={vg} mode={mode}", flush=True)
     k, v = synthetic.make_kv(B, Hkv, S, D, seed)
     q0 = synthetic.make_query(B, Hq, D, seed)
     imp = torch.from_numpy(synthetic.make_importance(B, Hkv, S, seed)).cuda()
@@ -56,13 +61,40 @@ def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, st
     dkt, dvt = torch.from_numpy(dk).cuda(), torch.from_numpy(dv).cuda()
     lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).astype(np.float64)
     flagged = 0
+    q_st = torch.empty((B, Hq, 1, D), dtype=torch.float16, device="cuda")
+    step_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    n_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    graph = graph_res = None
+
+    def one():  # the captured step: count from the step, attention, drain, advance
+        torch.add(step_d, 1, out=n_d)
+        res = h(q_st, dkt, dvt, n_decode=n_d)
+        pipe.drain_spikes_device(0, res[1], res[2], fdev, step_d)
+        step_d.add_(1)
+        return res
+
     for t in range(steps):
-        if not dev_drain:
+        if mode == "host":
             pipe.order(0)
         q = torch.from_numpy(qs[t]).cuda()
         n = t + 1
-        out, flags, toks = h(q[:, :, None], dkt[:, :, :n].contiguous(), dvt[:, :, :n].contiguous())
+        if mode == "graph":
+            q_st.copy_(q[:, :, None])
+            if t == 0:
+                out, flags, toks = one()  # eager: sizes the workspaces before capture
+            else:
+                if graph is None:
+                    torch.cuda.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        graph_res = one()
+                graph.replay()
+                out, flags, toks = graph_res
+        else:
+            out, flags, toks = h(q[:, :, None], dkt[:, :, :n].contiguous(), dvt[:, :, :n].contiguous())
         torch.cuda.synchronize()
+        if mode == "graph":
+            assert int(step_d.item()) == n
         o, kf, kt, mf, mn = orc.attend_kernel(qs[t], near_k[0], near_v[0], nv[0], *far, dk[:, :, :n], dv[:, :, :n],
                                               spike_margin=10.0)
         got = _np(out)[:, :, 0].astype(np.float64)
@@ -77,9 +109,9 @@ def test_decode_promote_loop_matches_oracle_every_step(orc, B, Hq, Hkv, D, S, st
             assert abs(sc[tk[b, hq]] - sc[kt[b, hq]]) <= 1e-5 * (1 + abs(sc.max())), (t, b, hq)
         flagged += int(fl.sum())
         # both pipelines see the GPU's spike outputs, so their states stay comparable
-        if dev_drain:
+        if mode == "device":
             pipe.drain_spikes_device(0, flags, toks, fdev, t)
-        else:
+        elif mode == "host":
             pipe.drain_spikes(0, flags, toks, far_idx, t)
         ref.drain(0, fl, tk, far_idx, t)
         ref.commit(near_k, near_v, nv, {0: cl.near_k.shape[2]})

@@ -285,7 +285,7 @@ def test_promotion_from_archive_files(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,cooldown,budget,headroom_min", [(1, 0, 8, 8), (2, 3, 2, 8), (1, 1, 8, 2)])
+@pytest.mark.parametrize("B,cooldown,budget,headroom_min", [(1, 0, 8, 8), (2, 3, 2, 8), (1, 1, 8, 2), (3, 2, 3, 8)])
 def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroom_min):
     """drain_spikes_device (filter + promotion in one kernel, spike outputs
     and far_idx in device memory) against the CPU restatement of the host
