@@ -254,7 +254,9 @@ __global__ void cast_to_f16_kernel(const void* __restrict__ src, int dtype, int6
 // ---------------------------------------------------------------------------
 
 constexpr int kHeads = 16;  // query heads per workgroup row: up to 4 quads of 4
-constexpr int kHdr = 5;     // record header: m, l, min_near, max_far, first argmax
+// record header: m, l, min_near, max_far, first argmax, 3 unused (records
+// of kHdr + D floats stay 16-byte aligned for the direct merge's loads)
+constexpr int kHdr = 8;
 constexpr int kMaxSplits = 64;
 
 struct AttnArgs {
@@ -1433,156 +1435,109 @@ __device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, i
         tile, count, lane >> 2, a.inv_sqrt_d, qop, []() {});
 }
 
-// Merge of the partial records of all splits of one row into `fin`
+// Merge of the partial records of all splits of one row
 // (csrc/kernels/foveated_attn.metal:394-431 restated for partials in
 // memory): split maxima are rescaled to the global max; spike fields take
-// the min and the first-index max.  `hdr` / `scl` are LDS scratch.
-__device__ inline float ld_agent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// the min and the first-index max.
+//
+// Coherent 16-byte loads of split records: a buffer load with the sc1 cache
+// policy (the policy of agent-scope atomic loads), four dwords per lane;
+// offsets past the buffer read 0 without touching memory.
+constexpr int kCpolSc1 = 16;
+__device__ inline fkv_f4 ld_agent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
 }
 
-// The last split of a row when all records fit in LDS: one batch of
-// coherent loads (every load issued before the first wait), then each
-// thread merges its output elements straight into the outputs -- the same
-// arithmetic, in the same order, as merge_splits + finalize_rows.
+// The last split of a row merges every split's record.  One CU reading all
+// of them is bound by the bytes it keeps in flight, so the records are read with
+// 16-byte coherent loads, and every load of the split headers and of the
+// first batch of values (one 4-element chunk x 32 splits per thread) is
+// issued before the first wait.  The headers are merged in registers, one
+// wave per head with a lane per split, while the values arrive -- the same
+// arithmetic, in the same order, as merge_kernel, so both merges give the
+// same bits.  `lds` holds ng * ns + ng floats.
 template <int D>
-__device__ inline void merge_finalize_staged(const AttnArgs& a, const float* src, int ns, int ng, float* stage,
-                                             int b, int head0) {
+__device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, float* lds, int b,
+                                             int head0) {
     constexpr int RS = kHdr + D;
-    constexpr int kBatch = 16;
-    const int total = ns * ng * RS;
+    constexpr int C = D / 4;  // 16-byte chunks of one head's values
+    constexpr int kS = 32;    // splits per batch of value loads
+    constexpr int kG = kHeads / kWavesPerGroup;  // heads per wave
+    static_assert(RS % 4 == 0 && kHdr == 8, "records must be 16-byte aligned with an 8-float header");
+    static_assert(kMaxSplits <= kWave, "a lane per split");
     const int nt = (int)blockDim.x, t = (int)threadIdx.x;
-    for (int base = 0; base < total; base += kBatch * nt) {
-        float r[kBatch];
+    const int wave = t / kWave, lane = t % kWave;
+    float* scl = lds;             // (head, split) softmax rescale factors
+    float* linv = scl + ng * ns;  // (head) 1 / merged sum
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
+    const int nc = ng * C;
+    const int sp_l = lane < ns ? lane : ns - 1;
+    fkv_f4 h0[kG], h1[kG];
 #pragma unroll
-        for (int k = 0; k < kBatch; k++) {
-            const int i = base + k * nt + t;
-            r[k] = ld_agent(src + (i < total ? i : total - 1));
+    for (int j = 0; j < kG; j++) {
+        const int g = wave + j * kWavesPerGroup;
+        if (g < ng) {
+            h0[j] = ld_agent4(rs, (sp_l * ng + g) * RS * 4);
+            h1[j] = ld_agent4(rs, (sp_l * ng + g) * RS * 4 + 16);
         }
+    }
+    fkv_f4 r[kS];
+    auto issue = [&](int c, int s0) {  // chunks past the output load nothing
+        const int off = c < nc ? ((c / C) * RS + kHdr + 4 * (c % C)) * 4 : ns * ng * RS * 4;
 #pragma unroll
-        for (int k = 0; k < kBatch; k++) {
-            const int i = base + k * nt + t;
-            if (i < total) stage[i] = r[k];
+        for (int k = 0; k < kS; k++)
+            if (s0 + k < ns) r[k] = ld_agent4(rs, off + (s0 + k) * ng * RS * 4);
+    };
+    issue(t, 0);  // in flight while the headers are merged
+#pragma unroll
+    for (int j = 0; j < kG; j++) {
+        const int g = wave + j * kWavesPerGroup;
+        if (g < ng) {
+            const bool live = lane < ns;
+            const float ms = live ? h0[j].x : -INFINITY, ls = live ? h0[j].y : 0.f;
+            float mn = live ? h0[j].z : INFINITY, mx = live ? h0[j].w : -INFINITY;
+            int arg = live ? __float_as_int(h1[j].x) : INT_MAX;
+            const float M = wave_max(ms);
+            const float f = ms == -INFINITY ? 0.f : __expf(ms - M);
+            const float L = wave_sum(f * ls);
+            mn = wave_min(mn);
+            wave_argmax(mx, arg);
+            if (live) scl[g * ns + lane] = f;
+            if (lane == 0) {
+                linv[g] = L > 0.f ? 1.0f / L : 0.f;
+                const int64_t o = (int64_t)b * a.Hq + head0 + g;
+                a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
+                a.tokens[o] = mx == -INFINITY ? -1 : arg;
+            }
         }
     }
     __syncthreads();
-    for (int i = t; i < ng * D; i += nt) {
-        const int g = i / D, d = i % D;
-        float M = -INFINITY;
-        for (int sp = 0; sp < ns; sp++) M = fmaxf(M, stage[(sp * ng + g) * RS]);
-        float L = 0.f, v = 0.f;
-        for (int sp = 0; sp < ns; sp++) {
-            const float* h = stage + (sp * ng + g) * RS;
-            const float f = h[0] == -INFINITY ? 0.f : __expf(h[0] - M);
-            L += f * h[1];
-            v += f * h[kHdr + d];
+    for (int c0 = 0; c0 < nc; c0 += nt) {
+        const int c = c0 + t, g = (c < nc ? c : nc - 1) / C;
+        float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+        for (int s0 = 0; s0 < ns; s0 += kS) {
+            if (c0 != 0 || s0 != 0) issue(c, s0);
+#pragma unroll
+            for (int k = 0; k < kS; k++) {
+                if (s0 + k < ns) {
+                    const float f = scl[g * ns + s0 + k];
+                    v0 += f * r[k].x;
+                    v1 += f * r[k].y;
+                    v2 += f * r[k].z;
+                    v3 += f * r[k].w;
+                }
+            }
         }
-        const float inv_l = L > 0.f ? 1.0f / L : 0.f;
-        a.out[((int64_t)b * a.Hq + head0 + g) * D + d] = f2h(v * inv_l);
-    }
-    if (t < ng) {
-        const int g = t;
-        float mn = INFINITY, mx = -INFINITY;
-        int arg = INT_MAX;
-        for (int sp = 0; sp < ns; sp++) {
-            const float* h = stage + (sp * ng + g) * RS;
-            mn = fminf(mn, h[2]);
-            const float fx = h[3];
-            const int fa = __float_as_int(h[4]);
-            if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
+        if (c < nc) {
+            const float il = linv[g];
+            const uint2 w = {f2h(v0 * il) | ((uint32_t)f2h(v1 * il) << 16),
+                             f2h(v2 * il) | ((uint32_t)f2h(v3 * il) << 16)};
+            *(uint2*)(a.out + ((int64_t)b * a.Hq + head0 + g) * D + 4 * (c % C)) = w;
         }
-        const int64_t o = (int64_t)b * a.Hq + head0 + g;
-        a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
-        a.tokens[o] = mx == -INFINITY ? -1 : arg;
     }
 }
 
-template <int D>
-__device__ inline void merge_splits(const float* src, int ns, int ng, float* fin, float* hdr, float* scl,
-                                    float* stage, int stage_cap) {
-    constexpr int RS = kHdr + D;
-    // All records of the row in one batch of coherent loads (one memory
-    // round trip), then everything else from LDS.
-    if (ns * ng * RS <= stage_cap) {
-        const int total = ns * ng * RS;
-#pragma unroll 8
-        for (int i = threadIdx.x; i < total; i += blockDim.x) stage[i] = ld_agent(src + i);
-        __syncthreads();
-        for (int i = threadIdx.x; i < ns * ng * kHdr; i += blockDim.x) {
-            const int sp = i / (ng * kHdr), r = i % (ng * kHdr);
-            hdr[i] = stage[sp * ng * RS + (r / kHdr) * RS + r % kHdr];
-        }
-        __syncthreads();
-        if ((int)threadIdx.x < ng) {
-            const int g = threadIdx.x;
-            float M = -INFINITY;
-            for (int sp = 0; sp < ns; sp++) M = fmaxf(M, hdr[(sp * ng + g) * kHdr]);
-            float L = 0.f, mn = INFINITY, mx = -INFINITY;
-            int arg = INT_MAX;
-            for (int sp = 0; sp < ns; sp++) {
-                const float* h = hdr + (sp * ng + g) * kHdr;
-                const float f = h[0] == -INFINITY ? 0.f : __expf(h[0] - M);
-                scl[g * kMaxSplits + sp] = f;
-                L += f * h[1];
-                mn = fminf(mn, h[2]);
-                const float fx = h[3];
-                const int fa = __float_as_int(h[4]);
-                if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
-            }
-            fin[g * RS + 0] = M;
-            fin[g * RS + 1] = L;
-            fin[g * RS + 2] = mn;
-            fin[g * RS + 3] = mx;
-            fin[g * RS + 4] = __int_as_float(arg);
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
-            const int g = i / D, d = i % D;
-            float v = 0.f;
-            for (int sp = 0; sp < ns; sp++) v += scl[g * kMaxSplits + sp] * stage[(sp * ng + g) * RS + kHdr + d];
-            fin[g * RS + kHdr + d] = v;
-        }
-        __syncthreads();
-        return;
-    }
-    for (int i = threadIdx.x; i < ns * ng * kHdr; i += blockDim.x) {
-        const int sp = i / (ng * kHdr), r = i % (ng * kHdr);
-        hdr[i] = ld_agent(src + (int64_t)sp * ng * RS + (r / kHdr) * RS + r % kHdr);
-    }
-    __syncthreads();
-    if ((int)threadIdx.x < ng) {
-        const int g = threadIdx.x;
-        float M = -INFINITY;
-        for (int sp = 0; sp < ns; sp++) M = fmaxf(M, hdr[(sp * ng + g) * kHdr]);
-        float L = 0.f, mn = INFINITY, mx = -INFINITY;
-        int arg = INT_MAX;
-        for (int sp = 0; sp < ns; sp++) {
-            const float* h = hdr + (sp * ng + g) * kHdr;
-            const float f = h[0] == -INFINITY ? 0.f : __expf(h[0] - M);
-            scl[g * kMaxSplits + sp] = f;
-            L += f * h[1];
-            mn = fminf(mn, h[2]);
-            const float fx = h[3];
-            const int fa = __float_as_int(h[4]);
-            if (fx > mx || (fx == mx && fa < arg)) { mx = fx; arg = fa; }
-        }
-        fin[g * RS + 0] = M;
-        fin[g * RS + 1] = L;
-        fin[g * RS + 2] = mn;
-        fin[g * RS + 3] = mx;
-        fin[g * RS + 4] = __int_as_float(arg);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
-        const int g = i / D, d = i % D;
-        const float* col = src + g * RS + kHdr + d;
-        float v = 0.f;
-#pragma unroll 8
-        for (int sp = 0; sp < ns; sp++) v += scl[g * kMaxSplits + sp] * ld_agent(col + (int64_t)sp * ng * RS);
-        fin[g * RS + kHdr + d] = v;
-    }
-    __syncthreads();
-}
 
 // Unit u of one wave's stream: the wave's far tiles first (far tile
 // f0 + u*fs), then each of its near tiles w + j*N as two units, keys then
@@ -1717,11 +1672,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float qf[TQ ? 4 * NQ * D : 4];
     __shared__ float rsum[TQ ? 4 * NQ : 4];
     // The rings during the tile loop; afterwards (behind a barrier) the
-    // per-wave records, then past wave 0's records the split-merge scratch
-    // of the last workgroup.
+    // per-wave records; once they are published, the split-merge scratch of
+    // the last workgroup.
     constexpr int kRing = kWavesPerGroup * 2 * SLOT;
     constexpr int kRec = kWavesPerGroup * NHW * RS * 4;
-    constexpr int kMrg = (NHW * RS + kMaxSplits * NHW * kHdr + NHW * kMaxSplits) * 4;
+    constexpr int kMrg = (NHW * kMaxSplits + NHW) * 4;
     constexpr int kLds = kRing > kRec ? (kRing > kMrg ? kRing : kMrg) : (kRec > kMrg ? kRec : kMrg);
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
     float* smem = (float*)lds;
@@ -1957,17 +1912,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
-    if (a.num_splits * ng * RS <= kLds / 4) {
-        // every record (this split's included) is in global memory now: the
-        // whole LDS can stage them
-        merge_finalize_staged<D>(a, part, a.num_splits, ng, smem, b, head0);
-    } else {
-        float* hdr = smem + NHW * RS;
-        float* scl = hdr + kMaxSplits * NHW * kHdr;
-        float* stage = scl + NHW * kMaxSplits;
-        merge_splits<D>(part, a.num_splits, ng, smem, hdr, scl, stage, kLds / 4 - (int)(stage - smem));
-        finalize_rows<D>(a, smem, b, head0, ng);
-    }
+    // every record (this split's included) is in global memory now
+    static_assert((NHW * kMaxSplits + NHW) * 4 <= kLds, "direct-merge scratch");
+    merge_finalize_direct<D>(a, part, a.num_splits, ng, smem, b, head0);
     if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

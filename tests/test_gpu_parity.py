@@ -211,6 +211,8 @@ def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16
     dict(B=1, Hq=6, Hkv=2, D=128, S=36, n_dec=2, seed=7),        # no far tier
     dict(B=1, Hq=8, Hkv=2, D=64, S=40, n_dec=0, seed=8),         # 4 far tokens
     dict(B=3, Hq=12, Hkv=4, D=64, S=333, n_dec=70, seed=9),      # ragged tiles
+    dict(B=1, Hq=64, Hkv=8, D=128, S=32768, n_dec=5, seed=10),   # 32 splits x 8 heads: records exceed LDS
+    dict(B=1, Hq=32, Hkv=4, D=64, S=16384, n_dec=3, seed=11),    # the same at D = 64
 ])
 def test_attention_parity(fkv, orc, args):
     run_attention(fkv, orc, **args)
@@ -329,12 +331,13 @@ def test_e4m3_converter_matches_reference_lut(fkv, orc):
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,S,n_dec,vg", [(8, 32, 8, 128, 8192, 0, 0), (2, 32, 2, 64, 3000, 9, 0),
-                                                   (8, 32, 8, 128, 8192, 0, 32)])
+                                                   (8, 32, 8, 128, 8192, 0, 32), (1, 64, 8, 128, 65536, 7, 0)])
 def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
     """The last-arriving split merges the partial records in-kernel; its
     arrival counters are re-armed by the kernel itself.  200 launches queued
     back to back (no host sync between them) must all be bit-identical, and
-    must agree with the separate merge launch."""
+    must equal the separate merge launch bit for bit (both merges follow the
+    same arithmetic in the same order)."""
     from foveated_kv_amd import ext, synthetic
 
     _flush(f"fused merge stress B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} v_group={vg}")
@@ -361,3 +364,4 @@ def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
     assert torch.equal(first[1], ref[1]) and torch.equal(first[2], ref[2])
     diff = (first[0].float() - ref[0].float()).abs().max().item()
     assert diff <= 1e-3 * max(1.0, ref[0].float().abs().max().item()), diff
+    assert torch.equal(first[0], ref[0])
