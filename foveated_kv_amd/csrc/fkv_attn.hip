@@ -401,6 +401,8 @@ __device__ inline uint32_t word_of(const uint4& x, int i) {
 typedef uint32_t fkv_v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t fkv_v4u __attribute__((ext_vector_type(4)));
 #define FKV_LDS __attribute__((address_space(3)))
+// constant memory: read-only for the duration of a launch (scalar loads)
+#define FKV_CONST __attribute__((address_space(4)))
 
 // 32-bit LDS address of a pointer into a __shared__ array.
 __device__ inline uint32_t lds_addr(const void* p) {
@@ -1557,9 +1559,13 @@ struct Units {
 // tile count, so the split needs no device read).  Contiguous ranges when
 // every wave's share of far bytes covers at least one near tile (the
 // cumulative boundaries are then non-decreasing), else round-robin.
+struct FarPlan {
+    int f0, fs, nf;
+};
+
 template <int D>
-__device__ inline void plan_far(Units& un, int nt_far, int near_plan, int64_t FB) {
-    const int64_t NB = 256 * D, N = un.N;
+__device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int near_plan, int64_t FB) {
+    const int64_t NB = 256 * D, N = n_waves;
     if ((int64_t)nt_far * FB >= N * NB) {
         const int64_t q = near_plan / N, r = near_plan % N;
         const int64_t total = near_plan * NB + (int64_t)nt_far * FB;
@@ -1570,14 +1576,10 @@ __device__ inline void plan_far(Units& un, int nt_far, int near_plan, int64_t FB
             const int64_t g = (2 * num + N * FB) / (2 * N * FB);  // round to nearest
             return (int)(g < 0 ? 0 : g > nt_far ? nt_far : g);
         };
-        un.f0 = bound(un.w);
-        un.nf = bound(un.w + 1) - un.f0;
-        un.fs = 1;
-    } else {
-        un.f0 = un.w;
-        un.fs = un.N;
-        un.nf = un.w < nt_far ? (int)cdiv(nt_far - un.w, un.N) : 0;
+        const int f0 = bound(w);
+        return FarPlan{f0, 1, bound(w + 1) - f0};
     }
+    return FarPlan{w, n_waves, w < nt_far ? (int)cdiv(nt_far - w, n_waves) : 0};
 }
 
 // TurboQuant query rotation and sketch inside the attention kernel:
@@ -1697,7 +1699,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     Units un;
     un.N = kWavesPerGroup * a.num_splits;
     un.w = kWavesPerGroup * split + wave;
-    plan_far<D>(un, (int)cdiv(a.L.F, kTile), a.near_plan, REC);
+    {
+        const FarPlan fp = plan_far<D>(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC);
+        un.f0 = fp.f0;
+        un.fs = fp.fs;
+        un.nf = fp.nf;
+    }
     un.nn = 0;
     auto issue = [&](int u) {  // DMA of unit u into slot u % 2; returns its vector-memory op count
         const int kd = un.kind(u);
@@ -1710,19 +1717,46 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         else if (kd != kNone) dma_near<D>(a, bkv, un.tile(u), kd == kNearV, lane, slot);
         return kd == kNone ? 0 : kd == kFarUnit ? FAR_OPS : NEAR_OPS;
     };
-    if (un.nf > 0) issue(0);
-
-    // ---- query -> LDS as the B operand of the score MFMA: [qd][s][j][4 halves]
-    for (int i = threadIdx.x; i < NQ * NS * 16; i += blockDim.x) {
-        const int e = i & 3, jj = (i >> 2) & 3, sq = i >> 4;
-        const int s = sq % NS, qd = sq / NS;
-        const int h = 4 * qd + jj;
-        qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
+    // ---- the query -> LDS as the B operand of the score MFMA,
+    // [qd][s][j][4 halves], by LDS DMA issued before the ring's: the waits
+    // below then cover it without waiting for the ring, and no LDS store is
+    // needed (the compiler orders LDS stores after every in-flight DMA).
+    // Dword w = ((qd * NS + s) * 4 + j) * 2 + e holds dims 4s + 2e, +1 of
+    // head 4qd + j; heads past the group read head 0's row (finite values
+    // whose results are never written).  TurboQuant stages its own query.
+    if constexpr (!TQ) {
+        constexpr int QW = NQ * NS * 8;
+        static_assert(QW % kWave == 0, "whole-wave query DMA");
+#pragma unroll
+        for (int k = 0; k < (QW / kWave + kWavesPerGroup - 1) / kWavesPerGroup; k++) {
+            const int w0 = (k * kWavesPerGroup + wave) * kWave;  // wave-uniform
+            if (w0 < QW) {
+                const int wd = w0 + lane, e = wd & 1, jj = (wd >> 1) & 3, s = (wd >> 3) % NS;
+                const int h = 4 * ((wd >> 3) / NS) + jj;
+                const uint16_t* src = a.q + ((int64_t)b * a.Hq + head0 + (h < ng ? h : 0)) * D + 4 * s + 2 * e;
+                __builtin_amdgcn_global_load_lds((const void*)src, (FKV_LDS void*)((uint8_t*)qs + w0 * 4), 4, 0, 0);
+            }
+        }
     }
+    // the wave's first two far tiles need no device state either
+    if (un.nf > 0) issue(0);
+    const bool early1 = !TQ && un.nf > 1;  // TurboQuant uses slot 1 of wave 0 until the stream starts
+    if (early1) issue(1);
+    // near_valid and a device decode count are written only by earlier
+    // launches, so they are read as constant memory (scalar loads, whose
+    // counter is not the one the ring's DMA uses)
+    const int nv = (int)*(const FKV_CONST uint32_t*)(uintptr_t)(a.blob + a.L.near_valid + 4 * (int64_t)kvh);
+    const int nd_raw = a.n_dec_dev ? *(const FKV_CONST int32_t*)(uintptr_t)a.n_dec_dev : a.n_dec;
     float asum[NQ];
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) asum[qd] = 0.f;
     if constexpr (TQ) {
+        for (int i = threadIdx.x; i < NQ * NS * 16; i += blockDim.x) {
+            const int e = i & 3, jj = (i >> 2) & 3, sq = i >> 4;
+            const int s = sq % NS, qd = sq / NS;
+            const int h = 4 * qd + jj;
+            qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
+        }
         for (int i = threadIdx.x; i < 4 * NQ * D; i += blockDim.x) {
             const int h = i / D;
             qf[i] = h < ng ? h2f(a.q[((int64_t)b * a.Hq + head0 + h) * D + i % D]) : 0.f;
@@ -1735,12 +1769,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             for (int qd = 0; qd < NQ; qd++) asum[qd] = rsum[4 * qd + j];
         }
     }
-    const int nv = (int)((const uint32_t*)(a.blob + a.L.near_valid))[kvh];
-    int n_dec = a.n_dec;
-    if (a.n_dec_dev) {  // a length kept on the device (graph-captured callers)
-        const int nd = *a.n_dec_dev;
-        n_dec = nd < 0 ? 0 : nd > a.dec_stride ? a.dec_stride : nd;
-    }
+    // a decode length kept on the device (graph-captured callers) is clamped
+    const int n_dec = a.n_dec_dev ? (nd_raw < 0 ? 0 : nd_raw > a.dec_stride ? a.dec_stride : nd_raw) : nd_raw;
     const int nt_near = (int)cdiv(nv, kTile);
     un.nn = un.w < nt_near ? (int)cdiv(nt_near - un.w, un.N) : 0;
     if (un.nf == 0) issue(0);
@@ -1761,7 +1791,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // q operand reads from LDS (see QOperand)
     const QOperand<NS> qop{qs, j * 4};
     const QOperand<NS> qrop{qt, j * 4}, qkop{qt + (TQ ? NQ * NS * 16 : 0), j * 4};
-    __syncthreads();
+    if constexpr (TQ) {
+        __syncthreads();
+    } else {
+        // the query DMA is this wave's oldest vector-memory op: wait for it
+        // but not for the ring, then for every wave's part of the query
+        if (early1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * FAR_OPS) : "memory");
+        else if (un.nf > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FAR_OPS) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+    }
 
     // ---- the stream: unit u is computed while unit u + 1 streams in ----
     fkv_f4 sacc[NQ];  // near scores, carried from a K unit to its V unit
@@ -1771,7 +1810,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (int u = 0; u < nu; u++) {
         // the slot refilled now was read by unit u - 1, whose reads completed
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const int pend = issue(u + 1);
+        const int pend = (u == 0 && early1) ? FAR_OPS : issue(u + 1);  // unit 1 may be in flight already
         // unit u's loads are complete once at most unit u + 1's are pending
         if (pend == FAR_OPS) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FAR_OPS) : "memory");
         else if (pend == NEAR_OPS) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NEAR_OPS) : "memory");
@@ -2222,6 +2261,8 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     if (n_decode < 0 || (n_decode > 0 && (!decode_k || !decode_v)))
         return set_error(name + ": bad decode buffer");
     if (q_dtype < FKV_F16 || q_dtype > FKV_F32) return set_error(name + ": unsupported query dtype");
+    if (q_dtype == FKV_F16 && ((uintptr_t)query & 7) != 0)
+        return set_error(name + ": an fp16 query must be 8-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int G = Hq / L.Hkv;
     const int head_groups = (int)fkv::cdiv(G, fkv::kHeads);
