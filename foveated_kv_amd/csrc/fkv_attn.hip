@@ -254,6 +254,7 @@ __global__ void cast_to_f16_kernel(const void* __restrict__ src, int dtype, int6
 // ---------------------------------------------------------------------------
 
 constexpr int kHeads = 16;  // query heads per workgroup row: up to 4 quads of 4
+constexpr int kSmallGrid = 64;  // fewer workgroups than this: rows of 4 query heads
 // record header: m, l, min_near, max_far, first argmax, 3 unused (records
 // of kHdr + D floats stay 16-byte aligned for the direct merge's loads)
 constexpr int kHdr = 8;
@@ -270,7 +271,8 @@ struct AttnArgs {
     const int32_t* n_dec_dev;  // when set, n_dec is read here (clamped to [0, dec_stride])
     int Hq;
     int G;            // query heads per kv head
-    int head_groups;  // workgroup rows per kv head (ceil(G / 16))
+    int head_groups;  // workgroup rows per kv head (ceil(G / hpg))
+    int hpg;          // query heads per workgroup row (4 or kHeads)
     int num_splits;
     float spike_margin;
     float inv_sqrt_d;
@@ -1689,8 +1691,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int hgrp = blockIdx.y % a.head_groups;
     const int b = blockIdx.z;
     const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
-    const int head0 = kvh * a.G + hgrp * kHeads;
-    const int ng = min(kHeads, a.G - hgrp * kHeads);
+    const int head0 = kvh * a.G + hgrp * a.hpg;
+    const int ng = min(a.hpg, a.G - hgrp * a.hpg);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int j = lane & 3, blk = lane >> 2;
     uint8_t* ring = lds + wave * 2 * SLOT;
@@ -1928,7 +1930,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     // ---- split-K: publish this split's record ----
     const int row = (int)(bkv * a.head_groups + hgrp);  // (b, kv_head, head group)
-    float* part = a.ws + (int64_t)row * a.num_splits * ng * RS;
+    // rows are spaced for the widest row (a last head group may be narrower)
+    float* part = a.ws + (int64_t)row * a.num_splits * min(a.hpg, a.G) * RS;
     if (a.arrive == nullptr) {  // merged by merge_kernel (kernel boundary orders it)
         for (int i = threadIdx.x; i < ng * RS; i += blockDim.x) part[(int64_t)split * ng * RS + i] = smem[i];
         return;
@@ -1967,11 +1970,11 @@ __global__ __launch_bounds__(64) void merge_kernel(AttnArgs a) {
     const int hgrp = row % a.head_groups;
     const int64_t bkv = row / a.head_groups;
     const int b = (int)(bkv / a.L.Hkv), kvh = (int)(bkv % a.L.Hkv);
-    const int head0 = kvh * a.G + hgrp * kHeads;
-    const int ng = min(kHeads, a.G - hgrp * kHeads);
+    const int head0 = kvh * a.G + hgrp * a.hpg;
+    const int ng = min(a.hpg, a.G - hgrp * a.hpg);
     if (g >= ng) return;
     const int ns = a.num_splits, lane = threadIdx.x;
-    const float* src = a.ws + (int64_t)row * ns * ng * RS + g * RS;
+    const float* src = a.ws + (int64_t)row * ns * min(a.hpg, a.G) * RS + g * RS;
     float ms = -INFINITY, ls = 0.f, mn = INFINITY, mx = -INFINITY;
     int arg = INT_MAX;
     if (lane < ns) {
@@ -2265,8 +2268,16 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         return set_error(name + ": an fp16 query must be 8-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int G = Hq / L.Hkv;
-    const int head_groups = (int)fkv::cdiv(G, fkv::kHeads);
-    const int ng_max = G < fkv::kHeads ? G : fkv::kHeads;
+    // Query heads per workgroup row: the whole GQA group (up to kHeads), so
+    // every compressed byte crosses HBM once -- unless that leaves most CUs
+    // idle (few batch x KV-head rows, short context): then rows of 4 heads,
+    // more workgroups re-reading the same small KV from L2.
+    int hpg = fkv::kHeads;
+    if (G > 4 && L.B * L.Hkv * (int)fkv::cdiv(G, hpg) * fkv::plan_splits(L, L.B * L.Hkv * (int)fkv::cdiv(G, hpg),
+                                                                          n_decode) < fkv::kSmallGrid)
+        hpg = 4;
+    const int head_groups = (int)fkv::cdiv(G, hpg);
+    const int ng_max = G < hpg ? G : hpg;
     const int rows = L.B * L.Hkv * head_groups;
     const int splits = fkv::plan_splits(L, rows, n_decode);
     const uint16_t* q16 = (const uint16_t*)query;
@@ -2315,6 +2326,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.Hq = Hq;
     a.G = G;
     a.head_groups = head_groups;
+    a.hpg = hpg;
     a.num_splits = splits;
     a.spike_margin = h->margin;
     a.inv_sqrt_d = (float)(1.0 / sqrt((double)L.D));

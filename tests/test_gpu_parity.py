@@ -213,6 +213,8 @@ def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16
     dict(B=3, Hq=12, Hkv=4, D=64, S=333, n_dec=70, seed=9),      # ragged tiles
     dict(B=1, Hq=64, Hkv=8, D=128, S=32768, n_dec=5, seed=10),   # 32 splits x 8 heads: records exceed LDS
     dict(B=1, Hq=32, Hkv=4, D=64, S=16384, n_dec=3, seed=11),    # the same at D = 64
+    dict(B=4, Hq=40, Hkv=2, D=128, S=4096, n_dec=5, seed=12),    # G = 20: a 16-head and a 4-head row
+    dict(B=1, Hq=12, Hkv=2, D=64, S=600, n_dec=2, seed=13),      # small grid: rows of 4 heads, G = 6
 ])
 def test_attention_parity(fkv, orc, args):
     run_attention(fkv, orc, **args)
