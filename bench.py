@@ -404,9 +404,10 @@ def run_e2e(args, torch, dev):
 
     def loop_graph():
         """The device-drain loop with the decode step captured once in a HIP
-        graph: gather step t's query, set the decode-row count from a device
-        step counter, attention over the fixed-capacity decode buffer, the
-        drain kernel, advance the counter.  Step 0 runs eagerly (it sizes the
+        graph: advance the decode-row count n (a device int32), gather the
+        query of step n - 1, attention over the fixed-capacity decode buffer,
+        the drain kernel with n as its step (the filter only compares steps,
+        so the +1 offset changes nothing).  Step 0 runs eagerly (it sizes the
         workspaces), steps 1.. are graph replays with nothing read back."""
         t0 = time.perf_counter()
         cl, h = compress()
@@ -415,16 +416,15 @@ def run_e2e(args, torch, dev):
         pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
         pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
         pipe.register_blob(0, h)
-        step_d = torch.zeros(1, dtype=torch.int32, device=dev)
-        n_d = torch.ones(1, dtype=torch.int32, device=dev)
+        n_d = torch.zeros(1, dtype=torch.int32, device=dev)
+        q1 = torch.cat([qs[:1], qs])  # row n holds the query of step n - 1
         q_d = torch.empty((1,) + tuple(qs.shape[1:]), dtype=qs.dtype, device=dev)
 
         def one():
-            torch.index_select(qs, 0, step_d, out=q_d)
-            torch.add(step_d, 1, out=n_d)
+            n_d.add_(1)
+            torch.index_select(q1, 0, n_d, out=q_d)
             out, flags, toks = h(q_d[0], dkt, dvt, n_decode=n_d)
-            pipe.drain_spikes_device(0, flags, toks, fdev, step_d)
-            step_d.add_(1)
+            pipe.drain_spikes_device(0, flags, toks, fdev, n_d)
             return out
 
         one()
@@ -438,7 +438,7 @@ def run_e2e(args, torch, dev):
             g.replay()
         torch.cuda.synchronize()
         loop_s = time.perf_counter() - t0
-        assert int(step_d.item()) == steps, "graph replays did not advance the step counter"
+        assert int(n_d.item()) == steps, "graph replays did not advance the step counter"
         return {"us_per_step": loop_s / max(steps - 1, 1) * 1e6, "compress_ms": compress_ms,
                 "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
 
@@ -465,7 +465,7 @@ def run_e2e(args, torch, dev):
                    "headroom": int(cl.near_k.shape[2] - cl.near_valid[0]), "spike_frac": args.spikes,
                    "partition": "importance (seeded N(0,1) scores)", "query_drift_eps": 0.05,
                    "drain": "device (filter + row copies in one kernel after each attention launch)",
-                   "launch": "one HIP graph replay per step (query gather, counters, attention, drain); "
+                   "launch": "one HIP graph replay per step (row counter, query gather, attention, drain); "
                              "step 0 eager",
                    "far_format": "fp8-e4m3 K + int4 group-32 V" if args.v_group else "fp8-e4m3 K + int4 per-token V"},
         "compress_ms": round(gres["compress_ms"], 3),
