@@ -75,6 +75,34 @@ def test_device_count_matches_host_count(fkv, v_group):
     _same(h(q, dk, dv, n_decode=ndev), h(q), "n < 0")
 
 
+def test_device_count_matches_host_count_turbo(fkv):
+    """The same for a TurboQuant far tier (its own query staging)."""
+    from foveated_kv_amd import ext, synthetic
+    from foveated_kv_amd import turbo as tq
+
+    B, Hq, Hkv, D, S, cap = 4, 32, 8, 128, 8192, 100
+    _flush(f"device n_decode turbo B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} capacity={cap}")
+    k, v = synthetic.make_kv(B, Hkv, S, D, 45)
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = 8
+    cl = ext.CompressHandle(cfg).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                               with_archive=True)
+    tc = tq.get_turbo_constants(D)
+    tfar = tq.turbo_compress_keys(cl.archive_k, tc) + tq.turbo_compress_values(cl.archive_v)
+    h = tq.TurboFoveatedHandle(cl.near_k, cl.near_v, *tfar, cl.near_valid, tc.Pi, tc.S, tc.centroids,
+                               spike_margin=10.0)
+    q = torch.from_numpy(synthetic.make_query(B, Hq, D, 45)).cuda()[:, :, None, :]
+    dk, dv = synthetic.make_decode(B, Hkv, cap, D, 45)
+    dk, dv = torch.from_numpy(dk).cuda(), torch.from_numpy(dv).cuda()
+    ndev = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for n in (0, 1, 64, 65, cap):
+        ndev.fill_(n)
+        got = h(q, dk, dv, n_decode=ndev)
+        want = h(q, dk[:, :, :n].contiguous(), dv[:, :, :n].contiguous()) if n else h(q)
+        torch.cuda.synchronize()
+        _same(got, want, f"turbo n={n}")
+
+
 def test_device_count_rejects_bad_arguments(fkv):
     h, q = _layer(1, 8, 2, 64, 8192, seed=43)
     dk = torch.zeros((1, 2, 4, 64), dtype=torch.float16, device="cuda")
