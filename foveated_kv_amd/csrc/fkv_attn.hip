@@ -282,6 +282,7 @@ struct AttnArgs {
     float* ws;      // split partials: [row][split][ng][kHdr + D]
     int* arrive;    // [row] split arrival counters (zero between calls)
     int near_plan;  // expected near tiles per row (balances the far split)
+    int dec_wave0;  // the wave that takes decode tile 0
     // TurboQuant far tier (fmt 1)
     const float* tq_PiT;    // (D, D) fp32, PiT[j][i] = Pi[i][j]
     const float* tq_ST;     // (D, D) fp32, ST[j][i] = S[i][j]
@@ -1842,9 +1843,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // no LDS write may land after the ring is reused or the wave ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // ---- decode buffer (row-major in global memory): tile d to wave d mod N
+    // ---- decode buffer (row-major in global memory): tile d to wave
+    // dec_wave0 + d mod N (the host picks the least loaded waves).  The far
+    // split does not depend on the decode length: a device-held count gives
+    // the same partition, and the same bits, as the host count.
     const int nt_dec = (int)cdiv(n_dec, kTile);
-    for (int d = un.w; d < nt_dec; d += un.N) dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop);
+    for (int d = (un.w - a.dec_wave0 + un.N) % un.N; d < nt_dec; d += un.N)
+        dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop);
 
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
     __syncthreads();  // every wave is done with its ring: the records reuse the LDS
@@ -2337,6 +2342,15 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     const bool fused_merge = fkv::env_int("FKV_FUSED_MERGE", 1) != 0;
     a.arrive = fused_merge ? h->arrive : nullptr;
     a.near_plan = h->near_plan;
+    {
+        // Decode tiles after the near tiles where the far tiles are dealt
+        // round-robin (the waves past the near tiles carry the least);
+        // where the far split is byte-balanced those waves already hold
+        // the near tiles' share in far tiles, slower per byte: from wave 0.
+        const int nw = splits * fkv::kWavesPerGroup;
+        const bool rr = (int64_t)fkv::cdiv(L.F, fkv::kTile) * (int64_t)L.far_rec < (int64_t)nw * 256LL * L.D;
+        a.dec_wave0 = rr ? h->near_plan % nw : 0;
+    }
     const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
     a.tq_PiT = h->tq.PiT;
     a.tq_ST = h->tq.ST;
