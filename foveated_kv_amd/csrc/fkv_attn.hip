@@ -1559,28 +1559,39 @@ struct Units {
 
 // Far tiles of wave w of a row, byte-balanced against the row's near tiles
 // (near tile t goes to wave t mod N; `near_plan` is the host's expected near
-// tile count, so the split needs no device read).  Contiguous ranges when
-// every wave's share of far bytes covers at least one near tile (the
-// cumulative boundaries are then non-decreasing), else round-robin.
+// tile count, so the split needs no device read): contiguous ranges whose
+// boundaries round v / N of the row's bytes minus the near bytes before
+// wave v, clamped to [0, F].  The unclamped boundary is linear in v with a
+// positive slope once v passes the waves with an extra near tile and passes
+// through 0 before, so the clamped boundaries never decrease; waves holding
+// more near tiles than their share take no far tiles.  TurboQuant far tiles
+// cost far more time per byte than near tiles, so where a wave's far share is
+// below one near tile they are dealt round-robin instead.  The host repeats
+// this plan (far_bound) to place decode tiles.
 struct FarPlan {
     int f0, fs, nf;
 };
 
+__host__ __device__ inline int far_bound(int64_t v, int64_t N, int NT, int FT, int64_t NB, int64_t FB) {
+    if (v >= N) return FT;
+    const int64_t q = NT / N, r = NT % N;
+    const int64_t total = NT * NB + (int64_t)FT * FB;
+    const int64_t near_before = v * q + (v < r ? v : r);
+    const int64_t num = v * total - N * near_before * NB;
+    const int64_t g = (2 * num + N * FB) / (2 * N * FB);  // round to nearest (negative: clamped)
+    return (int)(g < 0 ? 0 : g > FT ? FT : g);
+}
+
+__host__ __device__ inline bool far_round_robin(bool tq, int64_t N, int FT, int64_t NB, int64_t FB) {
+    return tq && (int64_t)FT * FB < N * NB;
+}
+
 template <int D>
-__device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int near_plan, int64_t FB) {
-    const int64_t NB = 256 * D, N = n_waves;
-    if ((int64_t)nt_far * FB >= N * NB) {
-        const int64_t q = near_plan / N, r = near_plan % N;
-        const int64_t total = near_plan * NB + (int64_t)nt_far * FB;
-        auto bound = [&](int64_t v) -> int {  // first far tile of wave v
-            if (v >= N) return nt_far;
-            const int64_t near_before = v * q + (v < r ? v : r);
-            const int64_t num = v * total - N * near_before * NB;  // >= 0 here
-            const int64_t g = (2 * num + N * FB) / (2 * N * FB);  // round to nearest
-            return (int)(g < 0 ? 0 : g > nt_far ? nt_far : g);
-        };
-        const int f0 = bound(w);
-        return FarPlan{f0, 1, bound(w + 1) - f0};
+__device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int near_plan, int64_t FB, bool tq) {
+    const int64_t NB = 256 * D;
+    if (!far_round_robin(tq, n_waves, nt_far, NB, FB)) {
+        const int f0 = far_bound(w, n_waves, near_plan, nt_far, NB, FB);
+        return FarPlan{f0, 1, far_bound(w + 1, n_waves, near_plan, nt_far, NB, FB) - f0};
     }
     return FarPlan{w, n_waves, w < nt_far ? (int)cdiv(nt_far - w, n_waves) : 0};
 }
@@ -1703,7 +1714,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     un.N = kWavesPerGroup * a.num_splits;
     un.w = kWavesPerGroup * split + wave;
     {
-        const FarPlan fp = plan_far<D>(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC);
+        const FarPlan fp = plan_far<D>(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC, TQ);
         un.f0 = fp.f0;
         un.fs = fp.fs;
         un.nf = fp.nf;
@@ -2343,13 +2354,32 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.arrive = fused_merge ? h->arrive : nullptr;
     a.near_plan = h->near_plan;
     {
-        // Decode tiles after the near tiles where the far tiles are dealt
-        // round-robin (the waves past the near tiles carry the least);
-        // where the far split is byte-balanced those waves already hold
-        // the near tiles' share in far tiles, slower per byte: from wave 0.
-        const int nw = splits * fkv::kWavesPerGroup;
-        const bool rr = (int64_t)fkv::cdiv(L.F, fkv::kTile) * (int64_t)L.far_rec < (int64_t)nw * 256LL * L.D;
-        a.dec_wave0 = rr ? h->near_plan % nw : 0;
+        // Decode tiles go to the wave with the fewest planned bytes where a
+        // wave's far share is below one near tile (the near tiles then
+        // decide the balance): after the near tiles when far tiles are dealt
+        // round-robin.  Where the far split is byte-balanced over many far
+        // tiles, from wave 0 (the waves without near tiles hold their share
+        // in far tiles, slower per byte).
+        const int nw = splits * fkv::kWavesPerGroup, FT = (int)fkv::cdiv(L.F, fkv::kTile);
+        const int64_t NB = 256LL * L.D, FB = (int64_t)L.far_rec;
+        a.dec_wave0 = 0;
+        if ((int64_t)FT * FB < nw * NB) {
+            if (fkv::far_round_robin(L.fmt == 1, nw, FT, NB, FB)) {
+                a.dec_wave0 = h->near_plan % nw;
+            } else {
+                int64_t best = -1;
+                for (int w = 0; w < nw; w++) {
+                    const int64_t nn = h->near_plan / nw + (w < h->near_plan % nw ? 1 : 0);
+                    const int64_t nf = fkv::far_bound(w + 1, nw, h->near_plan, FT, NB, FB) -
+                                       fkv::far_bound(w, nw, h->near_plan, FT, NB, FB);
+                    const int64_t cost = nn * NB + nf * FB;
+                    if (best < 0 || cost < best) {
+                        best = cost;
+                        a.dec_wave0 = w;
+                    }
+                }
+            }
+        }
     }
     const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
     a.tq_PiT = h->tq.PiT;
