@@ -274,13 +274,22 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
     const int nb = a.arc_B < a.L.B ? a.arc_B : a.L.B;
     uint16_t* nk = (uint16_t*)(a.blob + a.L.near_k);
     uint16_t* nv = (uint16_t*)(a.blob + a.L.near_v);
-    for (int e = tid; e < n * nb * D; e += blockDim.x) {
-        const int d = e % D, b = (e / D) % nb, i = e / (D * nb);
+    // 16-byte reads of the pinned archive (8 dims of a row: few, wide bus
+    // transactions); the 8 K dims are contiguous in the near tile, the V
+    // dims are 8 elements apart
+    const int DC = D / 8;
+    for (int e = tid; e < n * nb * DC; e += blockDim.x) {
+        const int c = e % DC, b = (e / DC) % nb, i = e / (DC * nb);
         const int h = rec_h[i], slot = rec_slot[i];
         const int64_t base = ((int64_t)b * a.L.Hkv + h) * a.L.Na_pad * D;
-        const int64_t src = (((int64_t)b * a.Hkv + h) * a.arc_S + rec_arc[i]) * D + d;
-        nk[base + fkv::near_k_index(slot, d, D)] = a.ark[src];
-        nv[base + fkv::near_v_index(slot, d, D)] = a.arv[src];
+        const int64_t src = (((int64_t)b * a.Hkv + h) * a.arc_S + rec_arc[i]) * D + 8 * c;
+        const uint4 kw = *(const uint4*)(a.ark + src);
+        const uint4 vw = *(const uint4*)(a.arv + src);
+        *(uint4*)(nk + base + fkv::near_k_index(slot, 8 * c, D)) = kw;
+        const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            nv[base + fkv::near_v_index(slot, 8 * c + k, D)] = (uint16_t)(vv[k >> 1] >> (16 * (k & 1)));
     }
     __syncthreads();
     if (tid < n) ((uint32_t*)(a.blob + a.L.near_valid))[rec_h[tid]] = (uint32_t)(rec_slot[tid] + 1);
