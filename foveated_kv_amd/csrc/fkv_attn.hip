@@ -1557,11 +1557,12 @@ struct Units {
     __device__ int tile(int u) const { return u < nf ? f0 + u * fs : w + ((u - nf) >> 1) * N; }
 };
 
-// Far tiles of wave w of a row, byte-balanced against the row's near tiles
+// Far tiles of wave w of a row, balanced against the row's near tiles
 // (near tile t goes to wave t mod N; `near_plan` is the host's expected near
-// tile count, so the split needs no device read): contiguous ranges whose
-// boundaries round v / N of the row's bytes minus the near bytes before
-// wave v, clamped to [0, F].  The unclamped boundary is linear in v with a
+// tile count, so the split needs no device read; a near tile weighs NB, a
+// far tile its record bytes FB): contiguous ranges whose boundaries round
+// v / N of the row's weight minus the near weight before wave v, clamped to
+// [0, F].  The unclamped boundary is linear in v with a
 // positive slope once v passes the waves with an extra near tile and passes
 // through 0 before, so the clamped boundaries never decrease; waves holding
 // more near tiles than their share take no far tiles.  TurboQuant far tiles
@@ -1586,9 +1587,14 @@ __host__ __device__ inline bool far_round_robin(bool tq, int64_t N, int FT, int6
     return tq && (int64_t)FT * FB < N * NB;
 }
 
+// The weight of a near tile in the far split, in bytes: its K and V bytes
+// (256 * D) where the stream is bound by HBM (one head quad); half of that
+// for 8-16 query heads per row, whose far tiles cost more arithmetic per
+// byte than the fp16 near tiles (measured: C5, 64K, G = 8, 42.6 -> 40.0 us).
+__host__ __device__ inline int64_t near_tile_weight(int nq, int D) { return (nq >= 2 ? 128 : 256) * (int64_t)D; }
+
 template <int D>
-__device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int near_plan, int64_t FB, bool tq) {
-    const int64_t NB = 256 * D;
+__device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int near_plan, int64_t FB, bool tq, int64_t NB) {
     if (!far_round_robin(tq, n_waves, nt_far, NB, FB)) {
         const int f0 = far_bound(w, n_waves, near_plan, nt_far, NB, FB);
         return FarPlan{f0, 1, far_bound(w + 1, n_waves, near_plan, nt_far, NB, FB) - f0};
@@ -1714,7 +1720,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     un.N = kWavesPerGroup * a.num_splits;
     un.w = kWavesPerGroup * split + wave;
     {
-        const FarPlan fp = plan_far<D>(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC, TQ);
+        const FarPlan fp =
+            plan_far<D>(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC, TQ, near_tile_weight(NQ, D));
         un.f0 = fp.f0;
         un.fs = fp.fs;
         un.nf = fp.nf;
@@ -2361,7 +2368,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         // tiles, from wave 0 (the waves without near tiles hold their share
         // in far tiles, slower per byte).
         const int nw = splits * fkv::kWavesPerGroup, FT = (int)fkv::cdiv(L.F, fkv::kTile);
-        const int64_t NB = 256LL * L.D, FB = (int64_t)L.far_rec;
+        const int64_t NB = fkv::near_tile_weight((ng_max + 3) / 4, L.D), FB = (int64_t)L.far_rec;
         a.dec_wave0 = 0;
         if ((int64_t)FT * FB < nw * NB) {
             if (fkv::far_round_robin(L.fmt == 1, nw, FT, NB, FB)) {
