@@ -1593,8 +1593,8 @@ __host__ __device__ inline bool far_round_robin(bool tq, int64_t N, int FT, int6
 // byte than the fp16 near tiles (measured: C5, 64K, G = 8, 42.6 -> 40.0 us).
 __host__ __device__ inline int64_t near_tile_weight(int nq, int D) { return (nq >= 2 ? 128 : 256) * (int64_t)D; }
 
-template <int D>
-__device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int near_plan, int64_t FB, bool tq, int64_t NB) {
+__host__ __device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int near_plan, int64_t FB, bool tq,
+                                            int64_t NB) {
     if (!far_round_robin(tq, n_waves, nt_far, NB, FB)) {
         const int f0 = far_bound(w, n_waves, near_plan, nt_far, NB, FB);
         return FarPlan{f0, 1, far_bound(w + 1, n_waves, near_plan, nt_far, NB, FB) - f0};
@@ -1721,7 +1721,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     un.w = kWavesPerGroup * split + wave;
     {
         const FarPlan fp =
-            plan_far<D>(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC, TQ, near_tile_weight(NQ, D));
+            plan_far(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC, TQ, near_tile_weight(NQ, D));
         un.f0 = fp.f0;
         un.fs = fp.fs;
         un.nf = fp.nf;
@@ -2420,6 +2420,19 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
                   int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
     return attn_call("fkv_attn_call", h, query, q_dtype, Hq, decode_k, decode_v, n_decode, nullptr, out, spike_flags,
                      spike_tokens, stream);
+}
+
+int fkv_far_plan(int32_t n_waves, int32_t near_plan, int32_t nt_far, int64_t near_weight, int64_t far_rec,
+                 int32_t turbo, int32_t* f0, int32_t* fs, int32_t* nf) {
+    if (n_waves <= 0 || near_plan < 0 || nt_far < 0 || near_weight <= 0 || far_rec <= 0 || !f0 || !fs || !nf)
+        return set_error("fkv_far_plan: bad argument");
+    for (int w = 0; w < n_waves; w++) {
+        const fkv::FarPlan p = fkv::plan_far(w, n_waves, nt_far, near_plan, far_rec, turbo != 0, near_weight);
+        f0[w] = p.f0;
+        fs[w] = p.fs;
+        nf[w] = p.nf;
+    }
+    return FKV_OK;
 }
 
 int fkv_attn_call_dev(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,

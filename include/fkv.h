@@ -191,6 +191,16 @@ int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
                   const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
                   int32_t* spike_flags, int32_t* spike_tokens, void* stream);
 
+/* The attention kernel's far-tile plan for one row (host only, no GPU): wave
+ * w of n_waves streams far tiles f0[w] + u * fs[w], u < nf[w].  near_weight
+ * is a near tile's weight in bytes (256 * D for one head quad per row, half
+ * for more), far_rec a far record's bytes, turbo nonzero for the TurboQuant
+ * layout.  No counterpart in the reference (its split is per q head, not per
+ * wave): an introspection hook so tests can check every far tile is planned
+ * exactly once. */
+int fkv_far_plan(int32_t n_waves, int32_t near_plan, int32_t nt_far, int64_t near_weight, int64_t far_rec,
+                 int32_t turbo, int32_t* f0, int32_t* fs, int32_t* nf);
+
 /* fkv_attn_call with the decode-buffer length in device memory, for callers
  * that capture decode steps in a HIP graph (no counterpart in the
  * reference): decode_k/v (B,Hkv,capacity,D) fp16, rows [0, *n_decode_dev)

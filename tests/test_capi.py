@@ -103,3 +103,55 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     from foveated_kv_amd import ext
 
     assert ext.is_available() is False
+
+
+def _far_plan(lib, N, NT, FT, NB, FB, turbo):
+    f0 = (ctypes.c_int32 * N)()
+    fs = (ctypes.c_int32 * N)()
+    nf = (ctypes.c_int32 * N)()
+    assert lib.fkv_far_plan(N, NT, FT, NB, FB, turbo, f0, fs, nf) == 0
+    return list(f0), list(fs), list(nf)
+
+
+def test_far_plan_covers_every_far_tile_once():
+    """The attention kernel's per-wave far-tile plan (the same function the
+    kernel runs): over random row shapes every far tile is streamed by
+    exactly one wave; outside TurboQuant's round-robin regime the waves take
+    contiguous, ordered ranges."""
+    import random
+
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+    rng = random.Random(11)
+    shapes = [(16, 26, 231), (16, 13, 116), (16, 52, 461), (128, 103, 922), (32, 10, 58), (4, 2, 8), (8, 0, 5),
+              (64, 300, 3), (256, 0, 0)]
+    shapes += [(rng.choice([4, 8, 12, 16, 32, 64, 128, 256]), rng.randint(0, 400), rng.randint(0, 4000))
+               for _ in range(1500)]
+    for N, NT, FT in shapes:
+        for NB, FB, turbo in ((256 * 128, 12544, 0), (128 * 128, 12544, 0), (256 * 64, 6272, 0),
+                              (256 * 128, 13312, 0), (256 * 128, 5888, 1), (256 * 64, 2944 + 256, 1)):
+            f0, fs, nf = _far_plan(lib, N, NT, FT, NB, FB, turbo)
+            tiles = [f0[w] + u * fs[w] for w in range(N) for u in range(nf[w])]
+            assert sorted(tiles) == list(range(FT)), (N, NT, FT, NB, FB, turbo)
+            if all(s == 1 for s in fs):
+                assert all(f0[w] + nf[w] == f0[w + 1] for w in range(N - 1)), (N, NT, FT, NB, FB, turbo)
+            elif not turbo:
+                pytest.fail(f"round-robin far plan outside TurboQuant: {(N, NT, FT, NB, FB)}")
+
+
+def test_far_plan_balances_c3_16k():
+    """C3-16K (16 waves per row, 26 near and 231 far tiles of 12,544 bytes,
+    near tiles round-robin): every wave's bytes within one far tile of the
+    mean, the worst within 0.6 of one."""
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+    N, NT, FT, NB, FB = 16, 26, 231, 256 * 128, 12544
+    f0, fs, nf = _far_plan(lib, N, NT, FT, NB, FB, 0)
+    cost = [(NT // N + (1 if w < NT % N else 0)) * NB + nf[w] * FB for w in range(N)]
+    mean = sum(cost) / N
+    assert max(abs(c - mean) for c in cost) <= FB
+    assert max(cost) - mean <= 0.6 * FB
+    with pytest.raises(Exception):
+        _lib.check(lib.fkv_far_plan(0, 1, 1, NB, FB, 0, None, None, None), "fkv_far_plan")
