@@ -74,7 +74,7 @@ def test_fp8_encoder_divergence_between_reference_encoders(orc):
     metal = orc.encode_fp8(ALL16)
     py = orc.encode_fp8(ALL16, python_semantics=True)
     diff = metal != py
-    # 18,688 fp16 patterns disagree (survey count); all sit in the underflow
+    # 18,688 fp16 patterns disagree (an exhaustive count); all sit in the underflow
     # rounding band or at/above the overflow threshold
     assert int(diff.sum()) == 18688
     a = np.abs(ALL16[diff].view(np.float16).astype(np.float64))
