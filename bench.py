@@ -212,7 +212,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16 operands, f32 accumulation",
         "data": "synthetic",
         "config": {"workload": args.config, "B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S,
                    "near_valid": R, "far": F, "n_decode": n_dec, "layers_per_step": L,
@@ -459,7 +459,7 @@ def run_e2e(args, torch, dev):
         "metric": "C5 end-to-end decode step (attention + spike drain + promotion), 70B-like layer, 64K ctx, 1 GPU",
         "value": round(gres["us_per_step"], 2), "unit": "us/step", "n_gpus": 1, "steps": steps - 1, "warmup": 1,
         "ms_per_step": round(gres["us_per_step"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "vs_baseline": None, "dtype": "f16 operands, f32 accumulation", "data": "synthetic",
         "config": {"workload": "c5_70b_64k_e2e", "B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S,
                    "near_valid": int(cl.near_valid[0]), "far": int(cl.far_k.shape[2]),
                    "headroom": int(cl.near_k.shape[2] - cl.near_valid[0]), "spike_frac": args.spikes,

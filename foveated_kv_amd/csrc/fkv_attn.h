@@ -121,14 +121,21 @@ struct fkv_attn_impl {
     fkv::BlobLayout L;
     uint8_t* blob = nullptr;
     float margin = 0.f;
-    float* ws = nullptr;  // split partials
+    // Call workspace, allocated once by the handle's first call for that
+    // call's query-head count and never re-allocated (a captured HIP graph
+    // keeps these pointers): split partials for the largest launch plan any
+    // decode length can produce, the per-row arrival counters, an fp16 copy
+    // of bf16 / f32 queries.
+    int ws_hq = 0;          // query heads the workspace is sized for (0: none yet)
+    float* ws = nullptr;    // split partials
     size_t ws_floats = 0;
-    uint16_t* qbuf = nullptr;  // fp16 copy of non-fp16 queries
-    size_t qbuf_n = 0;
+    uint16_t* qbuf = nullptr;
     int* arrive = nullptr;  // per-row split arrival counters (zero between calls)
     size_t arrive_n = 0;
     int near_plan = 0;      // expected near tiles per row: max near_valid / 64, rounded up
     int device = 0;
+    int target_wgs = 256;   // workgroups a launch aims for (FKV_TARGET_WGS at creation)
+    bool fused_merge = true;  // in-kernel split merge (FKV_FUSED_MERGE at creation)
     fkv::TurboConsts tq;    // fmt 1 only
 };
 
@@ -137,6 +144,18 @@ struct fkv_attn : fkv_attn_impl {};
 namespace fkv {
 
 int grid_for(int64_t n, int block);
+
+// How one call is launched: query heads per workgroup row, rows, splits,
+// and the split-partial floats it needs.
+struct LaunchPlan {
+    int hpg, head_groups, ng_max, rows, splits;
+    size_t ws_floats;
+};
+LaunchPlan plan_launch(const BlobLayout& L, int Hq, int n_decode, int target_wgs);
+// The workspace a handle's first call allocates for Hq query heads: enough
+// for every launch plan of that head count (any decode length).
+size_t workspace_floats(const BlobLayout& L, int Hq);
+int workspace_rows(const BlobLayout& L, int Hq);
 // Handle construction shared by the fp8 and TurboQuant formats: allocates
 // the blob (zeroed), packs the near tiers and near_valid (stream-ordered).
 int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, const void* near_k,

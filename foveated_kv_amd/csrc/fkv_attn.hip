@@ -23,7 +23,8 @@
 // products); 1/sqrt(D) is applied to the fp32 scores.
 // The blob stores every tier pre-arranged in these operand layouts so each
 // lane's operand bytes are contiguous and every wave load is a contiguous
-// 1 KB.  Split partials are merged by a small second kernel.
+// 1 KB.  Split partials are merged inside the kernel by the last split of a
+// row to arrive (merge_kernel, a separate launch, is kept for comparison).
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -2144,15 +2145,51 @@ static int env_int(const char* name, int dflt) {
 
 // Workgroups per (b, kv_head, head group): enough to fill 256 CUs, at least
 // two tiles per wave.
-int plan_splits(const BlobLayout& L, int rows, int n_dec) {
+static int plan_splits(const BlobLayout& L, int rows, int n_dec, int target) {
     const int tiles = (int)(cdiv(L.Na, kTile) + cdiv(L.F, kTile) + cdiv(n_dec, kTile));
-    const int target = env_int("FKV_TARGET_WGS", 256);
     int s = (int)cdiv(target, rows > 0 ? rows : 1);
     const int cap = tiles / (2 * kWavesPerGroup);
     if (s > cap) s = cap;
     if (s > kMaxSplits) s = kMaxSplits;
     return s < 1 ? 1 : s;
 }
+
+static size_t partial_floats(int rows, int splits, int ng_max, int D) {
+    return (size_t)rows * splits * ng_max * (kHdr + D);
+}
+
+// Query heads per workgroup row: the whole GQA group (up to kHeads), so
+// every compressed byte crosses HBM once -- unless that leaves most CUs idle
+// (few batch x KV-head rows, short context): then rows of 4 heads, more
+// workgroups re-reading the same small KV from L2.
+LaunchPlan plan_launch(const BlobLayout& L, int Hq, int n_decode, int target_wgs) {
+    const int G = Hq / L.Hkv;
+    int hpg = kHeads;
+    const int rows16 = L.B * L.Hkv * (int)cdiv(G, kHeads);
+    if (G > 4 && rows16 * plan_splits(L, rows16, n_decode, target_wgs) < kSmallGrid) hpg = 4;
+    LaunchPlan p;
+    p.hpg = hpg;
+    p.head_groups = (int)cdiv(G, hpg);
+    p.ng_max = G < hpg ? G : hpg;
+    p.rows = L.B * L.Hkv * p.head_groups;
+    p.splits = plan_splits(L, p.rows, n_decode, target_wgs);
+    p.ws_floats = p.splits > 1 ? partial_floats(p.rows, p.splits, p.ng_max, L.D) : 0;
+    return p;
+}
+
+// Both row widths at the largest split count: covers plan_launch for every
+// decode length and target.
+size_t workspace_floats(const BlobLayout& L, int Hq) {
+    const int G = Hq / L.Hkv;
+    size_t best = 0;
+    for (int hpg : {4, kHeads}) {
+        const size_t f = partial_floats(L.B * L.Hkv * (int)cdiv(G, hpg), kMaxSplits, G < hpg ? G : hpg, L.D);
+        best = f > best ? f : best;
+    }
+    return best;
+}
+
+int workspace_rows(const BlobLayout& L, int Hq) { return L.B * L.Hkv * (int)cdiv(Hq / L.Hkv, 4); }
 
 }  // namespace fkv
 
@@ -2165,6 +2202,10 @@ int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, 
                const void* near_v, int near_dtype, const int32_t* near_valid, float margin, hipStream_t st) {
     h->L = make_layout(B, Hkv, D, Na, F, fmt);
     h->margin = margin;
+    // tuning knobs are read once here, never on the call path
+    h->target_wgs = env_int("FKV_TARGET_WGS", 256);
+    if (h->target_wgs < 1) h->target_wgs = 1;
+    h->fused_merge = env_int("FKV_FUSED_MERGE", 1) != 0;
     int rc = check_hip(hipGetDevice(&h->device), "hipGetDevice");
     if (!rc) rc = check_hip(hipMalloc(&h->blob, h->L.total), "hipMalloc(blob)");
     if (!rc) rc = check_hip(hipMemsetAsync(h->blob, 0, h->L.total, st), "hipMemsetAsync(blob)");
@@ -2274,68 +2315,68 @@ int fkv_attn_create_g32(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32
 
 namespace {
 
-// n_decode: decode rows (host count) or, with n_dec_dev, the buffers' row
-// capacity (the count is then read by the kernel).
+// The handle's call workspace, allocated by its first call (sized for every
+// launch plan of that query-head count) and never re-allocated afterwards.
+int ensure_workspace(const std::string& name, fkv_attn* h, int Hq, hipStream_t st) {
+    if (h->ws_hq == Hq) return FKV_OK;
+    if (h->ws_hq != 0)
+        return set_error(name + ": this handle's workspace was sized by its first call for Hq=" +
+                         std::to_string(h->ws_hq) + "; a call with Hq=" + std::to_string(Hq) +
+                         " needs a handle of its own");
+    const fkv::BlobLayout& L = h->L;
+    const size_t wsf = fkv::workspace_floats(L, Hq);
+    const int rows = fkv::workspace_rows(L, Hq);
+    const size_t qn = (size_t)L.B * Hq * L.D;
+    int rc = check_hip(hipMalloc(&h->ws, wsf * sizeof(float)), "hipMalloc(ws)");
+    if (!rc) rc = check_hip(hipMalloc(&h->arrive, rows * sizeof(int)), "hipMalloc(arrive)");
+    if (!rc) rc = check_hip(hipMalloc(&h->qbuf, qn * 2), "hipMalloc(qbuf)");
+    if (rc) {
+        if (h->ws) (void)hipFree(h->ws);
+        if (h->arrive) (void)hipFree(h->arrive);
+        if (h->qbuf) (void)hipFree(h->qbuf);
+        h->ws = nullptr;
+        h->arrive = nullptr;
+        h->qbuf = nullptr;
+        return rc;
+    }
+    h->ws_floats = wsf;
+    h->arrive_n = rows;
+    h->ws_hq = Hq;
+    // counters start at zero; the kernel's last split re-arms them
+    hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(rows, 256)), dim3(256), 0, st, h->arrive, rows);
+    return check_hip(hipGetLastError(), "zero_ints_kernel launch");
+}
+
+// n_decode: valid decode rows (host count) or, with n_dec_dev, ignored (the
+// kernel reads the count there); dec_stride: rows per (batch, kv head)
+// block of decode_k / decode_v.
 int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
-              const void* decode_v, int32_t n_decode, const int32_t* n_dec_dev, void* out, int32_t* spike_flags,
-              int32_t* spike_tokens, void* stream) {
+              const void* decode_v, int32_t n_decode, int32_t dec_stride, const int32_t* n_dec_dev, void* out,
+              int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
     const std::string name(fn);
     if (!h || !query || !out || !spike_flags || !spike_tokens) return set_error(name + ": NULL argument");
     const fkv::BlobLayout& L = h->L;
     if (Hq <= 0 || Hq % L.Hkv != 0)
         return set_error(name + ": Hq=" + std::to_string(Hq) + " is not a multiple of H_kv=" + std::to_string(L.Hkv));
-    if (n_decode < 0 || (n_decode > 0 && (!decode_k || !decode_v)))
+    if (n_decode < 0 || dec_stride < n_decode || (dec_stride > 0 && (!decode_k || !decode_v)))
         return set_error(name + ": bad decode buffer");
     if (q_dtype < FKV_F16 || q_dtype > FKV_F32) return set_error(name + ": unsupported query dtype");
     if (q_dtype == FKV_F16 && ((uintptr_t)query & 7) != 0)
         return set_error(name + ": an fp16 query must be 8-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = ensure_workspace(name, h, Hq, st)) return rc;
     const int G = Hq / L.Hkv;
-    // Query heads per workgroup row: the whole GQA group (up to kHeads), so
-    // every compressed byte crosses HBM once -- unless that leaves most CUs
-    // idle (few batch x KV-head rows, short context): then rows of 4 heads,
-    // more workgroups re-reading the same small KV from L2.
-    int hpg = fkv::kHeads;
-    if (G > 4 && L.B * L.Hkv * (int)fkv::cdiv(G, hpg) * fkv::plan_splits(L, L.B * L.Hkv * (int)fkv::cdiv(G, hpg),
-                                                                          n_decode) < fkv::kSmallGrid)
-        hpg = 4;
-    const int head_groups = (int)fkv::cdiv(G, hpg);
-    const int ng_max = G < hpg ? G : hpg;
-    const int rows = L.B * L.Hkv * head_groups;
-    const int splits = fkv::plan_splits(L, rows, n_decode);
+    // the split count follows the longest decode length the call can see
+    const fkv::LaunchPlan p = fkv::plan_launch(L, Hq, n_dec_dev ? dec_stride : n_decode, h->target_wgs);
+    if (p.ws_floats > h->ws_floats || p.rows > (int)h->arrive_n)
+        return set_error(name + ": launch plan exceeds the workspace (internal error)");
+    const int hpg = p.hpg, head_groups = p.head_groups, ng_max = p.ng_max, rows = p.rows, splits = p.splits;
     const uint16_t* q16 = (const uint16_t*)query;
     const int64_t qn = (int64_t)L.B * Hq * L.D;
     if (q_dtype != FKV_F16) {
-        if ((size_t)qn > h->qbuf_n) {
-            if (h->qbuf) (void)hipFree(h->qbuf);
-            h->qbuf = nullptr;
-            h->qbuf_n = 0;
-            if (int rc = check_hip(hipMalloc(&h->qbuf, qn * 2), "hipMalloc(qbuf)")) return rc;
-            h->qbuf_n = qn;
-        }
         hipLaunchKernelGGL(fkv::cast_to_f16_kernel, dim3(fkv::grid_for(qn, 256)), dim3(256), 0, st, query,
                            q_dtype, qn, h->qbuf);
         q16 = h->qbuf;
-    }
-    if (splits > 1) {
-        const size_t need = (size_t)rows * splits * ng_max * (fkv::kHdr + L.D);
-        if (need > h->ws_floats) {
-            if (h->ws) (void)hipFree(h->ws);
-            h->ws = nullptr;
-            h->ws_floats = 0;
-            if (int rc = check_hip(hipMalloc(&h->ws, need * sizeof(float)), "hipMalloc(ws)")) return rc;
-            h->ws_floats = need;
-        }
-        if ((size_t)rows > h->arrive_n) {
-            if (h->arrive) (void)hipFree(h->arrive);
-            h->arrive = nullptr;
-            h->arrive_n = 0;
-            if (int rc = check_hip(hipMalloc(&h->arrive, rows * sizeof(int)), "hipMalloc(arrive)")) return rc;
-            h->arrive_n = rows;
-            // counters start at zero; the kernel's last split re-arms them
-            hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(rows, 256)), dim3(256), 0, st,
-                               h->arrive, rows);
-        }
     }
     fkv::AttnArgs a;
     a.blob = h->blob;
@@ -2344,7 +2385,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.dec_k = (const uint16_t*)decode_k;
     a.dec_v = (const uint16_t*)decode_v;
     a.n_dec = n_dec_dev ? 0 : n_decode;
-    a.dec_stride = n_decode;
+    a.dec_stride = dec_stride;
     a.n_dec_dev = n_dec_dev;
     a.Hq = Hq;
     a.G = G;
@@ -2357,7 +2398,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.flags = spike_flags;
     a.tokens = spike_tokens;
     a.ws = h->ws;
-    const bool fused_merge = fkv::env_int("FKV_FUSED_MERGE", 1) != 0;
+    const bool fused_merge = h->fused_merge;
     a.arrive = fused_merge ? h->arrive : nullptr;
     a.near_plan = h->near_plan;
     {
@@ -2418,8 +2459,31 @@ extern "C" {
 int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
                   const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
                   int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
-    return attn_call("fkv_attn_call", h, query, q_dtype, Hq, decode_k, decode_v, n_decode, nullptr, out, spike_flags,
-                     spike_tokens, stream);
+    return attn_call("fkv_attn_call", h, query, q_dtype, Hq, decode_k, decode_v, n_decode, n_decode, nullptr, out,
+                     spike_flags, spike_tokens, stream);
+}
+
+int fkv_attn_call_strided(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
+                          const void* decode_v, int32_t n_decode, int32_t row_stride, void* out,
+                          int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
+    return attn_call("fkv_attn_call_strided", h, query, q_dtype, Hq, decode_k, decode_v, n_decode, row_stride,
+                     nullptr, out, spike_flags, spike_tokens, stream);
+}
+
+int fkv_attn_plan(int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F, int32_t Hq, int32_t n_decode,
+                  int32_t target_wgs, int64_t* out) {
+    if (B <= 0 || Hkv <= 0 || (D != 64 && D != 128) || Na < 0 || F < 0 || Hq <= 0 || Hq % Hkv != 0 ||
+        n_decode < 0 || target_wgs < 1 || !out)
+        return set_error("fkv_attn_plan: bad argument");
+    const fkv::BlobLayout L = fkv::make_layout(B, Hkv, D, Na, F, 0);
+    const fkv::LaunchPlan p = fkv::plan_launch(L, Hq, n_decode, target_wgs);
+    out[0] = p.hpg;
+    out[1] = p.rows;
+    out[2] = p.splits;
+    out[3] = (int64_t)p.ws_floats;
+    out[4] = (int64_t)fkv::workspace_floats(L, Hq);
+    out[5] = fkv::workspace_rows(L, Hq);
+    return FKV_OK;
 }
 
 int fkv_far_plan(int32_t n_waves, int32_t near_plan, int32_t nt_far, int64_t near_weight, int64_t far_rec,
@@ -2439,8 +2503,8 @@ int fkv_attn_call_dev(fkv_attn* h, const void* query, int32_t q_dtype, int32_t H
                       const void* decode_v, const int32_t* n_decode_dev, int32_t capacity, void* out,
                       int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
     if (!n_decode_dev) return set_error("fkv_attn_call_dev: NULL n_decode_dev");
-    return attn_call("fkv_attn_call_dev", h, query, q_dtype, Hq, decode_k, decode_v, capacity, n_decode_dev, out,
-                     spike_flags, spike_tokens, stream);
+    return attn_call("fkv_attn_call_dev", h, query, q_dtype, Hq, decode_k, decode_v, capacity, capacity,
+                     n_decode_dev, out, spike_flags, spike_tokens, stream);
 }
 
 int fkv_e4m3_decode(const uint8_t* codes, void* out_f16, int64_t n, void* stream) {

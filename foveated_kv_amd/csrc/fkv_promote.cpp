@@ -60,6 +60,7 @@ struct DevDrain {
 };
 
 constexpr int32_t kNoStep = INT32_MIN;
+enum : uint8_t { kDrainNone = 0, kDrainHost = 1, kDrainDevice = 2 };
 constexpr int kMaxDrainHeads = 256;
 
 }  // namespace
@@ -70,6 +71,10 @@ struct fkv_promoter {
     std::vector<fkv_attn*> handles;
     std::vector<std::vector<uint32_t>> mirror;  // host copy of each layer's near_valid
     std::vector<int> n_alloc;                   // near slots per head, per layer
+    // per layer: which drain has committed into its blob (the host drain keeps
+    // `mirror` current, the device drain writes near_valid in the blob only),
+    // so the two are never mixed on one layer
+    std::vector<uint8_t> mode;
     std::unordered_set<uint64_t> promoted;
     std::unordered_map<uint32_t, int> last_step;
     std::vector<Record> queue;
@@ -359,6 +364,7 @@ int fkv_promoter_create(int32_t n_layers, int32_t cooldown_steps, int32_t max_pe
     p->arch.resize(n_layers);
     p->handles.assign(n_layers, nullptr);
     p->mirror.assign(n_layers, {});
+    p->mode.assign(n_layers, kDrainNone);
     p->n_alloc.assign(n_layers, 0);
     *out = p;
     return FKV_OK;
@@ -449,6 +455,7 @@ int fkv_promoter_register_handle(fkv_promoter* p, int32_t layer, fkv_attn* h, vo
     if (int rc = fkv_attn_read_near_valid(h, nv.data(), stream)) return rc;
     p->handles[layer] = h;
     p->mirror[layer] = std::move(nv);
+    p->mode[layer] = kDrainNone;  // a new blob: either drain may start on it
     p->n_alloc[layer] = bi.n_near_alloc;
     return FKV_OK;
 }
@@ -461,6 +468,10 @@ int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* flags, con
     const Archive& a = p->arch[layer];
     if (!a.k || a.S == 0) return 0;  // no archive registered for the layer
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || !flags || !tokens || !far_idx) return 0;
+    if (p->mode[layer] == kDrainDevice)
+        return set_error("fkv_promoter_drain: layer " + std::to_string(layer) +
+                         " is drained on the device; its headroom slots are assigned there");
+    p->mode[layer] = kDrainHost;
     const int gqa = Hq / Hkv > 0 ? Hq / Hkv : 1;
     std::vector<uint8_t> seen((size_t)Hkv, 0);
     int queued = 0;
@@ -523,6 +534,10 @@ int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* fla
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || !flags || !tokens || !far_idx) return 0;
     if (Hkv > kMaxDrainHeads || Hkv != arc.Hkv || Hkv != h->L.Hkv || arc.D != h->L.D)
         return set_error("fkv_promoter_drain_device: archive, handle and spike shapes disagree (or H_kv > 256)");
+    if (p->mode[layer] == kDrainHost)
+        return set_error("fkv_promoter_drain_device: layer " + std::to_string(layer) +
+                         " is drained on the host; its headroom slots are assigned there");
+    p->mode[layer] = kDrainDevice;
     hipStream_t st = (hipStream_t)stream;
     if (int rc = ensure_dev_drain(p, layer, st)) return rc;
     const DevDrain& d = p->dev[layer];
@@ -665,6 +680,15 @@ int fkv_promoter_get_stats(const fkv_promoter* p, fkv_promoter_stats* out) {
 int fkv_promoter_near_valid(const fkv_promoter* p, int32_t layer, uint32_t* out, int32_t n) {
     if (!p || !out) return set_error("fkv_promoter_near_valid: NULL argument");
     if (layer < 0 || layer >= p->n_layers) return set_error("fkv_promoter_near_valid: layer out of range");
+    if (p->mode[layer] == kDrainDevice && p->handles[layer]) {
+        // the device drain commits in the blob: read it there (after all queued work)
+        fkv_attn* h = p->handles[layer];
+        std::vector<uint32_t> nv((size_t)h->L.Hkv);
+        if (int rc = check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize")) return rc;
+        if (int rc = fkv_attn_read_near_valid(h, nv.data(), nullptr)) return rc;
+        for (int i = 0; i < n && i < (int)nv.size(); i++) out[i] = nv[i];
+        return (int)nv.size();
+    }
     const auto& m = p->mirror[layer];
     for (int i = 0; i < n && i < (int)m.size(); i++) out[i] = m[i];
     return (int)m.size();

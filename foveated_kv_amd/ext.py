@@ -68,6 +68,21 @@ def _require_device(*ts):
             raise TypeError("foveated_kv_amd tensors must live on a ROCm device (got a CPU tensor)")
 
 
+def _row_stride(k, v):
+    """Row capacity of fp16 decode views (B,H,n,D) that are the first n rows
+    of (B,H,cap,D) buffers (a growing decode buffer's views), else 0."""
+    if k.dtype != torch.float16 or v.dtype != torch.float16 or k.stride() != v.stride():
+        return 0
+    B, H, n, D = k.shape
+    sb, sh, sr, sd = k.stride()
+    if sd != 1 or sr != D or sh % D != 0:
+        return 0
+    cap = sh // D
+    if cap < n or (B > 1 and sb != H * sh) or (k.data_ptr() % 16) or (v.data_ptr() % 16):
+        return 0
+    return cap
+
+
 class CompressedLayer:
     """csrc/foveated_compress.h:100-118 (+ the fp16 far-row archive)."""
 
@@ -260,13 +275,18 @@ class FoveatedHandle:
             q = q.half()
         q = q.contiguous()
         n_dec = 0
+        row_stride = 0
         dk = dv = None
         if decode_k is not None and decode_k.shape[2] > 0:
             n_dec = decode_k.shape[2]
             if tuple(decode_k.shape) != (B, self.H_kv, n_dec, D) or decode_v.shape != decode_k.shape:
                 raise ValueError("decode_k/decode_v must be (B,H_kv,n,D)")
-            dk = decode_k.to(torch.float16).contiguous()
-            dv = decode_v.to(torch.float16).contiguous()
+            row_stride = _row_stride(decode_k, decode_v) if n_decode is None else 0
+            if row_stride:
+                dk, dv = decode_k, decode_v  # rows of a larger buffer, attended to in place
+            else:
+                dk = decode_k.to(torch.float16).contiguous()
+                dv = decode_v.to(torch.float16).contiguous()
         if n_decode is not None:
             if n_decode.dtype != torch.int32 or n_decode.numel() != 1:
                 raise TypeError("n_decode must be a one-element int32 device tensor")
@@ -276,7 +296,11 @@ class FoveatedHandle:
         flags = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
         tokens = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
         with torch.cuda.device(self.device):
-            if n_decode is None:
+            if row_stride:
+                check(self._lib.fkv_attn_call_strided(self._h, ptr(q), dtype_code(q.dtype), Hq, ptr(dk), ptr(dv),
+                                                      n_dec, row_stride, ptr(out), ptr(flags), ptr(tokens),
+                                                      _lib.stream_ptr(self.device)), "fkv_attn_call_strided")
+            elif n_decode is None:
                 check(self._lib.fkv_attn_call(self._h, ptr(q), dtype_code(q.dtype), Hq, ptr(dk), ptr(dv), n_dec,
                                               ptr(out), ptr(flags), ptr(tokens), _lib.stream_ptr(self.device)),
                       "fkv_attn_call")

@@ -126,8 +126,9 @@ class PromotionPipeline:
         (B, H_q) and far_idx (B, H_kv, N_far) int32 stay in device memory and
         nothing waits for the host; the layer's next attention launch on that
         stream sees the promoted rows.  Needs the archive registered with
-        ``register_archive_tensors`` (pinned copy) or from files; do not mix
-        with ``drain_spikes`` on one pipeline."""
+        ``register_archive_tensors`` (pinned copy) or from files.  A layer
+        drained here cannot also be drained by ``drain_spikes`` (the library
+        rejects the second kind of drain on a layer)."""
         if self._stopped:
             return
         for t in (spike_flags, spike_tokens, far_idx):

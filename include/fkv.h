@@ -186,10 +186,40 @@ int fkv_turbo_compress_values(const void* values, int32_t dtype, int64_t n_token
 /* Replaces FoveatedHandle::operator() (:164-240) and, for a TurboQuant
  * handle, TurboFoveatedHandle::operator() (:407-491): query (B,Hq,1,D) in
  * q_dtype, decode_k/v (B,Hkv,n_decode,D) fp16 (NULL when n_decode == 0).
- * Writes out (B,Hq,D) fp16, spike_flags/spike_tokens (B,Hq) int32. */
+ * Writes out (B,Hq,D) fp16, spike_flags/spike_tokens (B,Hq) int32.
+ *
+ * Workspace: a handle's first call (of any fkv_attn_call* variant)
+ * allocates the handle's split workspace for that call's Hq, large enough
+ * for every decode length; no later call allocates or frees anything, so
+ * a HIP graph captured around a call stays valid for the handle's life.
+ * Later calls with a different Hq return FKV_EINVAL (one handle serves one
+ * query-head count, as a model layer does).  The first call is therefore
+ * not capturable.  One handle owns one workspace and one set of split
+ * arrival counters: calls on one handle must not overlap on two streams
+ * (queue them on one stream, or order the streams). */
 int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
                   const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
                   int32_t* spike_flags, int32_t* spike_tokens, void* stream);
+
+/* fkv_attn_call on a decode buffer with a row stride (no counterpart in the
+ * reference, whose decode buffer is re-concatenated each step,
+ * mlx_foveated.py:404-428): decode_k/v (B,Hkv,row_stride,D) fp16, rows
+ * [0, n_decode) valid, row_stride >= n_decode.  A growing decode buffer is
+ * attended to in place, without a per-call copy. */
+int fkv_attn_call_strided(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
+                          const void* decode_v, int32_t n_decode, int32_t row_stride, void* out,
+                          int32_t* spike_flags, int32_t* spike_tokens, void* stream);
+
+/* The launch plan of one call (host only, no GPU; no counterpart in the
+ * reference, whose split sizing is foveated_attn.cpp:26-38): for a handle of
+ * shape (B, Hkv, D, Na, F) called with Hq query heads and n_decode decode
+ * rows, aiming at target_wgs workgroups, writes out[0] query heads per
+ * workgroup row, out[1] rows, out[2] splits per row, out[3] split-partial
+ * floats the call uses, out[4] floats the handle's workspace holds, out[5]
+ * arrival counters it holds.  An introspection hook: tests check that no
+ * decode length needs more workspace than the first call allocates. */
+int fkv_attn_plan(int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F, int32_t Hq, int32_t n_decode,
+                  int32_t target_wgs, int64_t* out);
 
 /* The attention kernel's far-tile plan for one row (host only, no GPU): wave
  * w of n_waves streams far tiles f0[w] + u * fs[w], u < nf[w].  near_weight
@@ -306,9 +336,12 @@ int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* spike_flag
  * `stream` sees the promoted rows.  For callers that keep a decode step on
  * the GPU.  Needs a registered handle and an archive registered with
  * copy_to_pinned (or from files); the first call per layer allocates (not
- * capturable).  A pipeline uses either this or the host drain + flush (the
- * host mirror of near_valid is not updated here); statistics accumulate on
- * the device and fkv_promoter_get_stats adds them (synchronising).
+ * capturable).  A layer is drained either here or by fkv_promoter_drain:
+ * the first drain on a layer fixes which, the other then returns
+ * FKV_EINVAL for that layer (registering its handle again resets this);
+ * fkv_promoter_near_valid reads a device-drained layer's near_valid from
+ * the blob (synchronising).  Statistics accumulate on the device and
+ * fkv_promoter_get_stats adds them (synchronising).
  * step_dev (may be NULL): the decode step is read from this device int32
  * instead of `step` (a graph-captured step keeps its counter on the GPU). */
 int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* spike_flags,
@@ -331,7 +364,8 @@ int fkv_promoter_flush(fkv_promoter* p);
 int fkv_promoter_order(fkv_promoter* p, int32_t layer, void* stream);
 int fkv_promoter_synchronize(fkv_promoter* p);
 int fkv_promoter_get_stats(const fkv_promoter* p, fkv_promoter_stats* out);
-/* The host mirror of a layer's near_valid (returns Hkv, copies up to n). */
+/* A layer's near_valid (returns Hkv, copies up to n): the host mirror for a
+ * host-drained layer, the blob's words for a device-drained one. */
 int fkv_promoter_near_valid(const fkv_promoter* p, int32_t layer, uint32_t* out, int32_t n);
 /* stop() + destructor (promotion_pipeline.cpp:30-38, 243-248). */
 void fkv_promoter_destroy(fkv_promoter* p);

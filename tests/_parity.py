@@ -1,0 +1,132 @@
+"""Shared helpers of the GPU parity tests: one fused-attention case through
+the C ABI against the CPU oracle, and a recorder of each case's error
+margins.
+
+With FKV_PARITY_LOG=<path> set, every checked case appends one JSON line
+(test, case, max-abs and cosine against each oracle, spike agreement) to
+<path>; tests/conftest.py turns the lines into a Markdown table beside it at
+the end of the session, so a GPU run leaves a record of how far inside the
+tolerance every case sits.
+"""
+
+import json
+import os
+
+import numpy as np
+import torch
+
+ATOL = 2e-3
+COS = 0.9999
+
+
+def flush(msg):
+    print(msg, flush=True)
+
+
+def record(case, **vals):
+    path = os.environ.get("FKV_PARITY_LOG")
+    if not path:
+        return
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    row = {"test": test, "case": case}
+    for k, v in vals.items():
+        row[k] = float(v) if isinstance(v, (np.floating, float)) else (int(v) if isinstance(v, (np.integer, int)) else v)
+    with open(path, "a") as f:
+        f.write(json.dumps(row) + "\n")
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+def tier_config(**kw):
+    from foveated_kv_amd import ext
+
+    c = ext.TierConfig()
+    c.promo_headroom_min = kw.get("promo_headroom_min", 8)
+    c.v_group = kw.get("v_group", 0)
+    return c
+
+
+def far_scores(orc, far_k, q, b, hq):
+    """Exact far scores of one (batch, q head) from the oracle's LUT decode."""
+    lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    Hq, D = q.shape[1], q.shape[2]
+    G = Hq // far_k.shape[1]
+    inv = np.float32(1.0) / np.sqrt(np.float32(D))
+    qs = (q[b, hq].astype(np.float32) * inv).astype(np.float64)
+    return lut[far_k[b, hq // G]] @ qs
+
+
+def check_spikes(orc, far_k, q16, flags, tokens, kf, kt, mf, mn, margin):
+    """GPU spike outputs against the oracle's: a token may differ only on a
+    near tie of the two candidates' exact scores, a flag only where
+    max_far - min_near sits within rounding of the margin.  Returns the
+    number of such tie-allowed differences."""
+    ties = 0
+    for b, hq in np.argwhere(tokens != kt):
+        s = far_scores(orc, far_k, q16, b, hq)
+        assert abs(s[tokens[b, hq]] - s[kt[b, hq]]) <= 1e-5 * (1 + abs(s.max())), (b, hq)
+        ties += 1
+    for b, hq in np.argwhere(flags != kf):
+        assert abs(mf[b, hq] - mn[b, hq] - margin) < 1e-4, (b, hq)
+        ties += 1
+    return ties
+
+
+def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16, spikes=0.0,
+                  margin=10.0, near_valid_delta=0, check_formulation=True, heavy_tail=False, v_group=0):
+    from foveated_kv_amd import ext, synthetic
+
+    case = (f"B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} seed={seed} q={str(q_dtype).split('.')[-1]} "
+            f"spikes={spikes} nv_delta={near_valid_delta} v_group={v_group}")
+    flush("attention " + case)
+    k, v = synthetic.make_kv(B, Hkv, S, D, seed, heavy_tail=heavy_tail)
+    q = synthetic.make_query(B, Hq, D, seed)
+    tb = orc.tier_boundaries(S)
+    synthetic.inject_spikes(k, q, tb["mid_start"], tb["far_count"], spikes, seed)
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
+    cl = ext.CompressHandle(tier_config(v_group=v_group)).compress_layer(
+        torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), with_archive=False)
+    nv = cl.near_valid.clone()
+    if near_valid_delta:
+        # promoted-looking rows: write copies of far rows into the headroom
+        npad = cl.near_k.shape[2]
+        for hh in range(Hkv):
+            add = min(near_valid_delta * (hh + 1), npad - int(nv[hh]))
+            src = torch.from_numpy(k[:, hh, tb["mid_start"]:tb["mid_start"] + add]).cuda()
+            cl.near_k[:, hh, int(nv[hh]):int(nv[hh]) + add] = src
+            cl.near_v[:, hh, int(nv[hh]):int(nv[hh]) + add] = src * 0.5
+            nv[hh] += add
+    del k, v
+    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero, nv,
+                           spike_margin=margin)
+    qt = torch.from_numpy(q).cuda().to(q_dtype)
+    dkt = torch.from_numpy(dk).cuda() if dk is not None else None
+    dvt = torch.from_numpy(dv).cuda() if dv is not None else None
+    out, flags, tokens = h(qt[:, :, None, :], dkt, dvt)
+    torch.cuda.synchronize()
+    out = np_(out)[:, :, 0].astype(np.float64)
+    c = {n: np_(getattr(cl, n)) for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale", "far_v_zero")}
+    del cl, h
+    q16 = np_(qt.to(torch.float16))
+    ko, kf, kt, mf, mn = orc.attend_kernel(q16, c["near_k"], c["near_v"], np_(nv), c["far_k"], c["far_v"],
+                                           c["far_v_scale"], c["far_v_zero"], dk, dv, spike_margin=margin)
+    assert np.all(np.isfinite(out))
+    err = np.abs(out - ko).max()
+    cos = orc.cosine(out, ko)
+    flush(f"  vs kernel oracle: max-abs {err:.3e} cos {cos:.8f}")
+    rec = {"maxabs_kernel": err, "cos_kernel": cos}
+    assert err <= ATOL and cos >= COS
+    if check_formulation and near_valid_delta == 0:
+        fo = orc.attend_formulation(q16, c["near_k"], c["near_v"], np_(nv), c["far_k"], c["far_v"],
+                                    c["far_v_scale"], c["far_v_zero"], dk, dv)
+        err_f = np.abs(out - fo).max()
+        cos_f = orc.cosine(out, fo)
+        flush(f"  vs formulation:   max-abs {err_f:.3e} cos {cos_f:.8f}")
+        rec.update(maxabs_formulation=err_f, cos_formulation=cos_f)
+        assert err_f <= ATOL and cos_f >= COS
+    flags, tokens = np_(flags), np_(tokens)
+    ties = check_spikes(orc, c["far_k"], q16, flags, tokens, kf, kt, mf, mn, margin)
+    record(case, flagged=int(flags.sum()), spike_ties=ties, **rec)
+    return out, flags, tokens, kf

@@ -155,3 +155,31 @@ def test_far_plan_balances_c3_16k():
     assert max(cost) - mean <= 0.6 * FB
     with pytest.raises(Exception):
         _lib.check(lib.fkv_far_plan(0, 1, 1, NB, FB, 0, None, None, None), "fkv_far_plan")
+
+
+@pytest.mark.parametrize("B,Hkv,D,S,Hq", [
+    (8, 8, 128, 16384, 32), (8, 8, 128, 32768, 32), (1, 8, 128, 65536, 64), (1, 2, 64, 512, 14),
+    (1, 8, 128, 4096, 32), (1, 2, 64, 600, 12), (4, 2, 128, 4096, 40), (1, 4, 128, 40, 24), (3, 4, 64, 333, 12),
+    (1, 1, 64, 100, 1), (2, 2, 128, 9000, 96),
+])
+def test_launch_plan_never_outgrows_the_first_call_workspace(orc, B, Hkv, D, S, Hq):
+    """A handle's workspace is allocated once, by its first call, and never
+    re-allocated (a captured HIP graph keeps its pointers): every decode
+    length and split target must plan within it."""
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+    tb = orc.tier_boundaries(S)
+    Na, F = tb["N_near_padded"], tb["far_count"]
+    out = (ctypes.c_int64 * 6)()
+    worst = 0
+    for n_dec in list(range(0, 130)) + [255, 256, 257, 1000, 4096, 70000]:
+        for target in (1, 64, 256, 1024, 4096):
+            assert lib.fkv_attn_plan(B, Hkv, D, Na, F, Hq, n_dec, target, out) == _lib.FKV_OK
+            hpg, rows, splits, need, have, rows_have = list(out)
+            assert hpg in (4, 16) and 1 <= splits <= 64
+            assert rows <= rows_have, (n_dec, target, rows, rows_have)
+            assert need <= have, (n_dec, target, need, have)
+            worst = max(worst, need)
+    assert worst > 0 or Na + F < 2 * 64 * 4
+    assert lib.fkv_attn_plan(B, Hkv, D, Na, F, Hq + 1 if Hkv > 1 else 0, 0, 256, out) == _lib.FKV_EINVAL

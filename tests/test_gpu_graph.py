@@ -68,6 +68,8 @@ def test_device_count_matches_host_count(fkv, v_group):
         want = h(q, dk[:, :, :n].contiguous(), dv[:, :, :n].contiguous()) if n else h(q)
         torch.cuda.synchronize()
         _same(got, want, f"n={n}")
+        if n:  # the first n rows of the capacity buffer, attended to in place (row stride = capacity)
+            _same(h(q, dk[:, :, :n], dv[:, :, :n]), want, f"strided n={n}")
     # counts outside [0, capacity] are clamped by the kernel
     ndev.fill_(cap + 77)
     _same(h(q, dk, dv, n_decode=ndev), h(q, dk, dv), "n > capacity")

@@ -14,12 +14,8 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-ATOL = 2e-3
-COS = 0.9999
-
-
-def _flush(msg):
-    print(msg, flush=True)
+from _parity import ATOL, COS, run_attention  # noqa: F401  (ATOL/COS: the tolerance of every case)
+from _parity import flush as _flush
 
 
 @pytest.fixture(scope="module")
@@ -123,83 +119,6 @@ def test_compress_exhaustive_fp16_patterns(fkv, orc):
 # ---------------------------------------------------------------------------
 # fused attention
 # ---------------------------------------------------------------------------
-
-def _far_scores(orc, c, q):
-    """Exact far scores per (b, q head) from the oracle's LUT decode."""
-    lut = orc.decode_fp8(np.arange(256, dtype=np.uint8)).astype(np.float64)
-    B, Hq, D = q.shape
-    Hkv = c["far_k"].shape[1]
-    G = Hq // Hkv
-    inv = np.float32(1.0) / np.sqrt(np.float32(D))
-    out = []
-    for b in range(B):
-        row = []
-        for h in range(Hq):
-            qs = (q[b, h].astype(np.float32) * inv).astype(np.float64)
-            row.append(lut[c["far_k"][b, h // G]] @ qs)
-        out.append(row)
-    return out
-
-
-def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16, spikes=0.0,
-                  margin=10.0, near_valid_delta=0, check_formulation=True, heavy_tail=False, v_group=0):
-    from foveated_kv_amd import ext, synthetic
-
-    _flush(f"attention B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} seed={seed} "
-           f"q={q_dtype} spikes={spikes} nv_delta={near_valid_delta} v_group={v_group}")
-    k, v = synthetic.make_kv(B, Hkv, S, D, seed, heavy_tail=heavy_tail)
-    q = synthetic.make_query(B, Hq, D, seed)
-    tb = orc.tier_boundaries(S)
-    synthetic.inject_spikes(k, q, tb["mid_start"], tb["far_count"], spikes, seed)
-    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
-    cl = ext.CompressHandle(_cfg(fkv, v_group=v_group)).compress_layer(
-        torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), with_archive=False)
-    nv = cl.near_valid.clone()
-    if near_valid_delta:
-        # promoted-looking rows: write copies of far rows into the headroom
-        npad = cl.near_k.shape[2]
-        for hh in range(Hkv):
-            add = min(near_valid_delta * (hh + 1), npad - int(nv[hh]))
-            src = torch.from_numpy(k[:, hh, tb["mid_start"]:tb["mid_start"] + add]).cuda()
-            cl.near_k[:, hh, int(nv[hh]):int(nv[hh]) + add] = src
-            cl.near_v[:, hh, int(nv[hh]):int(nv[hh]) + add] = src * 0.5
-            nv[hh] += add
-    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero, nv,
-                           spike_margin=margin)
-    qt = torch.from_numpy(q).cuda().to(q_dtype)
-    dkt = torch.from_numpy(dk).cuda() if dk is not None else None
-    dvt = torch.from_numpy(dv).cuda() if dv is not None else None
-    out, flags, tokens = h(qt[:, :, None, :], dkt, dvt)
-    torch.cuda.synchronize()
-    out = _np(out)[:, :, 0].astype(np.float64)
-    c = {n: _np(getattr(cl, n)) for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale", "far_v_zero")}
-    q16 = _np(qt.to(torch.float16))
-    ko, kf, kt, mf, mn = orc.attend_kernel(q16, c["near_k"], c["near_v"], _np(nv), c["far_k"], c["far_v"],
-                                           c["far_v_scale"], c["far_v_zero"], dk, dv, spike_margin=margin)
-    assert np.all(np.isfinite(out))
-    err = np.abs(out - ko).max()
-    cos = orc.cosine(out, ko)
-    _flush(f"  vs kernel oracle: max-abs {err:.3e} cos {cos:.8f}")
-    assert err <= ATOL and cos >= COS
-    if check_formulation and near_valid_delta == 0:
-        fo = orc.attend_formulation(q16, c["near_k"], c["near_v"], _np(nv), c["far_k"], c["far_v"],
-                                    c["far_v_scale"], c["far_v_zero"], dk, dv)
-        err_f = np.abs(out - fo).max()
-        cos_f = orc.cosine(out, fo)
-        _flush(f"  vs formulation:   max-abs {err_f:.3e} cos {cos_f:.8f}")
-        assert err_f <= ATOL and cos_f >= COS
-    flags, tokens = _np(flags), _np(tokens)
-    fs = _far_scores(orc, c, q16) if c["far_k"].shape[2] else None
-    for b in range(B):
-        for hq in range(Hq):
-            if tokens[b, hq] != kt[b, hq]:
-                # allowed only on a near tie of the two candidates' exact scores
-                s = fs[b][hq]
-                assert abs(s[tokens[b, hq]] - s[kt[b, hq]]) <= 1e-5 * (1 + abs(s.max())), (b, hq)
-            if flags[b, hq] != kf[b, hq]:
-                assert abs(mf[b, hq] - mn[b, hq] - margin) < 1e-4, (b, hq)
-    return out, flags, tokens, kf
-
 
 @pytest.mark.parametrize("args", [
     dict(B=1, Hq=14, Hkv=2, D=64, S=512, n_dec=16, seed=1),      # config 1
@@ -352,11 +271,14 @@ def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
         torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), with_archive=False)
     h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
                            cl.near_valid, spike_margin=10.0)
-    os.environ["FKV_FUSED_MERGE"] = "0"
+    os.environ["FKV_FUSED_MERGE"] = "0"  # read once, when a handle is created
     try:
-        ref = [t.clone() for t in h(q, dkt, dvt)]
+        h_sep = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                                   cl.near_valid, spike_margin=10.0)
     finally:
         del os.environ["FKV_FUSED_MERGE"]
+    ref = [t.clone() for t in h_sep(q, dkt, dvt)]
+    del h_sep
     outs = [h(q, dkt, dvt) for _ in range(200)]
     torch.cuda.synchronize()
     first = outs[0]
