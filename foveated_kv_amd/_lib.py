@@ -93,6 +93,7 @@ SIGNATURES = {
     "fkv_attn_call": (ctypes.c_int, [P, P, I32, I32, P, P, I32, P, P, P, P]),
     "fkv_attn_call_dev": (ctypes.c_int, [P, P, I32, I32, P, P, P, I32, P, P, P, P]),
     "fkv_attn_call_strided": (ctypes.c_int, [P, P, I32, I32, P, P, I32, I32, P, P, P, P]),
+    "fkv_attn_call_noalloc": (ctypes.c_int, [P, P, I32, I32, P, P, I32, P, P, P, P]),
     "fkv_attn_plan": (ctypes.c_int, [I32, I32, I32, I32, I32, I32, I32, I32, P]),
     "fkv_far_plan": (ctypes.c_int, [I32, I32, I32, ctypes.c_int64, ctypes.c_int64, I32, P, P, P]),
     "fkv_attn_blob_info": (ctypes.c_int, [P, ctypes.POINTER(BlobInfoC)]),

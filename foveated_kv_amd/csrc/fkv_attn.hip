@@ -30,6 +30,7 @@
 #include <climits>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "fkv_attn.h"
@@ -2313,6 +2314,46 @@ int fkv_attn_create_g32(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32
 
 }  // extern "C"
 
+// ---------------------------------------------------------------------------
+// Scratch of fkv_attn_call_noalloc: the call workspace in a fixed device
+// array instead of memory the library allocates.  Layout: [arrival counters
+// | fp16 query copy | split partial records]; the counter region has a
+// fixed size and place, is zeroed once per device and stays zero between
+// calls (the last split of a row re-arms its counter).  Every call on a
+// device shares that device's copy: calls that overlap on one device race.
+// ---------------------------------------------------------------------------
+
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+constexpr size_t kScratchArriveBytes = (size_t)64 << 10;  // 16384 rows
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};  // device address of `scratch`, per device
+
+// The current device's address of `scratch` (looked up once per device,
+// when its counter region is also cleared, stream-ordered before the call).
+int scratch_base(const std::string& name, int dev, hipStream_t st, uint8_t** out) {
+    if (dev < 0 || dev >= kScratchDevices) return set_error(name + ": device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (int rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+            return rc;
+        if (!ptr) return set_error(name + ": hipGetSymbolAddress(scratch) returned NULL");
+        const int n = (int)(kScratchArriveBytes / sizeof(int));
+        hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(n, 256)), dim3(256), 0, st, (int*)ptr, n);
+        if (int rc = check_hip(hipGetLastError(), "zero_ints_kernel launch")) return rc;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = (uint8_t*)g_scratch_ptr[dev];
+    return FKV_OK;
+}
+
+}  // namespace
+
 namespace {
 
 // The handle's call workspace, allocated by its first call (sized for every
@@ -2350,9 +2391,22 @@ int ensure_workspace(const std::string& name, fkv_attn* h, int Hq, hipStream_t s
 // n_decode: valid decode rows (host count) or, with n_dec_dev, ignored (the
 // kernel reads the count there); dec_stride: rows per (batch, kv head)
 // block of decode_k / decode_v.
+// The buffers one call's kernels use besides inputs and outputs.
+struct CallWorkspace {
+    float* ws;           // split partial records
+    int* arrive;         // per-row arrival counters, zero between calls
+    uint16_t* qbuf;      // fp16 copy of a bf16 / f32 query
+    size_t ws_floats, arrive_n, qbuf_n;
+};
+
+// Lays a call's workspace out in the no-alloc entry point's scratch array
+// (below); NULL when the call does not fit.
+int scratch_workspace(const std::string& name, fkv_attn* h, const fkv::LaunchPlan& p, int Hq, hipStream_t st,
+                      CallWorkspace* out);
+
 int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
               const void* decode_v, int32_t n_decode, int32_t dec_stride, const int32_t* n_dec_dev, void* out,
-              int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
+              int32_t* spike_flags, int32_t* spike_tokens, void* stream, bool no_alloc = false) {
     const std::string name(fn);
     if (!h || !query || !out || !spike_flags || !spike_tokens) return set_error(name + ": NULL argument");
     const fkv::BlobLayout& L = h->L;
@@ -2364,19 +2418,26 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     if (q_dtype == FKV_F16 && ((uintptr_t)query & 7) != 0)
         return set_error(name + ": an fp16 query must be 8-byte aligned");
     hipStream_t st = (hipStream_t)stream;
-    if (int rc = ensure_workspace(name, h, Hq, st)) return rc;
     const int G = Hq / L.Hkv;
     // the split count follows the longest decode length the call can see
     const fkv::LaunchPlan p = fkv::plan_launch(L, Hq, n_dec_dev ? dec_stride : n_decode, h->target_wgs);
-    if (p.ws_floats > h->ws_floats || p.rows > (int)h->arrive_n)
+    CallWorkspace w;
+    if (no_alloc) {
+        if (int rc = scratch_workspace(name, h, p, Hq, st, &w)) return rc;
+    } else {
+        if (int rc = ensure_workspace(name, h, Hq, st)) return rc;
+        w = CallWorkspace{h->ws, h->arrive, h->qbuf, h->ws_floats, h->arrive_n, (size_t)L.B * Hq * L.D};
+    }
+    if (p.ws_floats > w.ws_floats || p.rows > (int)w.arrive_n)
         return set_error(name + ": launch plan exceeds the workspace (internal error)");
     const int hpg = p.hpg, head_groups = p.head_groups, ng_max = p.ng_max, rows = p.rows, splits = p.splits;
     const uint16_t* q16 = (const uint16_t*)query;
     const int64_t qn = (int64_t)L.B * Hq * L.D;
     if (q_dtype != FKV_F16) {
+        if ((size_t)qn > w.qbuf_n) return set_error(name + ": query exceeds the workspace (internal error)");
         hipLaunchKernelGGL(fkv::cast_to_f16_kernel, dim3(fkv::grid_for(qn, 256)), dim3(256), 0, st, query,
-                           q_dtype, qn, h->qbuf);
-        q16 = h->qbuf;
+                           q_dtype, qn, w.qbuf);
+        q16 = w.qbuf;
     }
     fkv::AttnArgs a;
     a.blob = h->blob;
@@ -2397,9 +2458,9 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.out = (uint16_t*)out;
     a.flags = spike_flags;
     a.tokens = spike_tokens;
-    a.ws = h->ws;
+    a.ws = w.ws;
     const bool fused_merge = h->fused_merge;
-    a.arrive = fused_merge ? h->arrive : nullptr;
+    a.arrive = fused_merge ? w.arrive : nullptr;
     a.near_plan = h->near_plan;
     {
         // Decode tiles go to the wave with the fewest planned bytes where a
@@ -2452,6 +2513,30 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     return check_hip(hipGetLastError(), "attn_kernel launch");
 }
 
+int scratch_workspace(const std::string& name, fkv_attn* h, const fkv::LaunchPlan& p, int Hq, hipStream_t st,
+                      CallWorkspace* out) {
+    const fkv::BlobLayout& L = h->L;
+    const size_t qbytes = ((size_t)L.B * Hq * L.D * 2 + 255) & ~(size_t)255;
+    const size_t need = kScratchArriveBytes + qbytes + p.ws_floats * sizeof(float);
+    if ((size_t)p.rows * sizeof(int) > kScratchArriveBytes || need > kScratchBytes)
+        return set_error(name + ": this call needs " + std::to_string(need) + " bytes of scratch (" +
+                         std::to_string(p.rows) + " rows x " + std::to_string(p.splits) +
+                         " splits); the no-alloc entry point holds " + std::to_string(kScratchBytes) +
+                         " bytes -- use fkv_attn_call");
+    int dev = -1;
+    if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != h->device) return set_error(name + ": the handle's device must be current");
+    uint8_t* base = nullptr;
+    if (int rc = scratch_base(name, dev, st, &base)) return rc;
+    out->arrive = (int*)base;
+    out->arrive_n = kScratchArriveBytes / sizeof(int);
+    out->qbuf = (uint16_t*)(base + kScratchArriveBytes);
+    out->qbuf_n = qbytes / 2;
+    out->ws = (float*)(base + kScratchArriveBytes + qbytes);
+    out->ws_floats = (kScratchBytes - kScratchArriveBytes - qbytes) / sizeof(float);
+    return FKV_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2468,6 +2553,13 @@ int fkv_attn_call_strided(fkv_attn* h, const void* query, int32_t q_dtype, int32
                           int32_t* spike_flags, int32_t* spike_tokens, void* stream) {
     return attn_call("fkv_attn_call_strided", h, query, q_dtype, Hq, decode_k, decode_v, n_decode, row_stride,
                      nullptr, out, spike_flags, spike_tokens, stream);
+}
+
+int fkv_attn_call_noalloc(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
+                          const void* decode_v, int32_t n_decode, void* out, int32_t* spike_flags,
+                          int32_t* spike_tokens, void* stream) {
+    return attn_call("fkv_attn_call_noalloc", h, query, q_dtype, Hq, decode_k, decode_v, n_decode, n_decode,
+                     nullptr, out, spike_flags, spike_tokens, stream, true);
 }
 
 int fkv_attn_plan(int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F, int32_t Hq, int32_t n_decode,

@@ -210,6 +210,23 @@ int fkv_attn_call_strided(fkv_attn* h, const void* query, int32_t q_dtype, int32
                           const void* decode_v, int32_t n_decode, int32_t row_stride, void* out,
                           int32_t* spike_flags, int32_t* spike_tokens, void* stream);
 
+/* fkv_attn_call that allocates nothing.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory during a call (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, outputs and kernels as fkv_attn_call; the
+ * call's split records, arrival counters and fp16 query copy live in one
+ * fixed 8 MiB device array per GPU instead of the handle's workspace, so
+ * neither this call nor its first use allocates or frees anything.  Calls
+ * whose launch plan needs more than the array holds (arrival counters for
+ * at most 16384 rows, then the query copy and B*Hkv*(G rows)*splits*(8+D)
+ * floats of records; C3 at batch 8 needs 0.6 MiB, C5 1.2 MiB) return
+ * FKV_EINVAL, as does a call whose handle's device is not current.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two threads) race and must be ordered by the caller. */
+int fkv_attn_call_noalloc(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
+                          const void* decode_v, int32_t n_decode, void* out, int32_t* spike_flags,
+                          int32_t* spike_tokens, void* stream);
+
 /* The launch plan of one call (host only, no GPU; no counterpart in the
  * reference, whose split sizing is foveated_attn.cpp:26-38): for a handle of
  * shape (B, Hkv, D, Na, F) called with Hq query heads and n_decode decode
