@@ -6,7 +6,8 @@ A step is one decode step over L distinct layers (each with its own device
 blob, > 1 GB in total so the 256 MB Infinity Cache cannot hold the working
 set); each layer call is one launch of the fused kernel.  The L calls are
 captured once in a HIP graph and replayed; the timed region is K replays
-bracketed by HIP events on the capture stream.  Inputs are synthetic
+bracketed by HIP events on the capture stream, after 300 ms of untimed
+replays (the GPU's clocks settle) and the W warm-up replays.  Inputs are synthetic
 (seeded Gaussian K/V with outlier channels, 2% spike tokens) and resident in
 HBM before timing starts.
 
@@ -222,6 +223,7 @@ def main():
                                   else "fp8-e4m3 K + int4 per-token V")},
         "us_per_layer": round(us_layer, 3),
         "launch": "eager" if args.eager else "hip-graph",
+        "clock_settle_ms": SETTLE_MS,
         "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
     }
     if g32_side:
@@ -270,6 +272,24 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+SETTLE_MS = 300.0
+
+
+def settle_clocks(torch, stream, step, min_ms=SETTLE_MS):
+    """Untimed steps for ``min_ms`` of wall time before the warm-up steps.
+    From an idle start MI355X runs this workload at a transient rate for the
+    first tens of milliseconds of continuous work (measured from a cold
+    process: ~46 us/layer for 5 steps, 54-59 us at steps 10-25, steady ~44.5
+    us only after ~80 steps); a decode loop keeps the GPU busy, so the
+    steady state is the one measured.  The timed region is unchanged."""
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < min_ms:
+        with torch.cuda.stream(stream):
+            for _ in range(20):
+                step()
+        torch.cuda.synchronize()
+
+
 def time_layers(torch, dev, make_handle, layers, qt, dkt, dvt, steps, warmup, eager):
     """Build distinct layer handles (> 1 GiB of blobs unless ``layers``), run
     one decode step over all of them as a HIP graph (or eagerly), time
@@ -304,6 +324,7 @@ def time_layers(torch, dev, make_handle, layers, qt, dkt, dvt, steps, warmup, ea
                     outs.append(h(qt, dkt, dvt))
         step = graph.replay
     torch.cuda.synchronize()
+    settle_clocks(torch, stream, step)
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             step()
