@@ -1447,104 +1447,152 @@ __device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, i
 // memory): split maxima are rescaled to the global max; spike fields take
 // the min and the first-index max.
 //
-// Coherent 16-byte loads of split records: a buffer load with the sc1 cache
-// policy (the policy of agent-scope atomic loads), four dwords per lane;
-// offsets past the buffer read 0 without touching memory.
+// Coherent loads of split records: buffer loads with the sc1 cache policy
+// (the policy of agent-scope atomic loads); offsets past the buffer read 0
+// without touching memory.
 constexpr int kCpolSc1 = 16;
 __device__ inline fkv_f4 ld_agent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
 }
+__device__ inline int ld_agent1(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kCpolSc1);
+}
 
-// The last split of a row merges every split's record.  One CU reading all
-// of them is bound by the bytes it keeps in flight, so the records are read with
-// 16-byte coherent loads, and every load of the split headers and of the
-// first batch of values (one 4-element chunk x 32 splits per thread) is
-// issued before the first wait.  The headers are merged in registers, one
-// wave per head with a lane per split, while the values arrive -- the same
-// arithmetic, in the same order, as merge_kernel, so both merges give the
-// same bits.  `lds` holds ng * ns + ng floats.
-template <int D>
-__device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, float* lds, int b,
-                                             int head0) {
+// 64-lane reductions on DPP row rotations and lane swaps (no LDS permutes):
+// max / min / (max, first index) reach every lane; the sum is a fixed tree
+// whose lanes may round differently, so lane 0's value is returned.
+__device__ inline float wave_max_dpp(float v) {
+    v = fmaxf(v, __uint_as_float(row_ror<1>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(row_ror<2>(__float_as_uint(v))));
+    return head_max(v);
+}
+__device__ inline float wave_min_dpp(float v) {
+    v = fminf(v, __uint_as_float(row_ror<1>(__float_as_uint(v))));
+    v = fminf(v, __uint_as_float(row_ror<2>(__float_as_uint(v))));
+    return head_min(v);
+}
+__device__ inline float wave_sum_dpp(float v) {
+    v += __uint_as_float(row_ror<1>(__float_as_uint(v)));
+    v += __uint_as_float(row_ror<2>(__float_as_uint(v)));
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(head_sum<true>(v))));
+}
+__device__ inline void wave_argmax_dpp(float& mx, int& arg) {
+    pick_max(mx, arg, __uint_as_float(row_ror<1>(__float_as_uint(mx))), (int)row_ror<1>((uint32_t)arg));
+    pick_max(mx, arg, __uint_as_float(row_ror<2>(__float_as_uint(mx))), (int)row_ror<2>((uint32_t)arg));
+    head_argmax(mx, arg);
+}
+
+// Split records of NH heads (g0, g0 + step, ...) of one row merged by one
+// wave.  Lane s reads split s's header; lane (c, u) = (lane % CH, lane /
+// CH) reads value chunk c (4 dims) of the splits u, u + SUB, u + 2 SUB, ...
+// Every load of the NH heads is issued before the first wait.  The split
+// maxima, sums, minima and first-index maxima reduce on DPP; each value lane
+// accumulates its splits in order with the split scales read from the
+// scale's lane, and the SUB lane groups combine by lane swaps.  The
+// in-kernel merge and merge_kernel both run this, so both give the same
+// bits.  Needs nk = ceil(ns / SUB) <= KV / NH.
+template <int D, int NH>
+__device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs, int ns, int ng, int g0, int step,
+                                   int lane, int64_t o0) {
     constexpr int RS = kHdr + D;
-    constexpr int C = D / 4;  // 16-byte chunks of one head's values
-    constexpr int kS = 32;    // splits per batch of value loads
-    constexpr int kG = kHeads / kWavesPerGroup;  // heads per wave
-    static_assert(RS % 4 == 0 && kHdr == 8, "records must be 16-byte aligned with an 8-float header");
-    static_assert(kMaxSplits <= kWave, "a lane per split");
-    const int nt = (int)blockDim.x, t = (int)threadIdx.x;
-    const int wave = t / kWave, lane = t % kWave;
-    float* scl = lds;             // (head, split) softmax rescale factors
-    float* linv = scl + ng * ns;  // (head) 1 / merged sum
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
-    const int nc = ng * C;
-    const int sp_l = lane < ns ? lane : ns - 1;
-    fkv_f4 h0[kG], h1[kG];
+    constexpr int CH = D / 4;          // 16-byte value chunks of a head
+    constexpr int SUB = kWave / CH;    // lane groups over the splits
+    constexpr int KV = kMaxSplits / SUB / NH;  // value loads per lane and head
+    const int c = lane % CH, u = lane / CH;
+    const int sl = lane < ns ? lane : ns - 1;
+    const int nk = (ns + SUB - 1) / SUB;
+    fkv_f4 h[NH];
+    int harg[NH];
+    fkv_f4 v[NH][KV];
 #pragma unroll
-    for (int j = 0; j < kG; j++) {
-        const int g = wave + j * kWavesPerGroup;
-        if (g < ng) {
-            h0[j] = ld_agent4(rs, (sp_l * ng + g) * RS * 4);
-            h1[j] = ld_agent4(rs, (sp_l * ng + g) * RS * 4 + 16);
-        }
-    }
-    fkv_f4 r[kS];
-    auto issue = [&](int c, int s0) {  // chunks past the output load nothing
-        const int off = c < nc ? ((c / C) * RS + kHdr + 4 * (c % C)) * 4 : ns * ng * RS * 4;
+    for (int i = 0; i < NH; i++) {
+        const int g = g0 + i * step;
+        const int hoff = (sl * ng + g) * RS * 4;
+        h[i] = ld_agent4(rs, hoff);
+        harg[i] = ld_agent1(rs, hoff + 16);
 #pragma unroll
-        for (int k = 0; k < kS; k++)
-            if (s0 + k < ns) r[k] = ld_agent4(rs, off + (s0 + k) * ng * RS * 4);
-    };
-    issue(t, 0);  // in flight while the headers are merged
-#pragma unroll
-    for (int j = 0; j < kG; j++) {
-        const int g = wave + j * kWavesPerGroup;
-        if (g < ng) {
-            const bool live = lane < ns;
-            const float ms = live ? h0[j].x : -INFINITY, ls = live ? h0[j].y : 0.f;
-            float mn = live ? h0[j].z : INFINITY, mx = live ? h0[j].w : -INFINITY;
-            int arg = live ? __float_as_int(h1[j].x) : INT_MAX;
-            const float M = wave_max(ms);
-            const float f = ms == -INFINITY ? 0.f : __expf(ms - M);
-            const float L = wave_sum(f * ls);
-            mn = wave_min(mn);
-            wave_argmax(mx, arg);
-            if (live) scl[g * ns + lane] = f;
-            if (lane == 0) {
-                linv[g] = L > 0.f ? 1.0f / L : 0.f;
-                const int64_t o = (int64_t)b * a.Hq + head0 + g;
-                a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
-                a.tokens[o] = mx == -INFINITY ? -1 : arg;
+        for (int k = 0; k < KV; k++) {
+            if (k < nk) {
+                const int s = u + SUB * k;
+                v[i][k] = ld_agent4(rs, ((s < ns ? s : ns - 1) * ng + g) * RS * 4 + (kHdr + 4 * c) * 4);
             }
         }
     }
-    __syncthreads();
-    for (int c0 = 0; c0 < nc; c0 += nt) {
-        const int c = c0 + t, g = (c < nc ? c : nc - 1) / C;
-        float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
-        for (int s0 = 0; s0 < ns; s0 += kS) {
-            if (c0 != 0 || s0 != 0) issue(c, s0);
+    const bool live = lane < ns;
 #pragma unroll
-            for (int k = 0; k < kS; k++) {
-                if (s0 + k < ns) {
-                    const float f = scl[g * ns + s0 + k];
-                    v0 += f * r[k].x;
-                    v1 += f * r[k].y;
-                    v2 += f * r[k].z;
-                    v3 += f * r[k].w;
+    for (int i = 0; i < NH; i++) {
+        const float ms = live ? h[i].x : -INFINITY;
+        float mn = live ? h[i].z : INFINITY, mx = live ? h[i].w : -INFINITY;
+        int arg = live ? harg[i] : INT_MAX;
+        const float M = wave_max_dpp(ms);
+        const float f = ms == -INFINITY ? 0.f : __expf(ms - M);  // 0 past the last split
+        const float L = wave_sum_dpp(live ? f * h[i].y : 0.f);
+        mn = wave_min_dpp(mn);
+        wave_argmax_dpp(mx, arg);
+        const int64_t o = o0 + i * step;
+        if (lane == 0) {
+            a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
+            a.tokens[o] = mx == -INFINITY ? -1 : arg;
+        }
+        fkv_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < KV; k++) {
+            if (k < nk) {
+                // the scale of split u + SUB k sits in that lane (uniform reads per group)
+                float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k));
+#pragma unroll
+                for (int uu = 1; uu < SUB; uu++) {
+                    const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k + uu));
+                    fs = u == uu ? fu : fs;
                 }
+                acc.x = fmaf(fs, v[i][k].x, acc.x);
+                acc.y = fmaf(fs, v[i][k].y, acc.y);
+                acc.z = fmaf(fs, v[i][k].z, acc.z);
+                acc.w = fmaf(fs, v[i][k].w, acc.w);
             }
         }
-        if (c < nc) {
-            const float il = linv[g];
-            const uint2 w = {f2h(v0 * il) | ((uint32_t)f2h(v1 * il) << 16),
-                             f2h(v2 * il) | ((uint32_t)f2h(v3 * il) << 16)};
-            *(uint2*)(a.out + ((int64_t)b * a.Hq + head0 + g) * D + 4 * (c % C)) = w;
+        if (SUB == 4) {
+            LanePair px = swap16(__float_as_uint(acc.x)), py = swap16(__float_as_uint(acc.y));
+            LanePair pz = swap16(__float_as_uint(acc.z)), pw = swap16(__float_as_uint(acc.w));
+            acc = fkv_f4{__uint_as_float(px.a) + __uint_as_float(px.b), __uint_as_float(py.a) + __uint_as_float(py.b),
+                         __uint_as_float(pz.a) + __uint_as_float(pz.b), __uint_as_float(pw.a) + __uint_as_float(pw.b)};
+        }
+        {
+            LanePair px = swap32(__float_as_uint(acc.x)), py = swap32(__float_as_uint(acc.y));
+            LanePair pz = swap32(__float_as_uint(acc.z)), pw = swap32(__float_as_uint(acc.w));
+            acc = fkv_f4{__uint_as_float(px.a) + __uint_as_float(px.b), __uint_as_float(py.a) + __uint_as_float(py.b),
+                         __uint_as_float(pz.a) + __uint_as_float(pz.b), __uint_as_float(pw.a) + __uint_as_float(pw.b)};
+        }
+        if (u == 0) {
+            const float il = L > 0.f ? 1.0f / L : 0.f;
+            const uint2 w = {f2h(acc.x * il) | ((uint32_t)f2h(acc.y * il) << 16),
+                             f2h(acc.z * il) | ((uint32_t)f2h(acc.w * il) << 16)};
+            *(uint2*)(a.out + o * D + 4 * c) = w;
         }
     }
 }
 
+// The last split of a row merges every split's record: wave w takes heads
+// w, w + 4, ... (two at a time where their loads fit the registers).
+template <int D>
+__device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, int b, int head0) {
+    constexpr int RS = kHdr + D;
+    constexpr int SUB = kWave / (D / 4);
+    const int wave = (int)threadIdx.x / kWave, lane = (int)threadIdx.x % kWave;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
+    const int hw = wave < ng ? (ng - wave + kWavesPerGroup - 1) / kWavesPerGroup : 0;  // this wave's heads
+    const int nk = (ns + SUB - 1) / SUB;
+    const int64_t o0 = (int64_t)b * a.Hq + head0 + wave;
+    int j = 0;
+    if (hw >= 2 && nk <= kMaxSplits / SUB / 2) {
+        merge_heads<D, 2>(a, rs, ns, ng, wave, kWavesPerGroup, lane, o0);
+        j = 2;
+    }
+    for (; j < hw; j++)
+        merge_heads<D, 1>(a, rs, ns, ng, wave + j * kWavesPerGroup, kWavesPerGroup, lane,
+                          o0 + j * kWavesPerGroup);
+}
 
 // Unit u of one wave's stream: the wave's far tiles first (far tile
 // f0 + u*fs), then each of its near tiles w + j*N as two units, keys then
@@ -1980,14 +2028,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __syncthreads();
     if (!s_last) return;
     // every record (this split's included) is in global memory now
-    static_assert((NHW * kMaxSplits + NHW) * 4 <= kLds, "direct-merge scratch");
-    merge_finalize_direct<D>(a, part, a.num_splits, ng, smem, b, head0);
+    merge_finalize_direct<D>(a, part, a.num_splits, ng, b, head0);
     if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Split-K merge as its own launch: one wave per (row, head).  Lanes < ns
-// read the split headers; the wave reduces them (max, rescaled sum, min,
-// first-index max) and each lane merges D/64 output dims.
+// Split-K merge as its own launch (in-kernel merge switched off): one wave
+// per (row, head), the same per-head merge as the in-kernel one.
 template <int D>
 __global__ __launch_bounds__(64) void merge_kernel(AttnArgs a) {
     constexpr int RS = kHdr + D;
@@ -1998,39 +2044,11 @@ __global__ __launch_bounds__(64) void merge_kernel(AttnArgs a) {
     const int head0 = kvh * a.G + hgrp * a.hpg;
     const int ng = min(a.hpg, a.G - hgrp * a.hpg);
     if (g >= ng) return;
-    const int ns = a.num_splits, lane = threadIdx.x;
-    const float* src = a.ws + (int64_t)row * ns * min(a.hpg, a.G) * RS + g * RS;
-    float ms = -INFINITY, ls = 0.f, mn = INFINITY, mx = -INFINITY;
-    int arg = INT_MAX;
-    if (lane < ns) {
-        const float* h = src + (int64_t)lane * ng * RS;
-        ms = h[0];
-        ls = h[1];
-        mn = h[2];
-        mx = h[3];
-        arg = __float_as_int(h[4]);
-    }
-    const float M = wave_max(ms);
-    const float f = ms == -INFINITY ? 0.f : __expf(ms - M);
-    const float L = wave_sum(f * ls);
-    mn = wave_min(mn);
-    wave_argmax(mx, arg);
-    float acc[D / 64];
-#pragma unroll
-    for (int i = 0; i < D / 64; i++) acc[i] = 0.f;
-    for (int sp = 0; sp < ns; sp++) {
-        const float fs = __shfl(f, sp, kWave);
-#pragma unroll
-        for (int i = 0; i < D / 64; i++) acc[i] += fs * src[(int64_t)sp * ng * RS + kHdr + 64 * i + lane];
-    }
-    const float inv_l = L > 0.f ? 1.0f / L : 0.f;
-    const int64_t o = (int64_t)b * a.Hq + head0 + g;
-#pragma unroll
-    for (int i = 0; i < D / 64; i++) a.out[o * D + 64 * i + lane] = f2h(acc[i] * inv_l);
-    if (lane == 0) {
-        a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
-        a.tokens[o] = mx == -INFINITY ? -1 : arg;
-    }
+    const int ns = a.num_splits;
+    const float* src = a.ws + (int64_t)row * ns * min(a.hpg, a.G) * RS;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
+    merge_heads<D, 1>(a, rs, ns, ng, g, 1, (int)threadIdx.x, (int64_t)b * a.Hq + head0 + g);
 }
 
 // out = acc / l (fp16), spike flag and token for ng heads of one record set
