@@ -285,6 +285,7 @@ struct AttnArgs {
     int* arrive;    // [row] split arrival counters (zero between calls)
     int near_plan;  // expected near tiles per row (balances the far split)
     int dec_wave0;  // the wave that takes decode tile 0
+    int wave_recs;  // split records per split: 4 (one per wave) or 1 (merged in LDS)
     // TurboQuant far tier (fmt 1)
     const float* tq_PiT;    // (D, D) fp32, PiT[j][i] = Pi[i][j]
     const float* tq_ST;     // (D, D) fp32, ST[j][i] = S[i][j]
@@ -383,7 +384,9 @@ __device__ inline float head_sum(float v) {
 }
 // (max, first index of the max) over the lanes l' = l (mod 4)
 __device__ inline void pick_max(float& mx, int& arg, float ox, int oa) {
-    if (ox > mx || (ox == mx && oa < arg)) { mx = ox; arg = oa; }
+    const bool take = ox > mx || (ox == mx && oa < arg);  // selects, no branch
+    mx = take ? ox : mx;
+    arg = take ? oa : arg;
 }
 __device__ inline void head_argmax(float& mx, int& arg) {
     pick_max(mx, arg, __uint_as_float(row_ror<4>(__float_as_uint(mx))), (int)row_ror<4>((uint32_t)arg));
@@ -1482,6 +1485,82 @@ __device__ inline void wave_argmax_dpp(float& mx, int& arg) {
     head_argmax(mx, arg);
 }
 
+// Reductions over the 16 lanes of each row (DPP rotations only); lanes of
+// row 0 hold the result for lanes 0-15.
+__device__ inline float row_max16(float v) {
+    v = fmaxf(v, __uint_as_float(row_ror<1>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(row_ror<2>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(row_ror<4>(__float_as_uint(v))));
+    return fmaxf(v, __uint_as_float(row_ror<8>(__float_as_uint(v))));
+}
+__device__ inline float row_min16(float v) {
+    v = fminf(v, __uint_as_float(row_ror<1>(__float_as_uint(v))));
+    v = fminf(v, __uint_as_float(row_ror<2>(__float_as_uint(v))));
+    v = fminf(v, __uint_as_float(row_ror<4>(__float_as_uint(v))));
+    return fminf(v, __uint_as_float(row_ror<8>(__float_as_uint(v))));
+}
+__device__ inline float row_sum16(float v) {
+    v += __uint_as_float(row_ror<1>(__float_as_uint(v)));
+    v += __uint_as_float(row_ror<2>(__float_as_uint(v)));
+    v += __uint_as_float(row_ror<4>(__float_as_uint(v)));
+    return v + __uint_as_float(row_ror<8>(__float_as_uint(v)));
+}
+__device__ inline void row_argmax16(float& mx, int& arg) {
+    pick_max(mx, arg, __uint_as_float(row_ror<1>(__float_as_uint(mx))), (int)row_ror<1>((uint32_t)arg));
+    pick_max(mx, arg, __uint_as_float(row_ror<2>(__float_as_uint(mx))), (int)row_ror<2>((uint32_t)arg));
+    pick_max(mx, arg, __uint_as_float(row_ror<4>(__float_as_uint(mx))), (int)row_ror<4>((uint32_t)arg));
+    pick_max(mx, arg, __uint_as_float(row_ror<8>(__float_as_uint(mx))), (int)row_ror<8>((uint32_t)arg));
+}
+
+// Spike fields (lane 0) and the merged output of one head: value lane
+// (c, u) accumulates its splits u, u + SUB, ... in order, with each split's
+// scale read from that split's lane; the SUB lane groups combine by lane
+// swaps; lanes of group 0 write chunk c.
+template <int D, int NH, int KV>
+__device__ inline void merge_values(const AttnArgs& a, const fkv_f4 (&v)[KV], float f, float M, float L, float mn,
+                                    float mx, int arg, int nk, int u, int c, int lane, int64_t o) {
+    constexpr int SUB = kWave / (D / 4);
+    (void)M;
+    if (lane == 0) {
+        a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
+        a.tokens[o] = mx == -INFINITY ? -1 : arg;
+    }
+    fkv_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KV; k++) {
+        if (k < nk) {
+            float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k));
+#pragma unroll
+            for (int uu = 1; uu < SUB; uu++) {
+                const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k + uu));
+                fs = u == uu ? fu : fs;
+            }
+            acc.x = fmaf(fs, v[k].x, acc.x);
+            acc.y = fmaf(fs, v[k].y, acc.y);
+            acc.z = fmaf(fs, v[k].z, acc.z);
+            acc.w = fmaf(fs, v[k].w, acc.w);
+        }
+    }
+    if (SUB == 4) {
+        LanePair px = swap16(__float_as_uint(acc.x)), py = swap16(__float_as_uint(acc.y));
+        LanePair pz = swap16(__float_as_uint(acc.z)), pw = swap16(__float_as_uint(acc.w));
+        acc = fkv_f4{__uint_as_float(px.a) + __uint_as_float(px.b), __uint_as_float(py.a) + __uint_as_float(py.b),
+                     __uint_as_float(pz.a) + __uint_as_float(pz.b), __uint_as_float(pw.a) + __uint_as_float(pw.b)};
+    }
+    {
+        LanePair px = swap32(__float_as_uint(acc.x)), py = swap32(__float_as_uint(acc.y));
+        LanePair pz = swap32(__float_as_uint(acc.z)), pw = swap32(__float_as_uint(acc.w));
+        acc = fkv_f4{__uint_as_float(px.a) + __uint_as_float(px.b), __uint_as_float(py.a) + __uint_as_float(py.b),
+                     __uint_as_float(pz.a) + __uint_as_float(pz.b), __uint_as_float(pw.a) + __uint_as_float(pw.b)};
+    }
+    if (u == 0) {
+        const float il = L > 0.f ? 1.0f / L : 0.f;
+        const uint2 w = {f2h(acc.x * il) | ((uint32_t)f2h(acc.y * il) << 16),
+                         f2h(acc.z * il) | ((uint32_t)f2h(acc.w * il) << 16)};
+        *(uint2*)(a.out + o * D + 4 * c) = w;
+    }
+}
+
 // Split records of NH heads (g0, g0 + step, ...) of one row merged by one
 // wave.  Lane s reads split s's header; lane (c, u) = (lane % CH, lane /
 // CH) reads value chunk c (4 dims) of the splits u, u + SUB, u + 2 SUB, ...
@@ -1499,75 +1578,48 @@ __device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs,
     constexpr int SUB = kWave / CH;    // lane groups over the splits
     constexpr int KV = kMaxSplits / SUB / NH;  // value loads per lane and head
     const int c = lane % CH, u = lane / CH;
-    const int sl = lane < ns ? lane : ns - 1;
     const int nk = (ns + SUB - 1) / SUB;
+    const int sstride = ng * RS * 4;  // bytes from one split's record to the next
+    // Offsets past the last record read 0 without touching memory: lanes
+    // past ns are masked below, value loads of splits past ns meet scale 0.
     fkv_f4 h[NH];
     int harg[NH];
     fkv_f4 v[NH][KV];
 #pragma unroll
     for (int i = 0; i < NH; i++) {
         const int g = g0 + i * step;
-        const int hoff = (sl * ng + g) * RS * 4;
+        const int hoff = lane * sstride + g * RS * 4;
         h[i] = ld_agent4(rs, hoff);
         harg[i] = ld_agent1(rs, hoff + 16);
+        const int voff = u * sstride + (g * RS + kHdr + 4 * c) * 4;
 #pragma unroll
-        for (int k = 0; k < KV; k++) {
-            if (k < nk) {
-                const int s = u + SUB * k;
-                v[i][k] = ld_agent4(rs, ((s < ns ? s : ns - 1) * ng + g) * RS * 4 + (kHdr + 4 * c) * 4);
-            }
-        }
+        for (int k = 0; k < KV; k++)
+            if (k < nk)
+                v[i][k] = __builtin_bit_cast(
+                    fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, SUB * k * sstride, kCpolSc1));
     }
     const bool live = lane < ns;
+    const bool one_row = ns <= 16;  // the live lanes sit in the first 16: row reductions suffice
 #pragma unroll
     for (int i = 0; i < NH; i++) {
         const float ms = live ? h[i].x : -INFINITY;
         float mn = live ? h[i].z : INFINITY, mx = live ? h[i].w : -INFINITY;
         int arg = live ? harg[i] : INT_MAX;
-        const float M = wave_max_dpp(ms);
-        const float f = ms == -INFINITY ? 0.f : __expf(ms - M);  // 0 past the last split
-        const float L = wave_sum_dpp(live ? f * h[i].y : 0.f);
-        mn = wave_min_dpp(mn);
-        wave_argmax_dpp(mx, arg);
-        const int64_t o = o0 + i * step;
-        if (lane == 0) {
-            a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
-            a.tokens[o] = mx == -INFINITY ? -1 : arg;
-        }
-        fkv_f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < KV; k++) {
-            if (k < nk) {
-                // the scale of split u + SUB k sits in that lane (uniform reads per group)
-                float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k));
-#pragma unroll
-                for (int uu = 1; uu < SUB; uu++) {
-                    const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k + uu));
-                    fs = u == uu ? fu : fs;
-                }
-                acc.x = fmaf(fs, v[i][k].x, acc.x);
-                acc.y = fmaf(fs, v[i][k].y, acc.y);
-                acc.z = fmaf(fs, v[i][k].z, acc.z);
-                acc.w = fmaf(fs, v[i][k].w, acc.w);
-            }
-        }
-        if (SUB == 4) {
-            LanePair px = swap16(__float_as_uint(acc.x)), py = swap16(__float_as_uint(acc.y));
-            LanePair pz = swap16(__float_as_uint(acc.z)), pw = swap16(__float_as_uint(acc.w));
-            acc = fkv_f4{__uint_as_float(px.a) + __uint_as_float(px.b), __uint_as_float(py.a) + __uint_as_float(py.b),
-                         __uint_as_float(pz.a) + __uint_as_float(pz.b), __uint_as_float(pw.a) + __uint_as_float(pw.b)};
-        }
-        {
-            LanePair px = swap32(__float_as_uint(acc.x)), py = swap32(__float_as_uint(acc.y));
-            LanePair pz = swap32(__float_as_uint(acc.z)), pw = swap32(__float_as_uint(acc.w));
-            acc = fkv_f4{__uint_as_float(px.a) + __uint_as_float(px.b), __uint_as_float(py.a) + __uint_as_float(py.b),
-                         __uint_as_float(pz.a) + __uint_as_float(pz.b), __uint_as_float(pw.a) + __uint_as_float(pw.b)};
-        }
-        if (u == 0) {
-            const float il = L > 0.f ? 1.0f / L : 0.f;
-            const uint2 w = {f2h(acc.x * il) | ((uint32_t)f2h(acc.y * il) << 16),
-                             f2h(acc.z * il) | ((uint32_t)f2h(acc.w * il) << 16)};
-            *(uint2*)(a.out + o * D + 4 * c) = w;
+        float M, L;
+        if (one_row) {
+            M = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(row_max16(ms))));
+            const float f = ms == -INFINITY ? 0.f : __expf(ms - M);  // 0 past the last split
+            L = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(row_sum16(live ? f * h[i].y : 0.f))));
+            mn = row_min16(mn);
+            row_argmax16(mx, arg);
+            merge_values<D, NH, KV>(a, v[i], f, M, L, mn, mx, arg, nk, u, c, lane, o0 + i * step);
+        } else {
+            M = wave_max_dpp(ms);
+            const float f = ms == -INFINITY ? 0.f : __expf(ms - M);
+            L = wave_sum_dpp(live ? f * h[i].y : 0.f);
+            mn = wave_min_dpp(mn);
+            wave_argmax_dpp(mx, arg);
+            merge_values<D, NH, KV>(a, v[i], f, M, L, mn, mx, arg, nk, u, c, lane, o0 + i * step);
         }
     }
 }
@@ -1578,7 +1630,7 @@ template <int D>
 __device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, int b, int head0) {
     constexpr int RS = kHdr + D;
     constexpr int SUB = kWave / (D / 4);
-    const int wave = (int)threadIdx.x / kWave, lane = (int)threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = (int)threadIdx.x % kWave;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
     const int hw = wave < ng ? (ng - wave + kWavesPerGroup - 1) / kWavesPerGroup : 0;  // this wave's heads
@@ -1761,7 +1813,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
     const int head0 = kvh * a.G + hgrp * a.hpg;
     const int ng = min(a.hpg, a.G - hgrp * a.hpg);
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    // the wave index is wave-uniform: scalar registers, scalar branches
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = threadIdx.x % kWave;
     const int j = lane & 3, blk = lane >> 2;
     uint8_t* ring = lds + wave * 2 * SLOT;
 
@@ -1920,8 +1973,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop);
 
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
-    __syncthreads();  // every wave is done with its ring: the records reuse the LDS
+    // Rows of 2..16 splits: every wave publishes its own record (record
+    // split * 4 + wave) straight from registers and the last workgroup merges
+    // 4 records per split.  Otherwise the 4 waves merge their records in LDS
+    // first (one record per split, or the outputs when a row is one split).
+    const int row = (int)(bkv * a.head_groups + hgrp);  // (b, kv_head, head group)
+    // rows are spaced for the widest row (a last head group may be narrower)
+    float* part = a.ws + (int64_t)row * a.num_splits * a.wave_recs * min(a.hpg, a.G) * RS;
+    const bool own_rec = a.wave_recs == kWavesPerGroup;
     float* wr = smem + wave * NHW * RS;
+    // this wave's record in the workspace (coherent buffer stores, sc1: the
+    // cache policy of agent-scope atomic stores)
+    const __amdgpu_buffer_rsrc_t wrec = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(part + (int64_t)(split * kWavesPerGroup + wave) * ng * RS), (short)0, ng * RS * 4, 0x00020000);
+    if (!own_rec) __syncthreads();  // every wave is done with its ring: the records reuse the LDS
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         const float l = head_sum<true>(st.lsum[qd]), mn = head_min(st.mn[qd]);
@@ -1948,21 +2013,48 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             for (int dh = 0; dh < NH; dh++) corr[dh] = z;
         }
         const int h = 4 * qd + j;
-        if (lane < 4 && h < ng) {
-            wr[h * RS + 0] = st.m[qd];
-            wr[h * RS + 1] = l;
-            wr[h * RS + 2] = mn;
-            wr[h * RS + 3] = mx;
-            wr[h * RS + 4] = __int_as_float(arg);
+        const float hdr[5] = {st.m[qd], l, mn, mx, __int_as_float(arg)};
+        if (own_rec) {
+            if (lane < 4 && h < ng) {
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(fkv_v4u, fkv_f4{hdr[0], hdr[1], hdr[2], hdr[3]}), wrec, h * RS * 4, 0, kCpolSc1);
+                __builtin_amdgcn_raw_buffer_store_b32((uint32_t)arg, wrec, h * RS * 4 + 16, 0, kCpolSc1);
+            }
+        } else if (lane < 4 && h < ng) {
+#pragma unroll
+            for (int e = 0; e < 5; e++) wr[h * RS + e] = hdr[e];
         }
 #pragma unroll
         for (int dh = 0; dh < NH; dh++) {
             const float zz[4] = {quad_bcast<0>(corr[dh]), quad_bcast<1>(corr[dh]), quad_bcast<2>(corr[dh]),
                                  quad_bcast<3>(corr[dh])};
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (4 * qd + i < ng) wr[(4 * qd + i) * RS + kHdr + 64 * dh + lane] = st.acc[qd][dh][i] + zz[i];
+            for (int i = 0; i < 4; i++) {
+                if (4 * qd + i < ng) {
+                    const int e = (4 * qd + i) * RS + kHdr + 64 * dh + lane;
+                    if (own_rec)
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(st.acc[qd][dh][i] + zz[i]), wrec, e * 4,
+                                                              0, kCpolSc1);
+                    else wr[e] = st.acc[qd][dh][i] + zz[i];
+                }
+            }
         }
+    }
+    if (own_rec) {
+        if (a.arrive == nullptr) return;  // merged by merge_kernel (kernel boundary orders it)
+        // the arrival is counted once this workgroup's stores are complete
+        // (the ordering argument of the merged-record path below)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int prev = __hip_atomic_fetch_add(a.arrive + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = prev == a.num_splits - 1;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        merge_finalize_direct<D>(a, part, a.num_splits * kWavesPerGroup, ng, b, head0);
+        if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
     }
     __syncthreads();
 
@@ -2002,9 +2094,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         return;
     }
     // ---- split-K: publish this split's record ----
-    const int row = (int)(bkv * a.head_groups + hgrp);  // (b, kv_head, head group)
-    // rows are spaced for the widest row (a last head group may be narrower)
-    float* part = a.ws + (int64_t)row * a.num_splits * min(a.hpg, a.G) * RS;
     if (a.arrive == nullptr) {  // merged by merge_kernel (kernel boundary orders it)
         for (int i = threadIdx.x; i < ng * RS; i += blockDim.x) part[(int64_t)split * ng * RS + i] = smem[i];
         return;
@@ -2044,7 +2133,7 @@ __global__ __launch_bounds__(64) void merge_kernel(AttnArgs a) {
     const int head0 = kvh * a.G + hgrp * a.hpg;
     const int ng = min(a.hpg, a.G - hgrp * a.hpg);
     if (g >= ng) return;
-    const int ns = a.num_splits;
+    const int ns = a.num_splits * a.wave_recs;
     const float* src = a.ws + (int64_t)row * ns * min(a.hpg, a.G) * RS;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
@@ -2192,12 +2281,15 @@ LaunchPlan plan_launch(const BlobLayout& L, int Hq, int n_decode, int target_wgs
     p.ng_max = G < hpg ? G : hpg;
     p.rows = L.B * L.Hkv * p.head_groups;
     p.splits = plan_splits(L, p.rows, n_decode, target_wgs);
-    p.ws_floats = p.splits > 1 ? partial_floats(p.rows, p.splits, p.ng_max, L.D) : 0;
+    // rows of 2..16 splits keep one record per wave (their merge reads at most 64)
+    p.wave_recs = p.splits > 1 && p.splits * kWavesPerGroup <= kMaxSplits ? kWavesPerGroup : 1;
+    p.ws_floats = p.splits > 1 ? partial_floats(p.rows, p.splits * p.wave_recs, p.ng_max, L.D) : 0;
     return p;
 }
 
-// Both row widths at the largest split count: covers plan_launch for every
-// decode length and target.
+// Both row widths at the largest record count per row (64: kMaxSplits
+// merged records, or 16 splits of 4 wave records): covers plan_launch for
+// every decode length and target.
 size_t workspace_floats(const BlobLayout& L, int Hq) {
     const int G = Hq / L.Hkv;
     size_t best = 0;
@@ -2471,6 +2563,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.head_groups = head_groups;
     a.hpg = hpg;
     a.num_splits = splits;
+    a.wave_recs = p.wave_recs;
     a.spike_margin = h->margin;
     a.inv_sqrt_d = (float)(1.0 / sqrt((double)L.D));
     a.out = (uint16_t*)out;
