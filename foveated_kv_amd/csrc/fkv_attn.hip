@@ -31,6 +31,7 @@
 #include <cmath>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "fkv_attn.h"
@@ -459,6 +460,37 @@ struct QOperand {
         o[5] = __builtin_bit_cast(fkv_h4, r5);
         o[6] = __builtin_bit_cast(fkv_h4, r6);
         o[7] = __builtin_bit_cast(fkv_h4, r7);
+    }
+    // N (2, 4 or 8) k-steps s0.. of quad qd (see lds_q)
+    template <int N>
+    __device__ void readn(int qd, int s0, fkv_h4 (&o)[N]) const;
+};
+
+// q as the B operand of the score MFMA held in registers for the whole
+// launch (rows of one head quad): read once from the LDS operand array after
+// the prologue, so tiles issue no LDS reads (and no waits) for the query.
+template <int NS>
+struct QReg {
+    fkv_h4 q[NS];
+    __device__ void load(const QOperand<NS>& src) {
+#pragma unroll
+        for (int s0 = 0; s0 < NS; s0 += 8) {
+            fkv_h4 t[8];
+            src.read8(0, s0, t);
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[s0 + i] = t[i];
+        }
+    }
+    __device__ QReg fresh() const { return *this; }
+    __device__ fkv_h4 operator()(int, int s) const { return q[s]; }
+    __device__ void read8(int, int s0, fkv_h4 (&o)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = q[s0 + i];
+    }
+    template <int N>
+    __device__ void readn(int, int s0, fkv_h4 (&o)[N]) const {
+#pragma unroll
+        for (int i = 0; i < N; i++) o[i] = q[s0 + i];
     }
 };
 
@@ -903,6 +935,12 @@ __device__ inline void lds_q<2>(const uint16_t* p, fkv_h4 (&o)[2]) {
     o[0] = __builtin_bit_cast(fkv_h4, r0); o[1] = __builtin_bit_cast(fkv_h4, r1);
 }
 
+template <int NS>
+template <int N>
+__device__ inline void QOperand<NS>::readn(int qd, int s0, fkv_h4 (&o)[N]) const {
+    lds_q<N>(qs + base + (qd * NS + s0) * 16, o);
+}
+
 // Online-softmax update of head quad qd for a far tile: rescale on a new
 // maximum, then the gated weights p (the reference skips V of far tokens
 // with s < m - 16, foveated_attn.metal:713).  Returns whether any p > 0.
@@ -977,8 +1015,8 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
         fkv_h4 q_r[NQ][KS], q_k[NQ][KS];
 #pragma unroll
         for (int qd = 0; qd < NQ; qd++) {
-            lds_q<KS>(qr.qs + qr.base + (qd * NS + s0) * 16, q_r[qd]);
-            lds_q<KS>(qk.qs + qk.base + (qd * NS + s0) * 16, q_k[qd]);
+            qr.template readn<KS>(qd, s0, q_r[qd]);
+            qk.template readn<KS>(qd, s0, q_k[qd]);
         }
 #pragma unroll
         for (int s = s0; s < s0 + KS; s++) {
@@ -1926,6 +1964,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         __builtin_amdgcn_s_barrier();
     }
 
+    // rows of one head quad keep the query operands in registers
+    using QSel = std::conditional_t<NQ == 1, QReg<NS>, QOperand<NS>>;
+    QSel qx, qrx, qkx;
+    if constexpr (NQ == 1) {
+        if constexpr (TQ) {
+            qrx.load(qrop);
+            qkx.load(qkop);
+        } else {
+            qx.load(qop);
+        }
+    } else {
+        qx = qop;
+        qrx = qrop;
+        qkx = qkop;
+    }
+
     // ---- the stream: unit u is computed while unit u + 1 streams in ----
     fkv_f4 sacc[NQ];  // near scores, carried from a K unit to its V unit
 #pragma unroll
@@ -1945,18 +1999,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             if constexpr (TQ) {
                 TqTile<D> r;
                 lds_tq(r, slot, lane);
-                tq_far_compute<D, NQ>(st, r, tile, lane, a, qrop, qkop, asum);
+                tq_far_compute<D, NQ>(st, r, tile, lane, a, qrx, qkx, asum);
             } else if constexpr (G32) {
                 FarTileG<D> r;
                 lds_g32(r, slot, lane);
-                g32_far_compute<D, NQ>(st, r, tile, a.L.F, lane, a.inv_sqrt_d, qop);
+                g32_far_compute<D, NQ>(st, r, tile, a.L.F, lane, a.inv_sqrt_d, qx);
             } else {
                 FarTile<D> r;
                 lds_far(r, slot, lane);
-                far_compute<D, NQ>(st, r, tile, a.L.F, blk, a.inv_sqrt_d, qop);
+                far_compute<D, NQ>(st, r, tile, a.L.F, blk, a.inv_sqrt_d, qx);
             }
         } else if (kd == kNearK) {
-            near_scores_lds<D, NQ>(sacc, slot, lane, qop);
+            if constexpr (TQ) near_scores_lds<D, NQ>(sacc, slot, lane, qop);  // near tiles: the unrotated query
+            else near_scores_lds<D, NQ>(sacc, slot, lane, qx);
         } else {
             near_pv_lds<D, NQ>(st, sacc, slot, lane, tile, nv, a.inv_sqrt_d);
         }
@@ -1970,7 +2025,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // the same partition, and the same bits, as the host count.
     const int nt_dec = (int)cdiv(n_dec, kTile);
     for (int d = (un.w - a.dec_wave0 + un.N) % un.N; d < nt_dec; d += un.N)
-        dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop);
+    {
+        if constexpr (TQ) dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop);
+        else dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qx);
+    }
 
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
     // Rows of 2..16 splits: every wave publishes its own record (record
