@@ -18,8 +18,15 @@ outputs, near_valid; no credit for gated-V skipping) divided by the
 per-layer time.  ``us_per_layer`` and ``pct_peak`` are reported beside it,
 with a ``roofline`` object (traffic from the committed rocprof counter
 summary), the box's streaming-read ceiling measured in-run, and a
-``cpu_baseline`` (the C oracle's dequant+SDPA formulation on a bounded
-sample, on the host cores).
+``cpu_baseline``: the whole batch of one layer on the host cores, the
+faster of the C oracle's dequant+SDPA formulation and the reference's
+formulation in torch ops (dequant -> cat -> repeat_interleave -> SDPA), each
+timed over 100 calls or 20 s.
+
+Other modes (each prints its own JSON line): ``--e2e`` (the C5 decode +
+promotion loop), ``--generate`` (a tiny LM decoding through the closure,
+eager against one HIP graph per decode step), ``--crossover`` (the fused
+kernel against exact fp16 attention, 1K-32K, B=1 and B=8).
 """
 
 import argparse
@@ -73,33 +80,99 @@ def read_traffic(path):
     return None
 
 
-def cpu_baseline(c, q, dk, dv, D, sample_b=1, turbo=None):
-    """Oracle formulation (dequant + concat + SDPA, fp64 softmax; OpenMP over
-    (b, q head) for the fp8 tier, numpy for TurboQuant) on the first
-    ``sample_b`` batch rows of one layer."""
+def _timed(fn, warm_iters=10, warm_s=5.0, iters=100, time_s=20.0):
+    """Warm up (``warm_iters`` calls or ``warm_s`` seconds, whichever ends
+    first; at least one), then time calls until ``iters`` calls or
+    ``time_s`` seconds (at least one).  -> (seconds per call, calls timed)."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warm_iters and (n == 0 or time.perf_counter() - t0 < warm_s):
+        fn()
+        n += 1
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < iters and (reps == 0 or time.perf_counter() - t0 < time_s):
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def host_cpu():
+    """(model name, logical CPUs this process may run on)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return model, n
+
+
+def cpu_baseline(c, q, dk, dv, D, turbo=None):
+    """The C oracle's formulation (dequant + concat + SDPA, fp64 softmax;
+    OpenMP over (b, q head) for the fp8 tier, numpy for TurboQuant) on the
+    whole batch of one layer.  -> (seconds per call, calls timed)."""
     import oracle
     from oracle import turbo as oturbo
 
-    sl = slice(0, sample_b)
     if turbo is not None:
-        args = [q[sl], c["near_k"][sl], c["near_v"][sl], c["near_valid"]] + [t[sl] for t in turbo["far"]] + [
-            turbo["C"], dk[sl] if dk is not None else None, dv[sl] if dv is not None else None]
+        args = [q, c["near_k"], c["near_v"], c["near_valid"]] + list(turbo["far"]) + [turbo["C"], dk, dv]
         fn = oturbo.attend_formulation
     else:
-        args = [q[sl], c["near_k"][sl], c["near_v"][sl], c["near_valid"], c["far_k"][sl], c["far_v"][sl],
-                c["far_v_scale"][sl], c["far_v_zero"][sl], dk[sl] if dk is not None else None,
-                dv[sl] if dv is not None else None]
+        args = [q, c["near_k"], c["near_v"], c["near_valid"], c["far_k"], c["far_v"], c["far_v_scale"],
+                c["far_v_zero"], dk, dv]
         fn = oracle.attend_formulation
-    fn(*args)  # warm (page-in)
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        fn(*args)
-        reps += 1
-        if time.perf_counter() - t0 >= 10.0 or reps >= 20:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    return dt, reps
+    return _timed(lambda: fn(*args))
+
+
+def torch_cpu_baseline(torch, c, q, dk, dv, D, threads, turbo=None):
+    """The reference's formulation with torch ops on the host cores
+    (mlx_foveated.py:239-312): dequant the far tier, concatenate the valid
+    near rows, decode rows and far rows, repeat_interleave K and V to the
+    query heads, SDPA (fp32: the host has no fast fp16 path), on the whole
+    batch of one layer with ``threads`` torch threads.  -> (seconds per
+    call, calls timed)."""
+    import torch.nn.functional as Fn
+
+    from foveated_kv_amd.tier_cache import dequant_int4_per_token, e4m3_to_fp16
+
+    torch.set_num_threads(threads)
+    t = {n: torch.from_numpy(np.ascontiguousarray(a)) for n, a in c.items()}
+    qt = torch.from_numpy(q).float()[:, :, None, :]
+    mv = int(t["near_valid"].max())
+    nk, nv = t["near_k"][:, :, :mv], t["near_v"][:, :, :mv]
+    dkt = torch.from_numpy(dk) if dk is not None else None
+    dvt = torch.from_numpy(dv) if dv is not None else None
+    G = q.shape[1] // nk.shape[1]
+    if turbo is not None:
+        from foveated_kv_amd import turbo as tq
+
+        far = [torch.from_numpy(np.ascontiguousarray(a)) for a in turbo["far"]]
+        tc = turbo["tc"]
+
+        def dequant():
+            return tq.turbo_dequant_keys(*far[:4], tc), tq.turbo_dequant_values(far[4], far[5])
+    else:
+        def dequant():
+            return e4m3_to_fp16(t["far_k"]), dequant_int4_per_token(t["far_v"], t["far_v_scale"], t["far_v_zero"])
+
+    def run():
+        fk, fv = dequant()
+        ks = [nk] + ([dkt] if dkt is not None else []) + [fk]
+        vs = [nv] + ([dvt] if dvt is not None else []) + [fv]
+        ak = torch.cat(ks, dim=2).float().repeat_interleave(G, dim=1)
+        av = torch.cat(vs, dim=2).float().repeat_interleave(G, dim=1)
+        return Fn.scaled_dot_product_attention(qt, ak, av, scale=D ** -0.5)
+
+    with torch.no_grad():
+        return _timed(run)
 
 
 def main():
@@ -114,6 +187,17 @@ def main():
                     help="C5 end-to-end loop instead of the kernel line: importance partition + compress, then "
                          "--e2e-steps decode steps of attention + spike drain + promotion on one 64K layer")
     ap.add_argument("--e2e-steps", type=int, default=128)
+    ap.add_argument("--generate", action="store_true",
+                    help="model decode loop instead of the kernel line: a seeded tiny LM (tests/_tiny_lm.py) "
+                         "decoding through generate_fused, eager closure vs one HIP graph per decode step")
+    ap.add_argument("--gen-tokens", type=int, default=128)
+    ap.add_argument("--gen-layers", type=int, default=16)
+    ap.add_argument("--gen-context", type=int, default=4096)
+    ap.add_argument("--crossover", action="store_true",
+                    help="kernel crossover instead of the kernel line: fused kernel vs exact fp16 torch SDPA on "
+                         "the same GPU, 7B shapes, --cross-contexts x --cross-batches")
+    ap.add_argument("--cross-contexts", type=int, nargs="+", default=[1024, 2048, 4096, 8192, 16384, 32768])
+    ap.add_argument("--cross-batches", type=int, nargs="+", default=[1, 8])
     ap.add_argument("--no-group32", action="store_true",
                     help="C3 configs: skip the group-32 V layout measured beside the per-token headline")
     ap.add_argument("--v-group", type=int, default=0, choices=(0, 32),
@@ -148,6 +232,12 @@ def main():
     dev = torch.device("cuda:0")
     if args.e2e:
         run_e2e(args, torch, dev)
+        return
+    if args.generate:
+        run_generate(args, torch, dev)
+        return
+    if args.crossover:
+        run_crossover(args, torch, dev)
         return
     B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[args.config]
     cfg = ext.TierConfig()
@@ -250,17 +340,26 @@ def main():
         if turbo:
             from oracle import turbo as oturbo
 
-            tb_ = {"far": [t.cpu().numpy() for t in tfar], "C": oturbo.constants(D)}
-        dt, reps = cpu_baseline(c, q, dk, dv, D, sample_b=1, turbo=tb_)
-        sample_bytes = (algorithmic_bytes_turbo(1, Hq, Hkv, D, R, F, n_dec) if turbo
-                        else algorithmic_bytes(1, Hq, Hkv, D, R, F, n_dec, cfg.v_group))
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+            tb_ = {"far": [t.cpu().numpy() for t in tfar], "C": oturbo.constants(D), "tc": tc}
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or host_cpu()[1]
+        cpu_model, nproc = host_cpu()
+        dt_o, reps_o = cpu_baseline(c, q, dk, dv, D, turbo=tb_)
+        dt_t, reps_t = torch_cpu_baseline(torch, c, q, dk, dv, D, threads, turbo=tb_)
+        best = min(dt_o, dt_t)
         result["cpu_baseline"] = {
-            "value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_layer": round(dt * 1e6 * B, 1),
-            "sample": f"oracle dequant+SDPA formulation (fp64 softmax{', numpy' if turbo else ', OpenMP over (b, q head)'}) "
-                      f"on batch row 0 of 1 layer of {args.config}, {reps} reps; us_per_layer scaled x{B} to the "
-                      f"full batch",
+            "value": round(nbytes / best / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_layer": round(best * 1e6, 1),
+            "sample": f"the whole batch (B={B}) of one layer of {args.config}, the faster of two host "
+                      f"formulations; each warmed for 10 calls or 5 s, then timed over 100 calls or 20 s, "
+                      f"whichever ends first",
+            "cpu_model": cpu_model, "nproc": nproc,
+            "formulations": {
+                "oracle_c": {"us_per_layer": round(dt_o * 1e6, 1), "calls": reps_o,
+                             "what": "C oracle dequant + concat + SDPA, fp64 softmax, " +
+                                     ("numpy" if turbo else f"OpenMP over (b, q head), {threads} threads")},
+                "torch_cpu": {"us_per_layer": round(dt_t * 1e6, 1), "calls": reps_t,
+                              "what": f"torch dequant -> cat -> repeat_interleave -> SDPA (fp32), "
+                                      f"{threads} threads"}},
         }
     if args.copy_mib:
         result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)
@@ -503,6 +602,192 @@ def run_e2e(args, torch, dev):
                                             "spike_readback_drain_and_flush": round(hres["host_drain_us"], 2)},
                        "same_promotions": hres["stats"] == gres["stats"]
                        and hres["near_valid_end"] == gres["near_valid_end"]},
+    }
+    print(json.dumps(result), flush=True)
+
+
+def time_graph(torch, dev, fns, steps, warmup):
+    """Capture one call of every function in ``fns`` in a HIP graph, settle
+    the clocks, replay ``warmup`` times, then time ``steps`` replays with HIP
+    events on the replay stream.  -> ms per replay."""
+    for fn in fns:  # eager first call (workspaces, library handles) outside capture
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for fn in fns:
+                fn()
+    torch.cuda.synchronize()
+    settle_clocks(torch, stream, graph.replay)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def run_crossover(args, torch, dev):
+    """Kernel crossover (benchmark_crossover.py:45-82 of the reference, on
+    one GPU): one decode attention call at 7B shapes (Hq=32, Hkv=8, D=128),
+    exact fp16 attention over all S tokens against the fused kernel over the
+    compressed tiers of the same tokens (10 % near fp16, 90 % far fp8 K +
+    INT4 V).  Each side runs over distinct per-layer copies (>= 1 GiB in
+    total, at most 256 layers) captured in one HIP graph, so neither reads a
+    warm cache; the time is per layer.  Exact attention is timed three ways
+    and the fastest counts: torch SDPA with native GQA (``enable_gqa``), the
+    reference's formulation (``repeat_interleave`` + SDPA), and an explicit
+    fp16 GEMM formulation (K q^T, fp32 softmax, P V; no copies of K or V).
+    SDPA is limited to its fused (flash / memory-efficient) backends."""
+    import torch.nn.functional as Fn
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from foveated_kv_amd import ext
+
+    # SDPA's fused backends only: its math fallback runs batched products on
+    # transposed views, which the explicit GEMM formulation below avoids
+    fused_backends = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+    Hq, Hkv, D = 32, 8, 128
+    cap_layers, min_bytes = 256, 1 << 30
+    g = torch.Generator(device=dev)
+    rows = []
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = 8
+    for B in args.cross_batches:
+        for S in args.cross_contexts:
+            g.manual_seed(args.seed + S + B)
+            kv_bytes = 2 * B * Hkv * S * D * 2
+            n_exact = max(1, min(cap_layers, -(-min_bytes // kv_bytes)))
+            q = torch.randn((B, Hq, 1, D), generator=g, device=dev, dtype=torch.float32).half()
+            kvs = [(torch.randn((B, Hkv, S, D), generator=g, device=dev, dtype=torch.float32).half(),
+                    torch.randn((B, Hkv, S, D), generator=g, device=dev, dtype=torch.float32).half())
+                   for _ in range(n_exact)]
+            outs = torch.empty((B, Hq, 1, D), dtype=torch.float16, device=dev)
+            qg = q.view(B, Hkv, Hq // Hkv, D).transpose(2, 3).contiguous()  # (B,Hkv,D,G)
+            scale = D ** -0.5
+
+            def sdpa_gqa(k, v):
+                with sdpa_kernel(fused_backends):
+                    outs.copy_(Fn.scaled_dot_product_attention(q, k, v, scale=scale, enable_gqa=True))
+
+            def sdpa_ref(k, v):
+                kk = k.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+                vv = v.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+                with sdpa_kernel(fused_backends):
+                    outs.copy_(Fn.scaled_dot_product_attention(q, kk, vv, scale=scale))
+
+            def gemm(k, v):
+                sc = torch.matmul(k, qg).float() * scale                # (B,Hkv,S,G)
+                p = torch.softmax(sc, dim=2).half().transpose(2, 3).contiguous()  # (B,Hkv,G,S)
+                outs.copy_(torch.matmul(p, v).reshape(B, Hq, 1, D))
+
+            exact = {}
+            for name, fn in (("sdpa_gqa", sdpa_gqa), ("sdpa_repeat_interleave", sdpa_ref), ("fp16_gemm", gemm)):
+                try:
+                    ms = time_graph(torch, dev, [lambda kv=kv, fn=fn: fn(*kv) for kv in kvs], args.steps,
+                                    args.warmup)
+                    exact[name] = round(ms * 1e3 / n_exact, 3)
+                except RuntimeError as e:  # a formulation torch cannot run here
+                    exact[name] = f"unavailable: {str(e).splitlines()[0][:120]}"
+                torch.cuda.synchronize()
+            # fused: compress the first copy's tokens, replicate the blob per layer
+            k0, v0 = kvs[0]
+            cl = ext.CompressHandle(cfg).compress_layer(k0, v0, with_archive=False)
+            del kvs
+            torch.cuda.synchronize()
+            handles, blob = [], 0
+            while True:
+                h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                                       cl.near_valid, spike_margin=10.0)
+                handles.append(h)
+                blob += h.get_blob_info().blob_bytes
+                if blob >= min_bytes or len(handles) >= cap_layers:
+                    break
+            res = [(torch.empty((B, Hq, 1, D), dtype=torch.float16, device=dev),
+                    torch.empty((B, Hq), dtype=torch.int32, device=dev),
+                    torch.empty((B, Hq), dtype=torch.int32, device=dev)) for _ in handles]
+            ms = time_graph(torch, dev, [lambda h=h, r=r: h(q, out=r) for h, r in zip(handles, res)], args.steps,
+                            args.warmup)
+            fused_us = ms * 1e3 / len(handles)
+            best = min(v for v in exact.values() if isinstance(v, float))
+            row = {"B": B, "context": S, "exact_us": exact, "exact_best_us": best, "fused_us": round(fused_us, 3),
+                   "speedup": round(best / fused_us, 3), "exact_layers": n_exact, "fused_layers": len(handles)}
+            rows.append(row)
+            print(f"[crossover] B={B} S={S}: exact {exact} fused {fused_us:.2f} us -> {best / fused_us:.2f}x",
+                  file=sys.stderr, flush=True)
+            del handles, res, cl
+            torch.cuda.empty_cache()
+    result = {
+        "metric": "kernel crossover: fused two-tier attention vs exact fp16 attention, us/layer, 7B shapes, 1 GPU",
+        "value": None, "unit": "us/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 operands, f32 accumulation", "data": "synthetic (seeded N(0,1) K, V, q)",
+        "config": {"workload": "crossover_7b", "Hq": Hq, "Hkv": Hkv, "D": D, "near_pct": 0.10,
+                   "far_format": "fp8-e4m3 K + int4 per-token V", "launch": "hip-graph, distinct layer copies"},
+        "rows": rows,
+    }
+    print(json.dumps(result), flush=True)
+
+
+def run_generate(args, torch, dev):
+    """The closure's host overhead against one HIP graph per model decode
+    step: a seeded tiny LM (fp32 weights, --gen-layers layers of Hq=32,
+    Hkv=8, D=128 attention, model dim 1024) prefills a --gen-context byte
+    prompt, compresses, and decodes --gen-tokens greedy tokens through
+    ``generate_fused`` three ways: the eager closure with the reference's
+    host drain, the eager closure with the device drain, and the graph.
+    Prints one JSON line: graph tokens/s as the value, host us per layer of
+    each way (time spent issuing drain + model call, or the replay), and
+    whether every way generated the same tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from _tiny_lm import ByteTokenizer, TinyLM
+
+    from foveated_kv_amd import generate as gen
+
+    L, n_tok, S = args.gen_layers, args.gen_tokens, args.gen_context
+    model = TinyLM(vocab=256, dim=1024, n_layers=L, n_heads=32, n_kv_heads=8, head_dim=128, qk_gain=2.0,
+                   seed=args.seed).to(dev).eval()
+    tok = ByteTokenizer(vocab=256)
+    rng = np.random.default_rng(args.seed)
+    prompt = bytes(rng.integers(32, 127, size=S, dtype=np.uint8)).decode()
+    print(f"[generate] tiny LM layers={L} Hq=32 Hkv=8 D=128 dim=1024 prompt={S} tokens={n_tok}",
+          file=sys.stderr, flush=True)
+    gen.generate_fused(model, tok, prompt[:256], max_tokens=4, enable_promotion=True, graph=True)  # warm
+    torch.cuda.synchronize()
+    runs = {}
+    for name, kw in (("eager_host_drain", {}), ("eager_device_drain", {"device_drain": True}),
+                     ("graph", {"graph": True})):
+        text, st = gen.generate_fused(model, tok, prompt, max_tokens=n_tok, enable_promotion=True, **kw)
+        runs[name] = (text, st)
+        print(f"[generate] {name}: {st['tokens_per_second']:.1f} tok/s, host {st['host_us_per_layer']:.1f} "
+              f"us/layer, promotions {st.get('promotions_completed')}", file=sys.stderr, flush=True)
+    g = runs["graph"][1]
+    keys = ("spikes_detected", "spikes_queued", "promotions_completed")
+    result = {
+        "metric": "tiny-LM greedy decode through the fused kernel, tokens/s (one HIP graph per decode step)",
+        "value": round(g["tokens_per_second"], 2), "unit": "tokens/s", "n_gpus": 1, "steps": g["model_calls"],
+        "warmup": 2, "ms_per_step": round(g["decode_time_s"] / max(g["model_calls"], 1) * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 model, f16 attention operands", "data": "synthetic (seeded random weights and prompt)",
+        "config": {"workload": "tiny_lm_generate", "layers": L, "Hq": 32, "Hkv": 8, "D": 128, "dim": 1024,
+                   "prompt_tokens": S, "max_tokens": n_tok, "promotion": True, "qk_gain": 2.0},
+        "ways": {n: {"tokens_per_second": round(st["tokens_per_second"], 2),
+                     "host_us_per_layer": round(st["host_us_per_layer"], 2),
+                     "closure_us_per_layer": (None if st["closure_us_per_layer"] is None
+                                              else round(st["closure_us_per_layer"], 2)),
+                     "decode_ms_per_token": round(st["decode_time_s"] / max(st["model_calls"], 1) * 1e3, 4),
+                     **{k: st.get(k) for k in keys}} for n, (_, st) in runs.items()},
+        "same_tokens": len({text for text, _ in runs.values()}) == 1,
+        "same_promotions": len({tuple(st.get(k) for k in keys) for _, st in runs.values()}) == 1,
     }
     print(json.dumps(result), flush=True)
 

@@ -254,13 +254,16 @@ class FoveatedHandle:
             self._lib.fkv_attn_destroy(h)
             self._h = None
 
-    def __call__(self, query, decode_k=None, decode_v=None, n_decode=None):
+    def __call__(self, query, decode_k=None, decode_v=None, n_decode=None, out=None):
         """-> [out (B,Hq,1,D) fp16, spike_flags (B,Hq) int32, spike_tokens (B,Hq) int32]
 
         n_decode (optional): a one-element int32 device tensor holding how many
         rows of decode_k/decode_v (then a fixed-capacity buffer) are valid.
         The kernel reads it on the device, so a decode step can be captured
-        in a HIP graph once and replayed while the buffer fills."""
+        in a HIP graph once and replayed while the buffer fills.
+        out (optional): the three result tensors to write, preallocated with
+        the shapes and dtypes above (contiguous); the call then allocates
+        nothing for its results and returns them."""
         _require_device(query, decode_k, decode_v, n_decode)
         if query.dim() == 4:
             if query.shape[2] != 1:
@@ -292,9 +295,16 @@ class FoveatedHandle:
                 raise TypeError("n_decode must be a one-element int32 device tensor")
             if dk is None:
                 raise ValueError("a device n_decode needs a decode buffer of nonzero capacity")
-        out = torch.empty((B, Hq, 1, D), dtype=torch.float16, device=self.device)
-        flags = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
-        tokens = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
+        if out is None:
+            out = torch.empty((B, Hq, 1, D), dtype=torch.float16, device=self.device)
+            flags = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
+            tokens = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
+        else:
+            out, flags, tokens = out
+            for t, shape, dt in ((out, (B, Hq, 1, D), torch.float16), (flags, (B, Hq), torch.int32),
+                                 (tokens, (B, Hq), torch.int32)):
+                if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous() or t.device != self.device:
+                    raise ValueError(f"out tensors must be contiguous {shape} {dt} on {self.device}")
         with torch.cuda.device(self.device):
             if row_stride:
                 check(self._lib.fkv_attn_call_strided(self._h, ptr(q), dtype_code(q.dtype), Hq, ptr(dk), ptr(dv),

@@ -28,6 +28,16 @@ through ``drain_spikes``, each layer's decode launch is ordered after that
 layer's promotion copies (``PromotionPipeline.order``), because here the
 copies are asynchronous device work rather than CPU stores into unified
 memory.
+
+Extension: ``generate_fused(..., graph=True)`` keeps the decode-step state
+on the device (``_DeviceDecode``) and captures one whole model decode step
+-- every layer's projections, RoPE, decode-buffer write, fused attention
+(``fkv_attn_call_dev``: the decode count is read on the device), the device
+spike drain of the previous step, and the greedy next token -- in a single
+HIP graph that is replayed once per token.  The host then issues one launch
+per token instead of the closure's per-layer Python and library calls.  The
+model must accept a device tensor as ``cache.offset`` (its RoPE positions
+computed as ``offset + arange(L)``).
 """
 
 import math
@@ -99,6 +109,8 @@ class _FusedSDPAState:
         self._fused_wrappers = None
         self._fused_disabled = False
         self._promotion = None  # pipeline whose flushed copies decode launches wait for
+        self._dev = None  # _DeviceDecode while a device-count decode runs
+        self._closure_s = 0.0  # host seconds spent in decode calls of the closure
 
 
 _fused_state = _FusedSDPAState()
@@ -117,12 +129,16 @@ class FusedCacheWrapper:
         self._spike_flags = None
         self._spike_tokens = None
         self._far_idx_host = None
+        self._dev = None  # _DeviceDecode: offset is then a device tensor
 
     @property
     def state(self):
         return self.fov_layer.near_k, self.fov_layer.near_v
 
     def update_and_fetch(self, keys, values):
+        if self._dev is not None:  # row t of the fixed-capacity buffer, t on the device
+            self.fov_layer.add_token_at(keys, values, self._dev.idx)
+            return keys, values
         self.fov_layer.add_token(keys, values)
         self.offset += keys.shape[2]
         return keys, values
@@ -164,10 +180,15 @@ def _build_fused_interceptor(state: _FusedSDPAState):
             return original(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
                             is_causal=is_causal, scale=scale, **kwargs)
 
-        promo = state._promotion
-        if promo is not None:
-            promo.order(idx)
-        out, flags, tokens = layer.attend_fused_with_spikes(query)
+        t0 = time.perf_counter()
+        dev = state._dev
+        if dev is not None:
+            out, flags, tokens = layer.attend_fused_dev(query, dev.n, dev.results(idx, query))
+        else:
+            promo = state._promotion
+            if promo is not None:
+                promo.order(idx)
+            out, flags, tokens = layer.attend_fused_with_spikes(query)
 
         wrappers = state._fused_wrappers
         if wrappers is not None and idx < len(wrappers):
@@ -178,6 +199,7 @@ def _build_fused_interceptor(state: _FusedSDPAState):
 
         if out.dtype != query.dtype:
             out = out.to(query.dtype)
+        state._closure_s += time.perf_counter() - t0
         return out
 
     return interceptor
@@ -284,6 +306,79 @@ def reset_fused_layer_counter() -> None:
 
 
 # ---------------------------------------------------------------------------
+# device-count decode (one HIP graph per model decode step)
+# ---------------------------------------------------------------------------
+
+class _DeviceDecode:
+    """Decode-step state held in device memory, so that a model decode step
+    reads no host value that changes from step to step and can be captured
+    once in a HIP graph: the step t (int32; the device drain's step), the
+    decode count t + 1 (int32; read by the attention kernel), the decode
+    buffer row t (int64), each layer's RoPE offset prompt_len + t (int64,
+    0-d, handed to the model as ``cache.offset``), and per-layer result
+    tensors the kernel writes, so the next step's drain reads fixed
+    addresses.  ``refresh`` derives everything from t at the start of a
+    step; the step advances t at its end."""
+
+    def __init__(self, wrappers, capacity: int, device):
+        self.wrappers = wrappers
+        self.t = torch.zeros(1, dtype=torch.int32, device=device)
+        self.n = torch.ones(1, dtype=torch.int32, device=device)
+        self.idx = torch.zeros(1, dtype=torch.int64, device=device)
+        self._pos = {}
+        self._base = {}
+        self._out = {}
+        for w in wrappers:
+            if w is None:
+                continue
+            base = int(w.offset)
+            self._base[w.layer_idx] = base
+            if base not in self._pos:
+                self._pos[base] = torch.full((), base, dtype=torch.int64, device=device)
+            w.fov_layer.reserve_decode(capacity)
+            w.offset = self._pos[base]
+            w._dev = self
+
+    def results(self, layer_idx: int, query):
+        """The layer's (out, flags, tokens) tensors, made at its first call
+        (outside any capture)."""
+        r = self._out.get(layer_idx)
+        if r is None:
+            B, Hq, _, D = query.shape
+            r = (torch.zeros((B, Hq, 1, D), dtype=torch.float16, device=query.device),
+                 torch.zeros((B, Hq), dtype=torch.int32, device=query.device),
+                 torch.zeros((B, Hq), dtype=torch.int32, device=query.device))
+            self._out[layer_idx] = r
+        return r
+
+    def refresh(self) -> None:
+        torch.add(self.t, 1, out=self.n)
+        self.idx.copy_(self.t)
+        for base, p in self._pos.items():
+            torch.add(self.idx[0], base, out=p)
+
+    def drain(self, pipeline) -> None:
+        """The device drain of the previous step's spikes, every layer with
+        results, at step t (as ``_drain_into`` with ``device_drain``)."""
+        for w in self.wrappers:
+            if w is None or w.layer_idx not in self._out:
+                continue
+            _, flags, tokens = self._out[w.layer_idx]
+            pipeline.drain_spikes_device(w.layer_idx, flags, tokens, w.far_idx_device(), self.t)
+
+    def close(self, steps: int) -> None:
+        """Back to host-count decode after ``steps`` model calls: offsets and
+        decode-buffer counts become host ints again."""
+        for w in self.wrappers:
+            if w is None:
+                continue
+            w._dev = None
+            w.offset = self._base[w.layer_idx] + steps
+            w.fov_layer._decode.n = steps
+            w.fov_layer._next_pos += steps
+
+
+# ---------------------------------------------------------------------------
 # generation
 # ---------------------------------------------------------------------------
 
@@ -316,14 +411,22 @@ def _next_token(logits, temp):
 
 def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
                    cfg: Optional[MLXTierConfig] = None, disk_archive_dir: Optional[str] = None,
-                   temp: float = 0.0, enable_promotion: bool = True, device_drain: bool = False):
+                   temp: float = 0.0, enable_promotion: bool = True, device_drain: bool = False,
+                   graph: bool = False):
     """mlx_generate.py:266-387: prefill, compress, move archives to disk,
     register them and the handles with a ``PromotionPipeline``, then decode
     with the closure installed.  Returns (text, stats).  ``device_drain``
     (extension): drain and promote on the GPU after each step instead of
-    reading the spike outputs back (same promotions)."""
+    reading the spike outputs back (same promotions).  ``graph``
+    (extension, greedy only, implies ``device_drain``): capture one whole
+    model decode step in a HIP graph and replay it per token (same tokens
+    and promotions as the eager loop).  ``stats["host_us_per_layer"]`` is
+    the host time spent issuing the decode steps (drain + model call, or the
+    graph replay) per model call and layer."""
     from .disk_archive import offload_cache_to_disk
 
+    if graph and temp != 0:
+        raise ValueError("graph decode is greedy: it needs temp=0")
     dev = _model_device(model)
     tokens = torch.tensor(tokenizer.encode(prompt), dtype=torch.long, device=dev).reshape(1, -1)
 
@@ -341,7 +444,7 @@ def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
     pipeline = None
     if enable_promotion:
         pipeline = PromotionPipeline(len(fov_cache.layers))
-        pipeline.device_drain = bool(device_drain)
+        pipeline.device_drain = bool(device_drain or graph)
         for i, layer in enumerate(fov_cache.layers):
             if layer is None:
                 continue
@@ -354,26 +457,40 @@ def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
                 pipeline.register_archive(i, a.path_k, a.path_v, a.H_kv, a.S_arc, a.D, a.idx)
 
     wrappers = install_fused_attention(model, fov_cache)
+    eos = getattr(tokenizer, "eos_token_id", None)
     generated = []
     next_logits = prefill_logits[:, -1, :]
+    torch.cuda.synchronize(dev)
     t_dec = time.perf_counter()
+    t_issue = 0.0
+    calls = 0
+    _fused_state._closure_s = 0.0
     try:
         with torch.no_grad():
-            for step in range(max_tokens):
-                tok = _next_token(next_logits, temp)
-                token_id = int(tok.item())
-                if token_id == getattr(tokenizer, "eos_token_id", None):
-                    break
-                generated.append(token_id)
-                drain_spikes(wrappers, pipeline, step)
-                next_logits = model(tok.reshape(1, 1), cache=wrappers)[:, -1, :]
+            if graph:
+                generated, calls, t_issue = _decode_graph(model, wrappers, pipeline, next_logits, max_tokens,
+                                                          eos, dev)
+            else:
+                for step in range(max_tokens):
+                    tok = _next_token(next_logits, temp)
+                    token_id = int(tok.item())
+                    if token_id == eos:
+                        break
+                    generated.append(token_id)
+                    t0 = time.perf_counter()
+                    drain_spikes(wrappers, pipeline, step)
+                    next_logits = model(tok.reshape(1, 1), cache=wrappers)[:, -1, :]
+                    t_issue += time.perf_counter() - t0
+                    calls += 1
         torch.cuda.synchronize(dev)
     finally:
+        t_decode = time.perf_counter() - t_dec
+        closure_s = _fused_state._closure_s
         uninstall_fused_attention(model)
         if pipeline is not None:
             pipeline.stop()
         shutil.rmtree(disk_archive_dir, ignore_errors=True)
-    t_decode = time.perf_counter() - t_dec
+    n_fused = sum(1 for w in wrappers if w is not None)
 
     mb = 1024 * 1024
     stats = {
@@ -384,6 +501,12 @@ def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
         "prefill_time_s": t_prefill,
         "decode_time_s": t_decode,
         "tokens_per_second": len(generated) / max(t_decode, 1e-6),
+        "graph": bool(graph),
+        "model_calls": calls,
+        "host_us_per_layer": t_issue / max(calls * n_fused, 1) * 1e6,
+        # the closure's own share (layer lookup, library call, result
+        # tensors, spike stash); a replayed graph runs no closure
+        "closure_us_per_layer": None if graph else closure_s / max(calls * n_fused, 1) * 1e6,
         "mem_quantized_mb": mem_before["total_quantized"] / mb,
         "mem_archive_before_mb": mem_before["archive"] / mb,
         "mem_archive_after_mb": mem_after["archive"] / mb,
@@ -392,6 +515,68 @@ def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
     if pipeline is not None:
         stats.update(pipeline.get_stats())
     return tokenizer.decode(generated), stats
+
+
+def _decode_graph(model, wrappers, pipeline, next_logits, max_tokens, eos, dev, chunk=16):
+    """Greedy decode of up to ``max_tokens`` tokens with the step state on the
+    device.  Steps 0 and 1 run eagerly (they size every workspace and make
+    the drain's device tables, which must not happen under capture); step 2
+    is captured in one HIP graph and replayed for every later step.  Token
+    t + 1 = argmax of model call t is written into a device history; with an
+    EOS id the history is read every ``chunk`` steps and the tokens from the
+    first EOS on are dropped (the eager loop stops there), so the result is
+    the eager loop's.  -> (tokens, model calls, host issue seconds)."""
+    s = _fused_state
+    dd = _DeviceDecode(wrappers, max(max_tokens, 1), dev)
+    s._dev = dd
+    hist = torch.zeros(max_tokens + 1, dtype=torch.int64, device=dev)
+    hist[0:1].copy_(torch.argmax(next_logits, dim=-1))
+
+    def step():
+        s._layer_counter = 0
+        dd.refresh()
+        if pipeline is not None:
+            dd.drain(pipeline)
+        tok = hist.index_select(0, dd.idx).view(1, 1)
+        logits = model(tok, cache=wrappers)[:, -1, :]
+        hist.index_copy_(0, dd.idx + 1, torch.argmax(logits, dim=-1))
+        dd.t.add_(1)
+
+    calls, t_issue, n_tok = 0, 0.0, max_tokens
+    g = None
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(device=dev)  # the eager steps run here, as before any capture
+    try:
+        while calls < n_tok:
+            if eos is not None and calls % chunk == 0:
+                known = hist[: calls + 1].tolist()
+                if eos in known:
+                    n_tok = known.index(eos)
+                    break
+            if calls >= 2 and g is None:
+                main.wait_stream(side)
+                torch.cuda.synchronize(dev)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    step()
+            t0 = time.perf_counter()
+            if g is None:
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    step()
+                main.wait_stream(side)
+            else:
+                g.replay()
+            t_issue += time.perf_counter() - t0
+            calls += 1
+        known = hist[: min(calls, n_tok) + 1].tolist()
+    finally:
+        torch.cuda.synchronize(dev)
+        s._dev = None
+        dd.close(calls)
+    if eos is not None and eos in known:
+        n_tok = min(n_tok, known.index(eos))
+    return known[: min(n_tok, calls)], calls, t_issue
 
 
 def compute_perplexity(model, tokenizer, text: str, context_len: int = 4096, eval_len: int = 256,

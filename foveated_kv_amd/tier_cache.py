@@ -148,6 +148,20 @@ class _DecodeBuffer:
             return None, None
         return self.k[:, :, : self.n], self.v[:, :, : self.n]
 
+    def reserve(self, B, H, D, cap, device):
+        """Fixed-capacity mode: a zeroed (B,H,cap,D) buffer written by
+        ``write_at`` at device-held positions (the host count ``n`` is not
+        advanced; the owner sets it when it reads the rows on the host)."""
+        self.k = torch.zeros((B, H, cap, D), dtype=torch.float16, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.n = 0
+
+    def write_at(self, k, v, idx):
+        """Rows idx (int64 device tensor of length t) <- k, v (B,H,t,D); no
+        host synchronisation, so the write can be captured in a HIP graph."""
+        self.k.index_copy_(2, idx, k.to(torch.float16))
+        self.v.index_copy_(2, idx, v.to(torch.float16))
+
 
 @dataclass
 class FoveatedLayer:
@@ -278,6 +292,24 @@ class FoveatedLayer:
         """(out, spike_flags, spike_tokens); like the reference the margin
         argument is ignored -- the handle's margin (10.0) applies."""
         return tuple(self._dispatch_kernel(query))
+
+    # ---- device-count decode (graph-captured steps) ----
+    def reserve_decode(self, cap: int) -> None:
+        """Give the decode buffer a fixed capacity of ``cap`` rows, written at
+        device-held positions by ``add_token_at``."""
+        B, H, _, D = self.near_k.shape
+        self._decode.reserve(B, H, D, cap, self.near_k.device)
+
+    def add_token_at(self, new_k, new_v, idx) -> None:
+        self._decode.write_at(new_k, new_v, idx)
+
+    def attend_fused_dev(self, query, n_decode, out=None):
+        """The fused kernel over the whole fixed-capacity decode buffer, of
+        which the first ``n_decode`` rows (one-element int32 device tensor)
+        are valid; results into ``out`` when given."""
+        self._ensure_kcache()
+        return tuple(self._kcache["cpp_handle"](query, self._decode.k, self._decode.v, n_decode=n_decode,
+                                                out=out))
 
     # ---- python spike detection (mlx_foveated.py:451-499) ----
     def _query_to_kv_heads(self, query):

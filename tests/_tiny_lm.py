@@ -10,11 +10,13 @@ import torch.nn.functional as F
 
 
 def _rope(x, offset, base=10000.0):
-    """Rotary embedding on (B, H, L, D), positions offset .. offset+L-1."""
+    """Rotary embedding on (B, H, L, D), positions offset .. offset+L-1;
+    ``offset`` is an int or a 0-d integer device tensor (graph-captured
+    decode keeps it on the device)."""
     B, H, L, D = x.shape
     half = D // 2
     inv = base ** (-torch.arange(half, device=x.device, dtype=torch.float32) / half)
-    pos = torch.arange(offset, offset + L, device=x.device, dtype=torch.float32)
+    pos = torch.arange(L, device=x.device, dtype=torch.float32) + offset
     ang = pos[:, None] * inv[None, :]
     cos, sin = ang.cos().to(x.dtype), ang.sin().to(x.dtype)
     x1, x2 = x[..., :half], x[..., half:]

@@ -316,3 +316,94 @@ def test_generate_fused_promotes_spiking_far_tokens(closure, tmp_path):
     for key in ("spikes_detected", "spikes_queued", "spikes_deduplicated", "spikes_cooled_down",
                 "promotions_completed", "promotions_headroom_full"):
         assert stats_d[key] == stats[key], key
+
+
+class _EosTokenizer:
+    """ByteTokenizer with an end-of-sequence id."""
+
+    def __init__(self, base, eos):
+        self.base = base
+        self.eos_token_id = eos
+
+    def encode(self, text):
+        return self.base.encode(text)
+
+    def decode(self, ids):
+        return self.base.decode(ids)
+
+
+@pytest.mark.gpu
+def test_generate_graph_matches_eager_tokens_and_promotions(closure, tmp_path):
+    """One HIP graph per model decode step (device step state, device decode
+    count, device drain) generates the eager closure's tokens and promotes
+    the same rows; with an EOS id both stop at the same token."""
+    from _tiny_lm import ByteTokenizer, TinyLM
+
+    dev = torch.device("cuda:0")
+    model = TinyLM(seed=14, qk_gain=3.0).to(dev).eval()
+    tok = ByteTokenizer()
+    prompt = _prompt(700, 4)
+    print("case: generate_fused graph vs eager device drain, qk_gain 3, 24 tokens", flush=True)
+    text_e, st_e = gen.generate_fused(model, tok, prompt, max_tokens=24, disk_archive_dir=str(tmp_path / "a"),
+                                      device_drain=True)
+    text_g, st_g = gen.generate_fused(model, tok, prompt, max_tokens=24, disk_archive_dir=str(tmp_path / "b"),
+                                      graph=True)
+    assert st_g["graph"] and st_g["model_calls"] == st_e["model_calls"] == 24
+    assert text_g == text_e
+    assert st_e["promotions_completed"] > 0
+    for key in ("spikes_detected", "spikes_queued", "spikes_deduplicated", "spikes_cooled_down",
+                "promotions_completed", "promotions_headroom_full"):
+        assert st_g[key] == st_e[key], key
+    assert closure._fused_state._installed is False and closure._fused_state._dev is None
+    # an EOS id taken from the middle of the generated text: both loops stop there
+    ids = [int(x) for x in text_e.split()]
+    eos = ids[17]
+    want = ids[:ids.index(eos)]
+    print(f"case: graph vs eager with EOS id {eos} (first at {len(want)})", flush=True)
+    etok = _EosTokenizer(tok, eos)
+    text_e2, st_e2 = gen.generate_fused(model, etok, prompt, max_tokens=24, enable_promotion=True,
+                                        device_drain=True)
+    text_g2, st_g2 = gen.generate_fused(model, etok, prompt, max_tokens=24, enable_promotion=True, graph=True)
+    assert text_e2 == text_g2 == tok.decode(want)
+    assert st_g2["generated_tokens"] == len(want)
+
+
+@pytest.mark.gpu
+def test_graph_decode_leaves_host_state_consistent(closure):
+    """After a graph decode the caches hold the steps on the host again: the
+    decode buffers' row counts and the wrappers' offsets advance by the
+    model calls made, and the buffered rows are the ones eager decode
+    appends."""
+    from _tiny_lm import ByteTokenizer, TinyLM
+
+    dev = torch.device("cuda:0")
+    model = TinyLM(seed=15).to(dev).eval()
+    tok = ByteTokenizer()
+    ids = torch.tensor(tok.encode(_prompt(400, 5)), device=dev).reshape(1, -1)
+    print("case: graph decode host state, 6 steps", flush=True)
+    caches = []
+    for graph in (False, True):
+        fov_cache, logits, _ = gen.prefill_and_compress(model, ids)
+        wrappers = closure.install_fused_attention(model, fov_cache)
+        nxt = logits[:, -1, :]
+        with torch.no_grad():
+            if graph:
+                toks, calls, _ = gen._decode_graph(model, wrappers, None, nxt, 6, None, dev)
+                assert calls == 6
+            else:
+                toks = []
+                for step in range(6):
+                    t = torch.argmax(nxt, dim=-1)
+                    toks.append(int(t))
+                    closure.drain_spikes(wrappers, None, step)
+                    nxt = model(t.reshape(1, 1), cache=wrappers)[:, -1, :]
+        torch.cuda.synchronize()
+        closure.uninstall_fused_attention(model)
+        caches.append((toks, [(w.offset, w.fov_layer.decode_k.clone(), w.fov_layer.decode_v.clone())
+                              for w in wrappers]))
+    (te, ce), (tg, cg) = caches
+    assert te == tg
+    for (oe, ke, ve), (og, kg, vg) in zip(ce, cg):
+        assert oe == og == 400 + 6
+        assert ke.shape == kg.shape and ke.shape[2] == 6
+        assert torch.equal(ke, kg) and torch.equal(ve, vg)
