@@ -288,8 +288,7 @@ struct AttnArgs {
     int dec_wave0;  // the wave that takes decode tile 0
     int wave_recs;  // split records per split: 4 (one per wave) or 1 (merged in LDS)
     // TurboQuant far tier (fmt 1)
-    const float* tq_PiT;    // (D, D) fp32, PiT[j][i] = Pi[i][j]
-    const float* tq_ST;     // (D, D) fp32, ST[j][i] = S[i][j]
+    const uint16_t* tq_rot; // Pi, S as rotation MFMA operands (tq_rot_index)
     float tq_alpha;         // centroid constant term (0 for a symmetric codebook)
     float tq_beta, tq_gamma, tq_delta;  // centroid coefficients (TurboConsts)
     float tq_qjl;           // 1.2533141 / D
@@ -412,6 +411,12 @@ typedef uint32_t fkv_v4u __attribute__((ext_vector_type(4)));
 #define FKV_LDS __attribute__((address_space(3)))
 // constant memory: read-only for the duration of a launch (scalar loads)
 #define FKV_CONST __attribute__((address_space(4)))
+
+// Workgroup barrier for LDS traffic only: waits for the wave's own LDS
+// operations, not for its vector-memory loads (a __syncthreads would also
+// drain LDS-DMA transfers still in flight).  One asm block, so no memory
+// access moves across it.
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // 32-bit LDS address of a pointer into a __shared__ array.
 __device__ inline uint32_t lds_addr(const void* p) {
@@ -1743,73 +1748,79 @@ __host__ __device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int 
 }
 
 // TurboQuant query rotation and sketch inside the attention kernel:
-// q.Pi^T and q.S^T (foveated_attn.cpp:415-421) for the workgroup's heads, in
-// fp32 from the fp16 query, rounded to fp16 into the qt operand layout.
-// Thread = (matrix, 4-column block cb, j-slice js of D/4 rows); the matrix rows are read once per workgroup
-// (coalesced float4 per thread), the slices' partial sums meet in `part`
-// (a free ring slot, 4 * 4 * D * 2 floats); the quad's fp32 q.Pi^T then
-// replaces its query in `qf` and alpha * sum(q.Pi^T) per head goes to
-// `rsum`.  Must be entered by every thread of the workgroup.
-template <int D, int NQ>
-__device__ inline void tq_rotate_query(const AttnArgs& a, float* qf, uint16_t* qt, float* part, float* rsum) {
-    constexpr int NS = D / 4, CB = D / 4, SL = 4, JL = D / SL, TPM = CB * SL;
-    const int t = threadIdx.x;
-    const bool active = t < 2 * TPM;
-    const int mat = t / TPM, cb = t % CB, js = (t % TPM) / CB;
-    const float* M = mat ? a.tq_ST : a.tq_PiT;
-    float4 m[JL];
-    if (active) {
+// q.Pi^T and q.S^T (foveated_attn.cpp:415-421) for the workgroup's heads on
+// the matrix cores.  Wave w < D/32 takes matrix mat and the 64 output dims
+// 64 * rg .. + 63 (lane l: output dim 64 * rg + l as the A row of
+// v_mfma_f32_4x4x4f16, the head quad's fp16 query as B); M = hi + lo / 1024
+// (tq_rot_index), two accumulator chains over the D/4 k-steps.  The
+// products of fp16 values are exact and summed in fp32.  Lane l ends with
+// dims 64 * rg + 4 * (l / 4) .. + 3 of head l % 4, rounded to fp16 into the
+// qt operand layout; mat 0 also leaves q.Pi^T in fp32 in `qf` and alpha *
+// sum(q.Pi^T) per head in `rsum`.  Waves past D/32 repeat a part whose
+// results they do not write.  Must be entered by every thread of the
+// workgroup.
+template <int D>
+struct TqRotation {
+    fkv_v4u hl[2][D / 8];  // [hi, lo][s2]: k-steps 2 * s2, 2 * s2 + 1 of the lane's row
+};
+
+// The wave's A operands, loaded together with the query (before any use).
+template <int D>
+__device__ inline void tq_rotation_load(const AttnArgs& a, TqRotation<D>& r, int wave, int lane) {
+    constexpr int WR = D / 32, RG = D / 64;
+    const int wr = wave % WR, mat = wr / RG, rg = wr % RG;
 #pragma unroll
-        for (int jj = 0; jj < JL; jj++) m[jj] = *(const float4*)(M + (js * JL + jj) * D + 4 * cb);
-    }
+    for (int part = 0; part < 2; part++)
+#pragma unroll
+        for (int s2 = 0; s2 < D / 8; s2++)
+            r.hl[part][s2] = *(const fkv_v4u*)(a.tq_rot + tq_rot_index(D, mat, part, 64 * rg + lane, 8 * s2));
+}
+
+template <int D, int NQ>
+__device__ inline void tq_rotate_query(const AttnArgs& a, const TqRotation<D>& rot, const QOperand<D / 4>& qop,
+                                       float* qf, uint16_t* qt, float* rsum, int wave, int lane) {
+    constexpr int NS = D / 4, WR = D / 32, RG = D / 64;
+    const int wr = wave % WR, mat = wr / RG, rg = wr % RG;
+    const int c = lane & 3, blk = lane >> 2;
 #pragma unroll 1
     for (int qd = 0; qd < NQ; qd++) {
-        if (active) {
-            float acc[4][4];
+        fkv_f4 ch = fkv_f4{0.f, 0.f, 0.f, 0.f}, cl = fkv_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int h = 0; h < 4; h++)
+        for (int s0 = 0; s0 < NS; s0 += 8) {
+            fkv_h4 q8[8];
+            qop.template readn<8>(qd, s0, q8);
 #pragma unroll
-                for (int c = 0; c < 4; c++) acc[h][c] = 0.f;
-#pragma unroll
-            for (int jj = 0; jj < JL; jj++) {
-                const int jx = js * JL + jj;
-#pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    const float x = qf[(4 * qd + h) * D + jx];
-                    acc[h][0] = fmaf(x, m[jj].x, acc[h][0]);
-                    acc[h][1] = fmaf(x, m[jj].y, acc[h][1]);
-                    acc[h][2] = fmaf(x, m[jj].z, acc[h][2]);
-                    acc[h][3] = fmaf(x, m[jj].w, acc[h][3]);
-                }
+            for (int s = s0; s < s0 + 8; s++) {
+                const fkv_v4u& h = rot.hl[0][s / 2];
+                const fkv_v4u& l = rot.hl[1][s / 2];
+                const fkv_h4 ah = __builtin_bit_cast(fkv_h4, (s & 1) ? fkv_v2u{h.z, h.w} : fkv_v2u{h.x, h.y});
+                const fkv_h4 al = __builtin_bit_cast(fkv_h4, (s & 1) ? fkv_v2u{l.z, l.w} : fkv_v2u{l.x, l.y});
+                ch = mfma4_local(ah, q8[s - s0], ch);
+                cl = mfma4_local(al, q8[s - s0], cl);
             }
-#pragma unroll
-            for (int h = 0; h < 4; h++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) part[((js * 2 + mat) * 4 + h) * D + 4 * cb + c] = acc[h][c];
         }
-        __syncthreads();
-        for (int o = t; o < 2 * 4 * D; o += blockDim.x) {
-            const int mo = o / (4 * D), h = (o / D) % 4, col = o % D;
-            float v = 0.f;
+        if (wave < WR) {
+            float v[4];
 #pragma unroll
-            for (int k = 0; k < SL; k++) v += part[((k * 2 + mo) * 4 + h) * D + col];
-            const int idx = ((qd * NS + col / 4) * 4 + h) * 4 + col % 4;
-            qt[mo * NQ * NS * 16 + idx] = f2h(v);
-            if (mo == 0) qf[(4 * qd + h) * D + col] = v;  // q.Pi^T in fp32 (the quad's q is consumed)
+            for (int e = 0; e < 4; e++) v[e] = fmaf(cl[e], 1.f / 1024.f, ch[e]);
+            const int sq = 16 * rg + blk;  // k-step of output dims 4 * sq .. 4 * sq + 3
+            const uint32_t w0 = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+            const uint32_t w1 = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+            *(fkv_v2u*)(qt + mat * NQ * NS * 16 + ((qd * NS + sq) * 4 + c) * 4) = fkv_v2u{w0, w1};
+            if (mat == 0) *(float4*)(qf + (4 * qd + c) * D + 4 * sq) = float4{v[0], v[1], v[2], v[3]};
         }
         if (a.tq_alpha != 0.f) {
-            __syncthreads();
+            lds_barrier();
             // wave w sums head w's rotated query
-            const int w = t / kWave, ln = t % kWave;
-            if (w < 4) {
+            if (wave < 4) {
                 float v = 0.f;
-                for (int col = ln; col < D; col += kWave) v += qf[(4 * qd + w) * D + col];
+                for (int col = lane; col < D; col += kWave) v += qf[(4 * qd + wave) * D + col];
                 v = wave_sum(v);
-                if (ln == 0) rsum[4 * qd + w] = a.tq_alpha * v;
+                if (lane == 0) rsum[4 * qd + wave] = a.tq_alpha * v;
             }
         }
-        __syncthreads();
     }
+    lds_barrier();
 }
 
 // One workgroup of 4 waves per (batch, kv head, split, head group); each
@@ -1902,7 +1913,26 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     // the wave's first two far tiles need no device state either
     if (un.nf > 0) issue(0);
-    const bool early1 = !TQ && un.nf > 1;  // TurboQuant uses slot 1 of wave 0 until the stream starts
+    // TurboQuant: the rotation matrices' slices and the query are loaded
+    // together, right after the first tile's DMA, so their latencies overlap
+    // (a wait for any of them also waits for the older DMA)
+    TqRotation<D> rot;
+    uint16_t tq_q[TQ ? (NQ * NS * 16 + 255) / 256 : 1];
+    if constexpr (TQ) {
+        tq_rotation_load<D>(a, rot, wave, lane);
+        // unconditional loads (heads past the group read head 0 and are
+        // zeroed when stored; indices past the arrays wrap)
+#pragma unroll
+        for (int k = 0; k < (NQ * NS * 16 + 255) / 256; k++) {
+            const int i = (threadIdx.x + 256 * k) % (NQ * NS * 16);
+            const int e = i & 3, jj = (i >> 2) & 3, sq = i >> 4;
+            const int s = sq % NS, h = 4 * (sq / NS) + jj;
+            tq_q[k] = a.q[((int64_t)b * a.Hq + head0 + (h < ng ? h : 0)) * D + 4 * s + e];
+        }
+    }
+    // (TurboQuant: the waits for the rotation operands would also wait for a
+    // second tile issued here)
+    const bool early1 = !TQ && un.nf > 1;
     if (early1) issue(1);
     // near_valid and a device decode count are written only by earlier
     // launches, so they are read as constant memory (scalar loads, whose
@@ -1913,19 +1943,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) asum[qd] = 0.f;
     if constexpr (TQ) {
-        for (int i = threadIdx.x; i < NQ * NS * 16; i += blockDim.x) {
-            const int e = i & 3, jj = (i >> 2) & 3, sq = i >> 4;
-            const int s = sq % NS, qd = sq / NS;
-            const int h = 4 * qd + jj;
-            qs[i] = h < ng ? a.q[((int64_t)b * a.Hq + head0 + h) * D + 4 * s + e] : (uint16_t)0;
+#pragma unroll
+        for (int k = 0; k < (NQ * NS * 16 + 255) / 256; k++) {
+            const int i = threadIdx.x + 256 * k, h = 4 * ((i >> 4) / NS) + ((i >> 2) & 3);
+            if (i < NQ * NS * 16) qs[i] = h < ng ? tq_q[k] : (uint16_t)0;
         }
-        for (int i = threadIdx.x; i < 4 * NQ * D; i += blockDim.x) {
-            const int h = i / D;
-            qf[i] = h < ng ? h2f(a.q[((int64_t)b * a.Hq + head0 + h) * D + i % D]) : 0.f;
-        }
-        __syncthreads();
-        // slot 1 of wave 0 is free until the stream starts
-        tq_rotate_query<D, NQ>(a, qf, qt, (float*)(lds + SLOT), rsum);
+        lds_barrier();
+        tq_rotate_query<D, NQ>(a, rot, QOperand<NS>{qs, j * 4}, qf, qt, rsum, wave, lane);
         if (a.tq_alpha != 0.f) {
 #pragma unroll
             for (int qd = 0; qd < NQ; qd++) asum[qd] = rsum[4 * qd + j];
@@ -1954,7 +1978,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const QOperand<NS> qop{qs, j * 4};
     const QOperand<NS> qrop{qt, j * 4}, qkop{qt + (TQ ? NQ * NS * 16 : 0), j * 4};
     if constexpr (TQ) {
-        __syncthreads();
+        lds_barrier();
     } else {
         // the query DMA is this wave's oldest vector-memory op: wait for it
         // but not for the ring, then for every wave's part of the query
@@ -2031,7 +2055,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
 
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
-    // Rows of 2..16 splits: every wave publishes its own record (record
+    // Rows of 2..4 splits: every wave publishes its own record (record
     // split * 4 + wave) straight from registers and the last workgroup merges
     // 4 records per split.  Otherwise the 4 waves merge their records in LDS
     // first (one record per split, or the outputs when a row is one split).
@@ -2339,8 +2363,10 @@ LaunchPlan plan_launch(const BlobLayout& L, int Hq, int n_decode, int target_wgs
     p.ng_max = G < hpg ? G : hpg;
     p.rows = L.B * L.Hkv * p.head_groups;
     p.splits = plan_splits(L, p.rows, n_decode, target_wgs);
-    // rows of 2..16 splits keep one record per wave (their merge reads at most 64)
-    p.wave_recs = p.splits > 1 && p.splits * kWavesPerGroup <= kMaxSplits ? kWavesPerGroup : 1;
+    // rows of 2..4 splits keep one record per wave (their merge reads at most
+    // 16); rows of more splits merge their 4 waves in LDS first (C4's 8
+    // splits: 32 wave records merged 0.4 us slower than 8 merged records)
+    p.wave_recs = p.splits > 1 && p.splits <= 4 ? kWavesPerGroup : 1;
     p.ws_floats = p.splits > 1 ? partial_floats(p.rows, p.splits * p.wave_recs, p.ng_max, L.D) : 0;
     return p;
 }
@@ -2660,8 +2686,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         }
     }
     const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
-    a.tq_PiT = h->tq.PiT;
-    a.tq_ST = h->tq.ST;
+    a.tq_rot = h->tq.rot;
     a.tq_alpha = h->tq.alpha;
     a.tq_beta = h->tq.beta;
     a.tq_gamma = h->tq.gamma;
@@ -2830,8 +2855,7 @@ void fkv_attn_destroy(fkv_attn* h) {
     if (h->ws) (void)hipFree(h->ws);
     if (h->qbuf) (void)hipFree(h->qbuf);
     if (h->arrive) (void)hipFree(h->arrive);
-    if (h->tq.PiT) (void)hipFree(h->tq.PiT);
-    if (h->tq.ST) (void)hipFree(h->tq.ST);
+    if (h->tq.rot) (void)hipFree(h->tq.rot);
     delete h;
 }
 

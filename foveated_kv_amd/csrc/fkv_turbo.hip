@@ -113,6 +113,20 @@ __global__ void tq_pack_sn_kernel(const void* __restrict__ vscale, const void* _
 }
 
 // out[j][i] = in[i][j] for a (D, D) fp32 matrix.
+// Pi and S -> the rotation MFMAs' fp16 hi / lo operands (tq_rot_index).
+__global__ void rot_operand_kernel(const float* __restrict__ Pi, const float* __restrict__ S,
+                                   uint16_t* __restrict__ rot, int D) {
+    const int64_t n = 2 * (int64_t)D * D;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int mat = (int)(e / ((int64_t)D * D)), i = (int)(e / D % D), j = (int)(e % D);
+        const float m = (mat ? S : Pi)[(int64_t)i * D + j];
+        const uint16_t hi = f2h(m);
+        rot[tq_rot_index(D, mat, 0, i, j)] = hi;
+        rot[tq_rot_index(D, mat, 1, i, j)] = f2h((m - h2f(hi)) * 1024.f);
+    }
+}
+
 __global__ void transpose_kernel(const float* __restrict__ in, float* __restrict__ out, int D) {
     const int64_t n = (int64_t)D * D;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
@@ -290,17 +304,13 @@ int fkv_turbo_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t 
     hipStream_t st = (hipStream_t)stream;
     fkv_attn* h = new fkv_attn();
     int rc = fkv::attn_begin(h, B, Hkv, D, Na, F, 1, near_k, near_v, near_dtype, near_valid, spike_margin, st);
-    const size_t mat = (size_t)D * D * sizeof(float);
-    if (!rc) rc = check_hip(hipMalloc(&h->tq.PiT, mat), "hipMalloc(PiT)");
-    if (!rc) rc = check_hip(hipMalloc(&h->tq.ST, mat), "hipMalloc(ST)");
+    if (!rc) rc = check_hip(hipMalloc(&h->tq.rot, (size_t)8 * D * D), "hipMalloc(rotation operands)");
     float cb[4] = {0.f, 0.f, 0.f, 0.f};
     if (!rc) {
         const int blk = 256;
         const fkv::BlobLayout L = h->L;
-        hipLaunchKernelGGL(fkv::transpose_kernel, dim3(fkv::grid_for((int64_t)D * D, blk)), dim3(blk), 0, st, Pi,
-                           h->tq.PiT, D);
-        hipLaunchKernelGGL(fkv::transpose_kernel, dim3(fkv::grid_for((int64_t)D * D, blk)), dim3(blk), 0, st, S,
-                           h->tq.ST, D);
+        hipLaunchKernelGGL(fkv::rot_operand_kernel, dim3(fkv::grid_for(2 * (int64_t)D * D, blk)), dim3(blk), 0, st,
+                           Pi, S, h->tq.rot, D);
         if (F > 0) {
             hipLaunchKernelGGL(fkv::tq_pack_k_kernel, dim3(fkv::grid_for((int64_t)B * Hkv * L.F_pad * (D / 32), blk)),
                                dim3(blk), 0, st, k_idx, k_signs, L, h->blob);
