@@ -158,7 +158,8 @@ int grid_for(int64_t n, int block);
 // and the split-partial floats it needs.
 struct LaunchPlan {
     int hpg, head_groups, ng_max, rows, splits;
-    int wave_recs;  // split records per split (4: one per wave, 1: merged in LDS)
+    int waves;      // waves per workgroup
+    int wave_recs;  // split records per split (waves: one per wave, 1: merged in LDS)
     size_t ws_floats;
 };
 LaunchPlan plan_launch(const BlobLayout& L, int Hq, int n_decode, int target_wgs);

@@ -263,6 +263,15 @@ constexpr int kSmallGrid = 64;  // fewer workgroups than this: rows of 4 query h
 constexpr int kHdr = 8;
 constexpr int kMaxSplits = 64;
 
+// Waves per workgroup of the attention kernel (one workgroup per CU): 8 for
+// TurboQuant rows of one head quad at D = 128 -- two waves per SIMD, whose
+// far tile is bound by dependent VALU / MFMA chains that the second wave
+// overlaps (8 KB ring units, registers within 256) while the query rotation
+// is still loaded and computed once per CU -- and 4 elsewhere.
+__host__ __device__ constexpr int attn_waves(int D, int NQ, int fmt) {
+    return fmt == 1 && D == 128 && NQ == 1 ? 8 : kWavesPerGroup;
+}
+
 struct AttnArgs {
     const uint8_t* blob;
     BlobLayout L;
@@ -566,14 +575,18 @@ __device__ inline void dma_far(const AttnArgs& a, int64_t bkv, int tile, int lan
 
 __device__ inline uint4 u4_of(fkv_v4u v) { return make_uint4(v.x, v.y, v.z, v.w); }
 
-// One half (K: 0 or V: 1) of a near-tier tile -> an LDS slot: D/8 1-KB
-// chunks (the tile layout is already chunk-major).
-template <int D>
-__device__ inline void dma_near(const AttnArgs& a, int64_t bkv, int tile, int half, int lane, uint8_t* slot) {
+// Part `part` of NP of one half (K: 0 or V: 1) of a near-tier tile -> an
+// LDS slot: D / (8 NP) 1-KB chunks (the tile layout is already
+// chunk-major: K chunk c = dims 8c..8c+7, V chunks of dim half dh are
+// 8dh..8dh+7).
+template <int D, int NP = 1>
+__device__ inline void dma_near(const AttnArgs& a, int64_t bkv, int tile, int half, int part, int lane,
+                                uint8_t* slot) {
+    constexpr int NC = D / 8 / NP;
     const uint8_t* src = a.blob + (half ? a.L.near_v : a.L.near_k) +
-                         (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D * 2;
+                         (bkv * a.L.Na_pad + (int64_t)tile * kTile) * D * 2 + part * NC * 1024;
 #pragma unroll
-    for (int c = 0; c < D / 8; c++)
+    for (int c = 0; c < NC; c++)
         __builtin_amdgcn_global_load_lds((const void*)(src + c * 1024 + lane * 16), (FKV_LDS void*)(slot + c * 1024), 16,
                                          0, 2);
 }
@@ -1418,19 +1431,24 @@ __device__ inline void lds_chunks(fkv_v4u (&o)[8], const uint8_t* p) {
 }
 
 // Scores of a near-tier tile whose keys are in an LDS slot (chunk c = dims
-// 8c..8c+7 of the lane's token).
-template <int D, int NQ, typename QOp>
-__device__ inline void near_scores_lds(fkv_f4 (&sacc)[NQ], const uint8_t* slot, int lane, const QOp& q_lds) {
-    constexpr int NS = D / 4;
-    fkv_v4u kx[D / 8];
+// 8c..8c+7 of the lane's token).  With NP parts the slot holds part `part`
+// (dims part * D/NP ..); the scores accumulate over the parts, from zero at
+// part 0.
+template <int D, int NQ, int NP = 1, typename QOp>
+__device__ inline void near_scores_lds(fkv_f4 (&sacc)[NQ], const uint8_t* slot, int lane, const QOp& q_lds,
+                                       int part = 0) {
+    constexpr int NS = D / 4 / NP;
+    fkv_v4u kx[D / 8 / NP];
     lds_chunks(kx, slot + lane * 16);
+    if (part == 0) {
 #pragma unroll
-    for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+        for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int s0 = 0; s0 < NS; s0 += 8) {
         fkv_h4 q8[NQ][8];
 #pragma unroll
-        for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+        for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, part * NS + s0, q8[qd]);
 #pragma unroll
         for (int s = s0; s < s0 + 8; s++) {
             const fkv_v4u& x = kx[s >> 1];
@@ -1456,6 +1474,61 @@ __device__ inline void near_pv_lds(Lane<D, NQ>& st, const fkv_f4 (&sacc)[NQ], co
             return (xi & 1) ? h4_of(x.z, x.w) : h4_of(x.x, x.y);
         },
         tile, count, lane >> 2, inv_sqrt_d);
+}
+
+// The same over D = 128 values split in two parts (dim halves dh = 0, 1,
+// one ring slot each): part 0 runs the softmax and keeps the weights in w4
+// (and whether any is non-zero in `any`) for part 1.
+template <int D, int NQ, int G>
+__device__ inline void pv_group_dh(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], const fkv_v4u (&vx)[8], int dh) {
+    const fkv_v4u& x = vx[G >> 1];
+    const fkv_h4 v = (G & 1) ? h4_of(x.z, x.w) : h4_of(x.x, x.y);
+#pragma unroll
+    for (int qd = 0; qd < NQ; qd++) st.acc[qd][dh] = mfma4<G>(w4[qd], v, st.acc[qd][dh]);
+}
+
+template <int D, int NQ, int PART>
+__device__ inline void near_pv_lds_part(Lane<D, NQ>& st, const fkv_f4 (&sacc)[NQ], fkv_h4 (&w4)[NQ], bool& any,
+                                        const uint8_t* slot, int lane, int tile, int count, float inv_sqrt_d) {
+    constexpr int part = PART;
+    static_assert(D == 128, "two value parts are one 64-dim half each");
+    fkv_v4u vx[8];
+    lds_chunks(vx, slot + lane * 16);
+    if constexpr (part == 0) {
+        const uint32_t szd[4] = {0, 0, 0, 0};
+        const int blk = lane >> 2;
+        any = false;
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) {
+            float sc[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = tile * kTile + 4 * blk + e;
+                const float sv = sacc[qd][e] * inv_sqrt_d;
+                const bool ok = t < count;
+                sc[e] = ok ? sv : -INFINITY;
+                if (ok) st.mn[qd] = fminf(st.mn[qd], sv);
+            }
+            any |= softmax_w<D, NQ, false>(st, qd, sc, szd, w4[qd]);
+        }
+    }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;
+    pv_group_dh<D, NQ, 0>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 1>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 2>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 3>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 4>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 5>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 6>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 7>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 8>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 9>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 10>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 11>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 12>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 13>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 14>(st, w4, vx, part);
+    pv_group_dh<D, NQ, 15>(st, w4, vx, part);
 }
 
 // Decode-buffer tile: rows (n_dec, D) row-major fp16.  A lane reads its
@@ -1667,39 +1740,42 @@ __device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs,
     }
 }
 
-// The last split of a row merges every split's record: wave w takes heads
-// w, w + 4, ... (two at a time where their loads fit the registers).
-template <int D>
+// The last split of a row merges every split's record: wave w of the WPG
+// takes heads w, w + WPG, ... (two at a time where their loads fit the
+// registers).
+template <int D, int WPG = kWavesPerGroup>
 __device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, int b, int head0) {
     constexpr int RS = kHdr + D;
     constexpr int SUB = kWave / (D / 4);
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = (int)threadIdx.x % kWave;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
-    const int hw = wave < ng ? (ng - wave + kWavesPerGroup - 1) / kWavesPerGroup : 0;  // this wave's heads
+    const int hw = wave < ng ? (ng - wave + WPG - 1) / WPG : 0;  // this wave's heads
     const int nk = (ns + SUB - 1) / SUB;
     const int64_t o0 = (int64_t)b * a.Hq + head0 + wave;
     int j = 0;
     if (hw >= 2 && nk <= kMaxSplits / SUB / 2) {
-        merge_heads<D, 2>(a, rs, ns, ng, wave, kWavesPerGroup, lane, o0);
+        merge_heads<D, 2>(a, rs, ns, ng, wave, WPG, lane, o0);
         j = 2;
     }
-    for (; j < hw; j++)
-        merge_heads<D, 1>(a, rs, ns, ng, wave + j * kWavesPerGroup, kWavesPerGroup, lane,
-                          o0 + j * kWavesPerGroup);
+    for (; j < hw; j++) merge_heads<D, 1>(a, rs, ns, ng, wave + j * WPG, WPG, lane, o0 + j * WPG);
 }
 
 // Unit u of one wave's stream: the wave's far tiles first (far tile
-// f0 + u*fs), then each of its near tiles w + j*N as two units, keys then
-// values.  w is the wave's index among the N waves of its row.
+// f0 + u*fs), then each of its near tiles w + j*N as 2 * NP units: the keys
+// in NP parts of D / NP dims, then the values in NP parts of D / NP dims
+// (NP = 2 keeps every unit within an 8 KB ring slot at D = 128).  w is the
+// wave's index among the N waves of its row.
 enum UnitKind { kNone = 0, kFarUnit = 1, kNearK = 2, kNearV = 3 };
+template <int NP>
 struct Units {
     int w, N, f0, fs, nf, nn;
-    __device__ int count() const { return nf + 2 * nn; }
+    __device__ int count() const { return nf + 2 * NP * nn; }
     __device__ int kind(int u) const {
-        return u >= nf + 2 * nn ? kNone : u < nf ? kFarUnit : ((u - nf) & 1) ? kNearV : kNearK;
+        return u >= nf + 2 * NP * nn ? kNone : u < nf ? kFarUnit : (u - nf) % (2 * NP) < NP ? kNearK : kNearV;
     }
-    __device__ int tile(int u) const { return u < nf ? f0 + u * fs : w + ((u - nf) >> 1) * N; }
+    __device__ int part(int u) const { return (u - nf) % NP; }
+    __device__ int tile(int u) const { return u < nf ? f0 + u * fs : w + (u - nf) / (2 * NP) * N; }
 };
 
 // Far tiles of wave w of a row, balanced against the row's near tiles
@@ -1756,18 +1832,19 @@ __host__ __device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int 
 // products of fp16 values are exact and summed in fp32.  Lane l ends with
 // dims 64 * rg + 4 * (l / 4) .. + 3 of head l % 4, rounded to fp16 into the
 // qt operand layout; mat 0 also leaves q.Pi^T in fp32 in `qf` and alpha *
-// sum(q.Pi^T) per head in `rsum`.  Waves past D/32 repeat a part whose
-// results they do not write.  Must be entered by every thread of the
-// workgroup.
+// sum(q.Pi^T) per head in `rsum`.  Waves past D/32 only take part in the
+// barriers.  Must be entered by every thread of the workgroup.
 template <int D>
 struct TqRotation {
     fkv_v4u hl[2][D / 8];  // [hi, lo][s2]: k-steps 2 * s2, 2 * s2 + 1 of the lane's row
 };
 
-// The wave's A operands, loaded together with the query (before any use).
-template <int D>
+// The wave's A operands, loaded together with the query (before any use);
+// waves past D/32 load nothing.
+template <int D, int WPG>
 __device__ inline void tq_rotation_load(const AttnArgs& a, TqRotation<D>& r, int wave, int lane) {
     constexpr int WR = D / 32, RG = D / 64;
+    if (wave >= WR) return;
     const int wr = wave % WR, mat = wr / RG, rg = wr % RG;
 #pragma unroll
     for (int part = 0; part < 2; part++)
@@ -1776,14 +1853,15 @@ __device__ inline void tq_rotation_load(const AttnArgs& a, TqRotation<D>& r, int
             r.hl[part][s2] = *(const fkv_v4u*)(a.tq_rot + tq_rot_index(D, mat, part, 64 * rg + lane, 8 * s2));
 }
 
-template <int D, int NQ>
+template <int D, int NQ, int WPG>
 __device__ inline void tq_rotate_query(const AttnArgs& a, const TqRotation<D>& rot, const QOperand<D / 4>& qop,
                                        float* qf, uint16_t* qt, float* rsum, int wave, int lane) {
     constexpr int NS = D / 4, WR = D / 32, RG = D / 64;
     const int wr = wave % WR, mat = wr / RG, rg = wr % RG;
     const int c = lane & 3, blk = lane >> 2;
+    const bool idle = wave >= WR;  // no operands loaded
 #pragma unroll 1
-    for (int qd = 0; qd < NQ; qd++) {
+    for (int qd = 0; qd < NQ && !idle; qd++) {
         fkv_f4 ch = fkv_f4{0.f, 0.f, 0.f, 0.f}, cl = fkv_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s0 = 0; s0 < NS; s0 += 8) {
@@ -1809,10 +1887,12 @@ __device__ inline void tq_rotate_query(const AttnArgs& a, const TqRotation<D>& r
             *(fkv_v2u*)(qt + mat * NQ * NS * 16 + ((qd * NS + sq) * 4 + c) * 4) = fkv_v2u{w0, w1};
             if (mat == 0) *(float4*)(qf + (4 * qd + c) * D + 4 * sq) = float4{v[0], v[1], v[2], v[3]};
         }
-        if (a.tq_alpha != 0.f) {
-            lds_barrier();
-            // wave w sums head w's rotated query
-            if (wave < 4) {
+    }
+    if (a.tq_alpha != 0.f) {
+        lds_barrier();
+        // wave w sums head w's rotated query of every quad
+        if (wave < 4) {
+            for (int qd = 0; qd < NQ; qd++) {
                 float v = 0.f;
                 for (int col = lane; col < D; col += kWave) v += qf[(4 * qd + wave) * D + col];
                 v = wave_sum(v);
@@ -1823,20 +1903,25 @@ __device__ inline void tq_rotate_query(const AttnArgs& a, const TqRotation<D>& r
     lds_barrier();
 }
 
-// One workgroup of 4 waves per (batch, kv head, split, head group); each
-// wave streams its units through a 2-slot LDS ring with gfx950's direct
-// global->LDS loads: the next unit's bytes stream in while the current one
-// is computed.  The ring takes most of the CU's LDS (one workgroup per CU).
+// One workgroup of 4 waves (8: attn_waves) per (batch, kv head, split, head
+// group); each wave streams its units through a 2-slot LDS ring with
+// gfx950's direct global->LDS loads: the next unit's bytes stream in while
+// the current one is computed.  The ring takes most of the CU's LDS (one
+// workgroup per CU).
 template <int D, int NQ, int FMT>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnArgs a) {
+    constexpr int WPG = attn_waves(D, NQ, FMT);  // waves of the workgroup
     constexpr int NS = D / 4;   // 4-dim k-steps of QK
     constexpr int NH = D / 64;  // 64-dim halves of P.V
     constexpr int RS = kHdr + D;
     constexpr int NHW = 4 * NQ;  // head records per wave
     constexpr bool TQ = FMT == 1, G32 = FMT == 2;
     constexpr int REC = (int)(TQ ? tq_record_bytes(D) : G32 ? g32_record_bytes(D) : far_record_bytes(D));
-    constexpr int SLOT = REC > 128 * D ? REC : 128 * D;  // far record or a near K / V half
-    constexpr int FAR_OPS = TQ ? tq_dma_ops<D>() : G32 ? g32_dma_ops<D>() : far_dma_ops<D>(), NEAR_OPS = D / 8;
+    // near K / V halves in NP parts: TurboQuant at D = 128 streams 8 KB units
+    // (its 64 KB ring lets two workgroups share a CU)
+    constexpr int NP = TQ && D == 128 ? 2 : 1;
+    constexpr int SLOT = REC > 128 * D / NP ? REC : 128 * D / NP;  // far record or a near K / V part
+    constexpr int FAR_OPS = TQ ? tq_dma_ops<D>() : G32 ? g32_dma_ops<D>() : far_dma_ops<D>(), NEAR_OPS = D / 8 / NP;
     static_assert(FAR_OPS != NEAR_OPS, "the ring's vmcnt waits tell far and near units apart by op count");
     __shared__ __attribute__((aligned(16))) uint16_t qs[NQ * NS * 4 * 4];
     // TurboQuant: rotated and sketched query operands, same layout as qs;
@@ -1844,15 +1929,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t qt[TQ ? 2 * NQ * NS * 4 * 4 : 8];
     __shared__ __attribute__((aligned(16))) float qf[TQ ? 4 * NQ * D : 4];
     __shared__ float rsum[TQ ? 4 * NQ : 4];
-    // The rings during the tile loop; afterwards (behind a barrier) the
-    // per-wave records; once they are published, the split-merge scratch of
-    // the last workgroup.
-    constexpr int kRing = kWavesPerGroup * 2 * SLOT;
-    constexpr int kRec = kWavesPerGroup * NHW * RS * 4;
-    constexpr int kMrg = (NHW * kMaxSplits + NHW) * 4;
-    constexpr int kLds = kRing > kRec ? (kRing > kMrg ? kRing : kMrg) : (kRec > kMrg ? kRec : kMrg);
+    // The rings during the tile loop, and the per-wave records merged in LDS
+    // after it: past the rings where both fit the CU's 160 KB (a wave then
+    // writes its record as soon as its own stream ends), else over them
+    // (behind a barrier once every wave's stream has ended).
+    constexpr int kRing = WPG * 2 * SLOT;
+    constexpr int kRec = WPG * NHW * RS * 4;
+    constexpr int kQ = 2 * NQ * NS * 16 + (TQ ? 4 * NQ * NS * 16 + 16 * NQ * D + 16 * NQ : 64);
+    constexpr bool SEP_REC = kRing + kRec + kQ + 256 <= 160 * 1024;
+    constexpr int kLds = SEP_REC ? kRing + kRec : (kRing > kRec ? kRing : kRec);
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
-    float* smem = (float*)lds;
+    float* smem = (float*)(lds + (SEP_REC ? kRing : 0));
     __shared__ int s_last;
 
     const int split = blockIdx.x;
@@ -1868,9 +1955,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     uint8_t* ring = lds + wave * 2 * SLOT;
 
     // ---- the wave's far tiles need no device state: start streaming ----
-    Units un;
-    un.N = kWavesPerGroup * a.num_splits;
-    un.w = kWavesPerGroup * split + wave;
+    Units<NP> un;
+    un.N = WPG * a.num_splits;
+    // TurboQuant deals its far and near tiles round-robin over the row's
+    // waves (far_round_robin): numbered wave-major, so that consecutive tiles
+    // go to different workgroups and every workgroup gets an equal share
+    un.w = TQ ? wave * a.num_splits + split : WPG * split + wave;
     {
         const FarPlan fp =
             plan_far(un.w, un.N, (int)cdiv(a.L.F, kTile), a.near_plan, REC, TQ, near_tile_weight(NQ, D));
@@ -1887,7 +1977,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             else if constexpr (G32) dma_g32<D>(a, bkv, un.tile(u), lane, slot);
             else dma_far<D>(a, bkv, un.tile(u), lane, slot);
         }
-        else if (kd != kNone) dma_near<D>(a, bkv, un.tile(u), kd == kNearV, lane, slot);
+        else if (kd != kNone) dma_near<D, NP>(a, bkv, un.tile(u), kd == kNearV, un.part(u), lane, slot);
         return kd == kNone ? 0 : kd == kFarUnit ? FAR_OPS : NEAR_OPS;
     };
     // ---- the query -> LDS as the B operand of the score MFMA,
@@ -1901,8 +1991,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         constexpr int QW = NQ * NS * 8;
         static_assert(QW % kWave == 0, "whole-wave query DMA");
 #pragma unroll
-        for (int k = 0; k < (QW / kWave + kWavesPerGroup - 1) / kWavesPerGroup; k++) {
-            const int w0 = (k * kWavesPerGroup + wave) * kWave;  // wave-uniform
+        for (int k = 0; k < (QW / kWave + WPG - 1) / WPG; k++) {
+            const int w0 = (k * WPG + wave) * kWave;  // wave-uniform
             if (w0 < QW) {
                 const int wd = w0 + lane, e = wd & 1, jj = (wd >> 1) & 3, s = (wd >> 3) % NS;
                 const int h = 4 * ((wd >> 3) / NS) + jj;
@@ -1917,14 +2007,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // together, right after the first tile's DMA, so their latencies overlap
     // (a wait for any of them also waits for the older DMA)
     TqRotation<D> rot;
-    uint16_t tq_q[TQ ? (NQ * NS * 16 + 255) / 256 : 1];
+    constexpr int NT = kWave * WPG;  // threads of the workgroup
+    uint16_t tq_q[TQ ? (NQ * NS * 16 + NT - 1) / NT : 1];
     if constexpr (TQ) {
-        tq_rotation_load<D>(a, rot, wave, lane);
+        tq_rotation_load<D, WPG>(a, rot, wave, lane);
         // unconditional loads (heads past the group read head 0 and are
         // zeroed when stored; indices past the arrays wrap)
 #pragma unroll
-        for (int k = 0; k < (NQ * NS * 16 + 255) / 256; k++) {
-            const int i = (threadIdx.x + 256 * k) % (NQ * NS * 16);
+        for (int k = 0; k < (NQ * NS * 16 + NT - 1) / NT; k++) {
+            const int i = (threadIdx.x + NT * k) % (NQ * NS * 16);
             const int e = i & 3, jj = (i >> 2) & 3, sq = i >> 4;
             const int s = sq % NS, h = 4 * (sq / NS) + jj;
             tq_q[k] = a.q[((int64_t)b * a.Hq + head0 + (h < ng ? h : 0)) * D + 4 * s + e];
@@ -1944,12 +2035,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (int qd = 0; qd < NQ; qd++) asum[qd] = 0.f;
     if constexpr (TQ) {
 #pragma unroll
-        for (int k = 0; k < (NQ * NS * 16 + 255) / 256; k++) {
-            const int i = threadIdx.x + 256 * k, h = 4 * ((i >> 4) / NS) + ((i >> 2) & 3);
+        for (int k = 0; k < (NQ * NS * 16 + NT - 1) / NT; k++) {
+            const int i = threadIdx.x + NT * k, h = 4 * ((i >> 4) / NS) + ((i >> 2) & 3);
             if (i < NQ * NS * 16) qs[i] = h < ng ? tq_q[k] : (uint16_t)0;
         }
         lds_barrier();
-        tq_rotate_query<D, NQ>(a, rot, QOperand<NS>{qs, j * 4}, qf, qt, rsum, wave, lane);
+        tq_rotate_query<D, NQ, WPG>(a, rot, QOperand<NS>{qs, j * 4}, qf, qt, rsum, wave, lane);
         if (a.tq_alpha != 0.f) {
 #pragma unroll
             for (int qd = 0; qd < NQ; qd++) asum[qd] = rsum[4 * qd + j];
@@ -2008,6 +2099,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     fkv_f4 sacc[NQ];  // near scores, carried from a K unit to its V unit
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+    fkv_h4 w4n[NQ];   // near P.V weights, carried between V parts (NP = 2)
+    bool anyn = false;
     const int nu = un.count();
     for (int u = 0; u < nu; u++) {
         // the slot refilled now was read by unit u - 1, whose reads completed
@@ -2034,10 +2127,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 far_compute<D, NQ>(st, r, tile, a.L.F, blk, a.inv_sqrt_d, qx);
             }
         } else if (kd == kNearK) {
-            if constexpr (TQ) near_scores_lds<D, NQ>(sacc, slot, lane, qop);  // near tiles: the unrotated query
+            // near tiles: the unrotated query
+            if constexpr (TQ) near_scores_lds<D, NQ, NP>(sacc, slot, lane, qop, un.part(u));
             else near_scores_lds<D, NQ>(sacc, slot, lane, qx);
         } else {
-            near_pv_lds<D, NQ>(st, sacc, slot, lane, tile, nv, a.inv_sqrt_d);
+            if constexpr (NP == 2) {
+                if (un.part(u) == 0) near_pv_lds_part<D, NQ, 0>(st, sacc, w4n, anyn, slot, lane, tile, nv, a.inv_sqrt_d);
+                else near_pv_lds_part<D, NQ, 1>(st, sacc, w4n, anyn, slot, lane, tile, nv, a.inv_sqrt_d);
+            } else {
+                near_pv_lds<D, NQ>(st, sacc, slot, lane, tile, nv, a.inv_sqrt_d);
+            }
         }
     }
     // no LDS write may land after the ring is reused or the wave ends
@@ -2062,13 +2161,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int row = (int)(bkv * a.head_groups + hgrp);  // (b, kv_head, head group)
     // rows are spaced for the widest row (a last head group may be narrower)
     float* part = a.ws + (int64_t)row * a.num_splits * a.wave_recs * min(a.hpg, a.G) * RS;
-    const bool own_rec = a.wave_recs == kWavesPerGroup;
+    const bool own_rec = a.wave_recs == WPG;
     float* wr = smem + wave * NHW * RS;
     // this wave's record in the workspace (coherent buffer stores, sc1: the
     // cache policy of agent-scope atomic stores)
     const __amdgpu_buffer_rsrc_t wrec = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(part + (int64_t)(split * kWavesPerGroup + wave) * ng * RS), (short)0, ng * RS * 4, 0x00020000);
-    if (!own_rec) __syncthreads();  // every wave is done with its ring: the records reuse the LDS
+        (void*)(part + (int64_t)(split * WPG + wave) * ng * RS), (short)0, ng * RS * 4, 0x00020000);
+    if (!own_rec && !SEP_REC) __syncthreads();  // every wave is done with its ring: the records reuse it
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         const float l = head_sum<true>(st.lsum[qd]), mn = head_min(st.mn[qd]);
@@ -2134,20 +2233,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
         __syncthreads();
         if (!s_last) return;
-        merge_finalize_direct<D>(a, part, a.num_splits * kWavesPerGroup, ng, b, head0);
+        merge_finalize_direct<D, WPG>(a, part, a.num_splits * WPG, ng, b, head0);
         if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     __syncthreads();
 
     // ---- merge the 4 waves into wave 0's records ----
-    for (int h = wave; h < ng; h += kWavesPerGroup) {
+    for (int h = wave; h < ng; h += WPG) {
         float M = -INFINITY;
-        for (int w = 0; w < kWavesPerGroup; w++) M = fmaxf(M, smem[w * NHW * RS + h * RS]);
-        float sc[kWavesPerGroup];
+        for (int w = 0; w < WPG; w++) M = fmaxf(M, smem[w * NHW * RS + h * RS]);
+        float sc[WPG];
         float L = 0.f, mn2 = INFINITY, mx2 = -INFINITY;
         int arg2 = INT_MAX;
-        for (int w = 0; w < kWavesPerGroup; w++) {
+        for (int w = 0; w < WPG; w++) {
             const float* r = smem + w * NHW * RS + h * RS;
             sc[w] = r[0] == -INFINITY ? 0.f : __expf(r[0] - M);
             L += sc[w] * r[1];
@@ -2158,7 +2257,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
         for (int d = lane; d < D; d += kWave) {
             float v = 0.f;
-            for (int w = 0; w < kWavesPerGroup; w++) v += sc[w] * smem[w * NHW * RS + h * RS + kHdr + d];
+            for (int w = 0; w < WPG; w++) v += sc[w] * smem[w * NHW * RS + h * RS + kHdr + d];
             smem[h * RS + kHdr + d] = v;
         }
         if (lane == 0) {
@@ -2199,7 +2298,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __syncthreads();
     if (!s_last) return;
     // every record (this split's included) is in global memory now
-    merge_finalize_direct<D>(a, part, a.num_splits, ng, b, head0);
+    merge_finalize_direct<D, WPG>(a, part, a.num_splits, ng, b, head0);
     if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -2335,10 +2434,10 @@ static int env_int(const char* name, int dflt) {
 
 // Workgroups per (b, kv_head, head group): enough to fill 256 CUs, at least
 // two tiles per wave.
-static int plan_splits(const BlobLayout& L, int rows, int n_dec, int target) {
+static int plan_splits(const BlobLayout& L, int rows, int n_dec, int target, int waves = kWavesPerGroup) {
     const int tiles = (int)(cdiv(L.Na, kTile) + cdiv(L.F, kTile) + cdiv(n_dec, kTile));
     int s = (int)cdiv(target, rows > 0 ? rows : 1);
-    const int cap = tiles / (2 * kWavesPerGroup);
+    const int cap = tiles / (2 * waves);
     if (s > cap) s = cap;
     if (s > kMaxSplits) s = kMaxSplits;
     return s < 1 ? 1 : s;
@@ -2362,11 +2461,12 @@ LaunchPlan plan_launch(const BlobLayout& L, int Hq, int n_decode, int target_wgs
     p.head_groups = (int)cdiv(G, hpg);
     p.ng_max = G < hpg ? G : hpg;
     p.rows = L.B * L.Hkv * p.head_groups;
-    p.splits = plan_splits(L, p.rows, n_decode, target_wgs);
+    p.waves = attn_waves(L.D, (int)cdiv(p.ng_max, 4), L.fmt);
+    p.splits = plan_splits(L, p.rows, n_decode, target_wgs, p.waves);
     // rows of 2..4 splits keep one record per wave (their merge reads at most
     // 16); rows of more splits merge their 4 waves in LDS first (C4's 8
     // splits: 32 wave records merged 0.4 us slower than 8 merged records)
-    p.wave_recs = p.splits > 1 && p.splits <= 4 ? kWavesPerGroup : 1;
+    p.wave_recs = p.splits > 1 && p.splits <= 4 ? p.waves : 1;
     p.ws_floats = p.splits > 1 ? partial_floats(p.rows, p.splits * p.wave_recs, p.ng_max, L.D) : 0;
     return p;
 }
@@ -2664,7 +2764,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         // round-robin.  Where the far split is byte-balanced over many far
         // tiles, from wave 0 (the waves without near tiles hold their share
         // in far tiles, slower per byte).
-        const int nw = splits * fkv::kWavesPerGroup, FT = (int)fkv::cdiv(L.F, fkv::kTile);
+        const int nw = splits * p.waves, FT = (int)fkv::cdiv(L.F, fkv::kTile);
         const int64_t NB = fkv::near_tile_weight((ng_max + 3) / 4, L.D), FB = (int64_t)L.far_rec;
         a.dec_wave0 = 0;
         if ((int64_t)FT * FB < nw * NB) {
@@ -2685,7 +2785,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
             }
         }
     }
-    const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * fkv::kWavesPerGroup);
+    const dim3 grid(splits, L.Hkv * head_groups, L.B), block(fkv::kWave * p.waves);
     a.tq_rot = h->tq.rot;
     a.tq_alpha = h->tq.alpha;
     a.tq_beta = h->tq.beta;
