@@ -1770,13 +1770,15 @@ enum UnitKind { kNone = 0, kFarUnit = 1, kNearK = 2, kNearV = 3 };
 template <int NP>
 struct Units {
     int w, N, f0, fs, nf, nn;
+    int wn;  // the wave's place in the near-tile deal: near tiles wn, wn + N, ...
     __device__ int count() const { return nf + 2 * NP * nn; }
     __device__ int kind(int u) const {
         return u >= nf + 2 * NP * nn ? kNone : u < nf ? kFarUnit : (u - nf) % (2 * NP) < NP ? kNearK : kNearV;
     }
     __device__ int part(int u) const { return (u - nf) % NP; }
-    __device__ int tile(int u) const { return u < nf ? f0 + u * fs : w + (u - nf) / (2 * NP) * N; }
+    __device__ int tile(int u) const { return u < nf ? f0 + u * fs : wn + (u - nf) / (2 * NP) * N; }
 };
+
 
 // Far tiles of wave w of a row, balanced against the row's near tiles
 // (near tile t goes to wave t mod N; `near_plan` is the host's expected near
@@ -1806,6 +1808,13 @@ __host__ __device__ inline int far_bound(int64_t v, int64_t N, int NT, int FT, i
 
 __host__ __device__ inline bool far_round_robin(bool tq, int64_t N, int FT, int64_t NB, int64_t FB) {
     return tq && (int64_t)FT * FB < N * NB;
+}
+// Where the near-tile deal starts: wave 0, or, where far tiles are dealt
+// round-robin (waves from FT mod N on hold one far tile fewer), at FT mod N,
+// so the near tiles go to those waves first.  The host starts decode tiles
+// after the near tiles with the same rule.
+__host__ __device__ inline int near_deal_start(bool tq, int64_t N, int FT, int64_t NB, int64_t FB) {
+    return far_round_robin(tq, N, FT, NB, FB) ? (int)(FT % N) : 0;
 }
 
 // The weight of a near tile in the far split, in bytes: its K and V bytes
@@ -1969,6 +1978,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         un.nf = fp.nf;
     }
     un.nn = 0;
+    un.wn = un.w;
     auto issue = [&](int u) {  // DMA of unit u into slot u % 2; returns its vector-memory op count
         const int kd = un.kind(u);
         uint8_t* slot = ring + (u & 1) * SLOT;
@@ -2049,7 +2059,11 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     // a decode length kept on the device (graph-captured callers) is clamped
     const int n_dec = a.n_dec_dev ? (nd_raw < 0 ? 0 : nd_raw > a.dec_stride ? a.dec_stride : nd_raw) : nd_raw;
     const int nt_near = (int)cdiv(nv, kTile);
-    un.nn = un.w < nt_near ? (int)cdiv(nt_near - un.w, un.N) : 0;
+    {
+        const int n0 = near_deal_start(TQ, un.N, (int)cdiv(a.L.F, kTile), near_tile_weight(NQ, D), REC);
+        un.wn = (un.w - n0 + un.N) % un.N;
+    }
+    un.nn = un.wn < nt_near ? (int)cdiv(nt_near - un.wn, un.N) : 0;
     if (un.nf == 0) issue(0);
 
     Lane<D, NQ> st;
@@ -2769,7 +2783,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         a.dec_wave0 = 0;
         if ((int64_t)FT * FB < nw * NB) {
             if (fkv::far_round_robin(L.fmt == 1, nw, FT, NB, FB)) {
-                a.dec_wave0 = h->near_plan % nw;
+                a.dec_wave0 = (fkv::near_deal_start(true, nw, FT, NB, FB) + h->near_plan) % nw;
             } else {
                 int64_t best = -1;
                 for (int w = 0; w < nw; w++) {
