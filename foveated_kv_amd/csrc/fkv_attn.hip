@@ -1932,7 +1932,11 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     constexpr int SLOT = REC > 128 * D / NP ? REC : 128 * D / NP;  // far record or a near K / V part
     constexpr int FAR_OPS = TQ ? tq_dma_ops<D>() : G32 ? g32_dma_ops<D>() : far_dma_ops<D>(), NEAR_OPS = D / 8 / NP;
     static_assert(FAR_OPS != NEAR_OPS, "the ring's vmcnt waits tell far and near units apart by op count");
-    __shared__ __attribute__((aligned(16))) uint16_t qs[NQ * NS * 4 * 4];
+    // the query as score operands: one copy per wave (each wave stages its
+    // own by LDS DMA and waits for nothing but its own loads), one shared
+    // copy for TurboQuant (staged by all threads behind a barrier)
+    constexpr int QCOPY = NQ * NS * 4 * 4, NQC = TQ ? 1 : WPG;
+    __shared__ __attribute__((aligned(16))) uint16_t qs[NQC * QCOPY];
     // TurboQuant: rotated and sketched query operands, same layout as qs;
     // the fp32 query and the per-head alpha * sum(q.Pi^T)
     __shared__ __attribute__((aligned(16))) uint16_t qt[TQ ? 2 * NQ * NS * 4 * 4 : 8];
@@ -1944,7 +1948,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     // (behind a barrier once every wave's stream has ended).
     constexpr int kRing = WPG * 2 * SLOT;
     constexpr int kRec = WPG * NHW * RS * 4;
-    constexpr int kQ = 2 * NQ * NS * 16 + (TQ ? 4 * NQ * NS * 16 + 16 * NQ * D + 16 * NQ : 64);
+    constexpr int kQ = 2 * NQC * QCOPY + (TQ ? 4 * NQ * NS * 16 + 16 * NQ * D + 16 * NQ : 64);
     constexpr bool SEP_REC = kRing + kRec + kQ + 256 <= 160 * 1024;
     constexpr int kLds = SEP_REC ? kRing + kRec : (kRing > kRec ? kRing : kRec);
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
@@ -2000,15 +2004,13 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     if constexpr (!TQ) {
         constexpr int QW = NQ * NS * 8;
         static_assert(QW % kWave == 0, "whole-wave query DMA");
+        uint8_t* qw = (uint8_t*)(qs + wave * QCOPY);  // this wave's copy (wave-uniform)
 #pragma unroll
-        for (int k = 0; k < (QW / kWave + WPG - 1) / WPG; k++) {
-            const int w0 = (k * WPG + wave) * kWave;  // wave-uniform
-            if (w0 < QW) {
-                const int wd = w0 + lane, e = wd & 1, jj = (wd >> 1) & 3, s = (wd >> 3) % NS;
-                const int h = 4 * ((wd >> 3) / NS) + jj;
-                const uint16_t* src = a.q + ((int64_t)b * a.Hq + head0 + (h < ng ? h : 0)) * D + 4 * s + 2 * e;
-                __builtin_amdgcn_global_load_lds((const void*)src, (FKV_LDS void*)((uint8_t*)qs + w0 * 4), 4, 0, 0);
-            }
+        for (int k = 0; k < QW / kWave; k++) {
+            const int wd = k * kWave + lane, e = wd & 1, jj = (wd >> 1) & 3, s = (wd >> 3) % NS;
+            const int h = 4 * ((wd >> 3) / NS) + jj;
+            const uint16_t* src = a.q + ((int64_t)b * a.Hq + head0 + (h < ng ? h : 0)) * D + 4 * s + 2 * e;
+            __builtin_amdgcn_global_load_lds((const void*)src, (FKV_LDS void*)(qw + k * kWave * 4), 4, 0, 0);
         }
     }
     // the wave's first two far tiles need no device state either
@@ -2080,17 +2082,16 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         for (int dh = 0; dh < NH; dh++) st.acc[qd][dh] = fkv_f4{0.f, 0.f, 0.f, 0.f};
     }
     // q operand reads from LDS (see QOperand)
-    const QOperand<NS> qop{qs, j * 4};
+    const QOperand<NS> qop{qs + (TQ ? 0 : wave * QCOPY), j * 4};
     const QOperand<NS> qrop{qt, j * 4}, qkop{qt + (TQ ? NQ * NS * 16 : 0), j * 4};
     if constexpr (TQ) {
         lds_barrier();
     } else {
         // the query DMA is this wave's oldest vector-memory op: wait for it
-        // but not for the ring, then for every wave's part of the query
+        // but not for the ring (the wave's own copy: no barrier)
         if (early1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * FAR_OPS) : "memory");
         else if (un.nf > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FAR_OPS) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
     }
 
     // rows of one head quad keep the query operands in registers
