@@ -891,10 +891,20 @@ struct PmConst {
 // two +-1 fp16 values from the bits at 15 and 31 (set = -1)
 __device__ inline uint32_t pm1(uint32_t w, const PmConst& k) { return (w & k.m) | (k.c & ~k.m); }
 
-// the +-1 operand of 4 consecutive dims / tokens: pairs i, i+1 of word w
-template <int I>
-__device__ inline fkv_h4 pm1x4(uint32_t w, const PmConst& k) {
-    return h4_of(pm1(w << I, k), pm1(w << (I + 1), k));
+// A plane word held as the pair (w, w << 1) (high, low dword): one 64-bit
+// shift by an even i <= 14 gives w << i and w << (i + 1) together.  The
+// high dword also takes the top i bits of w << 1, but they land below bit
+// i, never at the bits 15 and 31 that pm1 reads.  The shift is inline asm:
+// with only those bits used the compiler would split it into two 32-bit
+// shifts.  v_lshlrev_b64 issues at the rate of v_lshlrev_b32.
+__device__ inline uint64_t plane_pair(uint32_t w) { return ((uint64_t)w << 32) | (uint64_t)(w << 1); }
+
+// the +-1 operand of 4 consecutive dims / tokens: pairs i, i+1 of the
+// plane word of w2 = plane_pair(w)
+__device__ inline fkv_h4 pm1x4(uint64_t w2, int i, const PmConst& k) {
+    uint64_t s = w2;
+    if (i != 0) asm("v_lshlrev_b64 %0, %1, %2" : "=v"(s) : "s"(i), "v"(w2));
+    return h4_of(pm1((uint32_t)(s >> 32), k), pm1((uint32_t)s, k));
 }
 
 // N q-operand k-steps s0.. of quad qd from an LDS operand array, one asm
@@ -992,10 +1002,10 @@ __device__ inline fkv_f4 mfma4_half(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
 // sums (own-half and other-half tokens) so consecutive MFMAs do not wait
 // on each other.
 template <int NQ, int A>
-__device__ inline void tq_pv_step(fkv_f4 (&po)[NQ], fkv_f4 (&px)[NQ], const fkv_v4u& v, const fkv_h4 (&w)[4][NQ],
+__device__ inline void tq_pv_step(fkv_f4 (&po)[NQ], fkv_f4 (&px)[NQ], const uint64_t (&v)[4], const fkv_h4 (&w)[4][NQ],
                                   const PmConst& k) {
-    const fkv_h4 b1h = pm1x4<2 * A>(v.x, k), b2h = pm1x4<2 * A>(v.y, k);
-    const fkv_h4 b1l = pm1x4<2 * A>(v.z, k), b2l = pm1x4<2 * A>(v.w, k);
+    const fkv_h4 b1h = pm1x4(v[0], 2 * A, k), b2h = pm1x4(v[1], 2 * A, k);
+    const fkv_h4 b1l = pm1x4(v[2], 2 * A, k), b2l = pm1x4(v[3], 2 * A, k);
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         po[qd] = mfma4_half<A>(w[0][qd], b1h, po[qd]);
@@ -1039,19 +1049,29 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
 #pragma unroll
         for (int s = s0; s < s0 + KS; s++) {
             const int k = s >> 3, i0 = 2 * (s & 7);
-            const uint32_t wh = r.kp[0][k], wl = r.kp[1][k], ws = r.kp[2][k];
-            const fkv_h4 ah = h4_of(pm1(wh << i0, pk), pm1(wh << (i0 + 1), pk));
-            const fkv_h4 al = h4_of(pm1(wl << i0, pk), pm1(wl << (i0 + 1), pk));
-            const fkv_h4 as = h4_of(pm1(ws << i0, pk), pm1(ws << (i0 + 1), pk));
+            const fkv_h4 ah = pm1x4(plane_pair(r.kp[0][k]), i0, pk);
+            const fkv_h4 al = pm1x4(plane_pair(r.kp[1][k]), i0, pk);
+            const fkv_h4 as = pm1x4(plane_pair(r.kp[2][k]), i0, pk);
 #pragma unroll
             for (int qd = 0; qd < NQ; qd++) {
                 sh[qd] = mfma4_local(ah, q_r[qd][s - s0], sh[qd]);
                 sl[qd] = mfma4_local(al, q_r[qd][s - s0], sl[qd]);
                 sq[qd] = mfma4_local(as, q_k[qd][s - s0], sq[qd]);
             }
-            if (general) {
-                const uint32_t wx = wh ^ wl;
-                const fkv_h4 ax = h4_of(pm1(wx << i0, pk), pm1(wx << (i0 + 1), pk));
+        }
+    }
+    // The sh*sl term of an asymmetric codebook in a pass of its own, so the
+    // common symmetric case takes no branch per k-step.
+    if (general) {
+#pragma unroll
+        for (int s0 = 0; s0 < NS; s0 += KS) {
+            fkv_h4 q_r[NQ][KS];
+#pragma unroll
+            for (int qd = 0; qd < NQ; qd++) qr.template readn<KS>(qd, s0, q_r[qd]);
+#pragma unroll
+            for (int s = s0; s < s0 + KS; s++) {
+                const int k = s >> 3, i0 = 2 * (s & 7);
+                const fkv_h4 ax = pm1x4(plane_pair(r.kp[0][k] ^ r.kp[1][k]), i0, pk);
 #pragma unroll
                 for (int qd = 0; qd < NQ; qd++) sx[qd] = mfma4_local(ax, q_r[qd][s - s0], sx[qd]);
             }
@@ -1103,7 +1123,8 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
             w[2][qd] = fkv_h4{w2[0], w2[1], w2[2], w2[3]};
             w[3][qd] = fkv_h4{w3[0], w3[1], w3[2], w3[3]};
         }
-        const fkv_v4u v = r.v[dh];
+        const uint64_t v[4] = {plane_pair(r.v[dh].x), plane_pair(r.v[dh].y), plane_pair(r.v[dh].z),
+                               plane_pair(r.v[dh].w)};
         fkv_f4 po[NQ], pxs[NQ];
 #pragma unroll
         for (int qd = 0; qd < NQ; qd++) po[qd] = pxs[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
