@@ -98,6 +98,7 @@ SIGNATURES = {
     "fkv_far_plan": (ctypes.c_int, [I32, I32, I32, ctypes.c_int64, ctypes.c_int64, I32, P, P, P]),
     "fkv_attn_blob_info": (ctypes.c_int, [P, ctypes.POINTER(BlobInfoC)]),
     "fkv_attn_read_near_valid": (ctypes.c_int, [P, P, P]),
+    "fkv_attn_dispatch_info": (ctypes.c_int, [P, ctypes.POINTER(I32)]),
     "fkv_attn_destroy": (None, [P]),
     "fkv_e4m3_decode": (ctypes.c_int, [P, P, ctypes.c_int64, P]),
     "fkv_hbm_read_probe": (ctypes.c_int, [P, ctypes.c_int64, I32, I32, I32, P, P]),

@@ -145,6 +145,10 @@ struct fkv_attn_impl {
     int device = 0;
     int target_wgs = 256;   // workgroups a launch aims for (FKV_TARGET_WGS at creation)
     bool fused_merge = true;  // in-kernel split merge (FKV_FUSED_MERGE at creation)
+    // XCD count of the device's workgroup -> XCD dispatch rule (xcd_rule);
+    // 0: rule not confirmed or FKV_XCD_LOCAL=0 at creation (merge through
+    // memory)
+    int xcd_mod = 0;
     fkv::TurboConsts tq;    // fmt 1 only
 };
 

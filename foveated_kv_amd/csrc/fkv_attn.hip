@@ -296,6 +296,9 @@ struct AttnArgs {
     int near_plan;  // expected near tiles per row (balances the far split)
     int dec_wave0;  // the wave that takes decode tile 0
     int wave_recs;  // split records per split: 4 (one per wave) or 1 (merged in LDS)
+    // XCD-local split merge (see the merge section): the XCD count X of the
+    // dispatch rule, 0 where the merge goes through memory instead
+    int xcd_mod;
     // TurboQuant far tier (fmt 1)
     const uint16_t* tq_rot; // Pi, S as rotation MFMA operands (tq_rot_index)
     float tq_alpha;         // centroid constant term (0 for a symmetric codebook)
@@ -1587,15 +1590,18 @@ __device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, i
 // memory): split maxima are rescaled to the global max; spike fields take
 // the min and the first-index max.
 //
-// Coherent loads of split records: buffer loads with the sc1 cache policy
-// (the policy of agent-scope atomic loads); offsets past the buffer read 0
-// without touching memory.
-constexpr int kCpolSc1 = 16;
-__device__ inline fkv_f4 ld_agent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
-    return __builtin_bit_cast(fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
+// Loads of split records: buffer loads with the sc1 cache policy (the
+// policy of agent-scope atomic loads: coherent across XCDs) or, where every
+// split of the row ran on one XCD (xcd_mod), sc0 (past the CU's L1, served
+// by the XCD's L2); offsets past the buffer read 0 without touching memory.
+constexpr int kCpolSc1 = 16, kCpolSc0 = 1;
+template <int CPOL>
+__device__ inline fkv_f4 ld_rec4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL));
 }
-__device__ inline int ld_agent1(__amdgpu_buffer_rsrc_t r, int byte_off) {
-    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kCpolSc1);
+template <int CPOL>
+__device__ inline int ld_rec1(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, CPOL);
 }
 
 // 64-lane reductions on DPP row rotations and lane swaps (no LDS permutes):
@@ -1708,33 +1714,46 @@ __device__ inline void merge_values(const AttnArgs& a, const fkv_f4 (&v)[KV], fl
 // in-kernel merge and merge_kernel both run this, so both give the same
 // bits.  Needs nk = ceil(ns / SUB) <= KV / NH.
 template <int D, int NH>
-__device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs, int ns, int ng, int g0, int step,
-                                   int lane, int64_t o0) {
+constexpr int merge_kv() { return kMaxSplits / (kWave / (D / 4)) / NH; }  // value loads per lane and head
+
+// The record loads of merge_heads with cache policy CPOL.
+template <int D, int NH, int CPOL>
+__device__ inline void merge_loads(__amdgpu_buffer_rsrc_t rs, int ng, int nk, int g0, int step, int lane,
+                                   fkv_f4 (&h)[NH], int (&harg)[NH], fkv_f4 (&v)[NH][merge_kv<D, NH>()]) {
     constexpr int RS = kHdr + D;
+    constexpr int CH = D / 4, SUB = kWave / CH;
+    const int c = lane % CH, u = lane / CH;
+    const int sstride = ng * RS * 4;  // bytes from one split's record to the next
+#pragma unroll
+    for (int i = 0; i < NH; i++) {
+        const int g = g0 + i * step;
+        const int hoff = lane * sstride + g * RS * 4;
+        h[i] = ld_rec4<CPOL>(rs, hoff);
+        harg[i] = ld_rec1<CPOL>(rs, hoff + 16);
+        const int voff = u * sstride + (g * RS + kHdr + 4 * c) * 4;
+#pragma unroll
+        for (int k = 0; k < merge_kv<D, NH>(); k++)
+            if (k < nk)
+                v[i][k] = __builtin_bit_cast(
+                    fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, SUB * k * sstride, CPOL));
+    }
+}
+
+template <int D, int NH>
+__device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs, int ns, int ng, int g0, int step,
+                                   int lane, int64_t o0, bool xcd_local = false) {
     constexpr int CH = D / 4;          // 16-byte value chunks of a head
     constexpr int SUB = kWave / CH;    // lane groups over the splits
-    constexpr int KV = kMaxSplits / SUB / NH;  // value loads per lane and head
+    constexpr int KV = merge_kv<D, NH>();
     const int c = lane % CH, u = lane / CH;
     const int nk = (ns + SUB - 1) / SUB;
-    const int sstride = ng * RS * 4;  // bytes from one split's record to the next
     // Offsets past the last record read 0 without touching memory: lanes
     // past ns are masked below, value loads of splits past ns meet scale 0.
     fkv_f4 h[NH];
     int harg[NH];
     fkv_f4 v[NH][KV];
-#pragma unroll
-    for (int i = 0; i < NH; i++) {
-        const int g = g0 + i * step;
-        const int hoff = lane * sstride + g * RS * 4;
-        h[i] = ld_agent4(rs, hoff);
-        harg[i] = ld_agent1(rs, hoff + 16);
-        const int voff = u * sstride + (g * RS + kHdr + 4 * c) * 4;
-#pragma unroll
-        for (int k = 0; k < KV; k++)
-            if (k < nk)
-                v[i][k] = __builtin_bit_cast(
-                    fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, SUB * k * sstride, kCpolSc1));
-    }
+    if (xcd_local) merge_loads<D, NH, kCpolSc0>(rs, ng, nk, g0, step, lane, h, harg, v);
+    else merge_loads<D, NH, kCpolSc1>(rs, ng, nk, g0, step, lane, h, harg, v);
     const bool live = lane < ns;
     const bool one_row = ns <= 16;  // the live lanes sit in the first 16: row reductions suffice
 #pragma unroll
@@ -1761,11 +1780,42 @@ __device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs,
     }
 }
 
+// XCD-local merge.  The command processor deals a dispatch's workgroups to
+// the X XCDs round-robin by linear workgroup index: index i runs on XCD
+// (c + i) mod X, with an offset c that is fixed for the dispatch (it
+// differs between hardware queues).  The host checks this rule once per
+// device (xcd_rule; a handle created with FKV_XCD_LOCAL=0 in the
+// environment does not use it).  Where a launch's rows are a multiple of X
+// the kernel numbers its workgroups split-major (i = split * rows + row),
+// so every split of a row runs on XCD (c + row) mod X whatever c is, and
+// the row's records, counter and merge stay in that XCD's L2: records are
+// written with plain stores (to L2), the arrival is an L2 atomic, the last
+// split reads the records with sc0 loads (past its L1).  Otherwise (and for
+// launches with one split) the merge is coherent across XCDs (sc1 and
+// agent scope), as described at the merged-record publish.
+__device__ inline uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xF;
+}
+// One workgroup's arrival at its row; true for the row's last split.
+__device__ inline bool arrive_last(const AttnArgs& a, int row, bool xcd_local) {
+    const int prev = xcd_local ? __hip_atomic_fetch_add(a.arrive + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                               : __hip_atomic_fetch_add(a.arrive + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return prev == a.num_splits - 1;
+}
+// The last split re-arms the row's counter for the next launch.
+__device__ inline void rearm(const AttnArgs& a, int row, bool xcd_local) {
+    if (xcd_local) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The last split of a row merges every split's record: wave w of the WPG
 // takes heads w, w + WPG, ... (two at a time where their loads fit the
 // registers).
 template <int D, int WPG = kWavesPerGroup>
-__device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, int b, int head0) {
+__device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, int b, int head0,
+                                             bool xcd_local = false) {
     constexpr int RS = kHdr + D;
     constexpr int SUB = kWave / (D / 4);
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = (int)threadIdx.x % kWave;
@@ -1776,10 +1826,10 @@ __device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src
     const int64_t o0 = (int64_t)b * a.Hq + head0 + wave;
     int j = 0;
     if (hw >= 2 && nk <= kMaxSplits / SUB / 2) {
-        merge_heads<D, 2>(a, rs, ns, ng, wave, WPG, lane, o0);
+        merge_heads<D, 2>(a, rs, ns, ng, wave, WPG, lane, o0, xcd_local);
         j = 2;
     }
-    for (; j < hw; j++) merge_heads<D, 1>(a, rs, ns, ng, wave + j * WPG, WPG, lane, o0 + j * WPG);
+    for (; j < hw; j++) merge_heads<D, 1>(a, rs, ns, ng, wave + j * WPG, WPG, lane, o0 + j * WPG, xcd_local);
 }
 
 // Unit u of one wave's stream: the wave's far tiles first (far tile
@@ -1976,10 +2026,18 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     float* smem = (float*)(lds + (SEP_REC ? kRing : 0));
     __shared__ int s_last;
 
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y / a.head_groups;
-    const int hgrp = blockIdx.y % a.head_groups;
-    const int b = blockIdx.z;
+    // XCD-local merge: linear workgroup index = split * rows + row, so that
+    // every split of a row runs on one XCD (rows is a multiple of xcd_mod)
+    const bool xcd_local = a.xcd_mod != 0;
+    int split = blockIdx.x, rowl = blockIdx.y + gridDim.y * blockIdx.z;
+    if (xcd_local) {
+        const int rows = gridDim.y * gridDim.z, lin = blockIdx.x + gridDim.x * rowl;
+        split = lin / rows;
+        rowl = lin % rows;
+    }
+    const int kvh = (rowl % gridDim.y) / a.head_groups;
+    const int hgrp = (rowl % gridDim.y) % a.head_groups;
+    const int b = rowl / gridDim.y;
     const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
     const int head0 = kvh * a.G + hgrp * a.hpg;
     const int ng = min(a.hpg, a.G - hgrp * a.hpg);
@@ -2233,9 +2291,14 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         const float hdr[5] = {st.m[qd], l, mn, mx, __int_as_float(arg)};
         if (own_rec) {
             if (lane < 4 && h < ng) {
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(fkv_v4u, fkv_f4{hdr[0], hdr[1], hdr[2], hdr[3]}), wrec, h * RS * 4, 0, kCpolSc1);
-                __builtin_amdgcn_raw_buffer_store_b32((uint32_t)arg, wrec, h * RS * 4 + 16, 0, kCpolSc1);
+                const fkv_v4u hv = __builtin_bit_cast(fkv_v4u, fkv_f4{hdr[0], hdr[1], hdr[2], hdr[3]});
+                if (xcd_local) {
+                    __builtin_amdgcn_raw_buffer_store_b128(hv, wrec, h * RS * 4, 0, kCpolSc0);
+                    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)arg, wrec, h * RS * 4 + 16, 0, kCpolSc0);
+                } else {
+                    __builtin_amdgcn_raw_buffer_store_b128(hv, wrec, h * RS * 4, 0, kCpolSc1);
+                    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)arg, wrec, h * RS * 4 + 16, 0, kCpolSc1);
+                }
             }
         } else if (lane < 4 && h < ng) {
 #pragma unroll
@@ -2249,10 +2312,13 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
             for (int i = 0; i < 4; i++) {
                 if (4 * qd + i < ng) {
                     const int e = (4 * qd + i) * RS + kHdr + 64 * dh + lane;
-                    if (own_rec)
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(st.acc[qd][dh][i] + zz[i]), wrec, e * 4,
-                                                              0, kCpolSc1);
-                    else wr[e] = st.acc[qd][dh][i] + zz[i];
+                    const float v = st.acc[qd][dh][i] + zz[i];
+                    if (own_rec) {
+                        if (xcd_local) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), wrec, e * 4, 0, kCpolSc0);
+                        else __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), wrec, e * 4, 0, kCpolSc1);
+                    } else {
+                        wr[e] = v;
+                    }
                 }
             }
         }
@@ -2263,14 +2329,11 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         // (the ordering argument of the merged-record path below)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (threadIdx.x == 0) {
-            const int prev = __hip_atomic_fetch_add(a.arrive + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = prev == a.num_splits - 1;
-        }
+        if (threadIdx.x == 0) s_last = arrive_last(a, row, xcd_local);
         __syncthreads();
         if (!s_last) return;
-        merge_finalize_direct<D, WPG>(a, part, a.num_splits * WPG, ng, b, head0);
-        if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge_finalize_direct<D, WPG>(a, part, a.num_splits * WPG, ng, b, head0, xcd_local);
+        if (threadIdx.x == 0) rearm(a, row, xcd_local);
         return;
     }
     __syncthreads();
@@ -2323,19 +2386,25 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     // agent-scope RMW counts the arrival; the last workgroup reads the
     // records back with agent-scope atomic loads.  (A release/acquire fence
     // pair would write back and invalidate the whole L2 per workgroup.)
-    for (int i = threadIdx.x; i < ng * RS; i += blockDim.x)
-        __hip_atomic_store(part + (int64_t)split * ng * RS + i, smem[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // XCD-local: the row's splits share one L2, so plain stores, an L2
+    // atomic and sc0 loads order the same way without waiting for memory.
+    float* rec = part + (int64_t)split * ng * RS;
+    if (xcd_local) {
+        for (int i = threadIdx.x; i < ng * RS; i += blockDim.x)
+            __hip_atomic_store(rec + i, smem[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+        for (int i = threadIdx.x; i < ng * RS; i += blockDim.x)
+            __hip_atomic_store(rec + i, smem[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int prev = __hip_atomic_fetch_add(a.arrive + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == a.num_splits - 1;
-    }
+    if (threadIdx.x == 0) s_last = arrive_last(a, row, xcd_local);
     __syncthreads();
     if (!s_last) return;
-    // every record (this split's included) is in global memory now
-    merge_finalize_direct<D, WPG>(a, part, a.num_splits, ng, b, head0);
-    if (threadIdx.x == 0) __hip_atomic_store(a.arrive + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every record (this split's included) is in global memory (the row's
+    // L2) now
+    merge_finalize_direct<D, WPG>(a, part, a.num_splits, ng, b, head0, xcd_local);
+    if (threadIdx.x == 0) rearm(a, row, xcd_local);
 }
 
 // Split-K merge as its own launch (in-kernel merge switched off): one wave
@@ -2529,6 +2598,64 @@ using fkv::set_error;
 
 namespace fkv {
 
+// ---------------------------------------------------------------------------
+// The workgroup -> XCD dispatch rule, checked once per device: a probe
+// dispatch records the XCD (HW_REG_XCC_ID) of each of its workgroups; the
+// rule holds when, with the XCDs numbered x0 .. x0 + X - 1, workgroup i ran
+// on x0 + (c + i) mod X for one offset c.  X then enables the XCD-local
+// split merge; otherwise the merge goes through memory.  The probe writes
+// a file-scope device array (no allocation).
+// ---------------------------------------------------------------------------
+
+constexpr int kXcdProbeWGs = 4096;
+constexpr int kXcdDevices = 64;
+static __device__ uint32_t xcd_probe_out[kXcdProbeWGs];
+
+__global__ void xcd_probe_kernel(uint32_t* out) {
+    const uint32_t x = xcc_id();
+    if (threadIdx.x == 0) out[blockIdx.x] = x;
+}
+
+namespace {
+std::mutex g_xcd_mu;
+struct XcdRule {
+    bool done = false;
+    int mod = 0;
+};
+XcdRule g_xcd[kXcdDevices];
+}  // namespace
+
+int xcd_rule(int dev, hipStream_t st, int* mod) {
+    if (dev < 0 || dev >= kXcdDevices) return set_error("xcd_rule: device index out of range");
+    std::lock_guard<std::mutex> lock(g_xcd_mu);
+    XcdRule& r = g_xcd[dev];
+    if (!r.done) {
+        void* out = nullptr;
+        if (int rc = check_hip(hipGetSymbolAddress(&out, HIP_SYMBOL(xcd_probe_out)), "hipGetSymbolAddress(xcd_probe_out)"))
+            return rc;
+        if (!out) return set_error("xcd_rule: hipGetSymbolAddress returned NULL");
+        hipLaunchKernelGGL(xcd_probe_kernel, dim3(kXcdProbeWGs), dim3(kWave), 0, st, (uint32_t*)out);
+        std::vector<uint32_t> x(kXcdProbeWGs);
+        int rc = check_hip(hipGetLastError(), "xcd_probe_kernel launch");
+        if (!rc) rc = check_hip(hipMemcpyAsync(x.data(), out, kXcdProbeWGs * sizeof(uint32_t), hipMemcpyDeviceToHost, st),
+                                "hipMemcpyAsync(xcd probe)");
+        if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
+        if (rc) return rc;
+        uint32_t lo = x[0], hi = x[0];
+        for (uint32_t v : x) {
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
+        }
+        const uint32_t X = hi - lo + 1, c = x[0] - lo;
+        bool ok = true;
+        for (int i = 0; i < kXcdProbeWGs && ok; i++) ok = x[i] == lo + (c + (uint32_t)i) % X;
+        r.mod = ok ? (int)X : 0;
+        r.done = true;
+    }
+    *mod = r.mod;
+    return FKV_OK;
+}
+
 int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, const void* near_k,
                const void* near_v, int near_dtype, const int32_t* near_valid, float margin, hipStream_t st) {
     h->L = make_layout(B, Hkv, D, Na, F, fmt);
@@ -2551,6 +2678,8 @@ int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, 
 }
 
 int attn_finish(fkv_attn_impl* h, hipStream_t st) {
+    if (int rc = xcd_rule(h->device, st, &h->xcd_mod)) return rc;
+    if (env_int("FKV_XCD_LOCAL", 1) == 0) h->xcd_mod = 0;  // read once per handle, at creation
     std::vector<uint32_t> nv_h(h->L.Hkv, 0);
     int rc = check_hip(hipMemcpyAsync(nv_h.data(), h->blob + h->L.near_valid, h->L.Hkv * sizeof(uint32_t),
                                       hipMemcpyDeviceToHost, st), "hipMemcpyAsync(near_valid)");
@@ -2784,6 +2913,9 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.hpg = hpg;
     a.num_splits = splits;
     a.wave_recs = p.wave_recs;
+    // the XCD-local merge needs whole XCD groups of rows (the grid's rows,
+    // Hkv * head_groups * B, are p.rows)
+    a.xcd_mod = h->xcd_mod > 0 && splits > 1 && h->fused_merge && rows % h->xcd_mod == 0 ? h->xcd_mod : 0;
     a.spike_margin = h->margin;
     a.inv_sqrt_d = (float)(1.0 / sqrt((double)L.D));
     a.out = (uint16_t*)out;
@@ -2936,6 +3068,12 @@ int fkv_e4m3_decode(const uint8_t* codes, void* out_f16, int64_t n, void* stream
     hipLaunchKernelGGL(fkv::e4m3_decode_kernel, dim3(fkv::grid_for(n / 4, 256)), dim3(256), 0,
                        (hipStream_t)stream, codes, (uint16_t*)out_f16, n / 4);
     return check_hip(hipGetLastError(), "e4m3_decode_kernel launch");
+}
+
+int fkv_attn_dispatch_info(const fkv_attn* h, int32_t* xcd_mod) {
+    if (!h || !xcd_mod) return set_error("fkv_attn_dispatch_info: NULL argument");
+    *xcd_mod = h->xcd_mod;
+    return FKV_OK;
 }
 
 int fkv_attn_blob_info(const fkv_attn* h, fkv_blob_info* out) {

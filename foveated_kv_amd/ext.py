@@ -339,6 +339,13 @@ class FoveatedHandle:
                   "fkv_attn_export_near")
         return k, v
 
+    def dispatch_info(self):
+        """XCD count of the workgroup -> XCD dispatch rule this handle's split
+        merge uses (0: the merge goes through memory)."""
+        mod = _lib.I32(0)
+        check(self._lib.fkv_attn_dispatch_info(self._h, ctypes.byref(mod)), "fkv_attn_dispatch_info")
+        return mod.value
+
     def read_near_valid(self):
         """Current per-KV-head near_valid of the blob (host list)."""
         buf = (ctypes.c_uint32 * self.H_kv)()

@@ -248,6 +248,15 @@ int fkv_attn_plan(int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F, int3
 int fkv_far_plan(int32_t n_waves, int32_t near_plan, int32_t nt_far, int64_t near_weight, int64_t far_rec,
                  int32_t turbo, int32_t* f0, int32_t* fs, int32_t* nf);
 
+/* The workgroup -> XCD dispatch rule the handle's split merge relies on (no
+ * counterpart in the reference, whose Metal kernel has no merge across
+ * dies): *xcd_mod = X where the device deals a dispatch's workgroups to its X
+ * XCDs round-robin by linear index (checked once per device when its first
+ * handle is created), so that the splits of one row can merge in one XCD's
+ * L2; 0 when the rule did not hold or the handle was created with
+ * FKV_XCD_LOCAL=0 (the merge then goes through memory).  Host only. */
+int fkv_attn_dispatch_info(const fkv_attn* h, int32_t* xcd_mod);
+
 /* fkv_attn_call with the decode-buffer length in device memory, for callers
  * that capture decode steps in a HIP graph (no counterpart in the
  * reference): decode_k/v (B,Hkv,capacity,D) fp16, rows [0, *n_decode_dev)

@@ -258,7 +258,8 @@ def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
     arrival counters are re-armed by the kernel itself.  200 launches queued
     back to back (no host sync between them) must all be bit-identical, and
     must equal the separate merge launch bit for bit (both merges follow the
-    same arithmetic in the same order)."""
+    same arithmetic in the same order), and the merge through memory
+    (FKV_XCD_LOCAL=0) must equal the XCD-local merge bit for bit."""
     from foveated_kv_amd import ext, synthetic
 
     _flush(f"fused merge stress B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} v_group={vg}")
@@ -277,8 +278,17 @@ def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
                                    cl.near_valid, spike_margin=10.0)
     finally:
         del os.environ["FKV_FUSED_MERGE"]
+    os.environ["FKV_XCD_LOCAL"] = "0"  # read once, when a handle is created
+    try:
+        h_mem = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                                   cl.near_valid, spike_margin=10.0)
+    finally:
+        del os.environ["FKV_XCD_LOCAL"]
     ref = [t.clone() for t in h_sep(q, dkt, dvt)]
     del h_sep
+    assert h_mem.dispatch_info() == 0
+    ref_mem = [t.clone() for t in h_mem(q, dkt, dvt)]
+    del h_mem
     outs = [h(q, dkt, dvt) for _ in range(200)]
     torch.cuda.synchronize()
     first = outs[0]
@@ -289,3 +299,45 @@ def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
     diff = (first[0].float() - ref[0].float()).abs().max().item()
     assert diff <= 1e-3 * max(1.0, ref[0].float().abs().max().item()), diff
     assert torch.equal(first[0], ref[0])
+    for a, b in zip(first, ref_mem):
+        assert torch.equal(a, b)
+    assert h.dispatch_info() > 0, "the workgroup -> XCD dispatch rule did not hold on this device"
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,n_dec", [(8, 32, 8, 128, 8192, 0), (4, 32, 8, 64, 4096, 5)])
+def test_xcd_local_merge_across_concurrent_streams(fkv, orc, B, Hq, Hkv, D, S, n_dec):
+    """The XCD-local merge relies on the dispatch rule holding for every
+    dispatch, whatever hardware queue it comes from (the rule's XCD offset
+    differs between queues) and whatever else runs: handles on three
+    streams, launched back to back without host synchronisation, must all
+    match the merge through memory bit for bit."""
+    from foveated_kv_amd import ext, synthetic
+
+    _flush(f"xcd-local merge, 3 streams B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec}")
+    k, v = synthetic.make_kv(B, Hkv, S, D, 23)
+    q = torch.from_numpy(synthetic.make_query(B, Hq, D, 23)).cuda()[:, :, None]
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, 23)
+    dkt = torch.from_numpy(dk).cuda() if dk is not None else None
+    dvt = torch.from_numpy(dv).cuda() if dv is not None else None
+    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                                      with_archive=False)
+    args = (cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero, cl.near_valid)
+    os.environ["FKV_XCD_LOCAL"] = "0"
+    try:
+        h_mem = ext.FoveatedHandle(*args, spike_margin=10.0)
+    finally:
+        del os.environ["FKV_XCD_LOCAL"]
+    ref = [t.clone() for t in h_mem(q, dkt, dvt)]
+    torch.cuda.synchronize()
+    hs = [ext.FoveatedHandle(*args, spike_margin=10.0) for _ in range(3)]
+    assert all(h.dispatch_info() > 0 for h in hs)
+    streams = [torch.cuda.Stream() for _ in hs]
+    outs = []
+    for _ in range(40):
+        for h, st in zip(hs, streams):
+            with torch.cuda.stream(st):
+                outs.append(h(q, dkt, dvt))
+    torch.cuda.synchronize()
+    for o in outs:
+        for a, b in zip(o, ref):
+            assert torch.equal(a, b)
