@@ -64,7 +64,11 @@ __host__ __device__ constexpr int64_t far_record_bytes(int D) { return (int64_t)
 //         of the 2-bit value codes; "own" = the 32 tokens 32*(l/32).. of
 //         the lane's half, "other" = the other 32; tokens 2i, 2i+1 of a
 //         half at bits 15-i, 31-i
-//   | SC: [token][D/32] fp16 value-group scales
+//   | SC: fp16 value-group scales as the P.V lanes read them: token t =
+//         4 blk + e of the tile, group g = 2 dh + half at
+//         ((2 blk + half) * 4 + e) * D/64 + dh (tq_sc_index), so a lane
+//         (block blk, half) reads its tokens' scales in its own groups as
+//         one 16-byte (D = 64: 8-byte) load
 //   | NG: [token] u32 = fp16 key norm | fp16 residual norm << 16 ]
 // Every plane bit is stored complemented (set = -1), so that
 // (w & 0x80008000) | 0x3C003C00 is the pair of +-1 fp16 operands.
@@ -72,6 +76,10 @@ __host__ __device__ constexpr int64_t tq_vp_section(int D) { return (int64_t)24 
 __host__ __device__ constexpr int64_t tq_sc_section(int D) { return (int64_t)40 * D; }
 __host__ __device__ constexpr int64_t tq_ng_section(int D) { return (int64_t)44 * D; }
 __host__ __device__ constexpr int64_t tq_record_bytes(int D) { return (int64_t)44 * D + 256; }
+// fp16 index in the SC section of the scale of token 4 blk + e, group 2 dh + half
+__host__ __device__ constexpr int tq_sc_index(int D, int blk, int half, int e, int dh) {
+    return ((2 * blk + half) * 4 + e) * (D / 64) + dh;
+}
 
 // fp8 K + group-32 INT4 V far record (fmt 2): the fmt-0 K section, then
 //   | V: per 64-dim half dh two 1 KB chunks (own, other), lane l = dim

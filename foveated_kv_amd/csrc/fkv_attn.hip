@@ -781,7 +781,11 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
 // and masking with 0x80008000 | 0x3C003C00 yields the two fp16 +-1
 // operands, so each 4-dim k-step is three exact MFMAs (high bit, low bit,
 // QJL sign) against the fp16 rotated / sketched query.
-// Values: level(c) = lvh*sh + lvl*sl times the group scale.  The scale
+// Values: level(c) = lvh*sh + lvl*sl times the group scale, and the
+// reference's levels {-1, -0.333333, 0.333333, 1} give lvh = 2*lvl (to 5e-7
+// relative, checked when the handle is created): the high-bit plane
+// expands to +-2 and the low-bit plane to +-1, and both take the one
+// weight p * scale * lvl.  The scale
 // differs between the two 32-dim groups of a 64-lane P.V block, so the
 // weights carry it: with cbsz = 3 the MFMA broadcasts block a's A operand
 // to blocks 0-7 and block 8+a's to blocks 8-15, i.e. lanes 0-31 (group
@@ -823,58 +827,58 @@ template <int D>
 struct TqTile {
     fkv_v4u kp[3];  // key planes of the lane's token (D = 64: .x/.y only)
     fkv_v4u v[D / 64];   // value planes of dim 64dh + lane: hi own, hi other, lo own, lo other
-    fkv_v4u so[D / 64];  // group scales of the lane's 4 tokens [e][g] (fp16)
-    fkv_v4u sx[D / 64];  // ... of the other half's 4 tokens (block blk ^ 8)
-    fkv_v4u ng;          // norm | gamma << 16 of the lane's 4 tokens
+    fkv_v4u so;  // scales of the lane's 4 tokens in the lane's groups 2dh + half, [e][dh] fp16 (D = 64: .x/.y)
+    fkv_v4u sx;  // ... of the other half's 4 tokens (block blk ^ 8)
+    fkv_v4u ng;  // norm | gamma << 16 of the lane's 4 tokens
 };
 
 __device__ inline void lds_tq(TqTile<128>& r, const uint8_t* slot, int lane) {
-    const int blk = lane >> 2;
+    const int blk = lane >> 2, half = lane >> 5;
     const uint32_t a = lds_addr(slot + lane * 16);
-    const uint32_t so = lds_addr(slot + tq_sc_section(128) + blk * 32);
-    const uint32_t sx = lds_addr(slot + tq_sc_section(128) + (blk ^ 8) * 32);
+    const uint32_t so = lds_addr(slot + tq_sc_section(128) + tq_sc_index(128, blk, half, 0, 0) * 2);
+    const uint32_t sx = lds_addr(slot + tq_sc_section(128) + tq_sc_index(128, blk ^ 8, half, 0, 0) * 2);
     const uint32_t ng = lds_addr(slot + tq_ng_section(128) + blk * 16);
     asm volatile(
-        "ds_read_b128 %0, %10\n"
-        "ds_read_b128 %1, %10 offset:1024\n"
-        "ds_read_b128 %2, %10 offset:2048\n"
-        "ds_read_b128 %3, %10 offset:3072\n"
-        "ds_read_b128 %4, %10 offset:4096\n"
-        "ds_read_b128 %5, %11\n"
-        "ds_read_b128 %6, %11 offset:16\n"
-        "ds_read_b128 %7, %12\n"
-        "ds_read_b128 %8, %12 offset:16\n"
-        "ds_read_b128 %9, %13\n"
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:1024\n"
+        "ds_read_b128 %2, %8 offset:2048\n"
+        "ds_read_b128 %3, %8 offset:3072\n"
+        "ds_read_b128 %4, %8 offset:4096\n"
+        "ds_read_b128 %5, %9\n"
+        "ds_read_b128 %6, %10\n"
+        "ds_read_b128 %7, %11\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(r.kp[0]), "=&v"(r.kp[1]), "=&v"(r.kp[2]), "=&v"(r.v[0]), "=&v"(r.v[1]), "=&v"(r.so[0]),
-          "=&v"(r.so[1]), "=&v"(r.sx[0]), "=&v"(r.sx[1]), "=&v"(r.ng)
+        : "=&v"(r.kp[0]), "=&v"(r.kp[1]), "=&v"(r.kp[2]), "=&v"(r.v[0]), "=&v"(r.v[1]), "=&v"(r.so), "=&v"(r.sx),
+          "=&v"(r.ng)
         : "v"(a), "v"(so), "v"(sx), "v"(ng)
         : "memory");
 }
 
 __device__ inline void lds_tq(TqTile<64>& r, const uint8_t* slot, int lane) {
-    const int blk = lane >> 2;
+    const int blk = lane >> 2, half = lane >> 5;
     const uint32_t a = lds_addr(slot + lane * 8);
     const uint32_t v = lds_addr(slot + tq_vp_section(64) + lane * 16);
-    const uint32_t so = lds_addr(slot + tq_sc_section(64) + blk * 16);
-    const uint32_t sx = lds_addr(slot + tq_sc_section(64) + (blk ^ 8) * 16);
+    const uint32_t so = lds_addr(slot + tq_sc_section(64) + tq_sc_index(64, blk, half, 0, 0) * 2);
+    const uint32_t sx = lds_addr(slot + tq_sc_section(64) + tq_sc_index(64, blk ^ 8, half, 0, 0) * 2);
     const uint32_t ng = lds_addr(slot + tq_ng_section(64) + blk * 16);
-    fkv_v2u k0, k1, k2;
+    fkv_v2u k0, k1, k2, s0, s1;
     asm volatile(
         "ds_read_b64 %0, %7\n"
         "ds_read_b64 %1, %7 offset:512\n"
         "ds_read_b64 %2, %7 offset:1024\n"
         "ds_read_b128 %3, %8\n"
-        "ds_read_b128 %4, %9\n"
-        "ds_read_b128 %5, %10\n"
+        "ds_read_b64 %4, %9\n"
+        "ds_read_b64 %5, %10\n"
         "ds_read_b128 %6, %11\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k0), "=&v"(k1), "=&v"(k2), "=&v"(r.v[0]), "=&v"(r.so[0]), "=&v"(r.sx[0]), "=&v"(r.ng)
+        : "=&v"(k0), "=&v"(k1), "=&v"(k2), "=&v"(r.v[0]), "=&v"(s0), "=&v"(s1), "=&v"(r.ng)
         : "v"(a), "v"(v), "v"(so), "v"(sx), "v"(ng)
         : "memory");
     r.kp[0] = fkv_v4u{k0.x, k0.y, 0u, 0u};
     r.kp[1] = fkv_v4u{k1.x, k1.y, 0u, 0u};
     r.kp[2] = fkv_v4u{k2.x, k2.y, 0u, 0u};
+    r.so = fkv_v4u{s0.x, s0.y, 0u, 0u};
+    r.sx = fkv_v4u{s1.x, s1.y, 0u, 0u};
 }
 
 // Bit-select constants held in registers: with the mask and the fp16 +1
@@ -882,32 +886,40 @@ __device__ inline void lds_tq(TqTile<64>& r, const uint8_t* slot, int lane) {
 // word (gfx9 VOP3 takes no literals, so folded constants cost an AND and
 // an OR).  The empty asm emits no instruction.
 struct PmConst {
-    uint32_t m, c;
+    uint32_t m, c, c2;  // sign mask, fp16 pairs (1, 1) and (2, 2)
     __device__ static PmConst make() {
-        PmConst k{0x80008000u, 0x3C003C00u};
+        PmConst k{0x80008000u, 0x3C003C00u, 0x40004000u};
         asm volatile("" : "+s"(k.m));
         asm volatile("" : "+v"(k.c));
+        asm volatile("" : "+v"(k.c2));
         return k;
     }
 };
 
-// two +-1 fp16 values from the bits at 15 and 31 (set = -1)
-__device__ inline uint32_t pm1(uint32_t w, const PmConst& k) { return (w & k.m) | (k.c & ~k.m); }
+// two fp16 values +-c from the bits at 15 and 31 (set = negative)
+__device__ inline uint32_t pm1(uint32_t w, uint32_t m, uint32_t c) { return (w & m) | (c & ~m); }
+__device__ inline uint32_t pm1(uint32_t w, const PmConst& k) { return pm1(w, k.m, k.c); }
 
 // A plane word held as the pair (w, w << 1) (high, low dword): one 64-bit
 // shift by an even i <= 14 gives w << i and w << (i + 1) together.  The
 // high dword also takes the top i bits of w << 1, but they land below bit
-// i, never at the bits 15 and 31 that pm1 reads.  The shift is inline asm:
-// with only those bits used the compiler would split it into two 32-bit
-// shifts.  v_lshlrev_b64 issues at the rate of v_lshlrev_b32.
+// i, never at the bits 15 and 31 that pm1 reads.  The shift amount is made
+// opaque (an empty asm on a scalar register), so the compiler keeps the one
+// v_lshlrev_b64 instead of splitting a constant shift into two 32-bit
+// ones; v_lshlrev_b64 issues at the rate of v_lshlrev_b32.
 __device__ inline uint64_t plane_pair(uint32_t w) { return ((uint64_t)w << 32) | (uint64_t)(w << 1); }
 
-// the +-1 operand of 4 consecutive dims / tokens: pairs i, i+1 of the
-// plane word of w2 = plane_pair(w)
-__device__ inline fkv_h4 pm1x4(uint64_t w2, int i, const PmConst& k) {
+// the +-c operand of 4 consecutive dims / tokens (c = 1: k.c, 2: k.c2):
+// pairs i, i+1 of the plane word of w2 = plane_pair(w)
+__device__ inline fkv_h4 pm1x4(uint64_t w2, int i, const PmConst& k, bool two = false) {
     uint64_t s = w2;
-    if (i != 0) asm("v_lshlrev_b64 %0, %1, %2" : "=v"(s) : "s"(i), "v"(w2));
-    return h4_of(pm1((uint32_t)(s >> 32), k), pm1((uint32_t)s, k));
+    if (i != 0) {
+        uint32_t n = (uint32_t)i;
+        asm("" : "+s"(n));
+        s = w2 << n;
+    }
+    const uint32_t c = two ? k.c2 : k.c;
+    return h4_of(pm1((uint32_t)(s >> 32), k.m, c), pm1((uint32_t)s, k.m, c));
 }
 
 // N q-operand k-steps s0.. of quad qd from an LDS operand array, one asm
@@ -1003,23 +1015,25 @@ __device__ inline fkv_f4 mfma4_half(fkv_h4 a, fkv_h4 b, fkv_f4 c) {
 
 // Step A of the P.V of one tile: 4 MFMAs per head quad into two partial
 // sums (own-half and other-half tokens) so consecutive MFMAs do not wait
-// on each other.
+// on each other; the high-bit planes expand to +-2, the low-bit ones to
+// +-1, against one weight per token.
 template <int NQ, int A>
-__device__ inline void tq_pv_step(fkv_f4 (&po)[NQ], fkv_f4 (&px)[NQ], const uint64_t (&v)[4], const fkv_h4 (&w)[4][NQ],
+__device__ inline void tq_pv_step(fkv_f4 (&po)[NQ], fkv_f4 (&px)[NQ], const uint64_t (&v)[4], const fkv_h4 (&w)[2][NQ],
                                   const PmConst& k) {
-    const fkv_h4 b1h = pm1x4(v[0], 2 * A, k), b2h = pm1x4(v[1], 2 * A, k);
+    const fkv_h4 b1h = pm1x4(v[0], 2 * A, k, true), b2h = pm1x4(v[1], 2 * A, k, true);
     const fkv_h4 b1l = pm1x4(v[2], 2 * A, k), b2l = pm1x4(v[3], 2 * A, k);
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         po[qd] = mfma4_half<A>(w[0][qd], b1h, po[qd]);
-        px[qd] = mfma4_half<A>(w[2][qd], b2h, px[qd]);
-        po[qd] = mfma4_half<A>(w[1][qd], b1l, po[qd]);
-        px[qd] = mfma4_half<A>(w[3][qd], b2l, px[qd]);
+        px[qd] = mfma4_half<A>(w[1][qd], b2h, px[qd]);
+        po[qd] = mfma4_half<A>(w[0][qd], b1l, po[qd]);
+        px[qd] = mfma4_half<A>(w[1][qd], b2l, px[qd]);
     }
 }
 
-__device__ inline float half_of(const fkv_v4u* s, int i) {
-    const uint32_t w = s[i >> 3][(i >> 1) & 3];
+// fp16 number i of the scale words s (compile-time i: a low or high half)
+__device__ inline float half_of(const fkv_v4u& s, int i) {
+    const uint32_t w = s[i >> 1];
     return h2f((uint16_t)((i & 1) ? (w >> 16) : (w & 0xFFFF)));
 }
 
@@ -1029,13 +1043,24 @@ __device__ inline float swap_halves(float v, int half) {
     return __uint_as_float(half ? r[0] : r[1]);
 }
 
+// The other half's copies of two values in two v_permlane32_swap (each
+// swaps the upper half of its first operand with the lower half of its
+// second): (x, y) -> ([x.lo, y.lo], [x.hi, y.hi]) -> ([x.hi, x.lo],
+// [y.hi, y.lo]), with no per-lane select.
+__device__ inline void swap_halves2(float x, float y, float& sx, float& sy) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    const auto t = __builtin_amdgcn_permlane32_swap(r[1], r[0], false, false);
+    sx = __uint_as_float(t[0]);
+    sy = __uint_as_float(t[1]);
+}
+
 // Scores, spike tracking, softmax and P.V of one TurboQuant far tile.
 template <int D, int NQ, typename QOp>
 __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int tile, int lane, const AttnArgs& a,
                                       const QOp& qr, const QOp& qk, const float (&asum)[NQ]) {
-    constexpr int NS = D / 4, NH = D / 64, NG = D / 32;
+    constexpr int NS = D / 4, NH = D / 64;
     constexpr int KS = NQ == 1 ? 8 : NQ == 2 ? 4 : 2;
-    const int blk = lane >> 2, half = lane >> 5;
+    const int blk = lane >> 2;
     const bool general = a.tq_delta != 0.f;
     const PmConst pk = PmConst::make();
     fkv_f4 sh[NQ], sl[NQ], sq[NQ], sx[NQ];
@@ -1102,29 +1127,28 @@ __device__ inline void tq_far_compute(Lane<D, NQ>& st, const TqTile<D>& r, int t
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
     float px[NQ][4];
 #pragma unroll
-    for (int qd = 0; qd < NQ; qd++)
+    for (int qd = 0; qd < NQ; qd++) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) px[qd][e] = swap_halves(p[qd][e], half);
+        for (int e = 0; e < 4; e += 2) swap_halves2(p[qd][e], p[qd][e + 1], px[qd][e], px[qd][e + 1]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            p[qd][e] *= a.tq_lvl;
+            px[qd][e] *= a.tq_lvl;
+        }
+    }
 #pragma unroll
     for (int dh = 0; dh < NH; dh++) {
-        const int g = 2 * dh + half;  // the value group of the lane's dim
-        fkv_h4 w[4][NQ];              // [hi own, lo own, hi other, lo other][qd]
+        fkv_h4 w[2][NQ];  // [own, other][qd]: p * lvl * the scale of the lane's group 2dh + half
 #pragma unroll
         for (int qd = 0; qd < NQ; qd++) {
-            _Float16 w0[4], w1[4], w2[4], w3[4];
+            _Float16 w0[4], w1[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float so = p[qd][e] * half_of(r.so, e * NG + g);
-                const float sx2 = px[qd][e] * half_of(r.sx, e * NG + g);
-                w0[e] = (_Float16)(so * a.tq_lvh);
-                w1[e] = (_Float16)(so * a.tq_lvl);
-                w2[e] = (_Float16)(sx2 * a.tq_lvh);
-                w3[e] = (_Float16)(sx2 * a.tq_lvl);
+                w0[e] = (_Float16)(p[qd][e] * half_of(r.so, e * NH + dh));
+                w1[e] = (_Float16)(px[qd][e] * half_of(r.sx, e * NH + dh));
             }
             w[0][qd] = fkv_h4{w0[0], w0[1], w0[2], w0[3]};
             w[1][qd] = fkv_h4{w1[0], w1[1], w1[2], w1[3]};
-            w[2][qd] = fkv_h4{w2[0], w2[1], w2[2], w2[3]};
-            w[3][qd] = fkv_h4{w3[0], w3[1], w3[2], w3[3]};
         }
         const uint64_t v[4] = {plane_pair(r.v[dh].x), plane_pair(r.v[dh].y), plane_pair(r.v[dh].z),
                                plane_pair(r.v[dh].w)};
@@ -1320,9 +1344,9 @@ __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, in
             st.zsum[qd][NH + dh] += (c2[0] + c2[1]) + (c2[2] + c2[3]);
             w1[dh][qd] = fkv_h4{a1[0], a1[1], a1[2], a1[3]};
             const uint2 x = __builtin_bit_cast(uint2, fkv_h4{a2[0], a2[1], a2[2], a2[3]});
-            const uint2 y = make_uint2(__float_as_uint(swap_halves(__uint_as_float(x.x), half)),
-                                       __float_as_uint(swap_halves(__uint_as_float(x.y), half)));
-            w2[dh][qd] = __builtin_bit_cast(fkv_h4, y);
+            float y0, y1;
+            swap_halves2(__uint_as_float(x.x), __uint_as_float(x.y), y0, y1);
+            w2[dh][qd] = __builtin_bit_cast(fkv_h4, make_uint2(__float_as_uint(y0), __float_as_uint(y1)));
         }
     }
     uint4 v4[4];

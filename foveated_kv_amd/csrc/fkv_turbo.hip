@@ -103,9 +103,11 @@ __global__ void tq_pack_sn_kernel(const void* __restrict__ vscale, const void* _
         const int64_t bkv = i / L.F_pad;
         uint8_t* rec = tq_record(L, blob, bkv, t);
         const int lt = t % kTile;
-        uint16_t* sc = (uint16_t*)(rec + tq_sc_section(D)) + lt * NG;
+        uint16_t* sc = (uint16_t*)(rec + tq_sc_section(D));
         const int64_t tok = bkv * L.F + t;
-        for (int g = 0; g < NG; g++) sc[g] = t < L.F ? load_as_f16(vscale, tok * NG + g, dtype) : (uint16_t)0;
+        for (int g = 0; g < NG; g++)
+            sc[tq_sc_index(D, lt / 4, g % 2, lt % 4, g / 2)] = t < L.F ? load_as_f16(vscale, tok * NG + g, dtype)
+                                                                      : (uint16_t)0;
         uint32_t w = 0;
         if (t < L.F) w = (uint32_t)load_as_f16(knorm, tok, dtype) | ((uint32_t)load_as_f16(kgamma, tok, dtype) << 16);
         ((uint32_t*)(rec + tq_ng_section(D)))[lt] = w;
@@ -335,6 +337,10 @@ int fkv_turbo_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t 
         const double l0 = -1.0, l1 = (double)-0.333333f, l2 = (double)0.333333f, l3 = 1.0;
         h->tq.lvh = (float)((l2 + l3 - l0 - l1) / 4);
         h->tq.lvl = (float)((l1 + l3 - l0 - l2) / 4);
+        // the kernel expands the high-bit value plane to +-2 against
+        // weights scaled by lvl (one weight for both planes)
+        if (std::fabs(h->tq.lvh - 2.0 * h->tq.lvl) > 2e-6 * h->tq.lvh)
+            rc = fkv::set_error("fkv_turbo_create: value levels with lvh != 2 lvl (internal error)");
     }
     if (rc) {
         fkv_attn_destroy(h);
