@@ -1,6 +1,8 @@
 """Decode-time routing of a PyTorch model's attention through the fused
 gfx950 kernel, and the prefill -> compress -> decode loop around it
-(samfurr/foveated_kv src/foveated_kv/mlx_generate.py:38-590).
+(samfurr/foveated_kv src/foveated_kv/mlx_generate.py:38-416; its
+perplexity and passkey evaluations, :419-590, are model-level and not
+rebuilt).
 
 ``install_fused_sdpa`` replaces ``torch.nn.functional.scaled_dot_product_attention``
 with a closure (mlx_generate.py:84-131):
@@ -40,7 +42,6 @@ model must accept a device tensor as ``cache.offset`` (its RoPE positions
 computed as ``offset + arange(L)``).
 """
 
-import math
 import shutil
 import tempfile
 import time
@@ -53,10 +54,6 @@ import torch.nn.functional as F
 from . import _lib
 from .promotion import PromotionPipeline
 from .tier_cache import MLXFoveatedKVCache, MLXTierConfig
-
-
-def _log_softmax(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
-    return x - torch.logsumexp(x, dim=dim, keepdim=True)
 
 
 # ---------------------------------------------------------------------------
@@ -577,86 +574,3 @@ def _decode_graph(model, wrappers, pipeline, next_logits, max_tokens, eos, dev, 
     if eos is not None and eos in known:
         n_tok = min(n_tok, known.index(eos))
     return known[: min(n_tok, calls)], calls, t_issue
-
-
-def compute_perplexity(model, tokenizer, text: str, context_len: int = 4096, eval_len: int = 256,
-                       cfg: Optional[MLXTierConfig] = None):
-    """mlx_generate.py:419-496 -> (standard_ppl, foveated_ppl)."""
-    cfg = cfg or MLXTierConfig()
-    dev = _model_device(model)
-    all_tokens = torch.tensor(tokenizer.encode(text), dtype=torch.long, device=dev)
-    total = context_len + eval_len
-    if all_tokens.shape[0] < total:
-        raise ValueError(f"Text too short: {all_tokens.shape[0]} tokens, need {total}")
-    context = all_tokens[:context_len].reshape(1, -1)
-    evals = all_tokens[context_len:total]
-
-    def nll_over(cache, before_step=None):
-        nll = 0.0
-        for i in range(eval_len):
-            if before_step is not None:
-                before_step()
-            logits = model(evals[i:i + 1].reshape(1, 1), cache=cache)
-            lp = _log_softmax(logits[:, -1, :].float())
-            if i + 1 < eval_len:
-                nll -= float(lp[0, int(evals[i + 1])].item())
-        return nll
-
-    with torch.no_grad():
-        std = make_prompt_cache(model)
-        model(context, cache=std)
-        std_ppl = math.exp(nll_over(std) / max(eval_len - 1, 1))
-
-        fov_cache, _, _ = prefill_and_compress(model, context, cfg)
-        wrappers = [FusedCacheWrapper(layer, i) if layer is not None else None
-                    for i, layer in enumerate(fov_cache.layers)]
-        install_fused_sdpa(fov_cache)
-        try:
-            fov_ppl = math.exp(nll_over(wrappers, reset_fused_layer_counter) / max(eval_len - 1, 1))
-        finally:
-            uninstall_fused_sdpa()
-    return std_ppl, fov_ppl
-
-
-def _generate_short(model, tokenizer, prompt: str, max_tokens: int = 20):
-    """mlx_generate.py:568-590: greedy decode with the standard cache."""
-    dev = _model_device(model)
-    tokens = torch.tensor(tokenizer.encode(prompt), dtype=torch.long, device=dev).reshape(1, -1)
-    cache = make_prompt_cache(model)
-    generated = []
-    with torch.no_grad():
-        next_logits = model(tokens, cache=cache)[:, -1, :]
-        for _ in range(max_tokens):
-            tok = torch.argmax(next_logits, dim=-1)
-            token_id = int(tok.item())
-            if token_id == getattr(tokenizer, "eos_token_id", None):
-                break
-            generated.append(token_id)
-            next_logits = model(tok.reshape(1, 1), cache=cache)[:, -1, :]
-    return tokenizer.decode(generated), {"generated_tokens": len(generated)}
-
-
-def needle_test(model, tokenizer, context_len: int = 4096, needle_depth: float = 0.5,
-                cfg: Optional[MLXTierConfig] = None, seed: Optional[int] = None):
-    """mlx_generate.py:499-565: passkey retrieval with the standard cache and
-    with the fused foveated path -> (standard_found, foveated_found, info)."""
-    import random
-
-    cfg = cfg or MLXTierConfig()
-    passkey = str(random.Random(seed).randint(10000, 99999))
-    needle = f"The secret passkey is {passkey}. Remember it."
-    filler = "This is a document about various topics in science and technology. "
-    ask = "\nWhat is the secret passkey mentioned in the text above? The passkey is: "
-    n_fill = len(tokenizer.encode(filler))
-    avail = context_len - len(tokenizer.encode(needle)) - len(tokenizer.encode(ask)) - 10
-    before = int((avail * needle_depth) / n_fill)
-    after = int((avail * (1 - needle_depth)) / n_fill)
-    prompt_tokens = tokenizer.encode(filler * before + needle + filler * after + ask)[:context_len]
-    prompt = tokenizer.decode(prompt_tokens)
-
-    std_text, _ = _generate_short(model, tokenizer, prompt, max_tokens=20)
-    fov_text, _ = generate_fused(model, tokenizer, prompt, max_tokens=20, cfg=cfg, enable_promotion=True)
-    return passkey in std_text, passkey in fov_text, {
-        "passkey": passkey, "context_len": len(prompt_tokens), "needle_depth": needle_depth,
-        "standard_output": std_text, "foveated_output": fov_text,
-    }
