@@ -203,6 +203,9 @@ def main():
     ap.add_argument("--v-group", type=int, default=0, choices=(0, 32),
                     help="fp8 far tier V: INT4 scale/zero per token (0) or per 32-dim group (32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip timing the other benchmark configurations (reported under other_configs)")
+    ap.add_argument("--other-steps", type=int, default=30, help="timed steps per other configuration")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "attn_c3_16k_b8_traffic.txt"))
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--eager", action="store_true",
@@ -361,6 +364,18 @@ def main():
                               "what": f"torch dequant -> cat -> repeat_interleave -> SDPA (fp32), "
                                       f"{threads} threads"}},
         }
+    if not args.no_other_configs:
+        # every other benchmark configuration, timed the same way in this run
+        # (fewer steps; not the headline value)
+        others = {}
+        for name in synthetic.CONFIGS:
+            if name == args.config:
+                continue
+            others[name] = config_line(torch, dev, ext, synthetic, name, args.other_steps, 5, args.seed,
+                                       args.spikes, args.eager)
+            print(f"[bench] {name}: {others[name]['us_per_layer']} us/layer, {others[name]['gbs']} GB/s",
+                  file=sys.stderr, flush=True)
+        result["other_configs"] = others
     if args.copy_mib:
         result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)
         result["read_ceiling_gbs"], result["read_ceiling_launch"] = read_ceiling(torch, dev, args.copy_mib,
@@ -372,6 +387,50 @@ def main():
 
 
 SETTLE_MS = 300.0
+
+
+def config_line(torch, dev, ext, synthetic, name, steps, warmup, seed, spikes, eager):
+    """One benchmark configuration timed like the headline (distinct layer
+    blobs, HIP-graph replays, HIP events): us per layer and algorithmic
+    GB/s of the reference's per-token V layout (TurboQuant for C4)."""
+    B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[name]
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = 8
+    turbo = name.startswith("c4_turbo")
+    tb = ext.tier_boundaries_c(cfg, S)
+    R, F = tb["R_actual"], tb["far_count"]
+    k, v = synthetic.make_kv(B, Hkv, S, D, seed)
+    q = synthetic.make_query(B, Hq, D, seed)
+    synthetic.inject_spikes(k, q, tb["mid_start"], F, spikes, seed)
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
+    cl = ext.CompressHandle(cfg).compress_layer(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                                                with_archive=turbo)
+    if turbo:
+        from foveated_kv_amd import turbo as tq
+
+        tc = tq.get_turbo_constants(D)
+        tfar = tq.turbo_compress_keys(cl.archive_k, tc) + tq.turbo_compress_values(cl.archive_v)
+        cl.archive_k = cl.archive_v = None
+
+        def make_handle():
+            return tq.TurboFoveatedHandle(cl.near_k, cl.near_v, *tfar, cl.near_valid, tc.Pi, tc.S, tc.centroids,
+                                          spike_margin=10.0)
+    else:
+        def make_handle():
+            return ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                                      cl.near_valid, spike_margin=10.0)
+    qt = torch.from_numpy(q).to(dev)[:, :, None, :]
+    dkt = torch.from_numpy(dk).to(dev) if dk is not None else None
+    dvt = torch.from_numpy(dv).to(dev) if dv is not None else None
+    nbytes = (algorithmic_bytes_turbo(B, Hq, Hkv, D, R, F, n_dec) if turbo
+              else algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec))
+    L, _, ms = time_layers(torch, dev, make_handle, 0, qt, dkt, dvt, steps, warmup, eager)
+    us = ms * 1000.0 / L
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S, "n_decode": n_dec,
+            "far_format": "turboquant" if turbo else "fp8-e4m3 K + int4 per-token V",
+            "us_per_layer": round(us, 3), "gbs": round(gbs, 2), "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
+            "algorithmic_bytes": nbytes, "layers_per_step": L, "steps": steps}
 
 
 def settle_clocks(torch, stream, step, min_ms=SETTLE_MS):
