@@ -2362,33 +2362,67 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     }
     __syncthreads();
 
-    // ---- merge the 4 waves into wave 0's records ----
-    for (int h = wave; h < ng; h += WPG) {
-        float M = -INFINITY;
-        for (int w = 0; w < WPG; w++) M = fmaxf(M, smem[w * NHW * RS + h * RS]);
-        float sc[WPG];
-        float L = 0.f, mn2 = INFINITY, mx2 = -INFINITY;
-        int arg2 = INT_MAX;
-        for (int w = 0; w < WPG; w++) {
-            const float* r = smem + w * NHW * RS + h * RS;
-            sc[w] = r[0] == -INFINITY ? 0.f : __expf(r[0] - M);
-            L += sc[w] * r[1];
-            mn2 = fminf(mn2, r[2]);
-            const float fx = r[3];
-            const int fa = __float_as_int(r[4]);
-            if (fx > mx2 || (fx == mx2 && fa < arg2)) { mx2 = fx; arg2 = fa; }
+    // ---- merge the waves' records into wave 0's ----
+    // Wave w merges heads w, w + WPG, ...: every record value of its heads
+    // is read into registers before the first merged value is written (the
+    // writes go to wave 0's records, which the same loads read), so the
+    // reads issue as one batch.
+    {
+        constexpr int HPW = (NHW + WPG - 1) / WPG;  // heads per wave, at most
+        constexpr int VD = D / kWave;               // values per lane and head
+        float hm[HPW][WPG], hl[HPW][WPG], hn[HPW][WPG], hx[HPW][WPG];
+        int ha[HPW][WPG];
+        float hv[HPW][WPG][VD];
+#pragma unroll
+        for (int i = 0; i < HPW; i++) {
+            const int h = wave + i * WPG;
+            if (h < ng) {
+#pragma unroll
+                for (int w = 0; w < WPG; w++) {
+                    const float* r = smem + w * NHW * RS + h * RS;
+                    hm[i][w] = r[0];
+                    hl[i][w] = r[1];
+                    hn[i][w] = r[2];
+                    hx[i][w] = r[3];
+                    ha[i][w] = __float_as_int(r[4]);
+#pragma unroll
+                    for (int k = 0; k < VD; k++) hv[i][w][k] = r[kHdr + lane + k * kWave];
+                }
+            }
         }
-        for (int d = lane; d < D; d += kWave) {
-            float v = 0.f;
-            for (int w = 0; w < WPG; w++) v += sc[w] * smem[w * NHW * RS + h * RS + kHdr + d];
-            smem[h * RS + kHdr + d] = v;
-        }
-        if (lane == 0) {
-            smem[h * RS + 0] = M;
-            smem[h * RS + 1] = L;
-            smem[h * RS + 2] = mn2;
-            smem[h * RS + 3] = mx2;
-            smem[h * RS + 4] = __int_as_float(arg2);
+#pragma unroll
+        for (int i = 0; i < HPW; i++) {
+            const int h = wave + i * WPG;
+            if (h >= ng) continue;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < WPG; w++) M = fmaxf(M, hm[i][w]);
+            float sc[WPG];
+            float L = 0.f, mn2 = INFINITY, mx2 = -INFINITY;
+            int arg2 = INT_MAX;
+#pragma unroll
+            for (int w = 0; w < WPG; w++) {
+                sc[w] = hm[i][w] == -INFINITY ? 0.f : __expf(hm[i][w] - M);
+                L += sc[w] * hl[i][w];
+                mn2 = fminf(mn2, hn[i][w]);
+                const float fx = hx[i][w];
+                const int fa = ha[i][w];
+                if (fx > mx2 || (fx == mx2 && fa < arg2)) { mx2 = fx; arg2 = fa; }
+            }
+#pragma unroll
+            for (int k = 0; k < VD; k++) {
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < WPG; w++) v += sc[w] * hv[i][w][k];
+                smem[h * RS + kHdr + lane + k * kWave] = v;
+            }
+            if (lane == 0) {
+                smem[h * RS + 0] = M;
+                smem[h * RS + 1] = L;
+                smem[h * RS + 2] = mn2;
+                smem[h * RS + 3] = mx2;
+                smem[h * RS + 4] = __int_as_float(arg2);
+            }
         }
     }
     __syncthreads();
