@@ -1692,20 +1692,24 @@ __device__ inline void merge_values(const AttnArgs& a, const fkv_f4 (&v)[KV], fl
         a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
         a.tokens[o] = mx == -INFINITY ? -1 : arg;
     }
+    // in the load groups of 4: splits past the last have scale 0 and value 0
     fkv_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < KV; k++) {
-        if (k < nk) {
-            float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k));
+    for (int k0 = 0; k0 < KV; k0 += 4) {
+        if (k0 < nk) {
 #pragma unroll
-            for (int uu = 1; uu < SUB; uu++) {
-                const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k + uu));
-                fs = u == uu ? fu : fs;
+            for (int k = k0; k < k0 + 4 && k < KV; k++) {
+                float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k));
+#pragma unroll
+                for (int uu = 1; uu < SUB; uu++) {
+                    const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), SUB * k + uu));
+                    fs = u == uu ? fu : fs;
+                }
+                acc.x = fmaf(fs, v[k].x, acc.x);
+                acc.y = fmaf(fs, v[k].y, acc.y);
+                acc.z = fmaf(fs, v[k].z, acc.z);
+                acc.w = fmaf(fs, v[k].w, acc.w);
             }
-            acc.x = fmaf(fs, v[k].x, acc.x);
-            acc.y = fmaf(fs, v[k].y, acc.y);
-            acc.z = fmaf(fs, v[k].z, acc.z);
-            acc.w = fmaf(fs, v[k].w, acc.w);
         }
     }
     if (SUB == 4) {
@@ -1755,11 +1759,15 @@ __device__ inline void merge_loads(__amdgpu_buffer_rsrc_t rs, int ng, int nk, in
         h[i] = ld_rec4<CPOL>(rs, hoff);
         harg[i] = ld_rec1<CPOL>(rs, hoff + 16);
         const int voff = u * sstride + (g * RS + kHdr + 4 * c) * 4;
+        // in groups of 4 behind one branch: loads past the last split read
+        // 0 without touching memory (and meet scale 0)
 #pragma unroll
-        for (int k = 0; k < merge_kv<D, NH>(); k++)
-            if (k < nk)
-                v[i][k] = __builtin_bit_cast(
-                    fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, SUB * k * sstride, CPOL));
+        for (int k0 = 0; k0 < merge_kv<D, NH>(); k0 += 4)
+            if (k0 < nk)
+#pragma unroll
+                for (int k = k0; k < k0 + 4 && k < merge_kv<D, NH>(); k++)
+                    v[i][k] = __builtin_bit_cast(
+                        fkv_f4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, SUB * k * sstride, CPOL));
     }
 }
 
