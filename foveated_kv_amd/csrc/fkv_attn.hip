@@ -2124,11 +2124,13 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
             __builtin_amdgcn_global_load_lds((const void*)src, (FKV_LDS void*)(qw + k * kWave * 4), 4, 0, 0);
         }
     }
-    // the wave's first two far tiles need no device state either.  Rows of
-    // two or more head quads (fp8 far tier) issue them only once the query
-    // has landed: behind 25 MB of tile requests the query's loads come back
-    // late, and these rows' heavier tiles gain more from starting early
-    // (measured: C5 34.5 -> 33.7 us; rows of one quad lose 0.1-0.2 us)
+    // the wave's first two far tiles need no device state either.  Behind
+    // the launch's first 25 MB of tile requests the query's loads come back
+    // late, so the second tile is issued only once the query has landed,
+    // and rows of two or more head quads (fp8 far tier), whose tiles are
+    // heavier, issue the first one then too (measured: C5 34.5 -> 33.7 us,
+    // C3-16K 41.6 -> 41.2 us; rows of one quad lose 0.1-0.2 us when their
+    // first tile waits as well)
     constexpr bool QFIRST = !TQ && NQ >= 2;
     if (!QFIRST && un.nf > 0) issue(0);
     // TurboQuant: the rotation matrices' slices and the query are loaded
@@ -2149,10 +2151,9 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
             tq_q[k] = a.q[((int64_t)b * a.Hq + head0 + (h < ng ? h : 0)) * D + 4 * s + e];
         }
     }
-    // (TurboQuant: the waits for the rotation operands would also wait for a
-    // second tile issued here)
+    // the second far tile follows the query wait below (TurboQuant: in the
+    // stream; the waits for the rotation operands would also wait for it)
     const bool early1 = !TQ && un.nf > 1;
-    if (!QFIRST && early1) issue(1);
     // near_valid and a device decode count are written only by earlier
     // launches, so they are read as constant memory (scalar loads, whose
     // counter is not the one the ring's DMA uses)
@@ -2204,14 +2205,15 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         lds_barrier();
     } else {
         // the query DMA is this wave's oldest vector-memory op: wait for it
-        // but not for the ring (the wave's own copy: no barrier); QFIRST
-        // rows then issue their first two far tiles
+        // but not for the ring (the wave's own copy: no barrier), then issue
+        // the second far tile (QFIRST rows: the first two)
         if (QFIRST) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             if (un.nf > 0) issue(0);
             if (early1) issue(1);
         } else if (early1) {
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * FAR_OPS) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FAR_OPS) : "memory");
+            issue(1);
         } else if (un.nf > 0) {
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FAR_OPS) : "memory");
         } else {
