@@ -2132,10 +2132,12 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     // C3-16K 41.6 -> 41.2 us; rows of one quad lose 0.1-0.2 us when their
     // first tile waits as well)
     constexpr bool QFIRST = !TQ && NQ >= 2;
-    if (!QFIRST && un.nf > 0) issue(0);
+    if (!TQ && !QFIRST && un.nf > 0) issue(0);
     // TurboQuant: the rotation matrices' slices and the query are loaded
-    // together, right after the first tile's DMA, so their latencies overlap
-    // (a wait for any of them also waits for the older DMA)
+    // together, before any tile: the first far tile's DMA is issued once the
+    // rotation is done, so the waits for the rotation's operands (in-order
+    // counter) do not also wait for a tile behind 25 MB of others (measured:
+    // C4 18.9 -> 18.3 us; issuing both first tiles then is slower, 19.3)
     TqRotation<D> rot;
     constexpr int NT = kWave * WPG;  // threads of the workgroup
     uint16_t tq_q[TQ ? (NQ * NS * 16 + NT - 1) / NT : 1];
@@ -2170,6 +2172,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         }
         lds_barrier();
         tq_rotate_query<D, NQ, WPG>(a, rot, QOperand<NS>{qs, j * 4}, qf, qt, rsum, wave, lane);
+        if (un.nf > 0) issue(0);
         if (a.tq_alpha != 0.f) {
 #pragma unroll
             for (int qd = 0; qd < NQ; qd++) asum[qd] = rsum[4 * qd + j];
