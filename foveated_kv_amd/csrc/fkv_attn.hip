@@ -330,10 +330,17 @@ __device__ inline fkv_h4 e4m3x4(uint32_t w) {
 // INT4 dword -> the 4 tokens of 4-token group 2u (bp = 0) or 2u+1 (bp = 1)
 // as fp16 (16 + c), exact: the nibble lands in mantissa bits 6..9 of an
 // exponent-19 half.
+// The mask and the exponent bits are held in registers (empty asm, no
+// instruction): gfx9 VOP3 takes no literal, so with folded constants each
+// half costs a shift, an AND and an OR instead of a shift and one
+// v_and_or_b32.
 __device__ inline fkv_h4 int4x4(uint32_t w, int bp) {
-    const uint32_t a = bp ? ((w >> 2) & 0x03C003C0u) : ((w << 6) & 0x03C003C0u);
-    const uint32_t b = bp ? ((w >> 6) & 0x03C003C0u) : ((w << 2) & 0x03C003C0u);
-    return h4_of(a | 0x4C004C00u, b | 0x4C004C00u);
+    uint32_t m = 0x03C003C0u, e = 0x4C004C00u;
+    asm("" : "+s"(m));
+    asm("" : "+v"(e));
+    const uint32_t a = bp ? (w >> 2) : (w << 6);
+    const uint32_t b = bp ? (w >> 6) : (w << 2);
+    return h4_of((a & m) | e, (b & m) | e);
 }
 
 // broadcast lane i of each lane quad (DPP quad_perm)
