@@ -485,6 +485,40 @@ struct QOperand {
         o[6] = __builtin_bit_cast(fkv_h4, r6);
         o[7] = __builtin_bit_cast(fkv_h4, r7);
     }
+    // read8 of quads 0 and 1 in one asm block: one wait for both
+    __device__ void read8x2(int s0, fkv_h4 (&o)[2][8]) const {
+        static_assert(NS * 32 + 224 < 65536, "ds_read offset");
+        const uint32_t addr = lds_addr(qs + base + s0 * 16);
+        fkv_v2u r[16];
+        asm volatile(
+            "ds_read_b64 %0, %16\n"
+            "ds_read_b64 %1, %16 offset:32\n"
+            "ds_read_b64 %2, %16 offset:64\n"
+            "ds_read_b64 %3, %16 offset:96\n"
+            "ds_read_b64 %4, %16 offset:128\n"
+            "ds_read_b64 %5, %16 offset:160\n"
+            "ds_read_b64 %6, %16 offset:192\n"
+            "ds_read_b64 %7, %16 offset:224\n"
+            "ds_read_b64 %8, %16 offset:%17\n"
+            "ds_read_b64 %9, %16 offset:%17+32\n"
+            "ds_read_b64 %10, %16 offset:%17+64\n"
+            "ds_read_b64 %11, %16 offset:%17+96\n"
+            "ds_read_b64 %12, %16 offset:%17+128\n"
+            "ds_read_b64 %13, %16 offset:%17+160\n"
+            "ds_read_b64 %14, %16 offset:%17+192\n"
+            "ds_read_b64 %15, %16 offset:%17+224\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
+              "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]),
+              "=&v"(r[14]), "=&v"(r[15])
+            : "v"(addr), "n"(NS * 32)
+            : "memory");
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            o[0][i] = __builtin_bit_cast(fkv_h4, r[i]);
+            o[1][i] = __builtin_bit_cast(fkv_h4, r[8 + i]);
+        }
+    }
     // N (2, 4 or 8) k-steps s0.. of quad qd (see lds_q)
     template <int N>
     __device__ void readn(int qd, int s0, fkv_h4 (&o)[N]) const;
@@ -744,8 +778,12 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
 #pragma unroll
     for (int s0 = 0; s0 < NS; s0 += 8) {
         fkv_h4 q8[NQ][8];
+        if constexpr (NQ == 2) {
+            q_lds.read8x2(s0, q8);
+        } else {
 #pragma unroll
-        for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+            for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+        }
 #pragma unroll
         for (int s = s0; s < s0 + 8; s++) {
             const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
@@ -1299,8 +1337,12 @@ __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, in
 #pragma unroll
     for (int s0 = 0; s0 < NS; s0 += 8) {
         fkv_h4 q8[NQ][8];
+        if constexpr (NQ == 2) {
+            q_lds.read8x2(s0, q8);
+        } else {
 #pragma unroll
-        for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+            for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+        }
 #pragma unroll
         for (int s = s0; s < s0 + 8; s++) {
             const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
