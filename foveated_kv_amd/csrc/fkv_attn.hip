@@ -485,6 +485,54 @@ struct QOperand {
         o[6] = __builtin_bit_cast(fkv_h4, r6);
         o[7] = __builtin_bit_cast(fkv_h4, r7);
     }
+    // read8x2 over 16 k-steps: one wait for 32 reads
+    __device__ void read16x2(int s0, fkv_h4 (&o)[2][16]) const {
+        static_assert(NS * 32 + 480 < 65536, "ds_read offset");
+        const uint32_t addr = lds_addr(qs + base + s0 * 16);
+        fkv_v2u r[32];
+        asm volatile(
+            "ds_read_b64 %0, %32\n"
+            "ds_read_b64 %1, %32 offset:32\n"
+            "ds_read_b64 %2, %32 offset:64\n"
+            "ds_read_b64 %3, %32 offset:96\n"
+            "ds_read_b64 %4, %32 offset:128\n"
+            "ds_read_b64 %5, %32 offset:160\n"
+            "ds_read_b64 %6, %32 offset:192\n"
+            "ds_read_b64 %7, %32 offset:224\n"
+            "ds_read_b64 %8, %32 offset:256\n"
+            "ds_read_b64 %9, %32 offset:288\n"
+            "ds_read_b64 %10, %32 offset:320\n"
+            "ds_read_b64 %11, %32 offset:352\n"
+            "ds_read_b64 %12, %32 offset:384\n"
+            "ds_read_b64 %13, %32 offset:416\n"
+            "ds_read_b64 %14, %32 offset:448\n"
+            "ds_read_b64 %15, %32 offset:480\n"
+            "ds_read_b64 %16, %32 offset:%33\n"
+            "ds_read_b64 %17, %32 offset:%33+32\n"
+            "ds_read_b64 %18, %32 offset:%33+64\n"
+            "ds_read_b64 %19, %32 offset:%33+96\n"
+            "ds_read_b64 %20, %32 offset:%33+128\n"
+            "ds_read_b64 %21, %32 offset:%33+160\n"
+            "ds_read_b64 %22, %32 offset:%33+192\n"
+            "ds_read_b64 %23, %32 offset:%33+224\n"
+            "ds_read_b64 %24, %32 offset:%33+256\n"
+            "ds_read_b64 %25, %32 offset:%33+288\n"
+            "ds_read_b64 %26, %32 offset:%33+320\n"
+            "ds_read_b64 %27, %32 offset:%33+352\n"
+            "ds_read_b64 %28, %32 offset:%33+384\n"
+            "ds_read_b64 %29, %32 offset:%33+416\n"
+            "ds_read_b64 %30, %32 offset:%33+448\n"
+            "ds_read_b64 %31, %32 offset:%33+480\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]), "=&v"(r[15]), "=&v"(r[16]), "=&v"(r[17]), "=&v"(r[18]), "=&v"(r[19]), "=&v"(r[20]), "=&v"(r[21]), "=&v"(r[22]), "=&v"(r[23]), "=&v"(r[24]), "=&v"(r[25]), "=&v"(r[26]), "=&v"(r[27]), "=&v"(r[28]), "=&v"(r[29]), "=&v"(r[30]), "=&v"(r[31])
+            : "v"(addr), "n"(NS * 32)
+            : "memory");
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            o[0][i] = __builtin_bit_cast(fkv_h4, r[i]);
+            o[1][i] = __builtin_bit_cast(fkv_h4, r[16 + i]);
+        }
+    }
     // read8 of quads 0 and 1 in one asm block: one wait for both
     __device__ void read8x2(int s0, fkv_h4 (&o)[2][8]) const {
         static_assert(NS * 32 + 224 < 65536, "ds_read offset");
@@ -775,20 +823,31 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
     fkv_f4 sacc[NQ];
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) sacc[qd] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (NQ == 2) {
+        // two quads: 16 k-steps of both quads' operands per LDS batch
 #pragma unroll
-    for (int s0 = 0; s0 < NS; s0 += 8) {
-        fkv_h4 q8[NQ][8];
-        if constexpr (NQ == 2) {
-            q_lds.read8x2(s0, q8);
-        } else {
+        for (int s0 = 0; s0 < NS; s0 += 16) {
+            fkv_h4 q16[2][16];
+            q_lds.read16x2(s0, q16);
+#pragma unroll
+            for (int s = s0; s < s0 + 16; s++) {
+                const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
+                sacc[0] = mfma4_local(k4, q16[0][s - s0], sacc[0]);
+                sacc[1] = mfma4_local(k4, q16[1][s - s0], sacc[1]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int s0 = 0; s0 < NS; s0 += 8) {
+            fkv_h4 q8[NQ][8];
 #pragma unroll
             for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
-        }
 #pragma unroll
-        for (int s = s0; s < s0 + 8; s++) {
-            const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
+            for (int s = s0; s < s0 + 8; s++) {
+                const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
 #pragma unroll
-            for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k4, q8[qd][s - s0], sacc[qd]);
+                for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k4, q8[qd][s - s0], sacc[qd]);
+            }
         }
     }
     fkv_h4 w4[NQ];
