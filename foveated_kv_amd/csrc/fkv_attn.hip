@@ -829,11 +829,15 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
         for (int s0 = 0; s0 < NS; s0 += 16) {
             fkv_h4 q16[2][16];
             q_lds.read16x2(s0, q16);
+            // every key operand of the batch converted before the first MFMA
+            // (a conversion feeding the next MFMA directly costs wait states)
+            fkv_h4 k16[16];
+#pragma unroll
+            for (int s = s0; s < s0 + 16; s++) k16[s - s0] = e4m3x4(word_of(r.k[s >> 2], s & 3));
 #pragma unroll
             for (int s = s0; s < s0 + 16; s++) {
-                const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
-                sacc[0] = mfma4_local(k4, q16[0][s - s0], sacc[0]);
-                sacc[1] = mfma4_local(k4, q16[1][s - s0], sacc[1]);
+                sacc[0] = mfma4_local(k16[s - s0], q16[0][s - s0], sacc[0]);
+                sacc[1] = mfma4_local(k16[s - s0], q16[1][s - s0], sacc[1]);
             }
         }
     } else {
@@ -842,12 +846,13 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
             fkv_h4 q8[NQ][8];
 #pragma unroll
             for (int qd = 0; qd < NQ; qd++) q_lds.read8(qd, s0, q8[qd]);
+            fkv_h4 k8[8];
 #pragma unroll
-            for (int s = s0; s < s0 + 8; s++) {
-                const fkv_h4 k4 = e4m3x4(word_of(r.k[s >> 2], s & 3));
+            for (int s = s0; s < s0 + 8; s++) k8[s - s0] = e4m3x4(word_of(r.k[s >> 2], s & 3));
 #pragma unroll
-                for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k4, q8[qd][s - s0], sacc[qd]);
-            }
+            for (int s = s0; s < s0 + 8; s++)
+#pragma unroll
+                for (int qd = 0; qd < NQ; qd++) sacc[qd] = mfma4_local(k8[s - s0], q8[qd][s - s0], sacc[qd]);
         }
     }
     fkv_h4 w4[NQ];
