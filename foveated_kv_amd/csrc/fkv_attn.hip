@@ -749,24 +749,61 @@ __device__ inline void pv_group(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vop
     }
 }
 
-template <int D, int NQ, typename VOp>
+// The MFMAs of group G with its value operands already formed.
+template <int D, int NQ, int G>
+__device__ inline void pv_mfma(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], const fkv_h4 (&v)[D / 64]) {
+#pragma unroll
+    for (int dh = 0; dh < D / 64; dh++)
+#pragma unroll
+        for (int qd = 0; qd < NQ; qd++) st.acc[qd][dh] = mfma4<G>(w4[qd], v[dh], st.acc[qd][dh]);
+}
+
+// Groups G0 .. G0 + 7: every value operand formed (or loaded) before the
+// first MFMA: an operand feeding the next MFMA directly costs wait states,
+// and operands gathered from global memory then share one round trip.
+template <int D, int NQ, int G0, typename VOp>
+__device__ inline void pv_batch8(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vop) {
+    fkv_h4 v[8][D / 64];
+#pragma unroll
+    for (int g = 0; g < 8; g++)
+#pragma unroll
+        for (int dh = 0; dh < D / 64; dh++) v[g][dh] = vop(G0 + g, dh);
+    pv_mfma<D, NQ, G0 + 0>(st, w4, v[0]);
+    pv_mfma<D, NQ, G0 + 1>(st, w4, v[1]);
+    pv_mfma<D, NQ, G0 + 2>(st, w4, v[2]);
+    pv_mfma<D, NQ, G0 + 3>(st, w4, v[3]);
+    pv_mfma<D, NQ, G0 + 4>(st, w4, v[4]);
+    pv_mfma<D, NQ, G0 + 5>(st, w4, v[5]);
+    pv_mfma<D, NQ, G0 + 6>(st, w4, v[6]);
+    pv_mfma<D, NQ, G0 + 7>(st, w4, v[7]);
+}
+
+// The P.V of one 64-token tile over the 16 groups of 4 tokens, the value
+// operands formed BATCH groups at a time (1 or 8).
+template <int D, int NQ, int BATCH = 1, typename VOp>
 __device__ inline void pv_all(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vop) {
-    pv_group<D, NQ, 0>(st, w4, vop);
-    pv_group<D, NQ, 1>(st, w4, vop);
-    pv_group<D, NQ, 2>(st, w4, vop);
-    pv_group<D, NQ, 3>(st, w4, vop);
-    pv_group<D, NQ, 4>(st, w4, vop);
-    pv_group<D, NQ, 5>(st, w4, vop);
-    pv_group<D, NQ, 6>(st, w4, vop);
-    pv_group<D, NQ, 7>(st, w4, vop);
-    pv_group<D, NQ, 8>(st, w4, vop);
-    pv_group<D, NQ, 9>(st, w4, vop);
-    pv_group<D, NQ, 10>(st, w4, vop);
-    pv_group<D, NQ, 11>(st, w4, vop);
-    pv_group<D, NQ, 12>(st, w4, vop);
-    pv_group<D, NQ, 13>(st, w4, vop);
-    pv_group<D, NQ, 14>(st, w4, vop);
-    pv_group<D, NQ, 15>(st, w4, vop);
+    static_assert(BATCH == 1 || BATCH == 8, "batch of 1 or 8 groups");
+    if constexpr (BATCH == 8) {
+        pv_batch8<D, NQ, 0>(st, w4, vop);
+        pv_batch8<D, NQ, 8>(st, w4, vop);
+    } else {
+        pv_group<D, NQ, 0>(st, w4, vop);
+        pv_group<D, NQ, 1>(st, w4, vop);
+        pv_group<D, NQ, 2>(st, w4, vop);
+        pv_group<D, NQ, 3>(st, w4, vop);
+        pv_group<D, NQ, 4>(st, w4, vop);
+        pv_group<D, NQ, 5>(st, w4, vop);
+        pv_group<D, NQ, 6>(st, w4, vop);
+        pv_group<D, NQ, 7>(st, w4, vop);
+        pv_group<D, NQ, 8>(st, w4, vop);
+        pv_group<D, NQ, 9>(st, w4, vop);
+        pv_group<D, NQ, 10>(st, w4, vop);
+        pv_group<D, NQ, 11>(st, w4, vop);
+        pv_group<D, NQ, 12>(st, w4, vop);
+        pv_group<D, NQ, 13>(st, w4, vop);
+        pv_group<D, NQ, 14>(st, w4, vop);
+        pv_group<D, NQ, 15>(st, w4, vop);
+    }
 }
 
 // Online-softmax update of head quad qd for one 64-token tile (scores s[e]
@@ -871,7 +908,9 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
         any |= softmax_w<D, NQ, true>(st, qd, sc, sz, w4[qd]);
     }
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
-    pv_all<D, NQ>(st, w4, [&](int g, int dh) {
+    // one head quad: operands in batches; more quads: group by group (their
+    // accumulators leave no registers for a batch)
+    pv_all<D, NQ, NQ == 1 ? 8 : 1>(st, w4, [&](int g, int dh) {
         const int u = dh * 8 + (g >> 1);
         return int4x4(word_of(r.v[u >> 2], u & 3), g & 1);
     });
@@ -1517,7 +1556,7 @@ __device__ inline void fp16_compute(Lane<D, NQ>& st, KOp kop, VOp vop, int tile,
         any |= softmax_w<D, NQ, false>(st, qd, sc, szd, w4[qd]);
     }
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;
-    pv_all<D, NQ>(st, w4, vop);
+    pv_all<D, NQ, 8>(st, w4, vop);
 }
 
 // Min-near tracking, softmax and P.V of an fp16 tile whose scores are in
