@@ -583,11 +583,12 @@ def run_e2e(args, torch, dev):
 
     def loop_graph():
         """The device-drain loop with the decode step captured once in a HIP
-        graph: advance the decode-row count n (a device int32), gather the
+        graph: with n (a device int32) the step's decode-row count, gather the
         query of step n - 1, attention over the fixed-capacity decode buffer,
         the drain kernel with n as its step (the filter only compares steps,
-        so the +1 offset changes nothing).  Step 0 runs eagerly (it sizes the
-        workspaces), steps 1.. are graph replays with nothing read back."""
+        so the +1 offset changes nothing), which then advances n.  Step 0
+        runs eagerly (it sizes the workspaces), steps 1.. are graph replays
+        with nothing read back."""
         t0 = time.perf_counter()
         cl, h = compress()
         torch.cuda.synchronize()
@@ -595,15 +596,14 @@ def run_e2e(args, torch, dev):
         pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
         pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
         pipe.register_blob(0, h)
-        n_d = torch.zeros(1, dtype=torch.int32, device=dev)
+        n_d = torch.ones(1, dtype=torch.int32, device=dev)
         q1 = torch.cat([qs[:1], qs])  # row n holds the query of step n - 1
         q_d = torch.empty((1,) + tuple(qs.shape[1:]), dtype=qs.dtype, device=dev)
 
         def one():
-            n_d.add_(1)
             torch.index_select(q1, 0, n_d, out=q_d)
             out, flags, toks = h(q_d[0], dkt, dvt, n_decode=n_d)
-            pipe.drain_spikes_device(0, flags, toks, fdev, n_d)
+            pipe.drain_spikes_device(0, flags, toks, fdev, n_d, advance_step=True)
             return out
 
         one()
@@ -617,7 +617,7 @@ def run_e2e(args, torch, dev):
             g.replay()
         torch.cuda.synchronize()
         loop_s = time.perf_counter() - t0
-        assert int(n_d.item()) == steps, "graph replays did not advance the step counter"
+        assert int(n_d.item()) == steps + 1, "graph replays did not advance the step counter"
         return {"us_per_step": loop_s / max(steps - 1, 1) * 1e6, "compress_ms": compress_ms,
                 "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
 
@@ -644,7 +644,7 @@ def run_e2e(args, torch, dev):
                    "headroom": int(cl.near_k.shape[2] - cl.near_valid[0]), "spike_frac": args.spikes,
                    "partition": "importance (seeded N(0,1) scores)", "query_drift_eps": 0.05,
                    "drain": "device (filter + row copies in one kernel after each attention launch)",
-                   "launch": "one HIP graph replay per step (row counter, query gather, attention, drain); "
+                   "launch": "one HIP graph replay per step (query gather, attention, drain + step advance); "
                              "step 0 eager",
                    "far_format": "fp8-e4m3 K + int4 group-32 V" if args.v_group else "fp8-e4m3 K + int4 per-token V"},
         "compress_ms": round(gres["compress_ms"], 3),

@@ -109,7 +109,7 @@ SIGNATURES = {
     "fkv_promoter_register_archive_files": (ctypes.c_int, [P, I32, ctypes.c_char_p, ctypes.c_char_p, I32, I32,
                                                            I32, P]),
     "fkv_promoter_register_handle": (ctypes.c_int, [P, I32, P, P]),
-    "fkv_promoter_drain_device": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, I32, I32, P, P]),
+    "fkv_promoter_drain_device": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, I32, I32, P, I32, P]),
     "fkv_promoter_drain": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, I32, I32]),
     "fkv_promoter_pending": (ctypes.c_int, [P, P, I32]),
     "fkv_promoter_flush": (ctypes.c_int, [P]),

@@ -170,7 +170,8 @@ struct DrainArgs {
     const int32_t* tokens;
     const int32_t* far_idx;
     int B, Hq, Hkv, N_far, step, cooldown, budget;
-    const int32_t* step_dev;  // when set, the step is read here
+    int32_t* step_dev;  // when set, the step is read here
+    int advance;        // then step + 1 is stored there once every thread has read it
     int32_t* last_step;
     uint32_t* promoted;
     const int32_t* pos_to_local;
@@ -298,6 +299,13 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
     }
     __syncthreads();
     if (tid < n) ((uint32_t*)(a.blob + a.L.near_valid))[rec_h[tid]] = (uint32_t)(rec_slot[tid] + 1);
+    // every thread read the step before the barriers above
+    if (a.advance && tid == 0) *a.step_dev = step + 1;
+}
+
+// The step advance of a drain that has nothing to launch.
+__global__ __launch_bounds__(64) void advance_step_kernel(int32_t* step_dev) {
+    if (threadIdx.x == 0) *step_dev += 1;
 }
 
 // Device state of a layer for the device drain, made on its first use.
@@ -525,20 +533,27 @@ int fkv_promoter_pending(const fkv_promoter* p, int32_t* out_records, int32_t ma
 
 int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* flags, const int32_t* tokens,
                               const int32_t* far_idx, int32_t B, int32_t Hq, int32_t Hkv, int32_t N_far, int32_t step,
-                              const int32_t* step_dev, void* stream) {
+                              int32_t* step_dev, int32_t advance_step, void* stream) {
     if (!p) return set_error("fkv_promoter_drain_device: NULL pipeline");
-    if (layer < 0 || layer >= p->n_layers) return 0;
+    if (advance_step && !step_dev) return set_error("fkv_promoter_drain_device: advance_step needs step_dev");
+    hipStream_t st = (hipStream_t)stream;
+    // a call with nothing to drain still advances the step
+    auto nothing = [&]() -> int {
+        if (!advance_step) return FKV_OK;
+        hipLaunchKernelGGL(advance_step_kernel, dim3(1), dim3(64), 0, st, step_dev);
+        return check_hip(hipGetLastError(), "advance_step_kernel launch");
+    };
+    if (layer < 0 || layer >= p->n_layers) return nothing();
     const Archive& arc = p->arch[layer];
     fkv_attn* h = p->handles[layer];
-    if (!arc.k || arc.S == 0 || !h) return 0;  // nothing to promote from or into (as the host drain)
-    if (B <= 0 || Hq <= 0 || Hkv <= 0 || !flags || !tokens || !far_idx) return 0;
+    if (!arc.k || arc.S == 0 || !h) return nothing();  // nothing to promote from or into (as the host drain)
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || !flags || !tokens || !far_idx) return nothing();
     if (Hkv > kMaxDrainHeads || Hkv != arc.Hkv || Hkv != h->L.Hkv || arc.D != h->L.D)
         return set_error("fkv_promoter_drain_device: archive, handle and spike shapes disagree (or H_kv > 256)");
     if (p->mode[layer] == kDrainHost)
         return set_error("fkv_promoter_drain_device: layer " + std::to_string(layer) +
                          " is drained on the host; its headroom slots are assigned there");
     p->mode[layer] = kDrainDevice;
-    hipStream_t st = (hipStream_t)stream;
     if (int rc = ensure_dev_drain(p, layer, st)) return rc;
     const DevDrain& d = p->dev[layer];
     DrainArgs a;
@@ -551,6 +566,7 @@ int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* fla
     a.N_far = N_far;
     a.step = step;
     a.step_dev = step_dev;
+    a.advance = advance_step != 0;
     a.cooldown = p->cooldown;
     a.budget = p->max_per_drain;
     a.last_step = d.last_step;

@@ -120,7 +120,7 @@ class PromotionPipeline:
             self.flush()
         return n
 
-    def drain_spikes_device(self, layer_idx, spike_flags, spike_tokens, far_idx, current_step):
+    def drain_spikes_device(self, layer_idx, spike_flags, spike_tokens, far_idx, current_step, advance_step=False):
         """The same drain and promotion as ``drain_spikes`` + ``flush``, as one
         kernel on torch's current stream of the tensors' device: spike outputs
         (B, H_q) and far_idx (B, H_kv, N_far) int32 stay in device memory and
@@ -128,7 +128,10 @@ class PromotionPipeline:
         stream sees the promoted rows.  Needs the archive registered with
         ``register_archive_tensors`` (pinned copy) or from files.  A layer
         drained here cannot also be drained by ``drain_spikes`` (the library
-        rejects the second kind of drain on a layer)."""
+        rejects the second kind of drain on a layer).  ``advance_step`` (with a
+        device step): the stream's work then stores step + 1 into
+        ``current_step`` once the drain has read it, so a captured decode
+        step needs no separate counter update."""
         if self._stopped:
             return
         for t in (spike_flags, spike_tokens, far_idx):
@@ -141,11 +144,14 @@ class PromotionPipeline:
         step_dev = current_step if isinstance(current_step, torch.Tensor) else None
         if step_dev is not None and not (step_dev.is_cuda and step_dev.dtype == torch.int32):
             raise TypeError("a device step must be an int32 device tensor")
+        if advance_step and step_dev is None:
+            raise TypeError("advance_step needs the step as an int32 device tensor")
         with torch.cuda.device(dev):
             check(self._lib.fkv_promoter_drain_device(self._h, int(layer_idx), _lib.ptr(spike_flags),
                                                       _lib.ptr(spike_tokens), _lib.ptr(far_idx), B, Hq, Hkv, n_far,
                                                       0 if step_dev is not None else int(current_step),
-                                                      _lib.ptr(step_dev), _lib.stream_ptr(dev)),
+                                                      _lib.ptr(step_dev), 1 if advance_step else 0,
+                                                      _lib.stream_ptr(dev)),
                   "fkv_promoter_drain_device")
         self._keep[("dev", int(layer_idx))] = (spike_flags, spike_tokens, far_idx)
 

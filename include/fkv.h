@@ -369,10 +369,15 @@ int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* spike_flag
  * the blob (synchronising).  Statistics accumulate on the device and
  * fkv_promoter_get_stats adds them (synchronising).
  * step_dev (may be NULL): the decode step is read from this device int32
- * instead of `step` (a graph-captured step keeps its counter on the GPU). */
+ * instead of `step` (a graph-captured step keeps its counter on the GPU).
+ * advance_step (needs step_dev): once the drain has read the step, the
+ * stream's work stores step + 1 into *step_dev, on every successful call,
+ * so a captured decode step needs no separate counter update; without
+ * step_dev it returns FKV_EINVAL. */
 int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* spike_flags,
                               const int32_t* spike_tokens, const int32_t* far_idx, int32_t B, int32_t Hq,
-                              int32_t Hkv, int32_t N_far, int32_t step, const int32_t* step_dev, void* stream);
+                              int32_t Hkv, int32_t N_far, int32_t step, int32_t* step_dev, int32_t advance_step,
+                              void* stream);
 
 /* Queued records (not yet flushed): returns their count and copies up to
  * max_records of them as int32 [layer, head, archive row, position]. */

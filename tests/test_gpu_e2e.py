@@ -86,11 +86,10 @@ def _loop(orc, B, Hq, Hkv, D, S, steps, vg, mode, check_every):
     n_d = torch.zeros(1, dtype=torch.int32, device="cuda")
     graph = graph_res = None
 
-    def one():  # the captured step: count from the step, attention, drain, advance
+    def one():  # the captured step: count from the step, attention, drain (which advances the step)
         torch.add(step_d, 1, out=n_d)
         res = h(q_st, dkt, dvt, n_decode=n_d)
-        pipe.drain_spikes_device(0, res[1], res[2], fdev, step_d)
-        step_d.add_(1)
+        pipe.drain_spikes_device(0, res[1], res[2], fdev, step_d, advance_step=True)
         return res
 
     for t in range(steps):

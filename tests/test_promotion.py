@@ -290,7 +290,8 @@ def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroo
     """drain_spikes_device (filter + promotion in one kernel, spike outputs
     and far_idx in device memory) against the CPU restatement of the host
     drain + flush on random flag streams: same near tiers, near_valid and
-    statistics."""
+    statistics.  Batches above 1 keep the step on the device and let the
+    drain advance it."""
     import torch
 
     from foveated_kv_amd.promotion import PromotionPipeline
@@ -313,16 +314,64 @@ def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroo
     nv = {0: cl.near_valid.cpu().numpy().copy()}
     rng = np.random.default_rng(B * 10 + budget)
     n_far = far_idx.shape[2]
+    step_d = torch.zeros(1, dtype=torch.int32, device="cuda") if B > 1 else None
     for step in range(30):
         flags = (rng.random((B, Hq)) < 0.4).astype(np.int32)
         tokens = rng.integers(0, min(n_far, 40), size=(B, Hq)).astype(np.int32)  # repeats exercise dedup
         tokens[rng.random((B, Hq)) < 0.05] = -1
-        pipe.drain_spikes_device(0, torch.from_numpy(flags).cuda(), torch.from_numpy(tokens).cuda(), fdev, step)
+        fl, tk = torch.from_numpy(flags).cuda(), torch.from_numpy(tokens).cuda()
+        if step_d is None:
+            pipe.drain_spikes_device(0, fl, tk, fdev, step)
+        else:
+            pipe.drain_spikes_device(0, fl, tk, fdev, step_d, advance_step=True)
         ref.drain(0, flags, tokens, far_idx, step)
         ref.commit(near_k, near_v, nv, {0: cl.near_k.shape[2]})
     torch.cuda.synchronize()
+    if step_d is not None:
+        assert int(step_d.item()) == 30
     gk, gv = h.export_near()
     assert h.read_near_valid() == [int(x) for x in nv[0]]
     assert np.array_equal(gk.cpu().numpy().view(np.uint16), near_k[0].view(np.uint16))
     assert np.array_equal(gv.cpu().numpy().view(np.uint16), near_v[0].view(np.uint16))
     assert pipe.get_stats() == ref.stats and ref.stats["promotions_completed"] > 0
+
+
+@pytest.mark.gpu
+def test_device_drain_step_advance_without_work():
+    """advance_step advances the device step on every successful call, also
+    where the drain has nothing to launch (a layer with no archive or blob
+    registered); it needs a device step (TypeError in Python, FKV_EINVAL
+    through the C ABI)."""
+    import ctypes
+
+    import torch
+
+    from foveated_kv_amd import _lib
+    from foveated_kv_amd.promotion import PromotionPipeline
+    from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
+
+    print("device drain step advance", flush=True)
+    B, Hkv, D, S = 1, 2, 64, 400
+    k, v, cl, h = _layer(B, Hkv, D, S, 7)
+    _, far_idx = tier_index_tensors(TierConfig(promo_headroom_min=8).tier_boundaries(S), S, B, Hkv, "cpu")
+    far_idx = far_idx.numpy()
+    pipe = PromotionPipeline(2, cooldown_steps=1, max_per_drain=4)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_blob(0, h)
+    fdev = torch.from_numpy(far_idx).cuda().contiguous()
+    flags = torch.zeros((B, 4 * Hkv), dtype=torch.int32, device="cuda")
+    toks = torch.full((B, 4 * Hkv), -1, dtype=torch.int32, device="cuda")
+    step_d = torch.full((1,), 5, dtype=torch.int32, device="cuda")
+    pipe.drain_spikes_device(0, flags, toks, fdev, step_d, advance_step=True)  # the drain kernel
+    pipe.drain_spikes_device(1, flags, toks, fdev, step_d, advance_step=True)  # nothing registered
+    pipe.drain_spikes_device(0, flags, toks, fdev, step_d)  # read only
+    torch.cuda.synchronize()
+    assert int(step_d.item()) == 7
+    with pytest.raises(TypeError):
+        pipe.drain_spikes_device(0, flags, toks, fdev, 3, advance_step=True)
+    lib = _lib.load()
+    rc = lib.fkv_promoter_drain_device(pipe._h, 0, _lib.ptr(flags), _lib.ptr(toks), _lib.ptr(fdev), B, 4 * Hkv,
+                                       Hkv, fdev.shape[2], 0, None, 1, _lib.stream_ptr(flags.device))
+    assert rc == _lib.FKV_EINVAL
+    torch.cuda.synchronize()
+    assert int(step_d.item()) == 7
