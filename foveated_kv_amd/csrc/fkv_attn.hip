@@ -1731,18 +1731,32 @@ __device__ inline void near_pv_lds_part(Lane<D, NQ>& st, const fkv_f4 (&sacc)[NQ
     pv_group_dh<D, NQ, 15>(st, w4, vx, part);
 }
 
-// Decode-buffer tile: rows (n_dec, D) row-major fp16.  A lane reads its
-// token's key row for the score operand; the value operand (dim
-// 64dh + lane of the 4 tokens of group g) is gathered when P.V needs it.
+// Decode-buffer tile: rows (n_dec, D) row-major fp16.  The tile's value
+// rows are copied into `stage` (the wave's idle ring, 2 * 64 * D bytes, row
+// t at byte 2 D t) by LDS DMA first, rows past `count` repeating the last
+// row (finite values that meet weight 0); then a lane reads its token's key
+// row for the score operand, so the two loads share one round trip; the
+// value operand (dim 64dh + lane of the 4 tokens of group g) is read from
+// the stage once the scores are done.
 template <int D, int NQ, typename QOp>
 __device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, int64_t bkv, int tile, int lane,
-                                const QOp& qop) {
+                                const QOp& qop, uint8_t* stage) {
+    constexpr int CPR = D / 8;                // 16-byte chunks of a row
+    constexpr int NI = kTile * CPR / kWave;  // DMA instructions of the tile
+    const int rows = min(count - tile * kTile, kTile);
+    const uint16_t* vt = a.dec_v + (bkv * a.dec_stride + (int64_t)tile * kTile) * D;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = i * kWave + lane, t = c / CPR;
+        __builtin_amdgcn_global_load_lds((const void*)(vt + (int64_t)(t < rows ? t : rows - 1) * D + (c % CPR) * 8),
+                                         (FKV_LDS void*)(stage + i * 1024), 16, 0, 0);
+    }
     const int tk = tile * kTile + lane;
     uint4 kx[D / 8];
     const uint16_t* kr = a.dec_k + (bkv * a.dec_stride + (tk < count ? tk : 0)) * D;
 #pragma unroll
     for (int c = 0; c < D / 8; c++) kx[c] = tk < count ? *(const uint4*)(kr + c * 8) : make_uint4(0, 0, 0, 0);
-    const uint16_t* vr = a.dec_v + bkv * a.dec_stride * D + lane;
+    const uint16_t* vs = (const uint16_t*)stage + lane;
     fp16_compute<D, NQ>(
         st,
         [&](int s) {
@@ -1750,15 +1764,12 @@ __device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, i
             return (s & 1) ? h4_of(x.z, x.w) : h4_of(x.x, x.y);
         },
         [&](int g, int dh) {
-            uint16_t hv[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int tv = tile * kTile + 4 * g + e;
-                hv[e] = tv < count ? vr[(int64_t)tv * D + 64 * dh] : (uint16_t)0;
-            }
-            return h4_of(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+            const uint16_t* p = vs + 4 * g * D + 64 * dh;
+            return h4_of(p[0] | ((uint32_t)p[D] << 16), p[2 * D] | ((uint32_t)p[3 * D] << 16));
         },
-        tile, count, lane >> 2, a.inv_sqrt_d, qop, []() {});
+        tile, count, lane >> 2, a.inv_sqrt_d, qop,
+        // the compiler does not order LDS reads after the DMA
+        []() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); });
 }
 
 // Merge of the partial records of all splits of one row
@@ -2202,6 +2213,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     // writes its record as soon as its own stream ends), else over them
     // (behind a barrier once every wave's stream has ended).
     constexpr int kRing = WPG * 2 * SLOT;
+    static_assert(2 * SLOT >= kTile * D * 2, "a wave's ring holds a decode tile's value rows");
     constexpr int kRec = WPG * NHW * RS * 4;
     constexpr int kQ = 2 * NQC * QCOPY + (TQ ? 4 * NQ * NS * 16 + 16 * NQ * D + 16 * NQ : 64);
     constexpr bool SEP_REC = kRing + kRec + kQ + 256 <= 160 * 1024;
@@ -2446,8 +2458,8 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     const int nt_dec = (int)cdiv(n_dec, kTile);
     for (int d = (un.w - a.dec_wave0 + un.N) % un.N; d < nt_dec; d += un.N)
     {
-        if constexpr (TQ) dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop);
-        else dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qx);
+        if constexpr (TQ) dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qop, ring);
+        else dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qx, ring);
     }
 
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
