@@ -403,7 +403,9 @@ __device__ inline float head_sum(float v) {
 }
 // (max, first index of the max) over the lanes l' = l (mod 4)
 __device__ inline void pick_max(float& mx, int& arg, float ox, int oa) {
-    const bool take = ox > mx || (ox == mx && oa < arg);  // selects, no branch
+    // bitwise, not short-circuit: three compares and two selects (a || / &&
+    // here compiles to branches around each compare)
+    const bool take = (ox > mx) | ((ox == mx) & (oa < arg));
     mx = take ? ox : mx;
     arg = take ? oa : arg;
 }
@@ -1753,9 +1755,13 @@ __device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, i
     }
     const int tk = tile * kTile + lane;
     uint4 kx[D / 8];
-    const uint16_t* kr = a.dec_k + (bkv * a.dec_stride + (tk < count ? tk : 0)) * D;
+    const bool kin = tk < count;
+    const uint16_t* kr = a.dec_k + (bkv * a.dec_stride + (kin ? tk : 0)) * D;  // a valid row: no branch per load
 #pragma unroll
-    for (int c = 0; c < D / 8; c++) kx[c] = tk < count ? *(const uint4*)(kr + c * 8) : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < D / 8; c++) {
+        const uint4 x = *(const uint4*)(kr + c * 8);
+        kx[c] = kin ? x : make_uint4(0, 0, 0, 0);
+    }
     const uint16_t* vs = (const uint16_t*)stage + lane;
     fp16_compute<D, NQ>(
         st,
@@ -2596,9 +2602,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
                 sc[w] = hm[i][w] == -INFINITY ? 0.f : __expf(hm[i][w] - M);
                 L += sc[w] * hl[i][w];
                 mn2 = fminf(mn2, hn[i][w]);
-                const float fx = hx[i][w];
-                const int fa = ha[i][w];
-                if (fx > mx2 || (fx == mx2 && fa < arg2)) { mx2 = fx; arg2 = fa; }
+                pick_max(mx2, arg2, hx[i][w], ha[i][w]);
             }
 #pragma unroll
             for (int k = 0; k < VD; k++) {
