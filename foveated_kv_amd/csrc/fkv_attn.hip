@@ -343,6 +343,27 @@ __device__ inline fkv_h4 int4x4(uint32_t w, int bp) {
     return h4_of((a & m) | e, (b & m) | e);
 }
 
+// int4x4 of two INT4 dwords at once: w = (w1 << 32) | w0, where w0 holds
+// 4-token groups 2u, 2u + 1 and w1 groups 2u + 2, 2u + 3.  One 64-bit shift
+// serves both dwords: the bits a shift carries across the dword boundary
+// land at bits 0-5 (left shifts) or 26-31 (right shifts), outside the mask
+// (bits 6-9, 22-25).  The shift amounts are opaque (empty asm on scalar
+// registers), so the compiler keeps one v_lshlrev_b64 / v_lshrrev_b64
+// (issued at the rate of the 32-bit shifts) instead of splitting each into
+// two 32-bit ones.  o[i] = int4x4(w_{i / 2}, i % 2).
+__device__ inline void int4x4_pair(uint64_t w, fkv_h4 (&o)[4]) {
+    uint32_t m = 0x03C003C0u, e = 0x4C004C00u, n2 = 2, n6 = 6;
+    asm("" : "+s"(m));
+    asm("" : "+v"(e));
+    asm("" : "+s"(n2));
+    asm("" : "+s"(n6));
+    const uint64_t a0 = w << n6, b0 = w << n2, a1 = w >> n2, b1 = w >> n6;
+    o[0] = h4_of(((uint32_t)a0 & m) | e, ((uint32_t)b0 & m) | e);
+    o[1] = h4_of(((uint32_t)a1 & m) | e, ((uint32_t)b1 & m) | e);
+    o[2] = h4_of(((uint32_t)(a0 >> 32) & m) | e, ((uint32_t)(b0 >> 32) & m) | e);
+    o[3] = h4_of(((uint32_t)(a1 >> 32) & m) | e, ((uint32_t)(b1 >> 32) & m) | e);
+}
+
 // broadcast lane i of each lane quad (DPP quad_perm)
 template <int I>
 __device__ inline float quad_bcast(float v) {
@@ -780,6 +801,49 @@ __device__ inline void pv_batch8(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vo
     pv_mfma<D, NQ, G0 + 7>(st, w4, v[7]);
 }
 
+// Groups G0 .. G0 + GB - 1 (GB = 4 or 8) of a tile whose values are INT4
+// dword pairs: pop(j, dh) is the pair of 4-token groups 4j .. 4j + 3 of
+// 64-dim half dh; every operand of the batch is formed before its first
+// MFMA.
+template <int D, int NQ, int G0, int GB, typename PairOp>
+__device__ inline void pv_pair_batch(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], PairOp pop) {
+    fkv_h4 v[GB][D / 64];
+#pragma unroll
+    for (int dh = 0; dh < D / 64; dh++)
+#pragma unroll
+        for (int j = 0; j < GB / 4; j++) {
+            fkv_h4 o[4];
+            int4x4_pair(pop(G0 / 4 + j, dh), o);
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[4 * j + i][dh] = o[i];
+        }
+    pv_mfma<D, NQ, G0 + 0>(st, w4, v[0]);
+    pv_mfma<D, NQ, G0 + 1>(st, w4, v[1]);
+    pv_mfma<D, NQ, G0 + 2>(st, w4, v[2]);
+    pv_mfma<D, NQ, G0 + 3>(st, w4, v[3]);
+    if constexpr (GB == 8) {
+        pv_mfma<D, NQ, G0 + 4>(st, w4, v[4]);
+        pv_mfma<D, NQ, G0 + 5>(st, w4, v[5]);
+        pv_mfma<D, NQ, G0 + 6>(st, w4, v[6]);
+        pv_mfma<D, NQ, G0 + 7>(st, w4, v[7]);
+    }
+}
+
+// The P.V of one 64-token tile from INT4 dword pairs, GB groups per batch.
+template <int D, int NQ, int GB, typename PairOp>
+__device__ inline void pv_pairs(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], PairOp pop) {
+    static_assert(GB == 4 || GB == 8, "batches of 4 or 8 groups");
+    if constexpr (GB == 8) {
+        pv_pair_batch<D, NQ, 0, 8>(st, w4, pop);
+        pv_pair_batch<D, NQ, 8, 8>(st, w4, pop);
+    } else {
+        pv_pair_batch<D, NQ, 0, 4>(st, w4, pop);
+        pv_pair_batch<D, NQ, 4, 4>(st, w4, pop);
+        pv_pair_batch<D, NQ, 8, 4>(st, w4, pop);
+        pv_pair_batch<D, NQ, 12, 4>(st, w4, pop);
+    }
+}
+
 // The P.V of one 64-token tile over the 16 groups of 4 tokens, the value
 // operands formed BATCH groups at a time (1 or 8).
 template <int D, int NQ, int BATCH = 1, typename VOp>
@@ -910,12 +974,21 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
         any |= softmax_w<D, NQ, true>(st, qd, sc, sz, w4[qd]);
     }
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
-    // one head quad: operands in batches; more quads: group by group (their
-    // accumulators leave no registers for a batch)
-    pv_all<D, NQ, NQ == 1 ? 8 : 1>(st, w4, [&](int g, int dh) {
-        const int u = dh * 8 + (g >> 1);
-        return int4x4(word_of(r.v[u >> 2], u & 3), g & 1);
-    });
+    // dword u = 8 dh + g / 2 of the section holds group g of half dh.  One
+    // head quad: operands in batches of 8 groups, from dword pairs (pair j =
+    // dwords 8 dh + 2j, + 1).  More quads: group by group (batches of
+    // operands there cost more accumulator moves than the pairs save).
+    if constexpr (NQ == 1) {
+        pv_pairs<D, NQ, 8>(st, w4, [&](int j, int dh) {
+            const uint4& x = r.v[dh * 2 + (j >> 1)];
+            return (j & 1) ? ((uint64_t)x.w << 32) | x.z : ((uint64_t)x.y << 32) | x.x;
+        });
+    } else {
+        pv_all<D, NQ, 1>(st, w4, [&](int g, int dh) {
+            const int u = dh * 8 + (g >> 1);
+            return int4x4(word_of(r.v[u >> 2], u & 3), g & 1);
+        });
+    }
 }
 
 // ---------------------------------------------------------------------------
