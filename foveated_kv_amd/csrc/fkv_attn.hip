@@ -1502,6 +1502,16 @@ __device__ inline void g32_pv_step(fkv_f4& acc0, fkv_f4& acc1, int qd, const uin
     acc0 = mfma4_half<A>(w2a, int4x4(word_of(v[1], A >> 1), A & 1), acc0);
     if (two) acc1 = mfma4_half<A>(w2b, int4x4(word_of(v[3], A >> 1), A & 1), acc1);
 }
+// g32_pv_step with the value operands already formed: o[c][A] is chunk c's
+// operand of step A.
+template <int A>
+__device__ inline void g32_pv_step_ops(fkv_f4& acc0, fkv_f4& acc1, const fkv_h4 (&o)[4][8], const fkv_h4& w1a,
+                                       const fkv_h4& w2a, const fkv_h4& w1b, const fkv_h4& w2b, bool two) {
+    acc0 = mfma4_half<A>(w1a, o[0][A], acc0);
+    if (two) acc1 = mfma4_half<A>(w1b, o[2][A], acc1);
+    acc0 = mfma4_half<A>(w2a, o[1][A], acc0);
+    if (two) acc1 = mfma4_half<A>(w2b, o[3][A], acc1);
+}
 
 // Scores, spike tracking, softmax and P.V of one group-32 far tile.
 template <int D, int NQ, typename QOp>
@@ -1579,6 +1589,37 @@ __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, in
     uint4 v4[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) v4[i] = r.v[i < NG ? i : 0];
+    if constexpr (NQ == 1) {
+        // one head quad: every value operand formed before the first MFMA,
+        // from dword pairs (words 0, 1 of a chunk serve steps 0-3, words 2, 3
+        // steps 4-7)
+        fkv_h4 o[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (i >= NG) continue;
+            fkv_h4 lo[4], hi[4];
+            int4x4_pair(((uint64_t)v4[i].y << 32) | v4[i].x, lo);
+            int4x4_pair(((uint64_t)v4[i].w << 32) | v4[i].z, hi);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                o[i][k] = lo[k];
+                o[i][4 + k] = hi[k];
+            }
+        }
+        fkv_f4 a0 = st.acc[0][0], a1 = st.acc[0][NH - 1];
+        const fkv_h4 w1b = w1[NH - 1][0], w2b = w2[NH - 1][0];
+        g32_pv_step_ops<0>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        g32_pv_step_ops<1>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        g32_pv_step_ops<2>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        g32_pv_step_ops<3>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        g32_pv_step_ops<4>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        g32_pv_step_ops<5>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        g32_pv_step_ops<6>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        g32_pv_step_ops<7>(a0, a1, o, w1[0][0], w2[0][0], w1b, w2b, NH == 2);
+        st.acc[0][0] = a0;
+        if (NH == 2) st.acc[0][NH - 1] = a1;
+        return;
+    }
 #pragma unroll
     for (int qd = 0; qd < NQ; qd++) {
         fkv_f4 a0 = st.acc[qd][0], a1 = st.acc[qd][NH - 1];
