@@ -1,8 +1,8 @@
-// fp8 and group-32 attention kernels of rows of one head quad (C2, C3).
-// A translation unit of their own so that the Makefile can compile them
-// with the max-ilp instruction scheduling, which measured fastest for them
-// (C3-16K -0.2 us, C2 unchanged; the same strategy slowed the TurboQuant
-// kernels down).
+// fp8 and group-32 attention kernels of rows of one head quad (C2, C3, and
+// C1's rows of 4 heads).  A translation unit of their own so that the
+// Makefile can compile them with the max-ilp instruction scheduling, which
+// measured fastest for them (C1 6.75 -> 6.38 us, C3 -0.05 to -0.2 us, C2
+// within noise; the same strategy slowed the TurboQuant kernels down).
 #include "fkv_attn_kernel.h"
 
 namespace fkv {

@@ -1,4 +1,5 @@
-// fp8 and group-32 attention kernels of rows of 2-4 head quads (C1, C5).
+// fp8 and group-32 attention kernels of rows of 2-4 head quads (GQA groups
+// of 5-16 query heads per KV head, e.g. C5's 8).
 // A translation unit of their own so that the Makefile can compile them
 // with the iterative-ilp instruction scheduling, which measured fastest for
 // them (C5 29.9 -> 29.0 us).
