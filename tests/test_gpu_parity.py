@@ -134,6 +134,8 @@ def test_compress_exhaustive_fp16_patterns(fkv, orc):
     dict(B=1, Hq=32, Hkv=4, D=64, S=16384, n_dec=3, seed=11),    # the same at D = 64
     dict(B=4, Hq=40, Hkv=2, D=128, S=4096, n_dec=5, seed=12),    # G = 20: a 16-head and a 4-head row
     dict(B=1, Hq=12, Hkv=2, D=64, S=600, n_dec=2, seed=13),      # small grid: rows of 4 heads, G = 6
+    dict(B=2, Hq=48, Hkv=4, D=128, S=8192, n_dec=9, seed=14),    # G = 12: rows of three head quads
+    dict(B=1, Hq=40, Hkv=4, D=64, S=16384, n_dec=4, seed=15),    # G = 10 at D = 64: three quads
 ])
 def test_attention_parity(fkv, orc, args):
     run_attention(fkv, orc, **args)
@@ -146,6 +148,7 @@ GROUP32 = [
     dict(B=1, Hq=32, Hkv=2, D=64, S=700, n_dec=5, seed=34),      # two head groups
     dict(B=3, Hq=12, Hkv=4, D=64, S=333, n_dec=70, seed=35),     # ragged tiles
     dict(B=1, Hq=8, Hkv=2, D=128, S=1000, n_dec=3, seed=36, near_valid_delta=5),
+    dict(B=2, Hq=36, Hkv=4, D=128, S=8192, n_dec=5, seed=37),    # G = 9: rows of three head quads
 ]
 
 

@@ -85,6 +85,7 @@ CASES = [
     (1, 16, 1, 128, 1000, 128, (100,), 0),
     (2, 4, 4, 64, 129, 64, (64, 10, 0, 33), 3),
     (1, 8, 2, 128, 0, 64, (40, 64), 2),
+    (2, 24, 2, 128, 8000, 896, (800, 750), 4),  # G = 12: rows of three head quads
 ]
 
 
