@@ -187,6 +187,10 @@ def main():
                     help="C5 end-to-end loop instead of the kernel line: importance partition + compress, then "
                          "--e2e-steps decode steps of attention + spike drain + promotion on one 64K layer")
     ap.add_argument("--e2e-steps", type=int, default=128)
+    ap.add_argument("--spike-k", type=int, default=32,
+                    help="--e2e: spiking far tokens per head per step (C5: up to 32; 1 = the reference's one)")
+    ap.add_argument("--budget", type=int, default=0,
+                    help="--e2e: promotions per drain (0: spike_k x H_kv, so the per-head limit binds)")
     ap.add_argument("--generate", action="store_true",
                     help="model decode loop instead of the kernel line: a seeded tiny LM (tests/_tiny_lm.py) "
                          "decoding through generate_fused, eager closure vs one HIP graph per decode step")
@@ -375,6 +379,16 @@ def main():
                                        args.spikes, args.eager)
             print(f"[bench] {name}: {others[name]['us_per_layer']} us/layer, {others[name]['gbs']} GB/s",
                   file=sys.stderr, flush=True)
+        # C1 as BASELINE names it: importance partition, per-head-scaled fp8
+        # K, INT4 V in groups of 32 (the line above keeps the reference's
+        # formats, recency partition, unscaled K, per-token V)
+        name = "c1_qwen05b_512"
+        if name != args.config:
+            key = name + "_scaled_k_g32"
+            others[key] = config_line(torch, dev, ext, synthetic, name, args.other_steps, 5, args.seed,
+                                      args.spikes, args.eager, v_group=32, k_scale=True, importance=True)
+            print(f"[bench] {key}: {others[key]['us_per_layer']} us/layer, {others[key]['gbs']} GB/s",
+                  file=sys.stderr, flush=True)
         result["other_configs"] = others
     if args.copy_mib:
         result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)
@@ -389,22 +403,32 @@ def main():
 SETTLE_MS = 300.0
 
 
-def config_line(torch, dev, ext, synthetic, name, steps, warmup, seed, spikes, eager):
+def config_line(torch, dev, ext, synthetic, name, steps, warmup, seed, spikes, eager, v_group=0, k_scale=False,
+                importance=False):
     """One benchmark configuration timed like the headline (distinct layer
     blobs, HIP-graph replays, HIP events): us per layer and algorithmic
-    GB/s of the reference's per-token V layout (TurboQuant for C4)."""
+    GB/s of the reference's per-token V layout (TurboQuant for C4), or of
+    group-32 V / per-head-scaled K / the importance partition when asked."""
     B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[name]
     cfg = ext.TierConfig()
     cfg.promo_headroom_min = 8
+    cfg.v_group = v_group
+    cfg.k_scale = 1 if k_scale else 0
     turbo = name.startswith("c4_turbo")
     tb = ext.tier_boundaries_c(cfg, S)
     R, F = tb["R_actual"], tb["far_count"]
     k, v = synthetic.make_kv(B, Hkv, S, D, seed)
     q = synthetic.make_query(B, Hq, D, seed)
-    synthetic.inject_spikes(k, q, tb["mid_start"], F, spikes, seed)
+    imp = None
+    if importance:
+        imp = torch.from_numpy(synthetic.make_importance(B, Hkv, S, seed)).to(dev)
+        _, fidx = ext.partition_importance(cfg, imp, B, Hkv, S)
+        synthetic.inject_spikes_at(k, q, fidx.cpu().numpy(), spikes, seed)
+    else:
+        synthetic.inject_spikes(k, q, tb["mid_start"], F, spikes, seed)
     dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
     cl = ext.CompressHandle(cfg).compress_layer(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
-                                                with_archive=turbo)
+                                                with_archive=turbo, importance=imp)
     if turbo:
         from foveated_kv_amd import turbo as tq
 
@@ -418,17 +442,19 @@ def config_line(torch, dev, ext, synthetic, name, steps, warmup, seed, spikes, e
     else:
         def make_handle():
             return ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
-                                      cl.near_valid, spike_margin=10.0)
+                                      cl.near_valid, spike_margin=10.0, far_k_scale=cl.far_k_scale)
     qt = torch.from_numpy(q).to(dev)[:, :, None, :]
     dkt = torch.from_numpy(dk).to(dev) if dk is not None else None
     dvt = torch.from_numpy(dv).to(dev) if dv is not None else None
     nbytes = (algorithmic_bytes_turbo(B, Hq, Hkv, D, R, F, n_dec) if turbo
-              else algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec))
+              else algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec, v_group) + (B * Hkv * 4 if k_scale else 0))
     L, _, ms = time_layers(torch, dev, make_handle, 0, qt, dkt, dvt, steps, warmup, eager)
     us = ms * 1000.0 / L
     gbs = nbytes / (us * 1e-6) / 1e9
+    fmt = ("turboquant" if turbo else ("per-head-scaled " if k_scale else "") + "fp8-e4m3 K + int4 " +
+           ("group-32" if v_group else "per-token") + " V" + (", importance partition" if importance else ""))
     return {"B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "context": S, "n_decode": n_dec,
-            "far_format": "turboquant" if turbo else "fp8-e4m3 K + int4 per-token V",
+            "far_format": fmt,
             "us_per_layer": round(us, 3), "gbs": round(gbs, 2), "pct_peak": round(100.0 * gbs / PEAK_GBS, 2),
             "algorithmic_bytes": nbytes, "layers_per_step": L, "steps": steps}
 
@@ -507,12 +533,15 @@ def run_e2e(args, torch, dev):
     """Workload C5: compress + decode + promote on one 70B-like layer (Hq=64,
     Hkv=8, D=128, 64K context, B=1).  Seeded importance partition, 2 % of
     far tokens aligned with the group query, per-step query drift, one
-    decode token appended per step, spike drain (GQA dedup, cooldown 5,
-    budget 8, the reference's filter) and promotion of exact fp16 rows from
-    the pinned host archive -- on the device, and again with the reference's
-    host-side drain for comparison.  Prints one JSON line: us per decode
-    step of the graph-replayed device-drain loop, with the eager device-drain
-    loop and the host-drain loop beside it."""
+    decode token appended per step, spike drain (GQA dedup, cooldown 5, up
+    to --spike-k far tokens per KV head and step -- C5's "up to 32 far
+    tokens per head per step" -- within a budget of --budget per drain) and
+    promotion of exact fp16 rows from the pinned host archive -- on the
+    device, and again with a host-side drain for comparison.  Prints one JSON
+    line: us per decode step of the graph-replayed device-drain loop, with
+    the eager device-drain loop, the host-drain loop and the reference's
+    single-token drain (spike_k 1, budget 8) beside it, and the promotions
+    per step of each."""
     from foveated_kv_amd import ext, synthetic
     from foveated_kv_amd.promotion import PromotionPipeline
 
@@ -531,29 +560,32 @@ def run_e2e(args, torch, dev):
     dk, dv = synthetic.make_decode(B, Hkv, steps, D, seed)
     dkt, dvt = torch.from_numpy(dk).to(dev), torch.from_numpy(dv).to(dev)
     kt, vt = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
-    print(f"[e2e] C5 B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps}", file=sys.stderr, flush=True)
+    spike_k = args.spike_k
+    budget = args.budget if args.budget > 0 else spike_k * Hkv
+    print(f"[e2e] C5 B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} spike_k={spike_k} budget={budget}",
+          file=sys.stderr, flush=True)
 
-    def compress():
+    def compress(kk=1):
         cl = ext.CompressHandle(cfg).compress_layer(kt, vt, importance=imp)
         h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
-                               cl.near_valid, spike_margin=10.0)
+                               cl.near_valid, spike_margin=10.0, spike_k=kk)
         return cl, h
 
     compress()  # warm (module load, first launches)
     torch.cuda.synchronize()
     fdev = torch.from_numpy(far_idx).to(dev).contiguous()
 
-    def loop(device_drain):
+    def loop(device_drain, kk, bud):
         """One compress + `steps` decode steps; returns timings and the
         promotion outcome.  device_drain: the filter and the row copies run as
         a kernel after each attention launch (no host round trip); else the
         spike outputs are read back and drained on the host, as the
         reference does."""
         t0 = time.perf_counter()
-        cl, h = compress()
+        cl, h = compress(kk)
         torch.cuda.synchronize()
         compress_ms = (time.perf_counter() - t0) * 1e3
-        pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
+        pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=bud, spike_k=kk)
         pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
         pipe.register_blob(0, h)
         h(qs[0], dkt[:, :, :1], dvt[:, :, :1])  # allocates the call's split workspace
@@ -570,8 +602,9 @@ def run_e2e(args, torch, dev):
             if device_drain:
                 pipe.drain_spikes_device(0, flags, toks, fdev, t)
             else:
-                both = torch.stack([flags, toks]).cpu().numpy()  # one copy, then the host filter
-                pipe.drain_spikes(0, both[0], both[1], far_idx, t)
+                both = torch.cat([flags.reshape(-1), toks.reshape(-1)]).cpu().numpy()  # one copy, then the filter
+                pipe.drain_spikes(0, both[:flags.numel()].reshape(tuple(flags.shape)), both[flags.numel():],
+                                  far_idx, t)
             t_call += tb_ - ta
             t_drain += time.perf_counter() - tb_
         pipe.synchronize()
@@ -581,7 +614,7 @@ def run_e2e(args, torch, dev):
                 "host_call_us": t_call / steps * 1e6, "host_drain_us": t_drain / steps * 1e6,
                 "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
 
-    def loop_graph():
+    def loop_graph(kk, bud):
         """The device-drain loop with the decode step captured once in a HIP
         graph: with n (a device int32) the step's decode-row count, gather the
         query of step n - 1, attention over the fixed-capacity decode buffer,
@@ -590,10 +623,10 @@ def run_e2e(args, torch, dev):
         runs eagerly (it sizes the workspaces), steps 1.. are graph replays
         with nothing read back."""
         t0 = time.perf_counter()
-        cl, h = compress()
+        cl, h = compress(kk)
         torch.cuda.synchronize()
         compress_ms = (time.perf_counter() - t0) * 1e3
-        pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
+        pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=bud, spike_k=kk)
         pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
         pipe.register_blob(0, h)
         n_d = torch.ones(1, dtype=torch.int32, device=dev)
@@ -621,9 +654,10 @@ def run_e2e(args, torch, dev):
         return {"us_per_step": loop_s / max(steps - 1, 1) * 1e6, "compress_ms": compress_ms,
                 "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
 
-    dres = loop(True)
-    hres = loop(False)
-    gres = loop_graph()
+    dres = loop(True, spike_k, budget)
+    hres = loop(False, spike_k, budget)
+    gres = loop_graph(spike_k, budget)
+    g1res = loop_graph(1, 8) if spike_k != 1 or budget != 8 else gres
     cl, h = dres["cl"], dres["h"]
     # device time of the attention call on the final state (queued back to back)
     dk_end, dv_end = dkt.contiguous(), dvt.contiguous()
@@ -649,6 +683,8 @@ def run_e2e(args, torch, dev):
                    "far_format": "fp8-e4m3 K + int4 group-32 V" if args.v_group else "fp8-e4m3 K + int4 per-token V"},
         "compress_ms": round(gres["compress_ms"], 3),
         "attn_us_device": round(attn_us, 3),
+        "spike_k": spike_k, "budget_per_drain": budget,
+        "promotions_per_step": round(gres["stats"]["promotions_completed"] / steps, 3),
         "promotion_stats": gres["stats"],
         "near_valid_end": gres["near_valid_end"],
         "eager_device_drain": {"us_per_step": round(dres["us_per_step"], 2),
@@ -656,6 +692,10 @@ def run_e2e(args, torch, dev):
                                                     "drain_launch": round(dres["host_drain_us"], 2)},
                                "same_promotions": gres["stats"] == dres["stats"]
                                and gres["near_valid_end"] == dres["near_valid_end"]},
+        "reference_single_token": {"spike_k": 1, "budget_per_drain": 8,
+                                   "us_per_step": round(g1res["us_per_step"], 2),
+                                   "promotions_per_step": round(g1res["stats"]["promotions_completed"] / steps, 3),
+                                   "promotion_stats": g1res["stats"]},
         "host_drain": {"us_per_step": round(hres["us_per_step"], 2),
                        "host_us_per_step": {"attention_call": round(hres["host_call_us"], 2),
                                             "spike_readback_drain_and_flush": round(hres["host_drain_us"], 2)},

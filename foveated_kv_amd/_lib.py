@@ -44,6 +44,7 @@ class TierConfigC(ctypes.Structure):
         ("promo_headroom_pct", ctypes.c_double),
         ("promo_headroom_min", ctypes.c_int32),
         ("v_group", ctypes.c_int32),
+        ("k_scale", ctypes.c_int32),
     ]
 
 
@@ -82,6 +83,8 @@ SIGNATURES = {
     "fkv_partition_importance": (ctypes.c_int, [ctypes.POINTER(TierConfigC), P, I32, I32, I32, P, P, P]),
     "fkv_compress_layer_indexed": (ctypes.c_int, [ctypes.POINTER(TierConfigC), P, P, I32, I32, I32, I32, I32,
                                                   P, P, P, P, P, P, P, P, P, P, P, P]),
+    "fkv_compress_layer_ex": (ctypes.c_int, [ctypes.POINTER(TierConfigC), P, P, I32, I32, I32, I32, I32,
+                                             P, P, P, P, P, P, P, P, P, P, P, P, P]),
     "fkv_attn_create": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P,
                                        I32, P, F32, P]),
     "fkv_attn_create_g32": (ctypes.c_int, [ctypes.POINTER(P), I32, I32, I32, I32, I32, P, P, I32, P, P, P, P,
@@ -100,11 +103,14 @@ SIGNATURES = {
     "fkv_attn_read_near_valid": (ctypes.c_int, [P, P, P]),
     "fkv_attn_dispatch_info": (ctypes.c_int, [P, ctypes.POINTER(I32)]),
     "fkv_attn_destroy": (None, [P]),
+    "fkv_attn_set_k_scale": (ctypes.c_int, [P, P, P]),
+    "fkv_attn_set_spike_k": (ctypes.c_int, [P, I32]),
     "fkv_e4m3_decode": (ctypes.c_int, [P, P, ctypes.c_int64, P]),
     "fkv_hbm_read_probe": (ctypes.c_int, [P, ctypes.c_int64, I32, I32, I32, P, P]),
     "fkv_attn_promote_rows": (ctypes.c_int, [P, I32, P, P, P, I32, P]),
     "fkv_attn_export_near": (ctypes.c_int, [P, P, P, P]),
     "fkv_promoter_create": (ctypes.c_int, [I32, I32, I32, ctypes.POINTER(P)]),
+    "fkv_promoter_set_spike_k": (ctypes.c_int, [P, I32]),
     "fkv_promoter_register_archive": (ctypes.c_int, [P, I32, P, P, I32, I32, I32, I32, P, I32]),
     "fkv_promoter_register_archive_files": (ctypes.c_int, [P, I32, ctypes.c_char_p, ctypes.c_char_p, I32, I32,
                                                            I32, P]),

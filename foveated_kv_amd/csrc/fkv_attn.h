@@ -24,12 +24,14 @@ namespace fkv {
 //   | V: 32*D bytes of INT4 nibbles, lane l = dim 64*dh + l
 //   | SZ: 64 x u32 = fp16 scale | fp16 zero << 16 per token ]
 //   near_valid : [Hkv] u32
+//   kscale     : [B*Hkv] fp32 per-head fp8 key scale (1 unless set with
+//                fkv_attn_set_k_scale; the kernel multiplies far scores by it)
 // A TurboQuant blob (fmt 1) keeps the near tiers and near_valid and stores
 // the far tier as TurboQuant records instead (layout below).
 struct BlobLayout {
     int B, Hkv, D, Na, F, Na_pad, F_pad;
     int fmt;  // 0: fp8-E4M3 K / INT4 V far records, 1: TurboQuant, 2: fp8 K / group-32 INT4 V
-    size_t near_k, near_v, far, far_rec, near_valid, total;
+    size_t near_k, near_v, far, far_rec, near_valid, kscale, total;
 };
 
 BlobLayout make_layout(int B, int Hkv, int D, int Na, int F, int fmt = 0);
@@ -158,6 +160,17 @@ struct fkv_attn_impl {
     // memory)
     int xcd_mod = 0;
     fkv::TurboConsts tq;    // fmt 1 only
+    // Top-K spikes (fkv_attn_set_spike_k): tokens per query head, and the
+    // selection's buffers for spk_hq query heads (allocated with the
+    // workspace, or by the setter after it): far tile maxima, thresholds,
+    // the attention kernel's own flag / argmax
+    int spike_k = 1;
+    bool has_kscale = false;  // fkv_attn_set_k_scale was called (else the scales are 1)
+    int spk_hq = 0;
+    float* spk_tmax = nullptr;
+    float* spk_thr = nullptr;
+    int32_t* spk_flags = nullptr;
+    int32_t* spk_tokens = nullptr;
 };
 
 struct fkv_attn : fkv_attn_impl {};

@@ -69,6 +69,7 @@ BlobLayout make_layout(int B, int Hkv, int D, int Na, int F, int fmt) {
     L.far_rec = (size_t)(fmt == 1 ? tq_record_bytes(D) : fmt == 2 ? g32_record_bytes(D) : far_record_bytes(D));
     L.far = place(bkv * (L.F_pad / kTile) * L.far_rec);
     L.near_valid = place((size_t)Hkv * 4);
+    L.kscale = place(bkv * 4);
     L.total = off;
     return L;
 }
@@ -231,6 +232,17 @@ __global__ void pack_valid_kernel(const int32_t* __restrict__ nv, int Hkv, BlobL
     }
 }
 
+// The blob's per-head fp8 key scales: 1 (src NULL) or src[i]; a scale that
+// is not a positive finite number raises *bad.
+__global__ void fill_kscale_kernel(const float* __restrict__ src, int n, BlobLayout L, uint8_t* __restrict__ blob,
+                                   unsigned* bad) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = src ? src[i] : 1.0f;
+    if (!(v > 0.f && v <= 3.402823466e38f)) *bad = 1u;
+    ((float*)(blob + L.kscale))[i] = v;
+}
+
 // E4M3 -> fp16 with the converter the fused kernel uses (4 codes per thread)
 __global__ void e4m3_decode_kernel(const uint8_t* __restrict__ codes, uint16_t* __restrict__ out, int64_t n4) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
@@ -268,6 +280,158 @@ __global__ __launch_bounds__(64) void merge_kernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
     merge_heads<D, 1>(a, rs, ns, ng, g, 1, (int)threadIdx.x, (int64_t)b * a.Hq + head0 + g);
+}
+
+// ---------------------------------------------------------------------------
+// Top-K spike selection (spike_k > 1; the benchmark's "up to 32 far tokens
+// per head per step", an extension of the reference's one token per query
+// head, csrc/kernels/foveated_attn.metal:323-327, 427-430)
+// ---------------------------------------------------------------------------
+
+struct SelectArgs {
+    const uint8_t* blob;
+    BlobLayout L;
+    const uint16_t* q;          // (B, Hq, D) fp16: the query the attention kernel read
+    int Hq, G, K;
+    float inv_sqrt_d;
+    const float* tmax;          // (B*Hq, ntf) far tile maxima
+    int ntf;
+    const float* thr;           // (B*Hq) min_near + margin
+    const int32_t* flags_in;    // (B*Hq) the attention kernel's flag and first-index argmax
+    const int32_t* tokens_in;
+    int32_t* flags;             // (B*Hq) number of spiking tokens, at most K
+    int32_t* tokens;            // (B*Hq, K)
+};
+
+// One wave per (batch, KV head, head quad).  A far token spikes when its
+// score exceeds its head's threshold min_near + margin (the attention
+// kernel's flag rule).  The wave scans the far tile maxima the attention
+// kernel stored, rescores each tile that can hold a spike -- its E4M3 keys
+// against the fp16 query with the attention kernel's MFMA chain (same
+// operands, same order: the same fp32 scores bit for bit) -- and keeps each
+// head's best K spiking tokens, score descending, ties to the smaller
+// index, in lanes 0..K-1 of two registers.  Tiles are visited in ascending
+// order, so once a head's list is full a later tile can only enter it with
+// a maximum above the list's last score.  Output: flags = the spike count,
+// tokens[0..count) the list; entry 0 is the attention kernel's first-index
+// argmax when nothing spikes (as the reference's single token), the rest
+// -1.
+template <int D>
+__global__ __launch_bounds__(64) void spike_select_kernel(SelectArgs a) {
+    constexpr int NS = D / 4;
+    const int quad = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x, j = lane & 3, blk = lane >> 2;
+    const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
+    const int64_t o0 = (int64_t)b * a.Hq + (int64_t)kvh * a.G + 4 * quad;  // head 0 of the quad
+    const int hg = 4 * quad + j;            // the lane's head within the group
+    const bool live = hg < a.G;
+    const float thr = live ? a.thr[o0 + j] : INFINITY;
+    const bool flagged = live && a.flags_in[o0 + j] != 0;
+    // per head jj (wave-uniform): threshold, flag, list length; the list in
+    // lane i = entry i
+    float th[4], ls[4];
+    int fl[4], n[4], li[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        th[jj] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(thr), jj));
+        fl[jj] = __builtin_amdgcn_readlane((int)flagged, jj);
+        n[jj] = 0;
+        ls[jj] = -INFINITY;
+        li[jj] = INT_MAX;
+    }
+    if (fl[0] | fl[1] | fl[2] | fl[3]) {
+        const float far_scale = a.inv_sqrt_d * *(const float*)(a.blob + a.L.kscale + 4 * bkv);
+        // the score MFMA's B operand: head j of the quad, dims 4s..4s+3
+        // (heads past the group read the group's first head, as the
+        // attention kernel does; their scores are never kept)
+        fkv_h4 qv[NS];
+        const uint16_t* qrow = a.q + (o0 + (live ? j : -4 * quad)) * D;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            uint2 w;
+            __builtin_memcpy(&w, qrow + 4 * s, 8);
+            qv[s] = __builtin_bit_cast(fkv_h4, w);
+        }
+        for (int c0 = 0; c0 < a.ntf; c0 += kWave) {
+            // tiles of this chunk that can hold a spike (or, once a head's list
+            // is full, beat its last entry)
+            float cut[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float kth = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls[jj]), a.K - 1));
+                cut[jj] = n[jj] == a.K ? fmaxf(th[jj], kth) : th[jj];
+            }
+            const int tl = c0 + lane;
+            bool cand = false;
+            if (tl < a.ntf) {
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++)
+                    if (fl[jj]) cand |= a.tmax[(o0 + jj) * a.ntf + tl] > cut[jj];
+            }
+            uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
+            while (mask) {
+                const int tile = c0 + (int)__builtin_ctzll(mask);
+                mask &= mask - 1;
+                // rescore: lane = token; the keys of dims 16c..16c+15 in chunk c
+                const uint8_t* rec = a.blob + a.L.far + far_rec_index(a.L, bkv, tile) * (int64_t)a.L.far_rec;
+                uint4 kc[D / 16];
+#pragma unroll
+                for (int c = 0; c < D / 16; c++) kc[c] = *(const uint4*)(rec + c * 1024 + lane * 16);
+                fkv_f4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < NS; s++) sacc = mfma4_local(e4m3x4(word_of(kc[s >> 2], s & 3)), qv[s], sacc);
+                float sv[4];
+                bool sp[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = tile * kTile + 4 * blk + e;
+                    sv[e] = sacc[e] * far_scale;
+                    sp[e] = flagged && t < a.L.F && sv[e] > thr;
+                }
+                // insert the spiking tokens, head by head
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    if (!fl[jj]) continue;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        uint64_t m = __builtin_amdgcn_ballot_w64(sp[e] && j == jj);
+                        while (m) {
+                            const int src = (int)__builtin_ctzll(m);
+                            m &= m - 1;
+                            const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[e]), src));
+                            const int t = tile * kTile + 4 * (src >> 2) + e;
+                            // entries ahead of the token: higher score, or equal and earlier
+                            const bool ahead = lane < n[jj] && (ls[jj] > s || (ls[jj] == s && li[jj] < t));
+                            const int pos = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ahead));
+                            if (pos >= a.K) continue;
+                            const float ps = __shfl_up(ls[jj], 1);
+                            const int pi = __shfl_up(li[jj], 1);
+                            if (lane > pos) {
+                                ls[jj] = ps;
+                                li[jj] = pi;
+                            } else if (lane == pos) {
+                                ls[jj] = s;
+                                li[jj] = t;
+                            }
+                            n[jj] = n[jj] < a.K ? n[jj] + 1 : a.K;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // lanes 0..K-1 of head jj's list -> tokens[o_jj][0..K)
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        if (4 * quad + jj >= a.G) continue;
+        const int64_t oj = o0 + jj;
+        if (lane < a.K) {
+            int t = lane < n[jj] ? li[jj] : -1;
+            if (lane == 0 && n[jj] == 0) t = a.tokens_in[oj];
+            a.tokens[oj * a.K + lane] = t;
+        }
+        if (lane == 0) a.flags[oj] = n[jj];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -498,7 +662,9 @@ int attn_begin(fkv_attn_impl* h, int B, int Hkv, int D, int Na, int F, int fmt, 
     if (Na > 0)
         hipLaunchKernelGGL(pack_near_kernel, dim3(grid_for((int64_t)B * Hkv * L.Na_pad * (D / 16), blk)), dim3(blk),
                            0, st, near_k, near_v, near_dtype, L, h->blob);
-    hipLaunchKernelGGL(pack_valid_kernel, dim3(1), dim3(blk), 0, st, near_valid, Hkv, L, h->blob);
+    hipLaunchKernelGGL(pack_valid_kernel, dim3(grid_for(Hkv, blk)), dim3(blk), 0, st, near_valid, Hkv, L, h->blob);
+    hipLaunchKernelGGL(fill_kscale_kernel, dim3(grid_for((int64_t)B * Hkv, blk)), dim3(blk), 0, st, nullptr, B * Hkv,
+                       L, h->blob, nullptr);
     return check_hip(hipGetLastError(), "pack kernels");
 }
 
@@ -640,10 +806,33 @@ int scratch_base(const std::string& name, int dev, hipStream_t st, uint8_t** out
 
 namespace {
 
+// The top-K spike selection's buffers for Hq query heads (spike_k > 1).
+int ensure_spike_buffers(fkv_attn* h, int Hq) {
+    if (h->spike_k <= 1 || h->spk_hq == Hq) return FKV_OK;
+    if (h->spk_hq != 0) return set_error("fkv_attn: spike buffers sized for another query-head count");
+    const fkv::BlobLayout& L = h->L;
+    const size_t heads = (size_t)L.B * Hq, ntf = (size_t)fkv::cdiv(L.F, fkv::kTile);
+    int rc = check_hip(hipMalloc(&h->spk_tmax, (heads * ntf > 0 ? heads * ntf : 1) * sizeof(float)), "hipMalloc(tmax)");
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_thr, heads * sizeof(float)), "hipMalloc(thr)");
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_flags, heads * sizeof(int32_t)), "hipMalloc(flags)");
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_tokens, heads * sizeof(int32_t)), "hipMalloc(tokens)");
+    if (rc) {
+        (void)hipFree(h->spk_tmax);
+        (void)hipFree(h->spk_thr);
+        (void)hipFree(h->spk_flags);
+        (void)hipFree(h->spk_tokens);
+        h->spk_tmax = h->spk_thr = nullptr;
+        h->spk_flags = h->spk_tokens = nullptr;
+        return rc;
+    }
+    h->spk_hq = Hq;
+    return FKV_OK;
+}
+
 // The handle's call workspace, allocated by its first call (sized for every
 // launch plan of that query-head count) and never re-allocated afterwards.
 int ensure_workspace(const std::string& name, fkv_attn* h, int Hq, hipStream_t st) {
-    if (h->ws_hq == Hq) return FKV_OK;
+    if (h->ws_hq == Hq) return ensure_spike_buffers(h, Hq);
     if (h->ws_hq != 0)
         return set_error(name + ": this handle's workspace was sized by its first call for Hq=" +
                          std::to_string(h->ws_hq) + "; a call with Hq=" + std::to_string(Hq) +
@@ -667,6 +856,7 @@ int ensure_workspace(const std::string& name, fkv_attn* h, int Hq, hipStream_t s
     h->ws_floats = wsf;
     h->arrive_n = rows;
     h->ws_hq = Hq;
+    if (int rc2 = ensure_spike_buffers(h, Hq)) return rc2;
     // counters start at zero; the kernel's last split re-arms them
     hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(rows, 256)), dim3(256), 0, st, h->arrive, rows);
     return check_hip(hipGetLastError(), "zero_ints_kernel launch");
@@ -703,6 +893,10 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         return set_error(name + ": an fp16 query must be 8-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int G = Hq / L.Hkv;
+    const bool topk = h->spike_k > 1;
+    if (topk && no_alloc && h->spk_hq != Hq)
+        return set_error(name + ": spike_k > 1 needs the selection buffers of a call with Hq=" + std::to_string(Hq) +
+                         " (fkv_attn_call once, or fkv_attn_set_spike_k after one)");
     // the split count follows the longest decode length the call can see
     const fkv::LaunchPlan p = fkv::plan_launch(L, Hq, n_dec_dev ? dec_stride : n_decode, h->target_wgs);
     CallWorkspace w;
@@ -744,8 +938,15 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.spike_margin = h->margin;
     a.inv_sqrt_d = (float)(1.0 / sqrt((double)L.D));
     a.out = (uint16_t*)out;
-    a.flags = spike_flags;
-    a.tokens = spike_tokens;
+    // spike_k > 1: the attention kernel's flag / argmax, tile maxima and
+    // thresholds go to the selection's buffers; spike_select_kernel writes
+    // the caller's spike outputs
+    a.flags = topk ? h->spk_flags : spike_flags;
+    a.tokens = topk ? h->spk_tokens : spike_tokens;
+    a.tmax = topk ? h->spk_tmax : nullptr;
+    a.tmax_stride = (int)fkv::cdiv(L.F, fkv::kTile);
+    a.thr = topk ? h->spk_thr : nullptr;
+    a.kscale = h->has_kscale ? (const float*)(h->blob + L.kscale) : nullptr;
     a.ws = w.ws;
     const bool fused_merge = h->fused_merge;
     a.arrive = fused_merge ? w.arrive : nullptr;
@@ -796,6 +997,26 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         const dim3 mgrid(rows, ng_max);
         if (L.D == 128) hipLaunchKernelGGL(fkv::merge_kernel<128>, mgrid, dim3(fkv::kWave), 0, st, a);
         else hipLaunchKernelGGL(fkv::merge_kernel<64>, mgrid, dim3(fkv::kWave), 0, st, a);
+    }
+    if (topk) {
+        fkv::SelectArgs sa;
+        sa.blob = h->blob;
+        sa.L = L;
+        sa.q = q16;
+        sa.Hq = Hq;
+        sa.G = G;
+        sa.K = h->spike_k;
+        sa.inv_sqrt_d = a.inv_sqrt_d;
+        sa.tmax = h->spk_tmax;
+        sa.ntf = a.tmax_stride;
+        sa.thr = h->spk_thr;
+        sa.flags_in = h->spk_flags;
+        sa.tokens_in = h->spk_tokens;
+        sa.flags = spike_flags;
+        sa.tokens = spike_tokens;
+        const dim3 sgrid((unsigned)fkv::cdiv(G, 4), L.Hkv, L.B);
+        if (L.D == 128) hipLaunchKernelGGL(fkv::spike_select_kernel<128>, sgrid, dim3(fkv::kWave), 0, st, sa);
+        else hipLaunchKernelGGL(fkv::spike_select_kernel<64>, sgrid, dim3(fkv::kWave), 0, st, sa);
     }
     return check_hip(hipGetLastError(), "attn_kernel launch");
 }
@@ -948,9 +1169,51 @@ int fkv_attn_export_near(const fkv_attn* h, void* near_k_out, void* near_v_out, 
     return check_hip(hipGetLastError(), "export_near_kernel launch");
 }
 
+int fkv_attn_set_spike_k(fkv_attn* h, int32_t spike_k) {
+    if (!h) return set_error("fkv_attn_set_spike_k: NULL handle");
+    if (spike_k < 1 || spike_k > FKV_MAX_SPIKE_K)
+        return set_error("fkv_attn_set_spike_k: spike_k must be in [1, " + std::to_string(FKV_MAX_SPIKE_K) + "], got " +
+                         std::to_string(spike_k));
+    if (spike_k > 1 && h->L.fmt == 1)
+        return set_error("fkv_attn_set_spike_k: TurboQuant handles select one spike token per head (spike_k = 1)");
+    h->spike_k = spike_k;
+    // a handle whose workspace exists gets the selection buffers now, so
+    // later calls (and fkv_attn_call_noalloc) allocate nothing
+    return h->ws_hq ? ensure_spike_buffers(h, h->ws_hq) : FKV_OK;
+}
+
+int fkv_attn_set_k_scale(fkv_attn* h, const float* k_scale, void* stream) {
+    if (!h || !k_scale) return set_error("fkv_attn_set_k_scale: NULL argument");
+    if (h->L.fmt == 1) return set_error("fkv_attn_set_k_scale: TurboQuant handles have no fp8 keys");
+    hipStream_t st = (hipStream_t)stream;
+    const int n = h->L.B * h->L.Hkv;
+    unsigned* bad = nullptr;
+    unsigned bad_h = 0;
+    int rc = check_hip(hipMalloc(&bad, sizeof(unsigned)), "hipMalloc(flag)");
+    if (!rc) rc = check_hip(hipMemsetAsync(bad, 0, sizeof(unsigned), st), "hipMemsetAsync");
+    if (!rc) {
+        hipLaunchKernelGGL(fkv::fill_kscale_kernel, dim3(fkv::grid_for(n, 256)), dim3(256), 0, st, k_scale, n, h->L,
+                           h->blob, bad);
+        rc = check_hip(hipGetLastError(), "fill_kscale_kernel launch");
+    }
+    if (!rc) rc = check_hip(hipMemcpyAsync(&bad_h, bad, sizeof(unsigned), hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+    if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
+    if (bad) (void)hipFree(bad);
+    if (!rc && bad_h) {
+        set_error("fkv_attn_set_k_scale: a key scale is not a positive finite number");
+        return FKV_EDATA;
+    }
+    if (!rc) h->has_kscale = true;
+    return rc;
+}
+
 void fkv_attn_destroy(fkv_attn* h) {
     if (!h) return;
     if (h->blob) (void)hipFree(h->blob);
+    if (h->spk_tmax) (void)hipFree(h->spk_tmax);
+    if (h->spk_thr) (void)hipFree(h->spk_thr);
+    if (h->spk_flags) (void)hipFree(h->spk_flags);
+    if (h->spk_tokens) (void)hipFree(h->spk_tokens);
     if (h->ws) (void)hipFree(h->ws);
     if (h->qbuf) (void)hipFree(h->qbuf);
     if (h->arrive) (void)hipFree(h->arrive);

@@ -62,6 +62,16 @@ struct AttnArgs {
     uint16_t* out;  // (B, Hq, D) fp16
     int32_t* flags;
     int32_t* tokens;
+    // Top-K spike selection (spike_k > 1, else NULL): every far tile's
+    // maximum score per query head, (B*Hq, tmax_stride = far tiles) fp32,
+    // and each head's spike threshold min_near + margin, (B*Hq) fp32; the
+    // selection kernel (spike_select_kernel) reads both after the launch
+    float* tmax;
+    int tmax_stride;
+    float* thr;
+    // per-head fp8 key scales, (B*Hkv) fp32 in the blob; NULL for a handle
+    // whose keys are unscaled (no load then: the scale is 1)
+    const float* kscale;
     float* ws;      // split partials: [row][split][ng][kHdr + D]
     int* arrive;    // [row] split arrival counters (zero between calls)
     int near_plan;  // expected near tiles per row (balances the far split)
@@ -544,6 +554,7 @@ __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b,
         const int64_t o = (int64_t)b * a.Hq + head0 + g;
         a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
         a.tokens[o] = mx == -INFINITY ? -1 : arg;
+        if (a.thr) a.thr[o] = mn + a.spike_margin;
     }
 }
 
@@ -705,10 +716,30 @@ __device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], c
     return any;
 }
 
+// Where a wave stores its far tiles' per-head maxima for the top-K spike
+// selection: p = the row's first head's tile maxima (NULL: spike_k = 1, no
+// stores), stride = far tiles per head, ng = heads of the row.
+struct SpikeTiles {
+    float* p;
+    int stride, ng;
+};
+
+// The far tile's maximum score of each head of quad qd (sc: the lane's 4
+// scores, -inf past the far tier), stored by lanes 0-3.  The far-tile
+// functions take SPK as a template argument and the stream picks the
+// instantiation once per tile, so the spike_k = 1 path carries no branch.
+template <bool SPK>
+__device__ inline void store_tile_max(const SpikeTiles& sp, int qd, int tile, const float (&sc)[4]) {
+    if (!SPK) return;
+    const float c = head_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    const int lane = (int)threadIdx.x % kWave, h = 4 * qd + lane;
+    if (lane < 4 && h < sp.ng) sp.p[(int64_t)h * sp.stride + tile] = c;
+}
+
 // Scores, spike tracking, softmax and P.V of one loaded far tile.
-template <int D, int NQ, typename QOp>
+template <int D, int NQ, bool SPK, typename QOp>
 __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int tile, int F, int blk,
-                                   float inv_sqrt_d, const QOp& q_lds) {
+                                   float inv_sqrt_d, const QOp& q_lds, const SpikeTiles& sp) {
     constexpr int NS = D / 4;
     const uint32_t sz[4] = {r.sz.x, r.sz.y, r.sz.z, r.sz.w};
     fkv_f4 sacc[NQ];
@@ -759,6 +790,7 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
             sc[e] = ok ? sv : -INFINITY;
             if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
         }
+        store_tile_max<SPK>(sp, qd, tile, sc);
         any |= softmax_w<D, NQ, true>(st, qd, sc, sz, w4[qd]);
     }
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
@@ -1302,9 +1334,9 @@ __device__ inline void g32_pv_step_ops(fkv_f4& acc0, fkv_f4& acc1, const fkv_h4 
 }
 
 // Scores, spike tracking, softmax and P.V of one group-32 far tile.
-template <int D, int NQ, typename QOp>
+template <int D, int NQ, bool SPK, typename QOp>
 __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, int tile, int F, int lane,
-                                       float inv_sqrt_d, const QOp& q_lds) {
+                                       float inv_sqrt_d, const QOp& q_lds, const SpikeTiles& sp) {
     constexpr int NS = D / 4, NH = D / 64, NG = D / 32;
     const int blk = lane >> 2, half = lane >> 5;
     fkv_f4 sacc[NQ];
@@ -1339,6 +1371,7 @@ __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, in
             sc[e] = ok ? sv : -INFINITY;
             if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
         }
+        store_tile_max<SPK>(sp, qd, tile, sc);
         any |= tq_softmax<D, NQ>(st, qd, sc, p[qd]);
     }
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
@@ -1762,6 +1795,7 @@ __device__ inline void merge_values(const AttnArgs& a, const fkv_f4 (&v)[KV], fl
     if (lane == 0) {
         a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
         a.tokens[o] = mx == -INFINITY ? -1 : arg;
+        if (a.thr) a.thr[o] = mn + a.spike_margin;
     }
     // in the load groups of 4: splits past the last have scale 0 and value 0
     fkv_f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -2232,6 +2266,12 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     // launches, so they are read as constant memory (scalar loads, whose
     // counter is not the one the ring's DMA uses)
     const int nv = (int)*(const FKV_CONST uint32_t*)(uintptr_t)(a.blob + a.L.near_valid + 4 * (int64_t)kvh);
+    // far keys' score factor: 1/sqrt(D) times the row's fp8 key scale (1
+    // unless the handle holds per-head-scaled keys: the scale folds into the
+    // score instead of the keys, so the far tile's arithmetic is unchanged)
+    const float far_scale =
+        TQ || !a.kscale ? a.inv_sqrt_d : a.inv_sqrt_d * *(const FKV_CONST float*)(uintptr_t)(a.kscale + bkv);
+    const SpikeTiles spk{a.tmax ? a.tmax + ((int64_t)b * a.Hq + head0) * a.tmax_stride : nullptr, a.tmax_stride, ng};
     const int nd_raw = a.n_dec_dev ? *(const FKV_CONST int32_t*)(uintptr_t)a.n_dec_dev : a.n_dec;
     float asum[NQ];
 #pragma unroll
@@ -2337,11 +2377,13 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
             } else if constexpr (G32) {
                 FarTileG<D> r;
                 lds_g32(r, slot, lane);
-                g32_far_compute<D, NQ>(st, r, tile, a.L.F, lane, a.inv_sqrt_d, qx);
+                if (spk.p) g32_far_compute<D, NQ, true>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
+                else g32_far_compute<D, NQ, false>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
             } else {
                 FarTile<D> r;
                 lds_far(r, slot, lane);
-                far_compute<D, NQ>(st, r, tile, a.L.F, blk, a.inv_sqrt_d, qx);
+                if (spk.p) far_compute<D, NQ, true>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
+                else far_compute<D, NQ, false>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
             }
         } else if (kd == kNearK) {
             // near tiles: the unrotated query

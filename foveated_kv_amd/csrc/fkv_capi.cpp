@@ -28,7 +28,7 @@ extern "C" {
 
 const char* fkv_last_error(void) { return fkv::g_last_error.c_str(); }
 
-int fkv_version(void) { return 100; }
+int fkv_version(void) { return 200; }
 
 int fkv_is_available(void) {
     int n = 0;

@@ -38,6 +38,9 @@ struct CompressArgs {
     int32_t* near_valid;
     uint16_t* arc_k;
     uint16_t* arc_v;
+    // per-head-scaled fp8 keys (cfg->k_scale): (B*H) fp32 scales the far
+    // keys are divided by before encoding; NULL = unscaled (the reference)
+    const float* kscale;
 };
 
 __device__ inline uint8_t encode_e4m3(uint16_t bits) {
@@ -96,16 +99,23 @@ __device__ inline uint4 pack8(const uint16_t (&x)[8]) {
 
 // One far row (fr = bh * F + f) from its fp16 K / V (8 elements per lane):
 // E4M3 keys, INT4 values per token (VG = 0) or per VG-dim group, archive.
+// The fp16 value a key is encoded from: the key itself, or with a per-head
+// scale fp16(key / scale) (fp32 division, rounded to nearest even).
+__device__ inline uint16_t scaled_key(uint16_t k, const float* kscale, int bh) {
+    return kscale ? f2h(h2f(k) / kscale[bh]) : k;
+}
+
 template <int D, int VG>
 __device__ inline void far_row(const CompressArgs& a, int64_t fr, int sub, const uint16_t (&kx)[8],
                                const uint16_t (&vx)[8]) {
     constexpr int LPR = D / 8;
     // far K: E4M3 codes
+    const int bh = a.tb.far_count > 0 ? (int)(fr / a.tb.far_count) : 0;
     uint32_t c0 = 0, c1 = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        c0 |= (uint32_t)encode_e4m3(kx[i]) << (8 * i);
-        c1 |= (uint32_t)encode_e4m3(kx[4 + i]) << (8 * i);
+        c0 |= (uint32_t)encode_e4m3(scaled_key(kx[i], a.kscale, bh)) << (8 * i);
+        c1 |= (uint32_t)encode_e4m3(scaled_key(kx[4 + i], a.kscale, bh)) << (8 * i);
     }
     *(uint2*)(a.far_k + fr * D + sub * 8) = make_uint2(c0, c1);
     // far V: INT4 per token (VG = 0) or per 32-dim group
@@ -182,6 +192,48 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressArgs a) {
     far_row<D, VG>(a, (int64_t)bh * F + f, sub, kx, vx);
 }
 
+
+// ---------------------------------------------------------------------------
+// Per-head fp8 key scale (the benchmark's "per-head-scaled fp8 E4M3" keys;
+// an extension: the reference encodes keys unscaled,
+// foveated_compress.metal:39-66).  scale = amax / 240 over the finite
+// values of the head's far keys (fp32 division; 1 when amax is 0), so the
+// head's largest |key| encodes to 240 (0x77): the encoder above emits
+// exponent 15 only as the saturation code 0x7E (448), so 240 is the top of
+// its 3-bit-mantissa range, and a scale of amax / 448 would put every key
+// in (240, 448] x scale on 448.
+// ---------------------------------------------------------------------------
+
+constexpr int kScaleThreads = 256;
+
+// One workgroup per (batch, head): the far rows are positions mid_start..
+// (far_idx NULL) or far_idx[bh][f]; out-of-range indices are zero rows.
+template <int D>
+__global__ __launch_bounds__(kScaleThreads) void kscale_kernel(CompressArgs a, const int32_t* __restrict__ far_idx,
+                                                               float* __restrict__ out) {
+    constexpr int LPR = D / 8, RPB = kScaleThreads / LPR;
+    __shared__ float red[kScaleThreads / kWave];
+    const int bh = blockIdx.x, sub = threadIdx.x % LPR;
+    const int F = a.tb.far_count;
+    float amax = 0.f;
+    for (int f = threadIdx.x / LPR; f < F; f += RPB) {
+        const int t = far_idx ? far_idx[(int64_t)bh * F + f] : a.tb.mid_start + f;
+        if (t < 0 || t >= a.S) continue;
+        uint16_t kx[8];
+        load8(a.k, a.dtype, ((int64_t)bh * a.S + t) * D + sub * 8, kx);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (((kx[i] >> 10) & 0x1f) != 0x1f) amax = fmaxf(amax, fabsf(h2f(kx[i])));
+    }
+    amax = wave_max(amax);
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = 0.f;
+        for (int w = 0; w < kScaleThreads / kWave; w++) m = fmaxf(m, red[w]);
+        out[bh] = m > 0.f ? m / 240.0f : 1.0f;
+    }
+}
 
 // ---------------------------------------------------------------------------
 // Importance partition: near = sinks + the near_from_mid middle tokens of
@@ -368,6 +420,8 @@ int compress_setup(const char* fn, const fkv_tier_config* cfg, const void* keys,
     if (in_dtype < FKV_F16 || in_dtype > FKV_F32) return set_error(name + ": unsupported dtype");
     if (cfg->v_group != 0 && cfg->v_group != 32)
         return set_error(name + ": v_group must be 0 (per token) or 32, got " + std::to_string(cfg->v_group));
+    if (cfg->k_scale != 0 && cfg->k_scale != 1)
+        return set_error(name + ": k_scale must be 0 (unscaled) or 1 (per head), got " + std::to_string(cfg->k_scale));
     fkv_tiers tb;
     if (int rc = fkv_tier_boundaries(cfg, S, &tb)) return rc;
     if ((S > 0 && (!keys || !values)) || !near_k || !near_v || !near_valid ||
@@ -389,7 +443,38 @@ int compress_setup(const char* fn, const fkv_tier_config* cfg, const void* keys,
     a.near_valid = near_valid;
     a.arc_k = (uint16_t*)archive_k;
     a.arc_v = (uint16_t*)archive_v;
+    a.kscale = nullptr;
     return FKV_OK;
+}
+
+// Recency (near_idx == NULL) or indexed compress of one layer, with the
+// per-head key scales computed first when cfg->k_scale is set.
+int compress_launch(const char* fn, const fkv_tier_config* cfg, fkv::CompressArgs& a, int D, const int32_t* near_idx,
+                    const int32_t* far_idx, float* far_k_scale, hipStream_t st) {
+    const int B = a.B, H = a.H;
+    const bool g32 = cfg->v_group == 32;
+    if (cfg->k_scale) {
+        if (!far_k_scale) return fkv::set_error(std::string(fn) + ": k_scale needs far_k_scale");
+        hipLaunchKernelGGL(D == 128 ? fkv::kscale_kernel<128> : fkv::kscale_kernel<64>, dim3((unsigned)(B * H)),
+                           dim3(fkv::kScaleThreads), 0, st, a, near_idx ? far_idx : nullptr, far_k_scale);
+        a.kscale = far_k_scale;
+    }
+    const int rpb = 256 / (D / 8);
+    if (!near_idx) {
+        const int rows = a.S + a.tb.headroom;
+        dim3 grid((unsigned)fkv::cdiv(rows > 0 ? rows : 1, rpb), (unsigned)(B * H));
+        void (*kern)(fkv::CompressArgs) = D == 128 ? (g32 ? fkv::compress_kernel<128, 32> : fkv::compress_kernel<128, 0>)
+                                                   : (g32 ? fkv::compress_kernel<64, 32> : fkv::compress_kernel<64, 0>);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, a);
+        return fkv::check_hip(hipGetLastError(), "compress_kernel launch");
+    }
+    const int rows = a.tb.n_near_padded + a.tb.far_count;
+    dim3 grid((unsigned)fkv::cdiv(rows > 0 ? rows : 1, rpb), (unsigned)(B * H));
+    void (*kern)(fkv::CompressArgs, const int32_t*, const int32_t*) =
+        D == 128 ? (g32 ? fkv::compress_gather_kernel<128, 32> : fkv::compress_gather_kernel<128, 0>)
+                 : (g32 ? fkv::compress_gather_kernel<64, 32> : fkv::compress_gather_kernel<64, 0>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, a, near_idx, far_idx);
+    return fkv::check_hip(hipGetLastError(), "compress_gather_kernel launch");
 }
 
 }  // namespace
@@ -403,15 +488,8 @@ extern "C" int fkv_compress_layer(const fkv_tier_config* cfg, const void* keys, 
     if (int rc = compress_setup("fkv_compress_layer", cfg, keys, values, in_dtype, B, H, S, D, near_k, near_v, far_k,
                                 far_v, far_v_scale, far_v_zero, near_valid, archive_k, archive_v, a))
         return rc;
-    const int rows = S + a.tb.headroom;
-    const int rpb = 256 / (D / 8);
-    dim3 grid((unsigned)fkv::cdiv(rows > 0 ? rows : 1, rpb), (unsigned)(B * H));
-    hipStream_t st = (hipStream_t)stream;
-    const bool g32 = cfg->v_group == 32;
-    void (*kern)(fkv::CompressArgs) = D == 128 ? (g32 ? fkv::compress_kernel<128, 32> : fkv::compress_kernel<128, 0>)
-                                               : (g32 ? fkv::compress_kernel<64, 32> : fkv::compress_kernel<64, 0>);
-    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, a);
-    return fkv::check_hip(hipGetLastError(), "compress_kernel launch");
+    if (cfg->k_scale) return fkv::set_error("fkv_compress_layer: k_scale needs fkv_compress_layer_ex (far_k_scale)");
+    return compress_launch("fkv_compress_layer", cfg, a, D, nullptr, nullptr, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int fkv_partition_importance(const fkv_tier_config* cfg, const float* importance, int32_t B, int32_t H,
@@ -440,13 +518,23 @@ extern "C" int fkv_compress_layer_indexed(const fkv_tier_config* cfg, const void
         return rc;
     if (!near_idx || (a.tb.far_count > 0 && !far_idx))
         return fkv::set_error("fkv_compress_layer_indexed: NULL index array");
-    const int rows = a.tb.n_near_padded + a.tb.far_count;
-    const int rpb = 256 / (D / 8);
-    dim3 grid((unsigned)fkv::cdiv(rows > 0 ? rows : 1, rpb), (unsigned)(B * H));
-    const bool g32 = cfg->v_group == 32;
-    void (*kern)(fkv::CompressArgs, const int32_t*, const int32_t*) =
-        D == 128 ? (g32 ? fkv::compress_gather_kernel<128, 32> : fkv::compress_gather_kernel<128, 0>)
-                 : (g32 ? fkv::compress_gather_kernel<64, 32> : fkv::compress_gather_kernel<64, 0>);
-    hipLaunchKernelGGL(kern, grid, dim3(256), 0, (hipStream_t)stream, a, near_idx, far_idx);
-    return fkv::check_hip(hipGetLastError(), "compress_gather_kernel launch");
+    if (cfg->k_scale)
+        return fkv::set_error("fkv_compress_layer_indexed: k_scale needs fkv_compress_layer_ex (far_k_scale)");
+    return compress_launch("fkv_compress_layer_indexed", cfg, a, D, near_idx, far_idx, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int fkv_compress_layer_ex(const fkv_tier_config* cfg, const void* keys, const void* values,
+                                     int32_t in_dtype, int32_t B, int32_t H, int32_t S, int32_t D,
+                                     const int32_t* near_idx, const int32_t* far_idx, void* near_k, void* near_v,
+                                     uint8_t* far_k, uint8_t* far_v, void* far_v_scale, void* far_v_zero,
+                                     float* far_k_scale, int32_t* near_valid, void* archive_k, void* archive_v,
+                                     void* stream) {
+    fkv::CompressArgs a;
+    if (int rc = compress_setup("fkv_compress_layer_ex", cfg, keys, values, in_dtype, B, H, S, D, near_k, near_v,
+                                far_k, far_v, far_v_scale, far_v_zero, near_valid, archive_k, archive_v, a))
+        return rc;
+    if (!near_idx != !far_idx && a.tb.far_count > 0)
+        return fkv::set_error("fkv_compress_layer_ex: near_idx and far_idx are both given or both NULL");
+    return compress_launch("fkv_compress_layer_ex", cfg, a, D, near_idx, near_idx ? far_idx : nullptr, far_k_scale,
+                           (hipStream_t)stream);
 }

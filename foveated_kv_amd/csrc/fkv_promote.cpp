@@ -67,6 +67,9 @@ constexpr int kMaxDrainHeads = 256;
 
 struct fkv_promoter {
     int n_layers = 0, cooldown = 5, max_per_drain = 8;
+    // spiking tokens a drain takes per query head (fkv_promoter_set_spike_k;
+    // 1 = the reference's single token)
+    int spike_k = 1;
     std::vector<Archive> arch;
     std::vector<fkv_attn*> handles;
     std::vector<std::vector<uint32_t>> mirror;  // host copy of each layer's near_valid
@@ -170,6 +173,7 @@ struct DrainArgs {
     const int32_t* tokens;
     const int32_t* far_idx;
     int B, Hq, Hkv, N_far, step, cooldown, budget;
+    int spike_k;        // tokens per query head (tokens is (B*Hq, spike_k))
     int32_t* step_dev;  // when set, the step is read here
     int advance;        // then step + 1 is stored there once every thread has read it
     int32_t* last_step;
@@ -187,31 +191,53 @@ struct DrainArgs {
 // The drain filter (promotion_pipeline.cpp:99-175) and the promotion
 // (:192-241) of one layer as one workgroup, with the sequential scan
 // restated in parallel.  The scan visits (batch, query head) in order, keeps
-// only the first spike of each KV head (its GQA dedup), and stops once
-// `budget` spikes are queued.  Each KV head's state (last promotion step,
-// promoted bitmap, near_valid) is touched only by its own first spike, so
-// every head's outcome -- cooled down, no archived position, duplicate, or
-// queued -- is independent of the others; the scan's budget stop then means:
-// a head's first spike is processed iff fewer than `budget` queued first
-// spikes precede it in scan order.  Threads: one per (batch, query head) to
-// find each head's first spike, one per KV head for its outcome and the
-// budget rank, then all threads copy the exact fp16 rows of every archive
-// batch from pinned host memory into the assigned headroom slots; the
-// near_valid bumps are written last (the next launch on the stream sees rows
-// and counts together).  Records carry no order: each KV head has at most
-// one per drain and gets the slot at its own near_valid.
-enum : int { kNoSpike = 0, kCooled, kStamped, kDuplicate, kMarked, kQueued };
+// only the first spike of each KV head (its GQA dedup) and hands its tokens
+// (one, or with spike_k > 1 up to spike_k in descending score order) through
+// the position dedup and the archive lookup until `budget` tokens are
+// queued.  Each KV head's state (last promotion step, promoted bitmap,
+// near_valid) is touched only by its own first spike, and its tokens are
+// distinct positions, so every head's outcome -- cooled down, or per token
+// out of range, duplicate, no archived row, queued -- is independent of the
+// others; the scan's budget stop then becomes a prefix sum: a head is
+// processed iff the heads before it in scan order would queue fewer than
+// `budget` tokens, and it queues at most the rest of the budget.  Threads:
+// one per (batch, query head) to find each head's first spike, one per KV
+// head for its outcome, the budget prefix and its records, then all threads
+// copy the exact fp16 rows of every archive batch from pinned host memory
+// into the assigned headroom slots; the near_valid bumps are written last
+// (the next launch on the stream sees rows and counts together).  A head's
+// records take the slots from its near_valid on, in token order.
+enum : int { kTokSkip = 0, kTokDup, kTokMarked, kTokQueued };
+
+// The outcome of one token of KV head hkv's first spike (f: its flat
+// (batch, query head) index); pos / arc / bit are set for the last three.
+__device__ inline int drain_token(const DrainArgs& a, int f, int hkv, int j, int& pos, int& arc, uint32_t& bit,
+                                  int64_t& widx) {
+    const int fl = a.tokens[(int64_t)f * a.spike_k + j];
+    if (fl < 0 || fl >= a.N_far) return kTokSkip;
+    const int32_t p = a.far_idx[((int64_t)(f / a.Hq) * a.Hkv + hkv) * a.N_far + fl];
+    if (p < 0 || p >= a.P) return kTokSkip;
+    pos = p;
+    widx = (int64_t)hkv * a.words + (p >> 5);
+    bit = 1u << (p & 31);
+    if (a.promoted[widx] & bit) return kTokDup;
+    arc = a.pos_to_local[(int64_t)hkv * a.P + p];
+    return arc >= 0 ? kTokQueued : kTokMarked;
+}
 
 __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
     __shared__ int first[kMaxDrainHeads];
-    __shared__ uint8_t queues[kMaxDrainHeads];
+    __shared__ int nq[kMaxDrainHeads];                  // tokens each head would queue
+    __shared__ int n_rec[kMaxDrainHeads], slot0[kMaxDrainHeads];
+    __shared__ int rec_arc[kMaxDrainHeads][FKV_MAX_SPIKE_K];
     __shared__ unsigned cnt[6];  // detected, queued, deduplicated, cooled down, records, headroom full
-    __shared__ int n_rec;
-    __shared__ int rec_h[kMaxDrainHeads], rec_slot[kMaxDrainHeads], rec_arc[kMaxDrainHeads];
     const int tid = threadIdx.x;
-    for (int i = tid; i < kMaxDrainHeads; i += blockDim.x) first[i] = INT_MAX;
+    for (int i = tid; i < kMaxDrainHeads; i += blockDim.x) {
+        first[i] = INT_MAX;
+        nq[i] = 0;
+        n_rec[i] = 0;
+    }
     if (tid < 6) cnt[tid] = 0;
-    if (tid == 0) n_rec = 0;
     __syncthreads();
     const int gqa = a.Hq / a.Hkv > 0 ? a.Hq / a.Hkv : 1;
     const int total = a.B * a.Hq;
@@ -226,79 +252,91 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
     const int hkv = tid;
     const int f = hkv < a.Hkv ? first[hkv] : INT_MAX;
     const int step = a.step_dev ? *a.step_dev : a.step;
-    int kind = kNoSpike, pos = 0, arc = -1;
-    uint32_t word = 0;
+    const int K = a.spike_k;
+    bool cooled = false;
+    int n_tok = 0;
     if (f != INT_MAX) {
         const int32_t last = a.last_step[hkv];
-        kind = (last != kNoStep && step - last < a.cooldown) ? kCooled : kStamped;
-        const int fl = a.tokens[f];
-        if (kind == kStamped && fl >= 0 && fl < a.N_far) {
-            const int32_t p = a.far_idx[((int64_t)(f / a.Hq) * a.Hkv + hkv) * a.N_far + fl];
-            if (p >= 0 && p < a.P) {
-                pos = p;
-                word = a.promoted[(int64_t)hkv * a.words + (p >> 5)];
-                if (word & (1u << (p & 31))) {
-                    kind = kDuplicate;
-                } else {
-                    arc = a.pos_to_local[(int64_t)hkv * a.P + p];
-                    kind = arc >= 0 ? kQueued : kMarked;
-                }
+        cooled = last != kNoStep && step - last < a.cooldown;
+        n_tok = K > 1 ? (a.flags[f] < K ? a.flags[f] : K) : 1;
+        if (!cooled) {
+            int q = 0;
+            for (int j = 0; j < n_tok; j++) {
+                int pos = 0, arc = -1;
+                uint32_t bit = 0;
+                int64_t widx = 0;
+                q += drain_token(a, f, hkv, j, pos, arc, bit, widx) == kTokQueued;
             }
+            nq[hkv] = q;
         }
     }
-    if (hkv < kMaxDrainHeads) queues[hkv] = kind == kQueued;
     __syncthreads();
-    if (kind != kNoSpike) {
-        int before = 0;  // queued first spikes earlier in scan order
-        for (int j = 0; j < a.Hkv; j++) before += (queues[j] && first[j] < f) ? 1 : 0;
+    if (f != INT_MAX) {
+        int before = 0;  // tokens the heads earlier in scan order queue
+        for (int h = 0; h < a.Hkv; h++) before += first[h] < f ? nq[h] : 0;
         if (before < a.budget) {
             atomicAdd(&cnt[0], 1u);
-            if (kind == kCooled) {
+            if (cooled) {
                 atomicAdd(&cnt[3], 1u);
             } else {
                 a.last_step[hkv] = step;
-                if (kind == kDuplicate) atomicAdd(&cnt[2], 1u);
-                if (kind >= kMarked) a.promoted[(int64_t)hkv * a.words + (pos >> 5)] = word | (1u << (pos & 31));
-                if (kind == kQueued) {
-                    atomicAdd(&cnt[1], 1u);
-                    const uint32_t cur = ((const uint32_t*)(a.blob + a.L.near_valid))[hkv];
-                    if ((int)cur >= a.L.Na) {
-                        atomicAdd(&cnt[5], 1u);
-                    } else {
-                        const int r = atomicAdd(&n_rec, 1);
-                        rec_h[r] = hkv;
-                        rec_slot[r] = (int)cur;
-                        rec_arc[r] = arc;
+                const int allow = a.budget - before;
+                const uint32_t cur = ((const uint32_t*)(a.blob + a.L.near_valid))[hkv];
+                int queued = 0, recs = 0;
+                unsigned dups = 0, full = 0;
+                for (int j = 0; j < n_tok && queued < allow; j++) {
+                    int pos = 0, arc = -1;
+                    uint32_t bit = 0;
+                    int64_t widx = 0;
+                    const int kind = drain_token(a, f, hkv, j, pos, arc, bit, widx);
+                    if (kind == kTokSkip) continue;
+                    if (kind == kTokDup) {
+                        dups++;
+                        continue;
                     }
+                    a.promoted[widx] |= bit;
+                    if (kind != kTokQueued) continue;
+                    if ((int)cur + queued >= a.L.Na) full++;
+                    else rec_arc[hkv][recs++] = arc;
+                    queued++;
                 }
+                n_rec[hkv] = recs;
+                slot0[hkv] = (int)cur;
+                atomicAdd(&cnt[1], (unsigned)queued);
+                atomicAdd(&cnt[2], dups);
+                atomicAdd(&cnt[4], (unsigned)recs);
+                atomicAdd(&cnt[5], full);
             }
         }
     }
     __syncthreads();
-    const int n = n_rec, D = a.L.D;
-    if (tid < 6) a.stats[tid] += tid == 4 ? (unsigned long long)n : (unsigned long long)cnt[tid];
+    if (tid < 6) a.stats[tid] += (unsigned long long)cnt[tid];
     const int nb = a.arc_B < a.L.B ? a.arc_B : a.L.B;
     uint16_t* nk = (uint16_t*)(a.blob + a.L.near_k);
     uint16_t* nv = (uint16_t*)(a.blob + a.L.near_v);
     // 16-byte reads of the pinned archive (8 dims of a row: few, wide bus
     // transactions); the 8 K dims are contiguous in the near tile, the V
     // dims are 8 elements apart
-    const int DC = D / 8;
-    for (int e = tid; e < n * nb * DC; e += blockDim.x) {
-        const int c = e % DC, b = (e / DC) % nb, i = e / (DC * nb);
-        const int h = rec_h[i], slot = rec_slot[i];
-        const int64_t base = ((int64_t)b * a.L.Hkv + h) * a.L.Na_pad * D;
-        const int64_t src = (((int64_t)b * a.Hkv + h) * a.arc_S + rec_arc[i]) * D + 8 * c;
-        const uint4 kw = *(const uint4*)(a.ark + src);
-        const uint4 vw = *(const uint4*)(a.arv + src);
-        *(uint4*)(nk + base + fkv::near_k_index(slot, 8 * c, D)) = kw;
-        const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+    const int D = a.L.D, DC = D / 8;
+    for (int h = 0; h < a.Hkv; h++) {
+        const int n = n_rec[h];
+        for (int e = tid; e < n * nb * DC; e += blockDim.x) {
+            const int c = e % DC, b = (e / DC) % nb, i = e / (DC * nb);
+            const int slot = slot0[h] + i;
+            const int64_t base = ((int64_t)b * a.L.Hkv + h) * a.L.Na_pad * D;
+            const int64_t src = (((int64_t)b * a.Hkv + h) * a.arc_S + rec_arc[h][i]) * D + 8 * c;
+            const uint4 kw = *(const uint4*)(a.ark + src);
+            const uint4 vw = *(const uint4*)(a.arv + src);
+            *(uint4*)(nk + base + fkv::near_k_index(slot, 8 * c, D)) = kw;
+            const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            nv[base + fkv::near_v_index(slot, 8 * c + k, D)] = (uint16_t)(vv[k >> 1] >> (16 * (k & 1)));
+            for (int k = 0; k < 8; k++)
+                nv[base + fkv::near_v_index(slot, 8 * c + k, D)] = (uint16_t)(vv[k >> 1] >> (16 * (k & 1)));
+        }
     }
     __syncthreads();
-    if (tid < n) ((uint32_t*)(a.blob + a.L.near_valid))[rec_h[tid]] = (uint32_t)(rec_slot[tid] + 1);
+    if (hkv < a.Hkv && n_rec[hkv] > 0)
+        ((uint32_t*)(a.blob + a.L.near_valid))[hkv] = (uint32_t)(slot0[hkv] + n_rec[hkv]);
     // every thread read the step before the barriers above
     if (a.advance && tid == 0) *a.step_dev = step + 1;
 }
@@ -498,24 +536,41 @@ int fkv_promoter_drain(fkv_promoter* p, int32_t layer, const int32_t* flags, con
                 continue;
             }
             p->last_step[cd_key] = step;
-            const int far_local = tokens[flat];
-            if (far_local < 0 || far_local >= N_far) continue;
-            const int32_t position = far_idx[((int64_t)b * Hkv + hkv) * N_far + far_local];
-            const uint64_t key = ((uint64_t)(layer & 0xFFFF) << 48) | ((uint64_t)(hkv & 0xFFFF) << 32) |
-                                 (uint64_t)(uint32_t)position;
-            if (!p->promoted.insert(key).second) {
-                p->stats.spikes_deduplicated++;
-                continue;
+            // the query head's spiking tokens (K > 1: flags holds their
+            // count, tokens their far-local indices in descending score
+            // order), each through the position dedup, the archive lookup
+            // and the budget
+            const int K = p->spike_k;
+            const int n_tok = K > 1 ? (flags[flat] < K ? flags[flat] : K) : 1;
+            for (int j = 0; j < n_tok && queued < p->max_per_drain; j++) {
+                const int far_local = tokens[(int64_t)flat * K + j];
+                if (far_local < 0 || far_local >= N_far) continue;
+                const int32_t position = far_idx[((int64_t)b * Hkv + hkv) * N_far + far_local];
+                const uint64_t key = ((uint64_t)(layer & 0xFFFF) << 48) | ((uint64_t)(hkv & 0xFFFF) << 32) |
+                                     (uint64_t)(uint32_t)position;
+                if (!p->promoted.insert(key).second) {
+                    p->stats.spikes_deduplicated++;
+                    continue;
+                }
+                if (hkv >= (int)a.pos_to_local.size()) continue;
+                auto pit = a.pos_to_local[hkv].find(position);
+                if (pit == a.pos_to_local[hkv].end()) continue;
+                p->queue.push_back({layer, hkv, pit->second, position});
+                p->stats.spikes_queued++;
+                queued++;
             }
-            if (hkv >= (int)a.pos_to_local.size()) continue;
-            auto pit = a.pos_to_local[hkv].find(position);
-            if (pit == a.pos_to_local[hkv].end()) continue;
-            p->queue.push_back({layer, hkv, pit->second, position});
-            p->stats.spikes_queued++;
-            queued++;
         }
     }
     return queued;
+}
+
+int fkv_promoter_set_spike_k(fkv_promoter* p, int32_t spike_k) {
+    if (!p) return set_error("fkv_promoter_set_spike_k: NULL pipeline");
+    if (spike_k < 1 || spike_k > FKV_MAX_SPIKE_K)
+        return set_error("fkv_promoter_set_spike_k: spike_k must be in [1, " + std::to_string(FKV_MAX_SPIKE_K) +
+                         "], got " + std::to_string(spike_k));
+    p->spike_k = spike_k;
+    return FKV_OK;
 }
 
 int fkv_promoter_pending(const fkv_promoter* p, int32_t* out_records, int32_t max_records) {
@@ -569,6 +624,7 @@ int fkv_promoter_drain_device(fkv_promoter* p, int32_t layer, const int32_t* fla
     a.advance = advance_step != 0;
     a.cooldown = p->cooldown;
     a.budget = p->max_per_drain;
+    a.spike_k = p->spike_k;
     a.last_step = d.last_step;
     a.promoted = d.promoted;
     a.pos_to_local = d.pos_to_local;

@@ -40,11 +40,14 @@ class TierConfig:
         # far V INT4 scale / zero per token (0, the reference) or per 32-dim
         # group (32): the benchmark's group-32 packed layout
         self.v_group = 0
+        # far K E4M3 unscaled (0, the reference) or per-head scaled (1): the
+        # benchmark's "per-head-scaled fp8 E4M3" keys, scale = amax / 240
+        self.k_scale = 0
 
     def to_c(self):
         return _lib.TierConfigC(float(self.near_pct), int(self.n_sinks), int(self.window_size),
                                 float(self.promo_headroom_pct), int(self.promo_headroom_min),
-                                int(self.v_group))
+                                int(self.v_group), int(self.k_scale))
 
 
 def tier_boundaries_c(cfg, S):
@@ -87,7 +90,8 @@ class CompressedLayer:
     """csrc/foveated_compress.h:100-118 (+ the fp16 far-row archive)."""
 
     def __init__(self, near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid,
-                 n_near_actual, archive_k=None, archive_v=None, near_idx=None, far_idx=None):
+                 n_near_actual, archive_k=None, archive_v=None, near_idx=None, far_idx=None,
+                 far_k_scale=None):
         self.near_k = near_k
         self.near_v = near_v
         self.far_k = far_k
@@ -102,6 +106,9 @@ class CompressedLayer:
         # partition (None: the recency partition of the tier boundaries)
         self.near_idx = near_idx
         self.far_idx = far_idx
+        # (B,H) fp32 per-head key scales of per-head-scaled far keys (None:
+        # unscaled keys, the reference)
+        self.far_k_scale = far_k_scale
 
 
 class CompressHandle:
@@ -143,23 +150,19 @@ class CompressHandle:
         near_valid = torch.empty((H,), dtype=torch.int32, device=dev)
         arc_k = torch.empty((B, H, F, D), dtype=torch.float16, device=dev) if with_archive else None
         arc_v = torch.empty_like(arc_k) if with_archive else None
+        ks = torch.empty((B, H), dtype=torch.float32, device=dev) if int(self.cfg.k_scale) else None
         lib = _lib.load()
         c = self.cfg.to_c()
         near_idx = far_idx = None
         with torch.cuda.device(dev):
-            if importance is None:
-                check(lib.fkv_compress_layer(ctypes.byref(c), ptr(k), ptr(v), dtype_code(k.dtype), B, H, S, D,
-                                             ptr(near_k), ptr(near_v), ptr(far_k), ptr(far_v), ptr(fvs), ptr(fvz),
-                                             ptr(near_valid), ptr(arc_k), ptr(arc_v), _lib.stream_ptr(dev)),
-                      "fkv_compress_layer")
-            else:
+            if importance is not None:
                 near_idx, far_idx = partition_importance(self.cfg, importance, B, H, S)
-                check(lib.fkv_compress_layer_indexed(
-                    ctypes.byref(c), ptr(k), ptr(v), dtype_code(k.dtype), B, H, S, D, ptr(near_idx), ptr(far_idx),
-                    ptr(near_k), ptr(near_v), ptr(far_k), ptr(far_v), ptr(fvs), ptr(fvz), ptr(near_valid),
-                    ptr(arc_k), ptr(arc_v), _lib.stream_ptr(dev)), "fkv_compress_layer_indexed")
+            check(lib.fkv_compress_layer_ex(
+                ctypes.byref(c), ptr(k), ptr(v), dtype_code(k.dtype), B, H, S, D, ptr(near_idx), ptr(far_idx),
+                ptr(near_k), ptr(near_v), ptr(far_k), ptr(far_v), ptr(fvs), ptr(fvz), ptr(ks), ptr(near_valid),
+                ptr(arc_k), ptr(arc_v), _lib.stream_ptr(dev)), "fkv_compress_layer_ex")
         return CompressedLayer(near_k, near_v, far_k, far_v, fvs, fvz, near_valid, tb["R_actual"],
-                               arc_k, arc_v, near_idx, far_idx)
+                               arc_k, arc_v, near_idx, far_idx, far_k_scale=ks)
 
     def compress_all(self, all_keys, all_values, with_archive=True):
         return [self.compress_layer(k, v, with_archive) for k, v in zip(all_keys, all_values)]
@@ -206,9 +209,17 @@ class FoveatedHandle:
     arrays into a private device blob; calling it launches the fused kernel.
     ``metallib_path`` is accepted for signature compatibility and ignored."""
 
+    spike_k = 1  # spiking far tokens per query head the calls report
+
     def __init__(self, near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid,
-                 spike_margin=0.5, metallib_path=""):
-        _require_device(near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid)
+                 spike_margin=0.5, metallib_path="", far_k_scale=None, spike_k=1):
+        """Extensions beyond the reference's arguments (bindings.cpp:20-31):
+        ``far_k_scale`` (B,H) fp32, the per-head scales of per-head-scaled
+        fp8 keys (CompressedLayer.far_k_scale); ``spike_k`` in [1, 32], the
+        spiking far tokens a call reports per query head (1: the
+        reference's single token; K > 1: spike_flags hold the counts and
+        spike_tokens are (B,Hq,K), see fkv_attn_set_spike_k)."""
+        _require_device(near_k, near_v, far_k, far_v, far_v_scale, far_v_zero, near_valid, far_k_scale)
         if near_k.dim() != 4 or near_k.shape != near_v.shape:
             raise ValueError("near_k/near_v must be (B,H,N,D) with equal shapes")
         B, H, Na, D = near_k.shape
@@ -247,6 +258,19 @@ class FoveatedHandle:
                   "fkv_attn_create_g32" if grouped else "fkv_attn_create")
         self._h = h
         self._lib = lib
+        self.spike_k = 1
+        if far_k_scale is not None:
+            if tuple(far_k_scale.shape) != (B, H):
+                raise ValueError(f"far_k_scale must be (B,H) = {(B, H)}, got {tuple(far_k_scale.shape)}")
+            ks = far_k_scale.to(torch.float32).contiguous()
+            with torch.cuda.device(self.device):
+                check(lib.fkv_attn_set_k_scale(h, ptr(ks), _lib.stream_ptr(self.device)), "fkv_attn_set_k_scale")
+        self.set_spike_k(spike_k)
+
+    def set_spike_k(self, spike_k):
+        """Spiking far tokens per query head reported by later calls."""
+        check(self._lib.fkv_attn_set_spike_k(self._h, int(spike_k)), "fkv_attn_set_spike_k")
+        self.spike_k = int(spike_k)
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -256,6 +280,7 @@ class FoveatedHandle:
 
     def __call__(self, query, decode_k=None, decode_v=None, n_decode=None, out=None):
         """-> [out (B,Hq,1,D) fp16, spike_flags (B,Hq) int32, spike_tokens (B,Hq) int32]
+        (spike_k > 1: spike_flags are spike counts, spike_tokens (B,Hq,K))
 
         n_decode (optional): a one-element int32 device tensor holding how many
         rows of decode_k/decode_v (then a fixed-capacity buffer) are valid.
@@ -295,14 +320,15 @@ class FoveatedHandle:
                 raise TypeError("n_decode must be a one-element int32 device tensor")
             if dk is None:
                 raise ValueError("a device n_decode needs a decode buffer of nonzero capacity")
+        tshape = (B, Hq) if self.spike_k == 1 else (B, Hq, self.spike_k)
         if out is None:
             out = torch.empty((B, Hq, 1, D), dtype=torch.float16, device=self.device)
             flags = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
-            tokens = torch.empty((B, Hq), dtype=torch.int32, device=self.device)
+            tokens = torch.empty(tshape, dtype=torch.int32, device=self.device)
         else:
             out, flags, tokens = out
             for t, shape, dt in ((out, (B, Hq, 1, D), torch.float16), (flags, (B, Hq), torch.int32),
-                                 (tokens, (B, Hq), torch.int32)):
+                                 (tokens, tshape, torch.int32)):
                 if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous() or t.device != self.device:
                     raise ValueError(f"out tensors must be contiguous {shape} {dt} on {self.device}")
         with torch.cuda.device(self.device):

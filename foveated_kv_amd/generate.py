@@ -264,11 +264,16 @@ def _drain_into(pipeline, wrappers, step: int) -> None:
                                              w._spike_tokens.to(torch.int32).contiguous(), w.far_idx_device(),
                                              step)
         elif isinstance(pipeline, PromotionPipeline):
-            both = torch.stack([torch.stack([w._spike_flags, w._spike_tokens]) for w in ready])
-            host = both.to("cpu", torch.int32).numpy()
-            for i, w in enumerate(ready):
-                pipeline.drain_spikes(w.layer_idx, host[i, 0], host[i, 1], w.far_idx_host(), step,
-                                      flush=False)
+            # every layer's flags and tokens (B,Hq[,K]) in one device-to-host copy
+            parts = [t.to(torch.int32).reshape(-1) for w in ready for t in (w._spike_flags, w._spike_tokens)]
+            host = torch.cat(parts).cpu().numpy()
+            at = 0
+            for w in ready:
+                nf, nt = w._spike_flags.numel(), w._spike_tokens.numel()
+                flags = host[at:at + nf].reshape(tuple(w._spike_flags.shape))
+                tokens = host[at + nf:at + nf + nt]
+                at += nf + nt
+                pipeline.drain_spikes(w.layer_idx, flags, tokens, w.far_idx_host(), step, flush=False)
             pipeline.flush()
         else:
             for w in ready:
@@ -325,6 +330,7 @@ class _DeviceDecode:
         self._pos = {}
         self._base = {}
         self._out = {}
+        self._spike_k = {}  # layer -> spike tokens per query head
         for w in wrappers:
             if w is None:
                 continue
@@ -335,6 +341,7 @@ class _DeviceDecode:
             w.fov_layer.reserve_decode(capacity)
             w.offset = self._pos[base]
             w._dev = self
+            self._spike_k[w.layer_idx] = int(getattr(w.fov_layer, "spike_k", 1))
 
     def results(self, layer_idx: int, query):
         """The layer's (out, flags, tokens) tensors, made at its first call
@@ -342,9 +349,10 @@ class _DeviceDecode:
         r = self._out.get(layer_idx)
         if r is None:
             B, Hq, _, D = query.shape
+            k = self._spike_k.get(layer_idx, 1)
             r = (torch.zeros((B, Hq, 1, D), dtype=torch.float16, device=query.device),
                  torch.zeros((B, Hq), dtype=torch.int32, device=query.device),
-                 torch.zeros((B, Hq), dtype=torch.int32, device=query.device))
+                 torch.zeros((B, Hq) if k == 1 else (B, Hq, k), dtype=torch.int32, device=query.device))
             self._out[layer_idx] = r
         return r
 
@@ -440,7 +448,7 @@ def generate_fused(model, tokenizer, prompt: str, max_tokens: int = 100,
 
     pipeline = None
     if enable_promotion:
-        pipeline = PromotionPipeline(len(fov_cache.layers))
+        pipeline = PromotionPipeline(len(fov_cache.layers), spike_k=int(getattr(cfg, "spike_k", 1)) if cfg else 1)
         pipeline.device_drain = bool(device_drain or graph)
         for i, layer in enumerate(fov_cache.layers):
             if layer is None:

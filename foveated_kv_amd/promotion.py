@@ -42,12 +42,17 @@ class PromotionPipeline:
     promoted rows and the new ``near_valid`` are seen together.
     """
 
-    def __init__(self, n_layers, cooldown_steps=5, max_per_drain=8):
+    def __init__(self, n_layers, cooldown_steps=5, max_per_drain=8, spike_k=1):
+        """``spike_k`` (an extension, see fkv_promoter_set_spike_k): spiking
+        tokens per query head the drains take, matching the attention
+        handles' spike_k (1: the reference's single token)."""
         self._lib = _lib.load()
         h = ctypes.c_void_p()
         check(self._lib.fkv_promoter_create(int(n_layers), int(cooldown_steps), int(max_per_drain), ctypes.byref(h)),
               "fkv_promoter_create")
         self._h = h
+        check(self._lib.fkv_promoter_set_spike_k(h, int(spike_k)), "fkv_promoter_set_spike_k")
+        self.spike_k = int(spike_k)
         self.n_layers = int(n_layers)
         self._keep = {}  # layer -> host arrays the C side borrows
         self._handles = {}
@@ -97,21 +102,27 @@ class PromotionPipeline:
 
     # ---- per step ----
     def drain_spikes(self, layer_idx, spike_flags, spike_tokens, far_idx, current_step, flush=True):
-        """promotion_pipeline.cpp:99-175; spike outputs (B, H_q) and far_idx
-        (B, H_kv, N_far).  Returns the number of promotions queued."""
+        """promotion_pipeline.cpp:99-175; spike outputs (B, H_q) (tokens (B,
+        H_q, spike_k) when spike_k > 1) and far_idx (B, H_kv, N_far).
+        Returns the number of promotions queued."""
         if self._stopped:
             return 0
         if isinstance(spike_flags, torch.Tensor) and isinstance(spike_tokens, torch.Tensor) and \
-                spike_flags.is_cuda and spike_flags.shape == spike_tokens.shape:
+                spike_flags.is_cuda and spike_tokens.is_cuda:
             # one device-to-host copy (one synchronisation) for both outputs
-            both = torch.stack([spike_flags.to(torch.int32), spike_tokens.to(torch.int32)]).cpu().numpy()
-            flags, tokens = np.ascontiguousarray(both[0]), np.ascontiguousarray(both[1])
+            both = torch.cat([spike_flags.to(torch.int32).reshape(-1),
+                              spike_tokens.to(torch.int32).reshape(-1)]).cpu().numpy()
+            nf = spike_flags.numel()
+            flags = np.ascontiguousarray(both[:nf].reshape(tuple(spike_flags.shape)))
+            tokens = np.ascontiguousarray(both[nf:])
         else:
             flags = _host_i32(spike_flags)
             tokens = _host_i32(spike_tokens)
         fidx = _host_i32(far_idx)
         B, Hq = flags.shape[0], flags.shape[1]
         Hkv, n_far = fidx.shape[1], fidx.shape[2]
+        if tokens.size != B * Hq * self.spike_k:
+            raise ValueError(f"spike_tokens must hold B*Hq*spike_k = {B * Hq * self.spike_k} tokens, got {tokens.size}")
         n = self._lib.fkv_promoter_drain(self._h, int(layer_idx), _np_ptr(flags), _np_ptr(tokens), _np_ptr(fidx),
                                          B, Hq, Hkv, n_far, int(current_step))
         if n < 0:
@@ -139,6 +150,8 @@ class PromotionPipeline:
                 raise TypeError("drain_spikes_device takes contiguous int32 device tensors")
         B, Hq = spike_flags.shape[0], spike_flags.shape[1]
         Hkv, n_far = far_idx.shape[1], far_idx.shape[2]
+        if spike_tokens.numel() != B * Hq * self.spike_k:
+            raise ValueError(f"spike_tokens must hold B*Hq*spike_k = {B * Hq * self.spike_k} tokens")
         dev = spike_flags.device
         # the step: a host int, or a device int32 tensor (read by the kernel)
         step_dev = current_step if isinstance(current_step, torch.Tensor) else None

@@ -70,6 +70,13 @@ class TierConfig:
     # fp8 far V: one INT4 scale / zero per token (0, the reference) or per
     # 32-dim group (32, the group-32 packed layout)
     v_group: int = 0
+    # fp8 far K: unscaled (False, the reference) or per-head scaled (True:
+    # scale = amax / 240 per (batch, head), the "per-head-scaled fp8 E4M3")
+    k_scale: bool = False
+    # spiking far tokens the fused kernel reports per query head (1: the
+    # reference's single token; up to 32: "up to 32 far tokens per head per
+    # step")
+    spike_k: int = 1
 
     def __post_init__(self):
         if self.compress_method not in ("fp8", "turbo"):
@@ -77,6 +84,10 @@ class TierConfig:
                 f"compress_method must be 'fp8' or 'turbo', got '{self.compress_method}'")
         if self.v_group not in (0, 32):
             raise ValueError(f"v_group must be 0 (per token) or 32, got {self.v_group}")
+        if not 1 <= int(self.spike_k) <= 32:
+            raise ValueError(f"spike_k must be in [1, 32], got {self.spike_k}")
+        if self.compress_method == "turbo" and (self.k_scale or self.spike_k != 1):
+            raise ValueError("k_scale and spike_k > 1 apply to the fp8 far tier only")
 
     def tier_boundaries(self, S: int) -> dict:
         n_sinks = min(self.n_sinks, S)
@@ -114,6 +125,7 @@ class TierConfig:
         c.promo_headroom_pct = self.promo_headroom_pct
         c.promo_headroom_min = self.promo_headroom_min
         c.v_group = self.v_group
+        c.k_scale = 1 if self.k_scale else 0
         return c
 
 
@@ -187,6 +199,8 @@ class FoveatedLayer:
     turbo_far_v_packed: Optional[torch.Tensor] = None
     turbo_far_v_scale: Optional[torch.Tensor] = None
     _turbo_constants: Optional[object] = None
+    far_k_scale: Optional[torch.Tensor] = None  # (B,H) fp32: per-head-scaled fp8 keys
+    spike_k: int = 1  # spiking far tokens per query head the fused kernel reports
 
     def __post_init__(self):
         max_pos = -1
@@ -243,23 +257,33 @@ class FoveatedLayer:
                                        self.turbo_far_k_norm, self.turbo_far_k_gamma,
                                        self._turbo_constants),
                     turbo_dequant_values(self.turbo_far_v_packed, self.turbo_far_v_scale))
-        return e4m3_to_fp16(self.far_k), dequant_int4_per_token(self.far_v, self.far_v_scale, self.far_v_zero)
+        far_k = e4m3_to_fp16(self.far_k)
+        if self.far_k_scale is not None:  # per-head-scaled keys: decode * scale in fp32
+            far_k = far_k.float() * self.far_k_scale.float()[:, :, None, None]
+        return far_k, dequant_int4_per_token(self.far_v, self.far_v_scale, self.far_v_zero)
 
     def attend(self, query: torch.Tensor) -> torch.Tensor:
-        """Dequant + concat + SDPA (mlx_foveated.py:239-312); returns query dtype."""
+        """Dequant + concat + SDPA (mlx_foveated.py:239-312); returns query
+        dtype.  Per-head-scaled keys (not representable in fp16) are
+        attended to in fp32."""
         far_k, far_v = self._far_dequant()
-        all_k = torch.cat([self.effective_near_k, far_k], dim=2)
-        all_v = torch.cat([self.effective_near_v, far_v], dim=2)
-        if all_k.dtype != query.dtype:
-            all_k = all_k.to(query.dtype)
-            all_v = all_v.to(query.dtype)
+        cdt = torch.float32 if far_k.dtype == torch.float32 else query.dtype
+        near_k, near_v = self.effective_near_k, self.effective_near_v
+        all_k = torch.cat([near_k.to(far_k.dtype), far_k], dim=2)
+        all_v = torch.cat([near_v, far_v.to(near_v.dtype)], dim=2)
+        if all_k.dtype != cdt:
+            all_k = all_k.to(cdt)
+        if all_v.dtype != cdt:
+            all_v = all_v.to(cdt)
+        out_dtype = query.dtype
+        query = query.to(cdt)
         hq, hkv = query.shape[1], all_k.shape[1]
         if hq != hkv:
             assert hq % hkv == 0
             all_k = all_k.repeat_interleave(hq // hkv, dim=1)
             all_v = all_v.repeat_interleave(hq // hkv, dim=1)
         scale = 1.0 / math.sqrt(query.shape[-1])
-        return _sdpa(query, all_k.contiguous(), all_v.contiguous(), scale=scale)
+        return _sdpa(query, all_k.contiguous(), all_v.contiguous(), scale=scale).to(out_dtype)
 
     # ---- fused kernel ----
     def _ensure_kcache(self):
@@ -277,7 +301,8 @@ class FoveatedLayer:
         else:
             handle = ext.FoveatedHandle(self.near_k, self.near_v, self.far_k, self.far_v,
                                         self.far_v_scale, self.far_v_zero, self.near_valid,
-                                        spike_margin=10.0)
+                                        spike_margin=10.0, far_k_scale=self.far_k_scale,
+                                        spike_k=self.spike_k)
         self._kcache = {"cpp_handle": handle, "B": self.near_k.shape[0],
                         "H_kv": self.near_k.shape[1], "D": self.near_k.shape[-1]}
 
@@ -445,7 +470,8 @@ class FoveatedKVCache:
         return FoveatedLayer(near_k=cl.near_k, near_v=cl.near_v, near_idx=near_idx, far_k=cl.far_k,
                              far_v=cl.far_v, far_v_scale=cl.far_v_scale, far_v_zero=cl.far_v_zero,
                              far_idx=far_idx, archive_k=cl.archive_k, archive_v=cl.archive_v,
-                             archive_idx=far_idx, near_valid=cl.near_valid)
+                             archive_idx=far_idx, near_valid=cl.near_valid, far_k_scale=cl.far_k_scale,
+                             spike_k=int(self.cfg.spike_k))
 
     def attend(self, layer_idx: int, query):
         layer = self.layers[layer_idx]

@@ -29,6 +29,9 @@ extern "C" {
 #define FKV_ENOMEM -3   /* device allocation failed */
 #define FKV_EDATA -4    /* input data outside what the reference can produce */
 
+/* most spiking far tokens a call reports per query head (fkv_attn_set_spike_k) */
+#define FKV_MAX_SPIKE_K 32
+
 /* element types accepted where noted */
 #define FKV_F16 0
 #define FKV_BF16 1
@@ -58,6 +61,8 @@ typedef struct fkv_tier_config {
     int32_t promo_headroom_min;
     int32_t v_group;           /* far V INT4 scale / zero: 0 = one per token (the
                                   reference), 32 = one per 32-dim group */
+    int32_t k_scale;           /* far K E4M3: 0 = unscaled (the reference), 1 = per
+                                  (batch, head) scale amax/240 (fkv_compress_layer_ex) */
 } fkv_tier_config;
 
 typedef struct fkv_tiers {
@@ -113,6 +118,26 @@ int fkv_compress_layer_indexed(const fkv_tier_config* cfg, const void* keys, con
                                const int32_t* near_idx, const int32_t* far_idx, void* near_k, void* near_v,
                                uint8_t* far_k, uint8_t* far_v, void* far_v_scale, void* far_v_zero,
                                int32_t* near_valid, void* archive_k, void* archive_v, void* stream);
+
+/* Both compress entry points above in one, plus the benchmark's
+ * per-head-scaled fp8 keys (no counterpart in the reference, whose keys are
+ * encoded unscaled, csrc/kernels/foveated_compress.metal:39-66, 120-142):
+ * near_idx / far_idx both NULL = fkv_compress_layer, both given =
+ * fkv_compress_layer_indexed.  With cfg->k_scale = 1 each (batch, head)
+ * gets scale = amax / 240 (fp32) over the finite values of its far keys (1
+ * when amax is 0), written to far_k_scale (B,H) fp32, and its far keys are
+ * encoded as Metal-encoder(fp16(key / scale)): the head's largest |key|
+ * encodes to 0x77 (240, the top of the Metal encoder's 3-bit-mantissa
+ * range: it emits exponent 15 only as the saturation code 0x7E = 448) and
+ * scale = 1 gives the unscaled codes.  The keys
+ * are read twice (scale, then encode).  far_k_scale may be NULL when
+ * cfg->k_scale = 0.  fkv_compress_layer / _indexed return FKV_EINVAL for
+ * cfg->k_scale = 1. */
+int fkv_compress_layer_ex(const fkv_tier_config* cfg, const void* keys, const void* values, int32_t in_dtype,
+                          int32_t B, int32_t H, int32_t S, int32_t D, const int32_t* near_idx,
+                          const int32_t* far_idx, void* near_k, void* near_v, uint8_t* far_k, uint8_t* far_v,
+                          void* far_v_scale, void* far_v_zero, float* far_k_scale, int32_t* near_valid,
+                          void* archive_k, void* archive_v, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* fused attention handle (FoveatedHandle, csrc/foveated_attn.cpp:135-254)  */
@@ -265,6 +290,37 @@ int fkv_attn_call_dev(fkv_attn* h, const void* query, int32_t q_dtype, int32_t H
                       const void* decode_v, const int32_t* n_decode_dev, int32_t capacity, void* out,
                       int32_t* spike_flags, int32_t* spike_tokens, void* stream);
 
+/* Per-head-scaled fp8 keys for an fp8 handle (fkv_attn_create /
+ * fkv_attn_create_g32; no counterpart in the reference, whose keys are
+ * unscaled): k_scale (B,Hkv) fp32 device array, as fkv_compress_layer_ex
+ * writes it; a far key is then decode(code) * scale.  The kernel applies
+ * the scale to the far scores (one multiply folded into 1/sqrt(D)), so the
+ * far tile's arithmetic is unchanged.  A new handle's scales are 1.  Returns
+ * FKV_EDATA for a scale that is not a positive finite number, FKV_EINVAL for
+ * a TurboQuant handle.  Synchronous. */
+int fkv_attn_set_k_scale(fkv_attn* h, const float* k_scale, void* stream);
+
+/* Top-K spike tokens (the benchmark's "up to 32 far tokens per head per
+ * step"; no counterpart in the reference, whose kernel reports one token per
+ * query head, csrc/kernels/foveated_attn.metal:323-327, 427-430).  With
+ * spike_k = K in [2, FKV_MAX_SPIKE_K] every later call writes
+ *   spike_flags  (B,Hq)   the number of far tokens whose score exceeds the
+ *                         head's min_near + margin, at most K (0 or 1 for K =
+ *                         1: the reference's flag);
+ *   spike_tokens (B,Hq,K) those tokens' far-local indices in descending
+ *                         score order, ties to the smaller index; entry 0 is
+ *                         the first-index argmax of the far scores when no
+ *                         token spikes (the reference's token), other
+ *                         entries past the count -1.
+ * A second kernel rescores the far tiles whose maximum can hold a spike (the
+ * attention kernel stores each far tile's per-head maximum), so with sparse
+ * spikes the extra work is a few tiles per head.  K = 1 (the default) is the
+ * reference's single token, with no extra work.  TurboQuant handles take K
+ * = 1 only.  Allocates the selection's buffers when the handle's workspace
+ * exists (else its next call does); fkv_attn_call_noalloc with K > 1 needs
+ * them to exist.  Host only. */
+int fkv_attn_set_spike_k(fkv_attn* h, int32_t spike_k);
+
 /* Replaces get_blob_info (:242-254): where promotions land. */
 typedef struct fkv_blob_info {
     void* blob;               /* device base pointer */
@@ -322,6 +378,18 @@ typedef struct fkv_promoter_stats {
 /* PromotionPipeline(n_layers, cooldown_steps=5, max_per_drain=8)
  * (bindings.cpp:43-47).  Host only: no GPU work until the first flush. */
 int fkv_promoter_create(int32_t n_layers, int32_t cooldown_steps, int32_t max_per_drain, fkv_promoter** out);
+
+/* Tokens per query head the drains take (no counterpart in the reference,
+ * whose drain takes one, promotion_pipeline.cpp:120-172): with spike_k = K in
+ * [2, FKV_MAX_SPIKE_K], spike_flags hold spike counts and spike_tokens are
+ * (B*Hq, K), as fkv_attn_call writes them for a handle with the same
+ * spike_k.  The first flagged query head of a KV head (GQA dedup) then hands
+ * up to K tokens, in order, through the position dedup and the archive
+ * lookup; the cooldown applies to the KV head once per drain, the per-call
+ * budget max_per_drain counts tokens and is checked before each token.  A
+ * KV head therefore promotes at most K rows per drain.  K = 1 (the default)
+ * is the reference's drain.  Host only. */
+int fkv_promoter_set_spike_k(fkv_promoter* p, int32_t spike_k);
 
 /* register_archive (promotion_pipeline.cpp:45-83) from host rows
  * [B_arc][Hkv][S_arc][D] fp16 and archive_idx [Hkv][S_arc] int32 (global

@@ -59,9 +59,9 @@ def _load():
     lib.orc_split_plan.restype = None
     lib.orc_split_plan.argtypes = [I, P]
     lib.orc_attend_kernel.restype = I
-    lib.orc_attend_kernel.argtypes = [I] * 7 + [P] * 11 + [ctypes.c_float, I, I, I, I] + [P] * 5
+    lib.orc_attend_kernel.argtypes = [I] * 7 + [P] * 12 + [ctypes.c_float, I, I, I, I] + [P] * 6
     lib.orc_attend_formulation.restype = I
-    lib.orc_attend_formulation.argtypes = [I] * 7 + [P, I] + [P] * 9 + [I, P]
+    lib.orc_attend_formulation.argtypes = [I] * 7 + [P, I] + [P] * 9 + [I, P, P]
     lib.orc_compress_foveal.restype = None
     lib.orc_compress_foveal.argtypes = [P, P] + [I] * 9
     _lib = lib
@@ -101,6 +101,40 @@ def decode_fp8(codes):
     lib = _load()
     table = np.array([lib.orc_e4m3_to_fp16(i) for i in range(256)], np.uint16)
     return table[np.asarray(codes, np.uint8)].view(np.float16)
+
+
+# The largest value the reference's Metal encoder represents to 3 mantissa
+# bits: it emits exponent 15 only as the saturation code 0x7E (448), so every
+# input from 240 up (after rounding) lands there (foveated_compress.metal:
+# 39-66).  Per-head scales map a head's largest |key| to 240 (code 0x77).
+E4M3_TOP = 240.0
+
+
+def k_head_scale(keys):
+    """Per-head fp8 key scale of the benchmark's "per-head-scaled fp8 E4M3"
+    keys (an extension; the reference encodes keys unscaled,
+    foveated_compress.metal:39-66): keys (..., N, D) fp16 -> scale (...) fp32
+    = amax / 240 over the finite values of each head's N x D keys (fp32
+    division), 1 where amax is 0 (or N = 0).  240 is the top of the Metal
+    encoder's accurate range (E4M3_TOP): with 448, the E4M3 maximum, every
+    key in (240, 448] x scale would saturate to 448."""
+    x = np.asarray(keys, np.float16).astype(np.float32)
+    x = np.where(np.isfinite(x), np.abs(x), np.float32(0))
+    amax = x.reshape(x.shape[:-2] + (-1,)).max(axis=-1, initial=np.float32(0)).astype(np.float32)
+    return np.where(amax > 0, amax / np.float32(E4M3_TOP), np.float32(1)).astype(np.float32)
+
+
+def encode_fp8_scaled(keys, scale):
+    """Per-head-scaled E4M3 (extension): keys (..., N, D) fp16, scale (...)
+    fp32 -> codes of the Metal encoder applied to fp16(key / scale), the
+    quotient an fp32 division rounded to fp16 (nearest even).  scale = 1
+    gives encode_fp8(keys); with k_head_scale the head's largest finite
+    |key| encodes to 0x77 (240)."""
+    x = np.asarray(keys, np.float16).astype(np.float32)
+    s = np.asarray(scale, np.float32)[..., None, None]
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = (x / s).astype(np.float16)
+    return encode_fp8(y)
 
 
 def quant_int4(x, python_semantics=False):
@@ -224,12 +258,14 @@ def _gather_rows(x, idx):
     return out
 
 
-def compress_layer(keys, values, v_group=0, importance=None, **cfg):
+def compress_layer(keys, values, v_group=0, importance=None, k_scale=False, **cfg):
     """The whole fp8 compress of one layer (foveated_compress.cpp:95-201):
     returns dict with near_k/near_v/far_k/far_v/far_v_scale/far_v_zero/
-    near_valid/near_idx/far_idx/archive_k/archive_v/tb.  v_group = 32
-    quantises V per 32-dim group (scales (B,H,F,D/32)) instead of per token;
-    ``importance`` selects the near middle by partition_importance."""
+    far_k_scale/near_valid/near_idx/far_idx/archive_k/archive_v/tb.
+    v_group = 32 quantises V per 32-dim group (scales (B,H,F,D/32)) instead
+    of per token; ``importance`` selects the near middle by
+    partition_importance; ``k_scale`` encodes the far keys per-head scaled
+    (k_head_scale / encode_fp8_scaled; far_k_scale (B,H) fp32, else None)."""
     keys = np.ascontiguousarray(keys, np.float16)
     values = np.ascontiguousarray(values, np.float16)
     B, H, S, D = keys.shape
@@ -245,10 +281,12 @@ def compress_layer(keys, values, v_group=0, importance=None, **cfg):
         fk_src, fv_src = _gather_rows(keys, far_idx), _gather_rows(values, far_idx)
         near_k, near_v = _gather_rows(keys, near_idx), _gather_rows(values, near_idx)
     far_v, fvs, fvz = quant_int4_groups(fv_src, v_group) if v_group else quant_int4(fv_src)
+    ks = k_head_scale(fk_src) if k_scale else None
     return {
         "near_k": near_k,
         "near_v": near_v,
-        "far_k": encode_fp8(fk_src),
+        "far_k": encode_fp8_scaled(fk_src, ks) if k_scale else encode_fp8(fk_src),
+        "far_k_scale": ks,
         "far_v": far_v,
         "far_v_scale": fvs,
         "far_v_zero": fvz,
@@ -291,11 +329,14 @@ def quant_int4_groups(x, group=32, python_semantics=False):
 
 def attend_kernel(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_vz,
                   dec_k=None, dec_v=None, spike_margin=10.0, split_size=0,
-                  num_splits=0, gate=True, far_k_f16=None):
+                  num_splits=0, gate=True, far_k_f16=None, far_k_scale=None,
+                  return_far_scores=False):
     """Fused-kernel semantics (foveated_attn.metal:181-432) in fp64.
     q (B,Hq,D) or (B,Hq,1,D) fp16.  ``far_k_f16`` (B,Hkv,F,D) fp16 replaces
-    the LUT decode of ``far_k`` when given.  Returns (out f64 (B,Hq,D),
-    flags i32, tokens i32, max_far f64, min_near f64)."""
+    the LUT decode of ``far_k`` when given; ``far_k_scale`` (B,Hkv) fp32
+    multiplies each head's decoded far keys (per-head-scaled fp8).  Returns
+    (out f64 (B,Hq,D), flags i32, tokens i32, max_far f64, min_near f64),
+    plus every far score (B,Hq,F) f64 with ``return_far_scores``."""
     lib = _load()
     q = _u16(q)
     B, Hq = q.shape[:2]
@@ -316,20 +357,55 @@ def attend_kernel(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_vz,
     tokens = np.zeros((B, Hq), np.int32)
     mf = np.zeros((B, Hq), np.float64)
     mn = np.zeros((B, Hq), np.float64)
+    ks = None if far_k_scale is None else np.ascontiguousarray(far_k_scale, np.float32).reshape(B, Hkv)
+    fsc = np.zeros((B, Hq, F), np.float64) if return_far_scores else None
     rc = lib.orc_attend_kernel(B, Hq, Hkv, D, Npad, F, ndec, _ptr(q), _ptr(nk), _ptr(nv_),
                                _ptr(valid), _ptr(fk), _ptr(fk16), _ptr(fv), _ptr(fs), _ptr(fz),
-                               _ptr(dk), _ptr(dv), float(spike_margin), int(split_size),
+                               _ptr(dk), _ptr(dv), _ptr(ks), float(spike_margin), int(split_size),
                                int(num_splits), int(bool(gate)), vg, _ptr(out), _ptr(flags),
-                               _ptr(tokens), _ptr(mf), _ptr(mn))
+                               _ptr(tokens), _ptr(mf), _ptr(mn), _ptr(fsc))
     if rc != 0:
         raise ValueError(f"orc_attend_kernel failed: {rc}")
+    if return_far_scores:
+        return out, flags, tokens, mf, mn, fsc
     return out, flags, tokens, mf, mn
 
 
+def spike_topk(far_scores, min_near, spike_margin, spike_k):
+    """Top-K spike selection (the benchmark's "up to 32 far tokens per head
+    per step", an extension of the reference's single token,
+    foveated_attn.metal:323-327, 427-430).  far_scores (B,Hq,F), min_near
+    (B,Hq).  A far token spikes when its score exceeds min_near + margin.
+    Returns counts (B,Hq) int32 = min(K, spiking tokens) and tokens
+    (B,Hq,K) int32: the far tokens in descending score order, ties to the
+    smaller index (the order the kernel's strict > over ascending tokens
+    gives), entries j < count the spiking ones; entry 0 is the first-index
+    argmax whatever its score (as the reference's single token; -1 when
+    F = 0), entries past the count -1.  K = 1 gives the reference's flag
+    and token."""
+    fsc = np.asarray(far_scores, np.float64)
+    B, Hq, F = fsc.shape
+    thr = np.asarray(min_near, np.float64) + float(spike_margin)
+    counts = np.zeros((B, Hq), np.int32)
+    tokens = np.full((B, Hq, spike_k), -1, np.int32)
+    idx = np.arange(F)
+    for b in range(B):
+        for h in range(Hq):
+            if F == 0:
+                continue
+            order = np.lexsort((idx, -fsc[b, h]))  # score descending, then index ascending
+            n = int(min(spike_k, np.count_nonzero(fsc[b, h] > thr[b, h])))
+            counts[b, h] = n
+            tokens[b, h, :n] = order[:n]
+            tokens[b, h, 0] = order[0]
+    return counts, tokens
+
+
 def attend_formulation(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_vz,
-                       dec_k=None, dec_v=None, q_dtype="float16"):
+                       dec_k=None, dec_v=None, q_dtype="float16", far_k_scale=None):
     """Reference formulation MLXFoveatedLayer.attend (mlx_foveated.py:239-278)
-    in fp64 softmax.  q (B,Hq,D) fp16 bits (or bf16 bits with q_dtype='bfloat16')."""
+    in fp64 softmax.  q (B,Hq,D) fp16 bits (or bf16 bits with q_dtype='bfloat16');
+    ``far_k_scale`` (B,Hkv) fp32: far keys are decode(code) * scale in fp32."""
     lib = _load()
     q = np.ascontiguousarray(q)
     qb = q.view(np.uint16) if q.dtype != np.uint16 else q
@@ -345,10 +421,11 @@ def attend_formulation(q, near_k, near_v, near_valid, far_k, far_v, far_vs, far_
     dk, dv, ndec = _dec_arrays(B, Hkv, D, dec_k, dec_v)
     valid = np.ascontiguousarray(near_valid, np.uint32)
     out = np.zeros((B, Hq, D), np.float64)
+    ks = None if far_k_scale is None else np.ascontiguousarray(far_k_scale, np.float32).reshape(B, Hkv)
     rc = lib.orc_attend_formulation(B, Hq, Hkv, D, Npad, F, ndec, _ptr(qb),
                                     1 if q_dtype == "bfloat16" else 0, _ptr(nk), _ptr(nv_),
                                     _ptr(valid), _ptr(fk), _ptr(fv), _ptr(fs), _ptr(fz),
-                                    _ptr(dk), _ptr(dv), _v_group(fs, D), _ptr(out))
+                                    _ptr(dk), _ptr(dv), _v_group(fs, D), _ptr(ks), _ptr(out))
     if rc != 0:
         raise ValueError(f"orc_attend_formulation failed: {rc}")
     return out

@@ -310,9 +310,15 @@ static void orc_accum(orc_state* st, double s, const double* v, int D) {
  *                            extension: the reference's per-token arithmetic
  *                            applied to each group)
  *   dec_k/v  (B,Hkv,n_dec,D) fp16 bits
+ *   far_k_scale (B,Hkv) fp32 or NULL: per-head fp8 key scale (the
+ *                            benchmark's "per-head-scaled fp8 E4M3" keys, an
+ *                            extension: the reference's keys are unscaled);
+ *                            a far key is decode(code) * scale
  *   split_size/num_splits <= 0 -> reference adaptive plan
  *   gate != 0 -> skip V of far tokens with s < m - 16 (:311-360)
- *   out (B,Hq,D) fp64; flags/tokens (B,Hq); max_far/min_near (B,Hq) optional
+ *   out (B,Hq,D) fp64; flags/tokens (B,Hq); max_far/min_near (B,Hq) optional;
+ *   far_scores (B,Hq,F) fp64 optional: every far token's score (the input
+ *   of the top-K spike selection, oracle/__init__.py spike_topk)
  */
 ORC_API int orc_attend_kernel(int B, int Hq, int Hkv, int D, int Npad, int F, int n_dec,
                               const uint16_t* q, const uint16_t* near_k, const uint16_t* near_v,
@@ -320,9 +326,10 @@ ORC_API int orc_attend_kernel(int B, int Hq, int Hkv, int D, int Npad, int F, in
                               const uint16_t* far_k_f16,
                               const uint8_t* far_v, const uint16_t* far_vs,
                               const uint16_t* far_vz, const uint16_t* dec_k,
-                              const uint16_t* dec_v, float spike_margin, int split_size,
-                              int num_splits, int gate, int v_group, double* out, int32_t* flags,
-                              int32_t* tokens, double* max_far_out, double* min_near_out) {
+                              const uint16_t* dec_v, const float* far_k_scale, float spike_margin,
+                              int split_size, int num_splits, int gate, int v_group, double* out,
+                              int32_t* flags, int32_t* tokens, double* max_far_out, double* min_near_out,
+                              double* far_scores_out) {
     if (Hkv <= 0 || Hq % Hkv != 0 || D <= 0) return -1;
     if (v_group < 0 || (v_group > 0 && D % v_group != 0)) return -1;
     const int G = Hq / Hkv;
@@ -379,6 +386,7 @@ ORC_API int orc_attend_kernel(int B, int Hq, int Hkv, int D, int Npad, int F, in
                     for (int d = 0; d < D; d++) vv[d] = orc_h2f(vr[d]);
                     orc_accum(st, sc, vv, D);
                 }
+                const double ks = far_k_scale ? (double)far_k_scale[bkv] : 1.0;
                 for (int t = far0; t < far1; t++) {
                     double sc = 0.0;
                     if (far_k_f16) {
@@ -389,6 +397,8 @@ ORC_API int orc_attend_kernel(int B, int Hq, int Hkv, int D, int Npad, int F, in
                         for (int d = 0; d < D; d++)
                             sc += qreg[d] * (double)orc_h2f(orc_e4m3_to_fp16(kr[d]));
                     }
+                    sc *= ks;
+                    if (far_scores_out) far_scores_out[((int64_t)b * Hq + hq) * F + t] = sc;
                     if (sc > st->max_far) { st->max_far = sc; st->far_tok = t; }
                     if (gate && sc < st->m - 16.0) continue;
                     const uint8_t* vr = far_v + (bkv * F + t) * (D / 2);
@@ -452,6 +462,8 @@ ORC_API int orc_attend_kernel(int B, int Hq, int Hkv, int D, int Npad, int F, in
 /* MLXFoveatedLayer.attend: src/foveated_kv/mlx_foveated.py:239-278.
  *   far K   = LUT decode (exact in fp16)                       :76-91
  *   far V   = half(half(nibble * scale) + zero)  (fp16 ops)    :94-108
+ *   far_k_scale (B,Hkv) fp32 or NULL: per-head key scale (extension, see
+ *             orc_attend_kernel): far K = decode(code) * scale in fp32
  *   keys    = near[:, :, :max(near_valid)] ++ decode ++ far    :256-260, :430-449
  *   q_dtype = 1 (bf16): K/V rounded to bf16 before SDPA        :262-266
  *   SDPA with scale 1/sqrt(D), GQA by repeat                   :268-278
@@ -463,7 +475,7 @@ ORC_API int orc_attend_formulation(int B, int Hq, int Hkv, int D, int Npad, int 
                                    const uint8_t* far_k, const uint8_t* far_v,
                                    const uint16_t* far_vs, const uint16_t* far_vz,
                                    const uint16_t* dec_k, const uint16_t* dec_v, int v_group,
-                                   double* out) {
+                                   const float* far_k_scale, double* out) {
     if (Hkv <= 0 || Hq % Hkv != 0) return -1;
     if (v_group < 0 || (v_group > 0 && D % v_group != 0)) return -1;
     const int NGV = v_group > 0 ? D / v_group : 1;
@@ -500,6 +512,9 @@ ORC_API int orc_attend_formulation(int B, int Hq, int Hkv, int D, int Npad, int 
                     if (t < nv_max) kf = orc_h2f(near_k[(bkv * Npad + t) * D + d]);
                     else if (t < nv_max + n_dec)
                         kf = orc_h2f(dec_k[(bkv * n_dec + (t - nv_max)) * D + d]);
+                    else if (far_k_scale)
+                        kf = orc_h2f(orc_e4m3_to_fp16(far_k[(bkv * F + (t - nv_max - n_dec)) * D + d])) *
+                             far_k_scale[bkv];
                     else
                         kf = orc_h2f(orc_e4m3_to_fp16(far_k[(bkv * F + (t - nv_max - n_dec)) * D + d]));
                     krow[d] = q_dtype ? orc_bf2f(orc_f2bf(kf)) : kf;

@@ -3,6 +3,13 @@ INFRASTRUCTURE ONLY (imported by tests/ only).
 
 drain():   csrc/promotion_pipeline.cpp:99-175 (GQA dedup, per-(layer, KV
            head) cooldown, position dedup, per-call budget, archive lookup).
+           With spike_k > 1 (the benchmark's "up to 32 far tokens per head
+           per step", an extension): flags[b, hq] is the number of spiking
+           tokens of the query head and tokens (B, Hq, K) lists them in
+           descending score order; the KV head's first flagged query head
+           (GQA dedup) hands its tokens, in that order, through the same
+           position dedup / archive lookup / budget, the budget checked
+           before each token.  spike_k = 1 is the reference's drain.
 commit():  csrc/promotion_pipeline.cpp:192-241 (headroom check against
            N_near_alloc, copy the fp16 K/V row into slot near_valid[h],
            near_valid[h] += 1).
@@ -20,10 +27,11 @@ STATS = ("spikes_detected", "spikes_queued", "spikes_deduplicated", "spikes_cool
 
 
 class Pipeline:
-    def __init__(self, n_layers, cooldown_steps=5, max_per_drain=8):
+    def __init__(self, n_layers, cooldown_steps=5, max_per_drain=8, spike_k=1):
         self.n_layers = n_layers
         self.cooldown = cooldown_steps
         self.max_per_drain = max_per_drain
+        self.spike_k = spike_k
         self.archives = {}  # layer -> (k, v, pos_to_local list of dicts)
         self.promoted = set()
         self.last_step = {}
@@ -40,6 +48,7 @@ class Pipeline:
             return 0
         _, _, maps = self.archives[layer]
         B, Hq = flags.shape
+        tokens = np.asarray(tokens).reshape(B, Hq, -1)
         Hkv, n_far = far_idx.shape[1], far_idx.shape[2]
         gqa = max(Hq // Hkv, 1)
         seen = [False] * Hkv
@@ -62,20 +71,24 @@ class Pipeline:
                     self.stats["spikes_cooled_down"] += 1
                     continue
                 self.last_step[key_cd] = step
-                fl = int(tokens[b, hq])
-                if fl < 0 or fl >= n_far:
-                    continue
-                pos = int(far_idx[b, hkv, fl])
-                key = (layer, hkv, pos)
-                if key in self.promoted:
-                    self.stats["spikes_deduplicated"] += 1
-                    continue
-                self.promoted.add(key)
-                if pos not in maps[hkv]:
-                    continue
-                self.queue.append((layer, hkv, maps[hkv][pos], pos))
-                self.stats["spikes_queued"] += 1
-                queued += 1
+                n_tok = min(int(flags[b, hq]), self.spike_k) if self.spike_k > 1 else 1
+                for j in range(n_tok):
+                    if queued >= self.max_per_drain:
+                        break
+                    fl = int(tokens[b, hq, j])
+                    if fl < 0 or fl >= n_far:
+                        continue
+                    pos = int(far_idx[b, hkv, fl])
+                    key = (layer, hkv, pos)
+                    if key in self.promoted:
+                        self.stats["spikes_deduplicated"] += 1
+                        continue
+                    self.promoted.add(key)
+                    if pos not in maps[hkv]:
+                        continue
+                    self.queue.append((layer, hkv, maps[hkv][pos], pos))
+                    self.stats["spikes_queued"] += 1
+                    queued += 1
         return queued
 
     def commit(self, near_k, near_v, near_valid, n_near_alloc):

@@ -130,3 +130,33 @@ def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16
     ties = check_spikes(orc, c["far_k"], q16, flags, tokens, kf, kt, mf, mn, margin)
     record(case, flagged=int(flags.sum()), spike_ties=ties, **rec)
     return out, flags, tokens, kf
+
+
+def check_topk(s, thr, K, cnt, tok):
+    """One head's top-K spike outputs (cnt, tok[K]) against the exact far
+    scores s (fp64) and threshold thr = min_near + margin: the count may
+    differ from the exact one only by scores within rounding of the
+    threshold, the tokens are distinct far tokens above it in descending
+    order, and their scores are the top scores (ties may reorder within
+    rounding).  Entry 0 is the argmax when nothing spikes; the rest are -1.
+    Returns the number of tie-allowed differences from the exact answer."""
+    F = s.size
+    tol = 1e-5 * (1 + (np.abs(s).max() if F else 0.0))
+    n_lo = min(K, int(np.count_nonzero(s > thr + tol)))
+    n_hi = min(K, int(np.count_nonzero(s > thr - tol)))
+    n_ex = min(K, int(np.count_nonzero(s > thr)))
+    assert n_lo <= cnt <= n_hi, (cnt, n_lo, n_hi)
+    lst = [int(t) for t in tok[:cnt]]
+    assert len(set(lst)) == cnt and all(0 <= t < F for t in lst), lst
+    got = s[lst] if cnt else np.zeros(0)
+    assert np.all(got > thr - tol)
+    assert np.all(np.diff(got) <= tol), got
+    top = np.sort(s)[::-1][:cnt]
+    assert np.allclose(np.sort(got)[::-1], top, rtol=0, atol=tol), (got, top)
+    rest = [int(t) for t in tok[cnt:]]
+    if cnt == 0 and F:
+        assert abs(s[rest[0]] - s.max()) <= tol
+        rest = rest[1:]
+    assert all(t == -1 for t in rest), rest
+    order = np.lexsort((np.arange(F), -s))[:cnt]
+    return int(cnt != n_ex) + int(np.count_nonzero(np.asarray(lst) != order[:len(lst)]) > 0)

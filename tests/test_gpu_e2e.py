@@ -44,14 +44,32 @@ def test_c5_full_loop(orc):
     _loop(orc, 1, 64, 8, 128, 65536, 128, 0, "graph", check_every=16)
 
 
-def _loop(orc, B, Hq, Hkv, D, S, steps, vg, mode, check_every):
+def test_c5_full_loop_top32(orc):
+    """C5 with its stated promotion rule, "up to 32 far tokens per head per
+    step (cooldown + GQA dedup)": spike_k = 32, a budget of 32 tokens per KV
+    head (256 per step), the rest as test_c5_full_loop.  The spike counts and
+    token lists of the checked steps match the oracle's top-32 of the exact
+    far scores (ties within rounding); the final near tier, near_valid and
+    statistics are bit-exact against the restated drain fed the GPU's own
+    spike outputs."""
+    _loop(orc, 1, 64, 8, 128, 65536, 128, 0, "graph", check_every=16, spike_k=32, budget=256)
+
+
+@pytest.mark.parametrize("mode", ["host", "device"])
+def test_decode_promote_loop_top_k(orc, mode):
+    """Several spiking tokens per head per step (spike_k = 6, budget 12)
+    through the host drain and the device drain, every step checked."""
+    _loop(orc, 2, 16, 4, 128, 6000, 20, 0, mode, check_every=1, spike_k=6, budget=12)
+
+
+def _loop(orc, B, Hq, Hkv, D, S, steps, vg, mode, check_every, spike_k=1, budget=8):
     from foveated_kv_amd import ext, synthetic
     from foveated_kv_amd.promotion import PromotionPipeline
 
-    from _parity import record
+    from _parity import check_topk, record
 
     seed = S + steps
-    case = f"e2e B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} v_group={vg} mode={mode}"
+    case = f"e2e B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} steps={steps} v_group={vg} mode={mode} spike_k={spike_k}"
     print(case, flush=True)
     worst_err, worst_cos, checked = 0.0, 1.0, 0
     k, v = synthetic.make_kv(B, Hkv, S, D, seed)
@@ -67,11 +85,11 @@ def _loop(orc, B, Hq, Hkv, D, S, steps, vg, mode, check_every):
                                                 importance=imp)
     assert np.array_equal(_np(cl.far_idx), far_idx)
     h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
-                           cl.near_valid, spike_margin=10.0)
-    pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=8)
+                           cl.near_valid, spike_margin=10.0, spike_k=spike_k)
+    pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=budget, spike_k=spike_k)
     pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
     pipe.register_blob(0, h)
-    ref = opromo.Pipeline(1, 5, 8)
+    ref = opromo.Pipeline(1, 5, budget, spike_k)
     ref.register_archive(0, _np(cl.archive_k), _np(cl.archive_v), far_idx[0])
     near_k, near_v, nv = {0: _np(cl.near_k).copy()}, {0: _np(cl.near_v).copy()}, {0: _np(cl.near_valid).copy()}
     far = [_np(getattr(cl, n)) for n in ("far_k", "far_v", "far_v_scale", "far_v_zero")]
@@ -116,19 +134,27 @@ def _loop(orc, B, Hq, Hkv, D, S, steps, vg, mode, check_every):
             assert int(step_d.item()) == n
         fl, tk = _np(flags), _np(toks)
         if t % check_every == 0 or t == steps - 1:
-            o, kf, kt, mf, mn = orc.attend_kernel(qs[t], near_k[0], near_v[0], nv[0], *far, dk[:, :, :n],
-                                                  dv[:, :, :n], spike_margin=10.0)
+            o, kf, kt, mf, mn, fsc = orc.attend_kernel(qs[t], near_k[0], near_v[0], nv[0], *far, dk[:, :, :n],
+                                                       dv[:, :, :n], spike_margin=10.0, return_far_scores=True)
             got = _np(out)[:, :, 0].astype(np.float64)
             err, cos = np.abs(got - o).max(), orc.cosine(got, o)
             assert err <= 2e-3 and cos >= 0.9999, (t, err, cos)
             worst_err, worst_cos, checked = max(worst_err, err), min(worst_cos, cos), checked + 1
+            if spike_k > 1:
+                for b in range(B):
+                    for hq in range(Hq):
+                        check_topk(fsc[b, hq], mn[b, hq] + 10.0, spike_k, int(fl[b, hq]), tk[b, hq])
+        if spike_k > 1:
+            flagged += int((fl > 0).sum())
+        elif t % check_every == 0 or t == steps - 1:
             for b, hq in np.argwhere(fl != kf):
                 assert abs(mf[b, hq] - mn[b, hq] - 10.0) < 1e-4, (t, b, hq)
             for b, hq in np.argwhere(tk != kt):  # only on a near tie of the exact far scores
                 qs32 = qs[t][b, hq].astype(np.float32) * np.float32(1 / np.sqrt(np.float32(D)))
                 sc = lut[far[0][b, hq // (Hq // Hkv)]] @ qs32.astype(np.float64)
                 assert abs(sc[tk[b, hq]] - sc[kt[b, hq]]) <= 1e-5 * (1 + abs(sc.max())), (t, b, hq)
-        flagged += int(fl.sum())
+        if spike_k == 1:
+            flagged += int(fl.sum())
         # both pipelines see the GPU's spike outputs, so their states stay comparable
         if mode == "device":
             pipe.drain_spikes_device(0, flags, toks, fdev, t)
@@ -145,3 +171,6 @@ def _loop(orc, B, Hq, Hkv, D, S, steps, vg, mode, check_every):
     assert pipe.get_stats() == ref.stats
     record(f"{case} (checked {checked} steps)", maxabs_kernel=worst_err, cos_kernel=worst_cos, flagged=flagged,
            promotions=ref.stats["promotions_completed"])
+    print(f"  promotions {ref.stats['promotions_completed']} over {steps} steps, stats {ref.stats}", flush=True)
+    if spike_k > 1:  # more than one row per head in some drain
+        assert ref.stats["promotions_completed"] > ref.stats["spikes_detected"] - ref.stats["spikes_cooled_down"]

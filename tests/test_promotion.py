@@ -15,7 +15,7 @@ from oracle import promotion as opromo
 
 
 class CDrain:
-    def __init__(self, n_layers, cooldown=5, budget=8):
+    def __init__(self, n_layers, cooldown=5, budget=8, spike_k=1):
         from foveated_kv_amd import _lib
 
         self.lib = _lib.load()
@@ -23,6 +23,7 @@ class CDrain:
         self.h = ctypes.c_void_p()
         _lib.check(self.lib.fkv_promoter_create(n_layers, cooldown, budget, ctypes.byref(self.h)),
                    "fkv_promoter_create")
+        _lib.check(self.lib.fkv_promoter_set_spike_k(self.h, spike_k), "fkv_promoter_set_spike_k")
         self.keep = []
 
     def archive(self, layer, k, v, idx):
@@ -69,8 +70,8 @@ def _archive(Hkv, S, D, start=4, seed=0):
     return k, v, idx
 
 
-def _both(n_layers=2, cooldown=5, budget=8):
-    return CDrain(n_layers, cooldown, budget), opromo.Pipeline(n_layers, cooldown, budget)
+def _both(n_layers=2, cooldown=5, budget=8, spike_k=1):
+    return CDrain(n_layers, cooldown, budget, spike_k), opromo.Pipeline(n_layers, cooldown, budget, spike_k)
 
 
 def _register(c, o, layer, k, v, idx):
@@ -152,6 +153,95 @@ def test_drain_matches_restatement_on_random_streams():
     assert c.pending() == o.queue
     assert c.stats() == o.stats
     assert o.stats["spikes_cooled_down"] > 0 and o.stats["spikes_deduplicated"] > 0
+
+
+# ---------------------------------------------------------------------------
+# several spiking tokens per query head (spike_k > 1: the benchmark's "up to
+# 32 far tokens per head per step"; flags are counts, tokens (B, Hq, K))
+# ---------------------------------------------------------------------------
+
+def test_spike_k_known_answers():
+    c, o = _both(n_layers=1, cooldown=2, budget=6, spike_k=4)
+    Hq, Hkv, S = 4, 2, 40
+    k, v, idx = _archive(Hkv, S, 4)
+    _register(c, o, 0, k, v, idx)
+    far_idx = idx[None]
+    flags = np.array([[0, 3, 2, 4]], np.int32)            # kv 0: head 1 (3 tokens); kv 1: head 2 wins over 3
+    tokens = np.full((1, Hq, 4), -1, np.int32)
+    tokens[0, 1, :3] = [7, 9, 11]
+    tokens[0, 2, :2] = [5, 5 + 0]                          # a repeated token: the second is a duplicate
+    tokens[0, 3] = [1, 2, 3, 4]
+    for impl in (c, o):
+        assert impl.drain(0, flags, tokens, far_idx, 0) == 4
+    assert c.pending() == o.queue == [(0, 0, 7, 11), (0, 0, 9, 13), (0, 0, 11, 15), (0, 1, 5, 9)]
+    s = c.stats()
+    assert s == o.stats
+    assert (s["spikes_detected"], s["spikes_queued"], s["spikes_deduplicated"]) == (2, 4, 1)
+    # step 1: both heads cooled down (once per head, not per token)
+    for impl in (c, o):
+        assert impl.drain(0, flags, tokens, far_idx, 1) == 0
+    assert c.stats()["spikes_cooled_down"] == o.stats["spikes_cooled_down"] == 2
+    # step 2: head 0 queues 4, head 1 the 2 tokens the budget (6) leaves
+    flags2 = np.array([[4, 4, 4, 4]], np.int32)
+    tokens2 = np.zeros((1, Hq, 4), np.int32)
+    tokens2[0, 0] = [20, 21, 22, 23]
+    tokens2[0, 2] = [30, 31, 32, 33]
+    for impl in (c, o):
+        assert impl.drain(0, flags2, tokens2, far_idx, 2) == 6
+    assert [r[3] for r in o.queue[-6:]] == [24, 25, 26, 27, 34, 35]
+    # step 5: head 1's first token is now a duplicate; the budget then
+    # stops it after two more
+    tokens2[0, 0] = [24, 25, 26, 27]
+    tokens2[0, 2] = [30, 34, 35, 36]
+    for impl in (c, o):
+        assert impl.drain(0, flags2, tokens2, far_idx, 5) == 6
+    assert [r[3] for r in o.queue[-6:]] == [28, 29, 30, 31, 38, 39]
+    assert c.pending() == o.queue
+    s = c.stats()
+    assert s == o.stats and s["spikes_deduplicated"] == 2
+
+
+def test_spike_k_counts_above_k_are_clamped_and_k1_ignores_counts():
+    c, o = _both(n_layers=1, cooldown=0, budget=100, spike_k=2)
+    k, v, idx = _archive(1, 30, 4)
+    _register(c, o, 0, k, v, idx)
+    tokens = np.array([[[3, 4]]], np.int32)
+    for impl in (c, o):
+        assert impl.drain(0, np.array([[9]], np.int32), tokens, idx[None], 0) == 2
+    assert c.pending() == o.queue
+    c1, o1 = _both(n_layers=1, cooldown=0, budget=100)
+    _register(c1, o1, 0, k, v, idx)
+    for impl in (c1, o1):   # spike_k = 1: any nonzero flag is one token, as the reference
+        assert impl.drain(0, np.array([[5]], np.int32), np.array([[3]], np.int32), idx[None], 0) == 1
+
+
+@pytest.mark.parametrize("K", [2, 5, 32])
+def test_spike_k_drain_matches_restatement_on_random_streams(K):
+    rng = np.random.default_rng(K)
+    c, o = _both(n_layers=2, cooldown=2, budget=3 * K, spike_k=K)
+    B, Hq, Hkv, S = 2, 16, 4, 80
+    for layer in range(2):
+        k, v, idx = _archive(Hkv, S, 10, seed=layer)
+        _register(c, o, layer, k, v, idx)
+    far_idx = np.broadcast_to(np.arange(10, 10 + S, dtype=np.int32), (B, Hkv, S)).copy()
+    for step in range(30):
+        for layer in range(2):
+            flags = np.where(rng.random((B, Hq)) < 0.3, rng.integers(1, K + 3, size=(B, Hq)), 0).astype(np.int32)
+            tokens = np.stack([rng.permutation(S)[:K] for _ in range(B * Hq)]).reshape(B, Hq, K).astype(np.int32)
+            tokens[rng.random((B, Hq, K)) < 0.05] = -1
+            assert c.drain(layer, flags, tokens, far_idx, step) == o.drain(layer, flags, tokens, far_idx, step)
+    assert c.pending() == o.queue
+    assert c.stats() == o.stats
+    assert o.stats["spikes_deduplicated"] > 0 and o.stats["spikes_cooled_down"] > 0
+
+
+def test_spike_k_range_is_checked():
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+    c = CDrain(1)
+    for bad in (0, 33, -1):
+        assert lib.fkv_promoter_set_spike_k(c.h, bad) == _lib.FKV_EINVAL
 
 
 # ---------------------------------------------------------------------------
