@@ -207,6 +207,9 @@ def main():
     ap.add_argument("--v-group", type=int, default=0, choices=(0, 32),
                     help="fp8 far tier V: INT4 scale/zero per token (0) or per 32-dim group (32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="per-workgroup phase timeline of --config's kernel from the phase-stamp build "
+                         "(make -C foveated_kv_amd/csrc STAMPS=1)")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip timing the other benchmark configurations (reported under other_configs)")
     ap.add_argument("--other-steps", type=int, default=30, help="timed steps per other configuration")
@@ -221,6 +224,8 @@ def main():
                     help="also time a plain device copy of this many MiB (HBM calibration; reported "
                          "as copy_gbs, read + write bytes)")
     args = ap.parse_args()
+    if args.phase_stamps:  # the phase-stamp build of the library (make -C foveated_kv_amd/csrc STAMPS=1)
+        os.environ["FKV_LIBRARY"] = os.path.join(ROOT, "foveated_kv_amd", "libfkv_stamps.so")
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -245,6 +250,9 @@ def main():
         return
     if args.crossover:
         run_crossover(args, torch, dev)
+        return
+    if args.phase_stamps:
+        run_phase_stamps(args, torch, dev)
         return
     B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[args.config]
     cfg = ext.TierConfig()
@@ -703,6 +711,111 @@ def run_e2e(args, torch, dev):
                        and hres["near_valid_end"] == gres["near_valid_end"]},
     }
     print(json.dumps(result), flush=True)
+
+
+def run_phase_stamps(args, torch, dev):
+    """Where one launch's time goes, from the phase-stamp build: --config's
+    handle (TurboQuant for C4) is called back to back for 300 ms, then
+    --steps more times; the stamps of the last launch (100 MHz clock, per
+    workgroup: entry, prologue done, each wave's stream done, records
+    published, arrival counted, the last split's merge done; the XCD id)
+    become one JSON line of phase durations in us: p50 / max over
+    workgroups, the spread of the XCDs' first starts and last stream ends,
+    and the last output relative to the first workgroup's entry."""
+    import ctypes
+
+    from foveated_kv_amd import _lib, ext
+
+    lib = _lib.load()
+    probe = (ctypes.c_uint64 * 64)()
+    if lib.fkv_phase_stamps(ctypes.cast(probe, ctypes.c_void_p), 0, 1) != 0:
+        raise SystemExit("the library has no phase stamps: build it with make -C foveated_kv_amd/csrc STAMPS=1")
+    name = args.config
+    B, Hq, Hkv, D, S, n_dec = __import__("foveated_kv_amd.synthetic", fromlist=["CONFIGS"]).CONFIGS[name]
+    make_handle, qt, dkt, dvt, _ = config_handles(torch, dev, ext, name, args.seed, args.spikes)
+    h = make_handle()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_MS / 1e3:
+        for _ in range(20):
+            h(qt, dkt, dvt)
+        torch.cuda.synchronize()
+    for _ in range(max(args.steps, 1)):
+        h(qt, dkt, dvt)
+    torch.cuda.synchronize()
+    n_wgs = 8192
+    raw = (ctypes.c_uint64 * (64 * n_wgs))()
+    _lib.check(lib.fkv_phase_stamps(ctypes.cast(raw, ctypes.c_void_p), n_wgs, 1), "fkv_phase_stamps")
+    st = np.frombuffer(raw, dtype=np.uint64).reshape(n_wgs, 64).astype(np.int64)
+    st = st[st[:, 0] > 0]
+    t_first = st[:, 0].min()
+    us = lambda x: np.asarray(x, np.float64) / 100.0  # 100 MHz ticks -> us
+    waves = [c for c in range(2, 18) if (st[:, c] > 0).any()]
+    wave_end = st[:, waves].max(axis=1)
+    xcc = st[:, 63]
+    # slot 22 is written only by the last split of a row to arrive, which
+    # varies between launches: keep the stamps of this launch (after its arrival)
+    merged = st[st[:, 22] > st[:, 21]]
+
+    def pq(x):
+        x = np.asarray(x, np.float64)
+        return {"p50": round(float(np.median(x)), 3), "max": round(float(x.max()), 3)} if x.size else None
+
+    ends = {int(x): us(wave_end[xcc == x].max() - t_first) for x in np.unique(xcc)}
+    starts = {int(x): us(st[xcc == x, 0].min() - t_first) for x in np.unique(xcc)}
+    out = {
+        "mode": "phase-stamps", "config": name, "workgroups": int(len(st)), "waves_per_wg": len(waves),
+        "launches_before": args.steps, "unit": "us",
+        "entry_spread": pq(us(st[:, 0] - t_first)),
+        "xcd_first_start": {k: round(v, 3) for k, v in sorted(starts.items())},
+        "prologue": pq(us(st[:, 1] - st[:, 0])),
+        "stream_to_last_wave": pq(us(wave_end - st[:, 1])),
+        "xcd_last_stream_end": {k: round(v, 3) for k, v in sorted(ends.items())},
+        "xcd_end_spread": round(max(ends.values()) - min(ends.values()), 3),
+        "records_published": pq(us(st[:, 20] - wave_end)) if (st[:, 20] > 0).all() else None,
+        "arrival": pq(us(st[:, 21] - st[:, 20])) if (st[:, 21] > 0).all() else None,
+        "last_split_merge": pq(us(merged[:, 22] - merged[:, 21])) if len(merged) else None,
+        "last_output": round(float(us(merged[:, 22].max() - t_first)), 3) if len(merged) else None,
+        "last_stream_end": round(float(us(wave_end.max() - t_first)), 3),
+    }
+    print(json.dumps(out), flush=True)
+
+
+def config_handles(torch, dev, ext, name, seed, spikes):
+    """make_handle, the query / decode tensors and the algorithmic bytes of
+    one benchmark configuration (the inputs config_line times)."""
+    from foveated_kv_amd import synthetic
+
+    B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[name]
+    cfg = ext.TierConfig()
+    cfg.promo_headroom_min = 8
+    turbo = name.startswith("c4_turbo")
+    tb = ext.tier_boundaries_c(cfg, S)
+    R, F = tb["R_actual"], tb["far_count"]
+    k, v = synthetic.make_kv(B, Hkv, S, D, seed)
+    q = synthetic.make_query(B, Hq, D, seed)
+    synthetic.inject_spikes(k, q, tb["mid_start"], F, spikes, seed)
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
+    cl = ext.CompressHandle(cfg).compress_layer(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                                                with_archive=turbo)
+    if turbo:
+        from foveated_kv_amd import turbo as tq
+
+        tc = tq.get_turbo_constants(D)
+        tfar = tq.turbo_compress_keys(cl.archive_k, tc) + tq.turbo_compress_values(cl.archive_v)
+
+        def make_handle():
+            return tq.TurboFoveatedHandle(cl.near_k, cl.near_v, *tfar, cl.near_valid, tc.Pi, tc.S, tc.centroids,
+                                          spike_margin=10.0)
+    else:
+        def make_handle():
+            return ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                                      cl.near_valid, spike_margin=10.0)
+    qt = torch.from_numpy(q).to(dev)[:, :, None, :]
+    dkt = torch.from_numpy(dk).to(dev) if dk is not None else None
+    dvt = torch.from_numpy(dv).to(dev) if dv is not None else None
+    nbytes = (algorithmic_bytes_turbo(B, Hq, Hkv, D, R, F, n_dec) if turbo
+              else algorithmic_bytes(B, Hq, Hkv, D, R, F, n_dec))
+    return make_handle, qt, dkt, dvt, nbytes
 
 
 def time_graph(torch, dev, fns, steps, warmup):

@@ -15,7 +15,9 @@ import os
 import torch  # noqa: F401  (binds the process to torch's HIP runtime first)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libfkv.so")
+# FKV_LIBRARY selects another build of the library (e.g. the phase-stamp
+# build, libfkv_stamps.so, that bench.py --phase-stamps reads)
+LIB_PATH = os.environ.get("FKV_LIBRARY") or os.path.join(_HERE, "libfkv.so")
 
 FKV_OK = 0
 FKV_EINVAL = -1
@@ -97,11 +99,15 @@ SIGNATURES = {
     "fkv_attn_call_dev": (ctypes.c_int, [P, P, I32, I32, P, P, P, I32, P, P, P, P]),
     "fkv_attn_call_strided": (ctypes.c_int, [P, P, I32, I32, P, P, I32, I32, P, P, P, P]),
     "fkv_attn_call_noalloc": (ctypes.c_int, [P, P, I32, I32, P, P, I32, P, P, P, P]),
-    "fkv_attn_plan": (ctypes.c_int, [I32, I32, I32, I32, I32, I32, I32, I32, P]),
+    "fkv_attn_plan": (ctypes.c_int, [I32, I32, I32, I32, I32, I32, I32, I32, I32, P]),
     "fkv_far_plan": (ctypes.c_int, [I32, I32, I32, ctypes.c_int64, ctypes.c_int64, I32, P, P, P]),
     "fkv_attn_blob_info": (ctypes.c_int, [P, ctypes.POINTER(BlobInfoC)]),
     "fkv_attn_read_near_valid": (ctypes.c_int, [P, P, P]),
     "fkv_attn_dispatch_info": (ctypes.c_int, [P, ctypes.POINTER(I32)]),
+    "fkv_attn_dispatch_check": (ctypes.c_int, [P, ctypes.POINTER(I32), P]),
+    "fkv_xcd_rule_fit": (ctypes.c_int, [P, I32, ctypes.POINTER(I32), ctypes.POINTER(I32)]),
+    "fkv_phase_stamps": (ctypes.c_int, [P, I32, I32]),
+    "fkv_xcd_watch_violations": (ctypes.c_int32, [P, I32]),
     "fkv_attn_destroy": (None, [P]),
     "fkv_attn_set_k_scale": (ctypes.c_int, [P, P, P]),
     "fkv_attn_set_spike_k": (ctypes.c_int, [P, I32]),

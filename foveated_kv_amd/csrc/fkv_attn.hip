@@ -41,6 +41,10 @@
 
 namespace fkv {
 
+#ifdef FKV_PHASE_STAMPS
+__device__ unsigned long long fkv_stamps[kStampSlots * kStampWGs];
+#endif
+
 // ---------------------------------------------------------------------------
 // Blob layout
 // ---------------------------------------------------------------------------
@@ -279,7 +283,7 @@ __global__ __launch_bounds__(64) void merge_kernel(AttnArgs a) {
     const float* src = a.ws + (int64_t)row * ns * min(a.hpg, a.G) * RS;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ns * ng * RS * 4, 0x00020000);
-    merge_heads<D, 1>(a, rs, ns, ng, g, 1, (int)threadIdx.x, (int64_t)b * a.Hq + head0 + g);
+    merge_heads<D, 1, true>(a, rs, ns, ng, g, 1, (int)threadIdx.x, (int64_t)b * a.Hq + head0 + g);
 }
 
 // ---------------------------------------------------------------------------
@@ -301,136 +305,353 @@ struct SelectArgs {
     const int32_t* tokens_in;
     int32_t* flags;             // (B*Hq) number of spiking tokens, at most K
     int32_t* tokens;            // (B*Hq, K)
+    const float* kscale;        // (B*Hkv) per-head fp8 key scales, or NULL (1)
+    // candidate buffers of the two selection kernels: per head a count
+    // (zero between calls), its cut, and up to cap (score, token) pairs
+    int* cand_n;                // (B*Hq)
+    float* cut;                 // (B*Hq)
+    float* cand_s;              // (B*Hq, cap)
+    int* cand_t;                // (B*Hq, cap)
+    int cap;                    // 64 * K
 };
 
-// One wave per (batch, KV head, head quad).  A far token spikes when its
-// score exceeds its head's threshold min_near + margin (the attention
-// kernel's flag rule).  The wave scans the far tile maxima the attention
-// kernel stored, rescores each tile that can hold a spike -- its E4M3 keys
-// against the fp16 query with the attention kernel's MFMA chain (same
-// operands, same order: the same fp32 scores bit for bit) -- and keeps each
-// head's best K spiking tokens, score descending, ties to the smaller
-// index, in lanes 0..K-1 of two registers.  Tiles are visited in ascending
-// order, so once a head's list is full a later tile can only enter it with
-// a maximum above the list's last score.  Output: flags = the spike count,
-// tokens[0..count) the list; entry 0 is the attention kernel's first-index
-// argmax when nothing spikes (as the reference's single token), the rest
-// -1.
+// Workgroups per (batch, KV head, head quad) of the first selection
+// kernel, and the far tiles per head whose maxima a workgroup stages in
+// LDS (beyond that it reads them from memory).
+constexpr int kSelParts = 8;
+constexpr int kSelStage = 4096;
+constexpr int kSelWaves = 4;
+
+// fp32 -> uint32 with the same order (no NaN among scores) and back.
+__device__ inline uint32_t fkey(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ inline float unfkey(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k); }
+
+// The score MFMA's B operand of the wave's head quad: head j = lane % 4 of
+// the quad, dims 4s..4s+3 (heads past the group read the group's first
+// head, as the attention kernel does; their scores are never kept).
 template <int D>
-__global__ __launch_bounds__(64) void spike_select_kernel(SelectArgs a) {
-    constexpr int NS = D / 4;
-    const int quad = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x, j = lane & 3, blk = lane >> 2;
+__device__ inline void load_qv(const SelectArgs& a, int64_t o0, int quad, int lane, fkv_h4 (&qv)[D / 4]) {
+    const int j = lane & 3;
+    const uint16_t* qrow = a.q + (4 * quad + j < a.G ? o0 + j : o0 - 4 * quad) * D;
+#pragma unroll
+    for (int s = 0; s < D / 4; s++) {
+        uint2 w;
+        __builtin_memcpy(&w, qrow + 4 * s, 8);
+        qv[s] = __builtin_bit_cast(fkv_h4, w);
+    }
+}
+
+// The far tiles' 64 scores for the wave's head quad as the attention
+// kernel computes them: lane = token 4 blk + e of the tile, e = 0..3, head
+// lane % 4 (the same E4M3 operands, fp16 query and MFMA chain in the same
+// order: the same fp32 bits).  N tiles, all loads issued before any MFMA.
+template <int D, int N>
+__device__ inline void rescore_tiles(const SelectArgs& a, int64_t bkv, const int (&tile)[N],
+                                     const fkv_h4 (&qv)[D / 4], float far_scale, int lane, float (&sv)[N][4]) {
+    uint4 kc[N][D / 16];
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        const uint8_t* rec = a.blob + a.L.far + far_rec_index(a.L, bkv, tile[n]) * (int64_t)a.L.far_rec;
+#pragma unroll
+        for (int c = 0; c < D / 16; c++) kc[n][c] = *(const uint4*)(rec + c * 1024 + lane * 16);
+    }
+    fkv_f4 acc[N];
+#pragma unroll
+    for (int n = 0; n < N; n++) acc[n] = fkv_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < D / 4; s++)
+#pragma unroll
+        for (int n = 0; n < N; n++) acc[n] = mfma4_local(e4m3x4(word_of(kc[n][s >> 2], s & 3)), qv[s], acc[n]);
+#pragma unroll
+    for (int n = 0; n < N; n++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) sv[n][e] = acc[n][e] * far_scale;
+}
+
+// (s, t) ahead of (s2, t2): higher score, or equal and the smaller token.
+__device__ inline bool ahead_of(float s, int t, float s2, int t2) { return s > s2 || (s == s2 && t < t2); }
+
+// Insert (s, t) into a list held in lanes 0..K-1 (n entries, in order);
+// the whole wave calls it with the same (s, t).
+__device__ inline void list_insert(float& ls, int& li, int& n, int K, float s, int t, int lane) {
+    const bool ahead = lane < n && ahead_of(ls, li, s, t);
+    const int pos = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ahead));
+    if (pos >= K) return;
+    const float ps = __shfl_up(ls, 1);
+    const int pi = __shfl_up(li, 1);
+    if (lane > pos) {
+        ls = ps;
+        li = pi;
+    } else if (lane == pos) {
+        ls = s;
+        li = t;
+    }
+    n = n < K ? n + 1 : K;
+}
+
+// One (score, token) per lane sorted across the wave, best first (bitonic
+// network on lane swaps; equal pairs are the padding (-inf, INT_MAX)).
+__device__ inline void wave_sort(float& s, int& t, int lane) {
+#pragma unroll
+    for (int k = 2; k <= kWave; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const float ps = __shfl_xor(s, j);
+            const int pt = __shfl_xor(t, j);
+            const bool pb = ahead_of(ps, pt, s, t);
+            const bool lower = (lane & j) == 0, want = (lane & k) == 0;
+            if (lower == want ? pb : ahead_of(s, t, ps, pt)) {
+                s = ps;
+                t = pt;
+            }
+        }
+}
+
+// Top-K spike selection, part 1: kSelParts workgroups per (batch, KV head,
+// head quad).  A far token spikes when its score exceeds its head's
+// threshold min_near + margin (the attention kernel's flag rule); each head
+// reports its best K spiking tokens, score descending, ties to the smaller
+// index.  The K best tokens lie in the K far tiles of highest maximum
+// (among the tiles whose maximum clears the threshold): a tile holding one
+// of them has a maximum at least that token's score, and at most K - 1
+// tokens -- so at most K - 1 tiles -- score higher.  So, from the tile
+// maxima the attention kernel stored (staged in LDS):
+//  A. wave j finds head j's cut, the K-th largest tile maximum above the
+//     threshold (a bitwise binary search on order-preserving keys), or -inf
+//     when at most K tiles clear the threshold (every workgroup of the
+//     quad computes the same cuts);
+//  B. the quad's kSelParts x 4 waves share out the tiles whose maximum
+//     clears some head's threshold and cut, rescore them four at a time
+//     (rescore_tiles: the attention kernel's bits) and append every token
+//     above its head's threshold and at or above its cut to the head's
+//     candidate buffer in memory -- at least K tokens when the cut is set
+//     (each of the K tiles contributes its maximum), all of them
+//     otherwise, at most 64 per tile at or above the cut.
+template <int D>
+__global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(SelectArgs a) {
+    constexpr int NS = D / 4, NR = 4;  // tiles rescored together
+    __shared__ float thr_s[4], cut_s[4];
+    __shared__ int fl_s[4];
+    __shared__ float tm_s[4][kSelStage];
+    const int quad = blockIdx.x / kSelParts, part = blockIdx.x % kSelParts, kvh = blockIdx.y, b = blockIdx.z;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = threadIdx.x % kWave;
+    const int j = lane & 3, blk = lane >> 2;
     const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
     const int64_t o0 = (int64_t)b * a.Hq + (int64_t)kvh * a.G + 4 * quad;  // head 0 of the quad
-    const int hg = 4 * quad + j;            // the lane's head within the group
-    const bool live = hg < a.G;
-    const float thr = live ? a.thr[o0 + j] : INFINITY;
-    const bool flagged = live && a.flags_in[o0 + j] != 0;
-    // per head jj (wave-uniform): threshold, flag, list length; the list in
-    // lane i = entry i
-    float th[4], ls[4];
-    int fl[4], n[4], li[4];
+    const int K = a.K, ntf = a.ntf;
+    const bool staged = ntf <= kSelStage;
+    if (threadIdx.x < 4) {
+        const int jj = threadIdx.x;
+        const bool live = 4 * quad + jj < a.G;
+        thr_s[jj] = live ? a.thr[o0 + jj] : INFINITY;
+        fl_s[jj] = live && a.flags_in[o0 + jj] != 0;
+        cut_s[jj] = INFINITY;
+    }
+    __syncthreads();
+    if (!(fl_s[0] | fl_s[1] | fl_s[2] | fl_s[3])) return;  // nothing spikes: part 2 writes the outputs
+    // the tile maxima of the quad's flagged heads -> LDS, eight loads in flight per thread
+    if (staged) {
+        constexpr int U = 8;
+        for (int i0 = threadIdx.x; i0 < 4 * ntf; i0 += U * (int)blockDim.x) {
+            float v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + u * (int)blockDim.x, jj = i / ntf;
+                v[u] = i < 4 * ntf && fl_s[jj] ? a.tmax[(o0 + jj) * ntf + i % ntf] : -INFINITY;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + u * (int)blockDim.x;
+                if (i < 4 * ntf) tm_s[i / ntf][i % ntf] = v[u];
+            }
+        }
+    }
+    __syncthreads();
+    auto tmv = [&](int jj, int t) -> float { return staged ? tm_s[jj][t] : a.tmax[(o0 + jj) * ntf + t]; };
+    // ---- A: head `wave`'s cut ----
+    if (wave < 4 && fl_s[wave]) {
+        const float th = thr_s[wave];
+        int above = 0;
+        for (int t = lane; t < ntf; t += kWave) above += tmv(wave, t) > th;
+        for (int o = 32; o >= 1; o >>= 1) above += __shfl_xor(above, o);
+        float cut = -INFINITY;
+        if (above > K) {
+            // the largest key x with at least K maxima (above th) at or above it
+            uint32_t x = 0;
+            for (int bit = 31; bit >= 0; bit--) {
+                const uint32_t trial = x | (1u << bit);
+                int c = 0;
+                for (int t = lane; t < ntf; t += kWave) {
+                    const float v = tmv(wave, t);
+                    c += v > th && fkey(v) >= trial;
+                }
+                for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o);
+                if (c >= K) x = trial;
+            }
+            cut = unfkey(x);
+        }
+        if (lane == 0) {
+            cut_s[wave] = cut;
+            if (part == 0) a.cut[o0 + wave] = cut;
+        }
+    }
+    __syncthreads();
+    float th[4], ct[4];
+    int fl[4];
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
-        th[jj] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(thr), jj));
-        fl[jj] = __builtin_amdgcn_readlane((int)flagged, jj);
-        n[jj] = 0;
-        ls[jj] = -INFINITY;
-        li[jj] = INT_MAX;
+        th[jj] = thr_s[jj];
+        ct[jj] = cut_s[jj];
+        fl[jj] = fl_s[jj];
     }
-    if (fl[0] | fl[1] | fl[2] | fl[3]) {
-        const float far_scale = a.inv_sqrt_d * *(const float*)(a.blob + a.L.kscale + 4 * bkv);
-        // the score MFMA's B operand: head j of the quad, dims 4s..4s+3
-        // (heads past the group read the group's first head, as the
-        // attention kernel does; their scores are never kept)
-        fkv_h4 qv[NS];
-        const uint16_t* qrow = a.q + (o0 + (live ? j : -4 * quad)) * D;
+    fkv_h4 qv[NS];
+    load_qv<D>(a, o0, quad, lane, qv);
+    const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
+    // ---- B: this wave's candidate tiles (every kSelParts * kSelWaves-th), NR at a time ----
+    const int gw = part * kSelWaves + wave, nw = kSelParts * kSelWaves;
+    int r = 0, np = 0;  // candidates seen (the same in every wave of the quad); tiles pending
+    int pend[NR];
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
-            uint2 w;
-            __builtin_memcpy(&w, qrow + 4 * s, 8);
-            qv[s] = __builtin_bit_cast(fkv_h4, w);
-        }
-        for (int c0 = 0; c0 < a.ntf; c0 += kWave) {
-            // tiles of this chunk that can hold a spike (or, once a head's list
-            // is full, beat its last entry)
-            float cut[4];
+    for (int n = 0; n < NR; n++) pend[n] = -1;
+    auto flush = [&](int count) {
+        int tl[NR];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const float kth = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls[jj]), a.K - 1));
-                cut[jj] = n[jj] == a.K ? fmaxf(th[jj], kth) : th[jj];
-            }
-            const int tl = c0 + lane;
-            bool cand = false;
-            if (tl < a.ntf) {
+        for (int n = 0; n < NR; n++) tl[n] = n < count ? pend[n] : pend[0];
+        float sv[NR][4];
+        rescore_tiles<D, NR>(a, bkv, tl, qv, far_scale, lane, sv);
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++)
-                    if (fl[jj]) cand |= a.tmax[(o0 + jj) * a.ntf + tl] > cut[jj];
-            }
-            uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
-            while (mask) {
-                const int tile = c0 + (int)__builtin_ctzll(mask);
-                mask &= mask - 1;
-                // rescore: lane = token; the keys of dims 16c..16c+15 in chunk c
-                const uint8_t* rec = a.blob + a.L.far + far_rec_index(a.L, bkv, tile) * (int64_t)a.L.far_rec;
-                uint4 kc[D / 16];
+        for (int n = 0; n < NR; n++) {
+            if (n >= count) break;
 #pragma unroll
-                for (int c = 0; c < D / 16; c++) kc[c] = *(const uint4*)(rec + c * 1024 + lane * 16);
-                fkv_f4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < NS; s++) sacc = mfma4_local(e4m3x4(word_of(kc[s >> 2], s & 3)), qv[s], sacc);
-                float sv[4];
-                bool sp[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int t = tile * kTile + 4 * blk + e;
-                    sv[e] = sacc[e] * far_scale;
-                    sp[e] = flagged && t < a.L.F && sv[e] > thr;
+            for (int e = 0; e < 4; e++) {
+                const int t = tl[n] * kTile + 4 * blk + e;
+                if (fl[j] && t < a.L.F && sv[n][e] > th[j] && sv[n][e] >= ct[j]) {
+                    const int64_t oj = o0 + j;
+                    const int slot = atomicAdd(a.cand_n + oj, 1);
+                    if (slot < a.cap) {
+                        a.cand_s[oj * a.cap + slot] = sv[n][e];
+                        a.cand_t[oj * a.cap + slot] = t;
+                    }
                 }
-                // insert the spiking tokens, head by head
+            }
+        }
+    };
+    for (int c0 = 0; c0 < ntf; c0 += kWave) {
+        const int tl = c0 + lane;
+        bool cand = false;
+        if (tl < ntf) {
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++) {
-                    if (!fl[jj]) continue;
+            for (int jj = 0; jj < 4; jj++)
+                if (fl[jj]) {
+                    const float v = tmv(jj, tl);
+                    cand |= v > th[jj] && v >= ct[jj];
+                }
+        }
+        uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
+        while (mask) {
+            const int bit = (int)__builtin_ctzll(mask);
+            mask &= mask - 1;
+            if (r++ % nw != gw) continue;
+#pragma unroll
+            for (int n = 0; n < NR; n++)
+                if (n == np) pend[n] = c0 + bit;
+            if (++np == NR) {
+                flush(NR);
+                np = 0;
+            }
+        }
+    }
+    if (np > 0) flush(np);
+}
+
+// Top-K spike selection, part 2: one workgroup of 4 waves per (batch, KV
+// head, head quad), wave j for head j.  Keeps the best K of the head's
+// candidates in lanes 0..K-1 (the first 64 sorted across the wave, the
+// rest inserted), writes the outputs and re-arms the head's candidate
+// count.  A buffer overflows only when more than K tiles tie exactly at the
+// cut; that head then re-scans its tiles itself.  Output: flags = the spike
+// count (at most K), tokens[0..count) the list; entry 0 is the attention
+// kernel's first-index argmax when nothing spikes (the reference's single
+// token), the rest -1.
+template <int D>
+__global__ __launch_bounds__(64 * kSelWaves) void spike_select_kernel(SelectArgs a) {
+    const int quad = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = threadIdx.x % kWave;
+    const int j = lane & 3, blk = lane >> 2;
+    if (4 * quad + wave >= a.G) return;
+    const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
+    const int64_t o0 = (int64_t)b * a.Hq + (int64_t)kvh * a.G + 4 * quad, oj = o0 + wave;
+    const int K = a.K;
+    float ls = -INFINITY;
+    int li = INT_MAX, n = 0;
+    if (a.flags_in[oj] != 0) {
+        const int nb = a.cand_n[oj];
+        if (nb <= a.cap) {
+            for (int c0 = 0; c0 < nb; c0 += kWave) {
+                const int i = c0 + lane;
+                float s = i < nb ? a.cand_s[oj * a.cap + i] : -INFINITY;
+                int t = i < nb ? a.cand_t[oj * a.cap + i] : INT_MAX;
+                if (c0 == 0) {  // the first 64: one sort, the best K become the list
+                    wave_sort(s, t, lane);
+                    ls = s;
+                    li = t;
+                    n = nb < K ? nb : K;
+                    continue;
+                }
+                const float ks = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls), K - 1));
+                const int kt = __builtin_amdgcn_readlane(li, K - 1);
+                uint64_t m = __builtin_amdgcn_ballot_w64(i < nb && (n < K || ahead_of(s, t, ks, kt)));
+                while (m) {
+                    const int src = (int)__builtin_ctzll(m);
+                    m &= m - 1;
+                    list_insert(ls, li, n, K, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), src)),
+                                __builtin_amdgcn_readlane(t, src), lane);
+                }
+            }
+        } else {
+            // more than K tiles tie at the cut: this head re-scans its tiles
+            fkv_h4 qv[D / 4];
+            load_qv<D>(a, o0, quad, lane, qv);
+            const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
+            const float thj = a.thr[oj], ctj = a.cut[oj];
+            const float* tm = a.tmax + oj * a.ntf;
+            for (int c0 = 0; c0 < a.ntf; c0 += kWave) {
+                const int tl = c0 + lane;
+                const bool cand = tl < a.ntf && tm[tl] > thj && tm[tl] >= ctj;
+                uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
+                while (mask) {
+                    const int tile[1] = {c0 + (int)__builtin_ctzll(mask)};
+                    mask &= mask - 1;
+                    float sv[1][4];
+                    rescore_tiles<D, 1>(a, bkv, tile, qv, far_scale, lane, sv);
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        uint64_t m = __builtin_amdgcn_ballot_w64(sp[e] && j == jj);
+                        const int t0 = tile[0] * kTile + e;
+                        uint64_t m = __builtin_amdgcn_ballot_w64(j == wave && t0 + 4 * blk < a.L.F &&
+                                                                  sv[0][e] > thj && sv[0][e] >= ctj);
                         while (m) {
                             const int src = (int)__builtin_ctzll(m);
                             m &= m - 1;
-                            const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[e]), src));
-                            const int t = tile * kTile + 4 * (src >> 2) + e;
-                            // entries ahead of the token: higher score, or equal and earlier
-                            const bool ahead = lane < n[jj] && (ls[jj] > s || (ls[jj] == s && li[jj] < t));
-                            const int pos = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ahead));
-                            if (pos >= a.K) continue;
-                            const float ps = __shfl_up(ls[jj], 1);
-                            const int pi = __shfl_up(li[jj], 1);
-                            if (lane > pos) {
-                                ls[jj] = ps;
-                                li[jj] = pi;
-                            } else if (lane == pos) {
-                                ls[jj] = s;
-                                li[jj] = t;
-                            }
-                            n[jj] = n[jj] < a.K ? n[jj] + 1 : a.K;
+                            list_insert(ls, li, n, K,
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0][e]), src)),
+                                        t0 + 4 * (src >> 2), lane);
                         }
                     }
                 }
             }
         }
     }
-    // lanes 0..K-1 of head jj's list -> tokens[o_jj][0..K)
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-        if (4 * quad + jj >= a.G) continue;
-        const int64_t oj = o0 + jj;
-        if (lane < a.K) {
-            int t = lane < n[jj] ? li[jj] : -1;
-            if (lane == 0 && n[jj] == 0) t = a.tokens_in[oj];
-            a.tokens[oj * a.K + lane] = t;
-        }
-        if (lane == 0) a.flags[oj] = n[jj];
+    if (lane < K) {
+        int t = lane < n ? li : -1;
+        if (lane == 0 && n == 0) t = a.tokens_in[oj];
+        a.tokens[oj * K + lane] = t;
+    }
+    if (lane == 0) {
+        a.flags[oj] = n;
+        a.cand_n[oj] = 0;  // re-armed for the next call
     }
 }
 
@@ -558,8 +779,9 @@ LaunchPlan plan_launch(const BlobLayout& L, int Hq, int n_decode, int target_wgs
     p.waves = attn_waves(L.D, (int)cdiv(p.ng_max, 4), L.fmt);
     p.splits = plan_splits(L, p.rows, n_decode, target_wgs, p.waves);
     // rows of 2..4 splits keep one record per wave (their merge reads at most
-    // 16); rows of more splits merge their 4 waves in LDS first (C4's 8
-    // splits: 32 wave records merged 0.4 us slower than 8 merged records)
+    // 16 records, 32 for 8-wave TurboQuant rows: within kMaxSplits); rows of
+    // more splits merge their waves in LDS first (C4's 8 splits: 32 wave
+    // records merged 0.4 us slower than 8 merged records)
     p.wave_recs = p.splits > 1 && p.splits <= 4 ? p.waves : 1;
     p.ws_floats = p.splits > 1 ? partial_floats(p.rows, p.splits * p.wave_recs, p.ng_max, L.D) : 0;
     return p;
@@ -630,15 +852,9 @@ int xcd_rule(int dev, hipStream_t st, int* mod) {
                                 "hipMemcpyAsync(xcd probe)");
         if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
         if (rc) return rc;
-        uint32_t lo = x[0], hi = x[0];
-        for (uint32_t v : x) {
-            lo = v < lo ? v : lo;
-            hi = v > hi ? v : hi;
-        }
-        const uint32_t X = hi - lo + 1, c = x[0] - lo;
-        bool ok = true;
-        for (int i = 0; i < kXcdProbeWGs && ok; i++) ok = x[i] == lo + (c + (uint32_t)i) % X;
-        r.mod = ok ? (int)X : 0;
+        int32_t X = 0, c = 0;
+        (void)fkv_xcd_rule_fit(x.data(), kXcdProbeWGs, &X, &c);
+        r.mod = X;
         r.done = true;
     }
     *mod = r.mod;
@@ -774,7 +990,9 @@ int fkv_attn_create_g32(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32
 // ---------------------------------------------------------------------------
 
 constexpr size_t kScratchBytes = (size_t)8 << 20;
-constexpr size_t kScratchArriveBytes = (size_t)64 << 10;  // 16384 rows
+constexpr int kScratchRows = 16384;  // rows the counter region serves
+// arrival counters [rows], then the XCD watch words [1 + rows]
+constexpr size_t kScratchArriveBytes = ((size_t)(2 * kScratchRows + 1) * 4 + 255) & ~(size_t)255;
 constexpr int kScratchDevices = 64;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -806,23 +1024,36 @@ int scratch_base(const std::string& name, int dev, hipStream_t st, uint8_t** out
 
 namespace {
 
+void free_spike_buffers(fkv_attn* h) {
+    void* bufs[] = {h->spk_tmax, h->spk_thr, h->spk_flags, h->spk_tokens, h->spk_cand_n, h->spk_cut, h->spk_cand_s,
+                    h->spk_cand_t};
+    for (void* p : bufs)
+        if (p) (void)hipFree(p);
+    h->spk_tmax = h->spk_thr = h->spk_cut = h->spk_cand_s = nullptr;
+    h->spk_flags = h->spk_tokens = nullptr;
+    h->spk_cand_n = h->spk_cand_t = nullptr;
+}
+
 // The top-K spike selection's buffers for Hq query heads (spike_k > 1).
 int ensure_spike_buffers(fkv_attn* h, int Hq) {
     if (h->spike_k <= 1 || h->spk_hq == Hq) return FKV_OK;
     if (h->spk_hq != 0) return set_error("fkv_attn: spike buffers sized for another query-head count");
     const fkv::BlobLayout& L = h->L;
     const size_t heads = (size_t)L.B * Hq, ntf = (size_t)fkv::cdiv(L.F, fkv::kTile);
+    // candidate buffers sized for the largest spike_k, so a later
+    // fkv_attn_set_spike_k needs no new allocation
+    const size_t cap = (size_t)fkv::kTile * FKV_MAX_SPIKE_K;
     int rc = check_hip(hipMalloc(&h->spk_tmax, (heads * ntf > 0 ? heads * ntf : 1) * sizeof(float)), "hipMalloc(tmax)");
     if (!rc) rc = check_hip(hipMalloc(&h->spk_thr, heads * sizeof(float)), "hipMalloc(thr)");
     if (!rc) rc = check_hip(hipMalloc(&h->spk_flags, heads * sizeof(int32_t)), "hipMalloc(flags)");
     if (!rc) rc = check_hip(hipMalloc(&h->spk_tokens, heads * sizeof(int32_t)), "hipMalloc(tokens)");
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_cand_n, heads * sizeof(int)), "hipMalloc(cand_n)");
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_cut, heads * sizeof(float)), "hipMalloc(cut)");
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_cand_s, heads * cap * sizeof(float)), "hipMalloc(cand_s)");
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_cand_t, heads * cap * sizeof(int)), "hipMalloc(cand_t)");
+    if (!rc) rc = check_hip(hipMemset(h->spk_cand_n, 0, heads * sizeof(int)), "hipMemset(cand_n)");
     if (rc) {
-        (void)hipFree(h->spk_tmax);
-        (void)hipFree(h->spk_thr);
-        (void)hipFree(h->spk_flags);
-        (void)hipFree(h->spk_tokens);
-        h->spk_tmax = h->spk_thr = nullptr;
-        h->spk_flags = h->spk_tokens = nullptr;
+        free_spike_buffers(h);
         return rc;
     }
     h->spk_hq = Hq;
@@ -842,7 +1073,8 @@ int ensure_workspace(const std::string& name, fkv_attn* h, int Hq, hipStream_t s
     const int rows = fkv::workspace_rows(L, Hq);
     const size_t qn = (size_t)L.B * Hq * L.D;
     int rc = check_hip(hipMalloc(&h->ws, wsf * sizeof(float)), "hipMalloc(ws)");
-    if (!rc) rc = check_hip(hipMalloc(&h->arrive, rows * sizeof(int)), "hipMalloc(arrive)");
+    // arrival counters [rows], then the XCD watch words [1 + rows]
+    if (!rc) rc = check_hip(hipMalloc(&h->arrive, (2 * (size_t)rows + 1) * sizeof(int)), "hipMalloc(arrive)");
     if (!rc) rc = check_hip(hipMalloc(&h->qbuf, qn * 2), "hipMalloc(qbuf)");
     if (rc) {
         if (h->ws) (void)hipFree(h->ws);
@@ -857,8 +1089,10 @@ int ensure_workspace(const std::string& name, fkv_attn* h, int Hq, hipStream_t s
     h->arrive_n = rows;
     h->ws_hq = Hq;
     if (int rc2 = ensure_spike_buffers(h, Hq)) return rc2;
-    // counters start at zero; the kernel's last split re-arms them
-    hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(rows, 256)), dim3(256), 0, st, h->arrive, rows);
+    // counters and watch words start at zero; the kernel's last split
+    // re-arms its row's counter and clears its watch word
+    hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(2 * rows + 1, 256)), dim3(256), 0, st, h->arrive,
+                       2 * rows + 1);
     return check_hip(hipGetLastError(), "zero_ints_kernel launch");
 }
 
@@ -869,6 +1103,7 @@ int ensure_workspace(const std::string& name, fkv_attn* h, int Hq, hipStream_t s
 struct CallWorkspace {
     float* ws;           // split partial records
     int* arrive;         // per-row arrival counters, zero between calls
+    uint32_t* watch;     // XCD watch words: [0] violations, [1 + row]
     uint16_t* qbuf;      // fp16 copy of a bf16 / f32 query
     size_t ws_floats, arrive_n, qbuf_n;
 };
@@ -904,7 +1139,8 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         if (int rc = scratch_workspace(name, h, p, Hq, st, &w)) return rc;
     } else {
         if (int rc = ensure_workspace(name, h, Hq, st)) return rc;
-        w = CallWorkspace{h->ws, h->arrive, h->qbuf, h->ws_floats, h->arrive_n, (size_t)L.B * Hq * L.D};
+        w = CallWorkspace{h->ws, h->arrive, (uint32_t*)(h->arrive + h->arrive_n), h->qbuf, h->ws_floats,
+                          h->arrive_n, (size_t)L.B * Hq * L.D};
     }
     if (p.ws_floats > w.ws_floats || p.rows > (int)w.arrive_n)
         return set_error(name + ": launch plan exceeds the workspace (internal error)");
@@ -947,9 +1183,18 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.tmax_stride = (int)fkv::cdiv(L.F, fkv::kTile);
     a.thr = topk ? h->spk_thr : nullptr;
     a.kscale = h->has_kscale ? (const float*)(h->blob + L.kscale) : nullptr;
+#ifdef FKV_PHASE_STAMPS
+    {
+        void* sp = nullptr;
+        if (int rc = check_hip(hipGetSymbolAddress(&sp, HIP_SYMBOL(fkv::fkv_stamps)), "hipGetSymbolAddress(stamps)"))
+            return rc;
+        a.stamps = (unsigned long long*)sp;
+    }
+#endif
     a.ws = w.ws;
     const bool fused_merge = h->fused_merge;
     a.arrive = fused_merge ? w.arrive : nullptr;
+    a.xcd_watch = w.watch;
     a.near_plan = h->near_plan;
     {
         // Decode tiles go to the wave with the fewest planned bytes where a
@@ -989,9 +1234,10 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.tq_lvh = h->tq.lvh;
     a.tq_lvl = h->tq.lvl;
     const int nq = (ng_max + 3) / 4;
+    const bool ext = topk || h->has_kscale;  // the kernels that carry the extensions
     fkv::AttnKernel k = L.fmt == 1 ? (L.D == 128 ? fkv::pick_attn_turbo<128>(nq) : fkv::pick_attn_turbo<64>(nq))
-                        : nq == 1  ? fkv::attn_kernel_one_quad(L.D, L.fmt)
-                                   : fkv::attn_kernel_quads(L.D, L.fmt, nq);
+                        : nq == 1  ? fkv::attn_kernel_one_quad(L.D, L.fmt, ext)
+                                   : fkv::attn_kernel_quads(L.D, L.fmt, nq, ext);
     hipLaunchKernelGGL(k, grid, block, 0, st, a);
     if (splits > 1 && !fused_merge) {
         const dim3 mgrid(rows, ng_max);
@@ -1014,9 +1260,22 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         sa.tokens_in = h->spk_tokens;
         sa.flags = spike_flags;
         sa.tokens = spike_tokens;
-        const dim3 sgrid((unsigned)fkv::cdiv(G, 4), L.Hkv, L.B);
-        if (L.D == 128) hipLaunchKernelGGL(fkv::spike_select_kernel<128>, sgrid, dim3(fkv::kWave), 0, st, sa);
-        else hipLaunchKernelGGL(fkv::spike_select_kernel<64>, sgrid, dim3(fkv::kWave), 0, st, sa);
+        sa.kscale = a.kscale;
+        sa.cand_n = h->spk_cand_n;
+        sa.cut = h->spk_cut;
+        sa.cand_s = h->spk_cand_s;
+        sa.cand_t = h->spk_cand_t;
+        sa.cap = fkv::kTile * h->spike_k;
+        const unsigned quads = (unsigned)fkv::cdiv(G, 4);
+        const dim3 cgrid(quads * fkv::kSelParts, L.Hkv, L.B), sgrid(quads, L.Hkv, L.B);
+        const dim3 sblock(fkv::kWave * fkv::kSelWaves);
+        if (L.D == 128) {
+            hipLaunchKernelGGL(fkv::spike_candidates_kernel<128>, cgrid, sblock, 0, st, sa);
+            hipLaunchKernelGGL(fkv::spike_select_kernel<128>, sgrid, sblock, 0, st, sa);
+        } else {
+            hipLaunchKernelGGL(fkv::spike_candidates_kernel<64>, cgrid, sblock, 0, st, sa);
+            hipLaunchKernelGGL(fkv::spike_select_kernel<64>, sgrid, sblock, 0, st, sa);
+        }
     }
     return check_hip(hipGetLastError(), "attn_kernel launch");
 }
@@ -1026,7 +1285,7 @@ int scratch_workspace(const std::string& name, fkv_attn* h, const fkv::LaunchPla
     const fkv::BlobLayout& L = h->L;
     const size_t qbytes = ((size_t)L.B * Hq * L.D * 2 + 255) & ~(size_t)255;
     const size_t need = kScratchArriveBytes + qbytes + p.ws_floats * sizeof(float);
-    if ((size_t)p.rows * sizeof(int) > kScratchArriveBytes || need > kScratchBytes)
+    if (p.rows > kScratchRows || need > kScratchBytes)
         return set_error(name + ": this call needs " + std::to_string(need) + " bytes of scratch (" +
                          std::to_string(p.rows) + " rows x " + std::to_string(p.splits) +
                          " splits); the no-alloc entry point holds " + std::to_string(kScratchBytes) +
@@ -1037,7 +1296,8 @@ int scratch_workspace(const std::string& name, fkv_attn* h, const fkv::LaunchPla
     uint8_t* base = nullptr;
     if (int rc = scratch_base(name, dev, st, &base)) return rc;
     out->arrive = (int*)base;
-    out->arrive_n = kScratchArriveBytes / sizeof(int);
+    out->arrive_n = kScratchRows;
+    out->watch = (uint32_t*)(base + (size_t)kScratchRows * sizeof(int));
     out->qbuf = (uint16_t*)(base + kScratchArriveBytes);
     out->qbuf_n = qbytes / 2;
     out->ws = (float*)(base + kScratchArriveBytes + qbytes);
@@ -1071,11 +1331,11 @@ int fkv_attn_call_noalloc(fkv_attn* h, const void* query, int32_t q_dtype, int32
 }
 
 int fkv_attn_plan(int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F, int32_t Hq, int32_t n_decode,
-                  int32_t target_wgs, int64_t* out) {
+                  int32_t target_wgs, int32_t fmt, int64_t* out) {
     if (B <= 0 || Hkv <= 0 || (D != 64 && D != 128) || Na < 0 || F < 0 || Hq <= 0 || Hq % Hkv != 0 ||
-        n_decode < 0 || target_wgs < 1 || !out)
+        n_decode < 0 || target_wgs < 1 || fmt < 0 || fmt > 2 || !out)
         return set_error("fkv_attn_plan: bad argument");
-    const fkv::BlobLayout L = fkv::make_layout(B, Hkv, D, Na, F, 0);
+    const fkv::BlobLayout L = fkv::make_layout(B, Hkv, D, Na, F, fmt);
     const fkv::LaunchPlan p = fkv::plan_launch(L, Hq, n_decode, target_wgs);
     out[0] = p.hpg;
     out[1] = p.rows;
@@ -1083,6 +1343,8 @@ int fkv_attn_plan(int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F, int3
     out[3] = (int64_t)p.ws_floats;
     out[4] = (int64_t)fkv::workspace_floats(L, Hq);
     out[5] = fkv::workspace_rows(L, Hq);
+    out[6] = p.waves;
+    out[7] = p.wave_recs;
     return FKV_OK;
 }
 
@@ -1119,6 +1381,96 @@ int fkv_e4m3_decode(const uint8_t* codes, void* out_f16, int64_t n, void* stream
 int fkv_attn_dispatch_info(const fkv_attn* h, int32_t* xcd_mod) {
     if (!h || !xcd_mod) return set_error("fkv_attn_dispatch_info: NULL argument");
     *xcd_mod = h->xcd_mod;
+    return FKV_OK;
+}
+
+int fkv_phase_stamps(uint64_t* out, int32_t n_wgs, int32_t clear) {
+#ifdef FKV_PHASE_STAMPS
+    if (n_wgs < 0 || n_wgs > fkv::kStampWGs || (n_wgs > 0 && !out)) return set_error("fkv_phase_stamps: bad argument");
+    const size_t bytes = sizeof(uint64_t) * fkv::kStampSlots * (size_t)n_wgs;
+    if (n_wgs > 0) {
+        if (int rc = check_hip(hipMemcpyFromSymbol(out, HIP_SYMBOL(fkv::fkv_stamps), bytes, 0, hipMemcpyDeviceToHost),
+                               "hipMemcpyFromSymbol(stamps)"))
+            return rc;
+    }
+    if (clear) {
+        std::vector<uint64_t> z((size_t)fkv::kStampSlots * fkv::kStampWGs, 0);
+        if (int rc = check_hip(hipMemcpyToSymbol(HIP_SYMBOL(fkv::fkv_stamps), z.data(), z.size() * 8, 0,
+                                                 hipMemcpyHostToDevice),
+                               "hipMemcpyToSymbol(stamps)"))
+            return rc;
+    }
+    return FKV_OK;
+#else
+    (void)out;
+    (void)n_wgs;
+    (void)clear;
+    return set_error("fkv_phase_stamps: this library was built without FKV_PHASE_STAMPS");
+#endif
+}
+
+int fkv_xcd_rule_fit(const uint32_t* xcc, int32_t n, int32_t* xcd_mod, int32_t* offset) {
+    if (!xcc || n <= 0 || !xcd_mod || !offset) return set_error("fkv_xcd_rule_fit: bad argument");
+    uint32_t lo = xcc[0], hi = xcc[0];
+    for (int32_t i = 0; i < n; i++) {
+        lo = xcc[i] < lo ? xcc[i] : lo;
+        hi = xcc[i] > hi ? xcc[i] : hi;
+    }
+    const uint32_t X = hi - lo + 1, c = xcc[0] - lo;
+    bool ok = X <= 32;
+    for (int32_t i = 0; i < n && ok; i++) ok = xcc[i] == lo + (c + (uint32_t)i) % X;
+    *xcd_mod = ok ? (int32_t)X : 0;
+    *offset = ok ? (int32_t)c : 0;
+    return FKV_OK;
+}
+
+int32_t fkv_xcd_watch_violations(const uint32_t* words, int32_t rows) {
+    if (!words || rows < 0) return set_error("fkv_xcd_watch_violations: bad argument");
+    int32_t v = words[0] != 0;
+    for (int32_t r = 0; r < rows; r++) v += words[1 + r] != 0;  // arrival counters left armed
+    return v;
+}
+
+int fkv_attn_dispatch_check(fkv_attn* h, int32_t* violations, void* stream) {
+    if (!h || !violations) return set_error("fkv_attn_dispatch_check: NULL argument");
+    *violations = 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (int rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize")) return rc;
+    // the handle's own watch words, and the device's no-alloc scratch words
+    struct Region {
+        int* arrive;
+        int rows;
+    };
+    std::vector<Region> regions;
+    if (h->arrive) regions.push_back({h->arrive, (int)h->arrive_n});
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (h->device >= 0 && h->device < kScratchDevices && g_scratch_ptr[h->device])
+            regions.push_back({(int*)g_scratch_ptr[h->device], kScratchRows});
+    }
+    int32_t total = 0;
+    for (const Region& r : regions) {
+        // [flag, counters of rows 0..rows-1]: at rest every counter is zero
+        // (each row's merging workgroup re-arms it)
+        std::vector<uint32_t> w((size_t)r.rows + 1);
+        int rc = check_hip(hipMemcpyAsync(w.data(), r.arrive + r.rows, 4, hipMemcpyDeviceToHost, st),
+                           "hipMemcpyAsync(xcd watch)");
+        if (!rc) rc = check_hip(hipMemcpyAsync(w.data() + 1, r.arrive, (size_t)r.rows * 4, hipMemcpyDeviceToHost, st),
+                                "hipMemcpyAsync(arrival counters)");
+        if (!rc) rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
+        if (rc) return rc;
+        const int32_t v = fkv_xcd_watch_violations(w.data(), r.rows);
+        if (v > 0) {
+            // the arrival counts of the broken dispatches were split across
+            // L2s: clear counters and watch words before the coherent merge
+            hipLaunchKernelGGL(fkv::zero_ints_kernel, dim3(fkv::grid_for(2 * r.rows + 1, 256)), dim3(256), 0, st,
+                               r.arrive, 2 * r.rows + 1);
+            if (int rc = check_hip(hipGetLastError(), "zero_ints_kernel launch")) return rc;
+        }
+        total += v;
+    }
+    if (total > 0) h->xcd_mod = 0;  // later calls merge through memory
+    *violations = total;
     return FKV_OK;
 }
 
@@ -1210,10 +1562,7 @@ int fkv_attn_set_k_scale(fkv_attn* h, const float* k_scale, void* stream) {
 void fkv_attn_destroy(fkv_attn* h) {
     if (!h) return;
     if (h->blob) (void)hipFree(h->blob);
-    if (h->spk_tmax) (void)hipFree(h->spk_tmax);
-    if (h->spk_thr) (void)hipFree(h->spk_thr);
-    if (h->spk_flags) (void)hipFree(h->spk_flags);
-    if (h->spk_tokens) (void)hipFree(h->spk_tokens);
+    free_spike_buffers(h);
     if (h->ws) (void)hipFree(h->ws);
     if (h->qbuf) (void)hipFree(h->qbuf);
     if (h->arrive) (void)hipFree(h->arrive);

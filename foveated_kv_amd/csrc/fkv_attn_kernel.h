@@ -23,6 +23,30 @@ typedef float fkv_f4 __attribute__((ext_vector_type(4)));
 
 namespace fkv {
 
+// Phase stamps (a build with -DFKV_PHASE_STAMPS only; the default build
+// compiles them out): per workgroup of an attention launch, thread 0 / each
+// wave's lane 0 stores the 100 MHz constant clock (s_memrealtime) at fixed
+// points into a.stamps[64 * linear workgroup index + slot] (a device array
+// of fkv_attn.hip), and the XCD id into slot 63; fkv_phase_stamps copies
+// them out.  Slots: 0 entry, 1 prologue done (query landed, stream about to
+// start), 2 + w wave w's stream and decode tiles done, 20 records published
+// (before the arrival), 21 arrival counted, 22 the last split's merge done.
+constexpr int kStampSlots = 64, kStampWGs = 8192;
+#ifdef FKV_PHASE_STAMPS
+#define FKV_STAMP_AT(cond, slot)                                                                             \
+    do {                                                                                                    \
+        if (cond) {                                                                                         \
+            const int wg_ = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;                 \
+            if (wg_ < kStampWGs) a.stamps[kStampSlots * wg_ + (slot)] = __builtin_amdgcn_s_memrealtime();  \
+        }                                                                                                   \
+    } while (0)
+#else
+#define FKV_STAMP_AT(cond, slot) \
+    do {                         \
+    } while (0)
+#endif
+
+
 // ---------------------------------------------------------------------------
 // Attention kernel
 // ---------------------------------------------------------------------------
@@ -62,18 +86,11 @@ struct AttnArgs {
     uint16_t* out;  // (B, Hq, D) fp16
     int32_t* flags;
     int32_t* tokens;
-    // Top-K spike selection (spike_k > 1, else NULL): every far tile's
-    // maximum score per query head, (B*Hq, tmax_stride = far tiles) fp32,
-    // and each head's spike threshold min_near + margin, (B*Hq) fp32; the
-    // selection kernel (spike_select_kernel) reads both after the launch
-    float* tmax;
-    int tmax_stride;
-    float* thr;
-    // per-head fp8 key scales, (B*Hkv) fp32 in the blob; NULL for a handle
-    // whose keys are unscaled (no load then: the scale is 1)
-    const float* kscale;
     float* ws;      // split partials: [row][split][ng][kHdr + D]
     int* arrive;    // [row] split arrival counters (zero between calls)
+    // XCD-local merge watch (xcd_mod != 0): a flag the merging workgroups
+    // raise when a split record of their row came from another XCD
+    uint32_t* xcd_watch;
     int near_plan;  // expected near tiles per row (balances the far split)
     int dec_wave0;  // the wave that takes decode tile 0
     int wave_recs;  // split records per split: 4 (one per wave) or 1 (merged in LDS)
@@ -86,6 +103,21 @@ struct AttnArgs {
     float tq_beta, tq_gamma, tq_delta;  // centroid coefficients (TurboConsts)
     float tq_qjl;           // 1.2533141 / D
     float tq_lvh, tq_lvl;   // value level coefficients
+    // Extensions (read by the EXT kernels only; last, so the fields above
+    // keep their kernel-argument offsets).  Top-K spike selection (spike_k >
+    // 1, else NULL): every far tile's maximum score per query head, (B*Hq,
+    // tmax_stride = far tiles) fp32, and each head's spike threshold
+    // min_near + margin, (B*Hq) fp32; spike_select_kernel reads both after
+    // the launch
+    float* tmax;
+    int tmax_stride;
+    float* thr;
+    // per-head fp8 key scales, (B*Hkv) fp32 in the blob; NULL for a handle
+    // whose keys are unscaled (no load then: the scale is 1)
+    const float* kscale;
+#ifdef FKV_PHASE_STAMPS
+    unsigned long long* stamps;  // kStampSlots per workgroup (fkv_phase_stamps)
+#endif
 };
 
 // v_mfma_f32_4x4x4f16: 16 independent 4x4x4 blocks; lane l supplies row /
@@ -538,7 +570,7 @@ __device__ inline void lds_far(FarTile<64>& r, const uint8_t* slot, int lane) {
 }
 
 // out = acc / l (fp16), spike flag and token for ng heads of one record set
-template <int D>
+template <int D, bool EXT = false>
 __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b, int head0, int ng) {
     constexpr int RS = kHdr + D;
     for (int i = threadIdx.x; i < ng * D; i += blockDim.x) {
@@ -554,7 +586,7 @@ __device__ inline void finalize_rows(const AttnArgs& a, const float* fin, int b,
         const int64_t o = (int64_t)b * a.Hq + head0 + g;
         a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
         a.tokens[o] = mx == -INFINITY ? -1 : arg;
-        if (a.thr) a.thr[o] = mn + a.spike_margin;
+        if (EXT && a.thr) a.thr[o] = mn + a.spike_margin;
     }
 }
 
@@ -1713,6 +1745,13 @@ __device__ inline void dec_tile(Lane<D, NQ>& st, const AttnArgs& a, int count, i
         []() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); });
 }
 
+// The XCD this wave runs on.
+__device__ inline uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xF;
+}
+
 // Merge of the partial records of all splits of one row
 // (csrc/kernels/foveated_attn.metal:394-431 restated for partials in
 // memory): split maxima are rescaled to the global max; spike fields take
@@ -1787,7 +1826,7 @@ __device__ inline void row_argmax16(float& mx, int& arg) {
 // (c, u) accumulates its splits u, u + SUB, ... in order, with each split's
 // scale read from that split's lane; the SUB lane groups combine by lane
 // swaps; lanes of group 0 write chunk c.
-template <int D, int NH, int KV>
+template <int D, int NH, int KV, bool EXT>
 __device__ inline void merge_values(const AttnArgs& a, const fkv_f4 (&v)[KV], float f, float M, float L, float mn,
                                     float mx, int arg, int nk, int u, int c, int lane, int64_t o) {
     constexpr int SUB = kWave / (D / 4);
@@ -1795,7 +1834,7 @@ __device__ inline void merge_values(const AttnArgs& a, const fkv_f4 (&v)[KV], fl
     if (lane == 0) {
         a.flags[o] = mx > mn + a.spike_margin ? 1 : 0;
         a.tokens[o] = mx == -INFINITY ? -1 : arg;
-        if (a.thr) a.thr[o] = mn + a.spike_margin;
+        if (EXT && a.thr) a.thr[o] = mn + a.spike_margin;
     }
     // in the load groups of 4: splits past the last have scale 0 and value 0
     fkv_f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1852,7 +1891,8 @@ constexpr int merge_kv() { return kMaxSplits / (kWave / (D / 4)) / NH; }  // val
 // The record loads of merge_heads with cache policy CPOL.
 template <int D, int NH, int CPOL>
 __device__ inline void merge_loads(__amdgpu_buffer_rsrc_t rs, int ng, int nk, int g0, int step, int lane,
-                                   fkv_f4 (&h)[NH], int (&harg)[NH], fkv_f4 (&v)[NH][merge_kv<D, NH>()]) {
+                                   fkv_f4 (&h)[NH], int (&harg)[NH], uint32_t (&hx)[NH],
+                                   fkv_f4 (&v)[NH][merge_kv<D, NH>()]) {
     constexpr int RS = kHdr + D;
     constexpr int CH = D / 4, SUB = kWave / CH;
     const int c = lane % CH, u = lane / CH;
@@ -1862,7 +1902,10 @@ __device__ inline void merge_loads(__amdgpu_buffer_rsrc_t rs, int ng, int nk, in
         const int g = g0 + i * step;
         const int hoff = lane * sstride + g * RS * 4;
         h[i] = ld_rec4<CPOL>(rs, hoff);
-        harg[i] = ld_rec1<CPOL>(rs, hoff + 16);
+        // header words 4, 5: the first-index argmax and the writer's XCD
+        const fkv_v2u ax = __builtin_bit_cast(fkv_v2u, __builtin_amdgcn_raw_buffer_load_b64(rs, hoff + 16, 0, CPOL));
+        harg[i] = (int)ax.x;
+        hx[i] = ax.y;
         const int voff = u * sstride + (g * RS + kHdr + 4 * c) * 4;
         // in groups of 4 behind one branch: loads past the last split read
         // 0 without touching memory (and meet scale 0)
@@ -1876,7 +1919,7 @@ __device__ inline void merge_loads(__amdgpu_buffer_rsrc_t rs, int ng, int nk, in
     }
 }
 
-template <int D, int NH>
+template <int D, int NH, bool EXT = false>
 __device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs, int ns, int ng, int g0, int step,
                                    int lane, int64_t o0, bool xcd_local = false) {
     constexpr int CH = D / 4;          // 16-byte value chunks of a head
@@ -1888,10 +1931,23 @@ __device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs,
     // past ns are masked below, value loads of splits past ns meet scale 0.
     fkv_f4 h[NH];
     int harg[NH];
+    uint32_t hx[NH];
     fkv_f4 v[NH][KV];
-    if (xcd_local) merge_loads<D, NH, kCpolSc0>(rs, ng, nk, g0, step, lane, h, harg, v);
-    else merge_loads<D, NH, kCpolSc1>(rs, ng, nk, g0, step, lane, h, harg, v);
+    if (xcd_local) merge_loads<D, NH, kCpolSc0>(rs, ng, nk, g0, step, lane, h, harg, hx, v);
+    else merge_loads<D, NH, kCpolSc1>(rs, ng, nk, g0, step, lane, h, harg, hx, v);
     const bool live = lane < ns;
+    // XCD-local merge: every split record of the row must come from this
+    // XCD (the dispatch rule); one from another XCD -- or a stale one a
+    // split left in another L2 -- means this merge may have read stale
+    // records, and raises the handle's watch flag for the host
+    if (xcd_local) {
+        const uint32_t me = xcc_id();
+        bool other = false;
+#pragma unroll
+        for (int i = 0; i < NH; i++) other |= live && hx[i] != me;
+        if (__builtin_amdgcn_ballot_w64(other) != 0 && lane == 0)
+            __hip_atomic_fetch_or(a.xcd_watch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const bool one_row = ns <= 16;  // the live lanes sit in the first 16: row reductions suffice
 #pragma unroll
     for (int i = 0; i < NH; i++) {
@@ -1905,14 +1961,14 @@ __device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs,
             L = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(row_sum16(live ? f * h[i].y : 0.f))));
             mn = row_min16(mn);
             row_argmax16(mx, arg);
-            merge_values<D, NH, KV>(a, v[i], f, M, L, mn, mx, arg, nk, u, c, lane, o0 + i * step);
+            merge_values<D, NH, KV, EXT>(a, v[i], f, M, L, mn, mx, arg, nk, u, c, lane, o0 + i * step);
         } else {
             M = wave_max_dpp(ms);
             const float f = ms == -INFINITY ? 0.f : __expf(ms - M);
             L = wave_sum_dpp(live ? f * h[i].y : 0.f);
             mn = wave_min_dpp(mn);
             wave_argmax_dpp(mx, arg);
-            merge_values<D, NH, KV>(a, v[i], f, M, L, mn, mx, arg, nk, u, c, lane, o0 + i * step);
+            merge_values<D, NH, KV, EXT>(a, v[i], f, M, L, mn, mx, arg, nk, u, c, lane, o0 + i * step);
         }
     }
 }
@@ -1930,11 +1986,7 @@ __device__ inline void merge_heads(const AttnArgs& a, __amdgpu_buffer_rsrc_t rs,
 // split reads the records with sc0 loads (past its L1).  Otherwise (and for
 // launches with one split) the merge is coherent across XCDs (sc1 and
 // agent scope), as described at the merged-record publish.
-__device__ inline uint32_t xcc_id() {
-    uint32_t x;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-    return x & 0xF;
-}
+
 // One workgroup's arrival at its row; true for the row's last split.
 __device__ inline bool arrive_last(const AttnArgs& a, int row, bool xcd_local) {
     const int prev = xcd_local ? __hip_atomic_fetch_add(a.arrive + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
@@ -1950,10 +2002,11 @@ __device__ inline void rearm(const AttnArgs& a, int row, bool xcd_local) {
 // The last split of a row merges every split's record: wave w of the WPG
 // takes heads w, w + WPG, ... (two at a time where their loads fit the
 // registers).
-template <int D, int WPG = kWavesPerGroup>
+template <int D, int WPG = kWavesPerGroup, bool EXT = false>
 __device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src, int ns, int ng, int b, int head0,
-                                             bool xcd_local = false) {
+                                             bool xcd_local, int row) {
     constexpr int RS = kHdr + D;
+    (void)row;
     constexpr int SUB = kWave / (D / 4);
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = (int)threadIdx.x % kWave;
     const __amdgpu_buffer_rsrc_t rs =
@@ -1963,10 +2016,10 @@ __device__ inline void merge_finalize_direct(const AttnArgs& a, const float* src
     const int64_t o0 = (int64_t)b * a.Hq + head0 + wave;
     int j = 0;
     if (hw >= 2 && nk <= kMaxSplits / SUB / 2) {
-        merge_heads<D, 2>(a, rs, ns, ng, wave, WPG, lane, o0, xcd_local);
+        merge_heads<D, 2, EXT>(a, rs, ns, ng, wave, WPG, lane, o0, xcd_local);
         j = 2;
     }
-    for (; j < hw; j++) merge_heads<D, 1>(a, rs, ns, ng, wave + j * WPG, WPG, lane, o0 + j * WPG, xcd_local);
+    for (; j < hw; j++) merge_heads<D, 1, EXT>(a, rs, ns, ng, wave + j * WPG, WPG, lane, o0 + j * WPG, xcd_local);
 }
 
 // Unit u of one wave's stream: the wave's far tiles first (far tile
@@ -2125,7 +2178,12 @@ __device__ inline void tq_rotate_query(const AttnArgs& a, const TqRotation<D>& r
 // gfx950's direct global->LDS loads: the next unit's bytes stream in while
 // the current one is computed.  The ring takes most of the CU's LDS (one
 // workgroup per CU).
-template <int D, int NQ, int FMT>
+// EXT: the kernel of handles that use an extension beyond the reference --
+// per-head-scaled fp8 keys (a.kscale) or top-K spike tokens (a.tmax,
+// a.thr) -- both chosen at run time; without EXT neither exists and the
+// reference's path keeps its registers (the extensions' pointers and the
+// second far-tile body raised the register pressure of every kernel).
+template <int D, int NQ, int FMT, bool EXT = false>
 __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnArgs a) {
     constexpr int WPG = attn_waves(D, NQ, FMT);  // waves of the workgroup
     constexpr int NS = D / 4;   // 4-dim k-steps of QK
@@ -2179,6 +2237,13 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
     const int head0 = kvh * a.G + hgrp * a.hpg;
     const int ng = min(a.hpg, a.G - hgrp * a.hpg);
+    FKV_STAMP_AT(threadIdx.x == 0, 0);
+#ifdef FKV_PHASE_STAMPS
+    if (threadIdx.x == 0) {
+        const int wg_ = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        if (wg_ < kStampWGs) a.stamps[kStampSlots * wg_ + kStampSlots - 1] = xcc_id();
+    }
+#endif
     // the wave index is wave-uniform: scalar registers, scalar branches
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = threadIdx.x % kWave;
     const int j = lane & 3, blk = lane >> 2;
@@ -2269,9 +2334,11 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     // far keys' score factor: 1/sqrt(D) times the row's fp8 key scale (1
     // unless the handle holds per-head-scaled keys: the scale folds into the
     // score instead of the keys, so the far tile's arithmetic is unchanged)
-    const float far_scale =
-        TQ || !a.kscale ? a.inv_sqrt_d : a.inv_sqrt_d * *(const FKV_CONST float*)(uintptr_t)(a.kscale + bkv);
-    const SpikeTiles spk{a.tmax ? a.tmax + ((int64_t)b * a.Hq + head0) * a.tmax_stride : nullptr, a.tmax_stride, ng};
+    const float far_scale = !EXT || TQ || !a.kscale
+                                ? a.inv_sqrt_d
+                                : a.inv_sqrt_d * *(const FKV_CONST float*)(uintptr_t)(a.kscale + bkv);
+    const SpikeTiles spk{EXT && a.tmax ? a.tmax + ((int64_t)b * a.Hq + head0) * a.tmax_stride : nullptr,
+                         a.tmax_stride, ng};
     const int nd_raw = a.n_dec_dev ? *(const FKV_CONST int32_t*)(uintptr_t)a.n_dec_dev : a.n_dec;
     float asum[NQ];
 #pragma unroll
@@ -2352,6 +2419,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         qkx = qkop;
     }
 
+    FKV_STAMP_AT(threadIdx.x == 0, 1);
     // ---- the stream: unit u is computed while unit u + 1 streams in ----
     fkv_f4 sacc[NQ];  // near scores, carried from a K unit to its V unit
 #pragma unroll
@@ -2377,12 +2445,12 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
             } else if constexpr (G32) {
                 FarTileG<D> r;
                 lds_g32(r, slot, lane);
-                if (spk.p) g32_far_compute<D, NQ, true>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
+                if (EXT && spk.p) g32_far_compute<D, NQ, true>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
                 else g32_far_compute<D, NQ, false>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
             } else {
                 FarTile<D> r;
                 lds_far(r, slot, lane);
-                if (spk.p) far_compute<D, NQ, true>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
+                if (EXT && spk.p) far_compute<D, NQ, true>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
                 else far_compute<D, NQ, false>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
             }
         } else if (kd == kNearK) {
@@ -2412,6 +2480,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         else dec_tile<D, NQ>(st, a, n_dec, bkv, d, lane, qx, ring);
     }
 
+    FKV_STAMP_AT(lane == 0, 2 + wave);
     // ---- per-head reduction over the 16 lanes (lane % 4 == head) ----
     // Rows of 2..4 splits: every wave publishes its own record (record
     // split * 4 + wave) straight from registers and the last workgroup merges
@@ -2457,12 +2526,14 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         if (own_rec) {
             if (lane < 4 && h < ng) {
                 const fkv_v4u hv = __builtin_bit_cast(fkv_v4u, fkv_f4{hdr[0], hdr[1], hdr[2], hdr[3]});
+                // header words 4, 5: the argmax and this workgroup's XCD
+                const fkv_v2u ax = fkv_v2u{(uint32_t)arg, xcc_id()};
                 if (xcd_local) {
                     __builtin_amdgcn_raw_buffer_store_b128(hv, wrec, h * RS * 4, 0, kCpolSc0);
-                    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)arg, wrec, h * RS * 4 + 16, 0, kCpolSc0);
+                    __builtin_amdgcn_raw_buffer_store_b64(ax, wrec, h * RS * 4 + 16, 0, kCpolSc0);
                 } else {
                     __builtin_amdgcn_raw_buffer_store_b128(hv, wrec, h * RS * 4, 0, kCpolSc1);
-                    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)arg, wrec, h * RS * 4 + 16, 0, kCpolSc1);
+                    __builtin_amdgcn_raw_buffer_store_b64(ax, wrec, h * RS * 4 + 16, 0, kCpolSc1);
                 }
             }
         } else if (lane < 4 && h < ng) {
@@ -2494,11 +2565,18 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
         // (the ordering argument of the merged-record path below)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        FKV_STAMP_AT(threadIdx.x == 0, 20);
         if (threadIdx.x == 0) s_last = arrive_last(a, row, xcd_local);
         __syncthreads();
+        FKV_STAMP_AT(threadIdx.x == 0, 21);
         if (!s_last) return;
-        merge_finalize_direct<D, WPG>(a, part, a.num_splits * WPG, ng, b, head0, xcd_local);
+        merge_finalize_direct<D, WPG, EXT>(a, part, a.num_splits * WPG, ng, b, head0, xcd_local, row);
         if (threadIdx.x == 0) rearm(a, row, xcd_local);
+#ifdef FKV_PHASE_STAMPS
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+#endif
+        FKV_STAMP_AT(threadIdx.x == 0, 22);
         return;
     }
     __syncthreads();
@@ -2561,13 +2639,14 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
                 smem[h * RS + 2] = mn2;
                 smem[h * RS + 3] = mx2;
                 smem[h * RS + 4] = __int_as_float(arg2);
+                smem[h * RS + 5] = __uint_as_float(xcc_id());  // the writer's XCD (merge check)
             }
         }
     }
     __syncthreads();
 
     if (a.num_splits == 1) {
-        finalize_rows<D>(a, smem, b, head0, ng);
+        finalize_rows<D, EXT>(a, smem, b, head0, ng);
         return;
     }
     // ---- split-K: publish this split's record ----
@@ -2595,20 +2674,28 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    FKV_STAMP_AT(threadIdx.x == 0, 20);
     if (threadIdx.x == 0) s_last = arrive_last(a, row, xcd_local);
     __syncthreads();
+    FKV_STAMP_AT(threadIdx.x == 0, 21);
     if (!s_last) return;
     // every record (this split's included) is in global memory (the row's
     // L2) now
-    merge_finalize_direct<D, WPG>(a, part, a.num_splits, ng, b, head0, xcd_local);
+    merge_finalize_direct<D, WPG, EXT>(a, part, a.num_splits, ng, b, head0, xcd_local, row);
     if (threadIdx.x == 0) rearm(a, row, xcd_local);
+#ifdef FKV_PHASE_STAMPS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#endif
+    FKV_STAMP_AT(threadIdx.x == 0, 22);
 }
 
 typedef void (*AttnKernel)(AttnArgs);
 
 // The fp8 and group-32 attention kernels (fmt 0, 2) of rows of one head
-// quad (fkv_attn_q1.hip) and of nq = 2..4 quads (fkv_attn_qn.hip).
-AttnKernel attn_kernel_one_quad(int D, int fmt);
-AttnKernel attn_kernel_quads(int D, int fmt, int nq);
+// quad (fkv_attn_q1.hip; EXT: fkv_attn_q1x.hip) and of nq = 2..4 quads
+// (fkv_attn_qn.hip, fkv_attn_qnx.hip).
+AttnKernel attn_kernel_one_quad(int D, int fmt, bool ext);
+AttnKernel attn_kernel_quads(int D, int fmt, int nq, bool ext);
 
 }  // namespace fkv

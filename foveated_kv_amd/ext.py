@@ -372,6 +372,16 @@ class FoveatedHandle:
         check(self._lib.fkv_attn_dispatch_info(self._h, ctypes.byref(mod)), "fkv_attn_dispatch_info")
         return mod.value
 
+    def dispatch_check(self):
+        """Violations of the XCD dispatch rule since the last check (0: every
+        XCD-local merge ran within one XCD); any violation switches the
+        handle to the merge through memory.  Synchronises the current stream."""
+        v = _lib.I32(0)
+        with torch.cuda.device(self.device):
+            check(self._lib.fkv_attn_dispatch_check(self._h, ctypes.byref(v), _lib.stream_ptr(self.device)),
+                  "fkv_attn_dispatch_check")
+        return v.value
+
     def read_near_valid(self):
         """Current per-KV-head near_valid of the blob (host list)."""
         buf = (ctypes.c_uint32 * self.H_kv)()

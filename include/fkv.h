@@ -242,26 +242,33 @@ int fkv_attn_call_strided(fkv_attn* h, const void* query, int32_t q_dtype, int32
  * call's split records, arrival counters and fp16 query copy live in one
  * fixed 8 MiB device array per GPU instead of the handle's workspace, so
  * neither this call nor its first use allocates or frees anything.  Calls
- * whose launch plan needs more than the array holds (arrival counters for
- * at most 16384 rows, then the query copy and B*Hkv*(G rows)*splits*(8+D)
- * floats of records; C3 at batch 8 needs 0.6 MiB, C5 1.2 MiB) return
- * FKV_EINVAL, as does a call whose handle's device is not current.  Every
- * call on one GPU shares that GPU's array: calls that overlap on one GPU
- * (two streams, two threads) race and must be ordered by the caller. */
+ * whose launch plan needs more than the array holds (64 KiB of arrival
+ * counters for at most 16384 rows, then the fp16 query copy, then rows x
+ * splits x records per split x heads per row x (8 + D) floats of split
+ * records, fkv_attn_plan out[1] x out[2] x out[7] x min(out[0], G); C3 at
+ * batch 8 needs 2.25 MiB: 64 rows x 4 splits x 4 wave records x 4 heads x
+ * 136 floats, C5 1.14 MiB) return FKV_EINVAL, as does a call whose handle's
+ * device is not current, or, with spike_k > 1, a handle whose top-K
+ * selection buffers do not exist yet (fkv_attn_set_spike_k).  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, two threads) race and must be ordered by the caller. */
 int fkv_attn_call_noalloc(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq, const void* decode_k,
                           const void* decode_v, int32_t n_decode, void* out, int32_t* spike_flags,
                           int32_t* spike_tokens, void* stream);
 
 /* The launch plan of one call (host only, no GPU; no counterpart in the
  * reference, whose split sizing is foveated_attn.cpp:26-38): for a handle of
- * shape (B, Hkv, D, Na, F) called with Hq query heads and n_decode decode
- * rows, aiming at target_wgs workgroups, writes out[0] query heads per
+ * shape (B, Hkv, D, Na, F) and far format fmt (0: fp8 K / per-token V, 1:
+ * TurboQuant, 2: fp8 K / group-32 V) called with Hq query heads and n_decode
+ * decode rows, aiming at target_wgs workgroups, writes out[0] query heads per
  * workgroup row, out[1] rows, out[2] splits per row, out[3] split-partial
  * floats the call uses, out[4] floats the handle's workspace holds, out[5]
- * arrival counters it holds.  An introspection hook: tests check that no
- * decode length needs more workspace than the first call allocates. */
+ * arrival counters it holds, out[6] waves per workgroup, out[7] split records
+ * per split (one per wave, or 1 when a split merges its waves in LDS).  An
+ * introspection hook: tests check that no decode length needs more
+ * workspace than the first call allocates. */
 int fkv_attn_plan(int32_t B, int32_t Hkv, int32_t D, int32_t Na, int32_t F, int32_t Hq, int32_t n_decode,
-                  int32_t target_wgs, int64_t* out);
+                  int32_t target_wgs, int32_t fmt, int64_t* out);
 
 /* The attention kernel's far-tile plan for one row (host only, no GPU): wave
  * w of n_waves streams far tiles f0[w] + u * fs[w], u < nf[w].  near_weight
@@ -281,6 +288,37 @@ int fkv_far_plan(int32_t n_waves, int32_t near_plan, int32_t nt_far, int64_t nea
  * L2; 0 when the rule did not hold or the handle was created with
  * FKV_XCD_LOCAL=0 (the merge then goes through memory).  Host only. */
 int fkv_attn_dispatch_info(const fkv_attn* h, int32_t* xcd_mod);
+
+/* Checks the dispatches since the last check against that rule (no
+ * counterpart in the reference): every split record carries the XCD that
+ * wrote it, and an XCD-local merge raises the handle's watch flag when a
+ * record of its row came from another XCD (or is a stale one another XCD
+ * left behind).  Synchronises `stream`, then reads the handle's flag and
+ * arrival counters and those of the device's no-alloc scratch:
+ * *violations = flags raised plus counters left nonzero (a broken pattern
+ * can also split a row's arrival count across L2s, so that no workgroup
+ * merges the row or re-arms its counter).  Any violation switches the
+ * handle to the merge through memory (fkv_attn_dispatch_info then reports
+ * 0) and clears the counters; the outputs of the violating dispatches may
+ * be stale. */
+int fkv_attn_dispatch_check(fkv_attn* h, int32_t* violations, void* stream);
+
+/* Host-only helpers of the two checks above, for tests: fkv_xcd_rule_fit
+ * sets *xcd_mod = X and *offset = c when xcc[i] = lo + (c + i) mod X for
+ * every i < n (lo the smallest id, X the id span), else 0 and 0;
+ * fkv_xcd_watch_violations returns the violations an array [flag, arrival
+ * counter of rows 0 .. rows-1] holds (a raised flag, counters not zero). */
+int fkv_xcd_rule_fit(const uint32_t* xcc, int32_t n, int32_t* xcd_mod, int32_t* offset);
+int32_t fkv_xcd_watch_violations(const uint32_t* words, int32_t rows);
+
+/* Per-workgroup phase timestamps of the attention kernels (no counterpart in
+ * the reference; a measurement hook): only a library built with
+ * -DFKV_PHASE_STAMPS records them (make STAMPS=1), any other returns
+ * FKV_EINVAL.  Copies the first n_wgs workgroups' 64 slots (100 MHz clock
+ * values; slot 63 = the workgroup's XCD; the slots are listed in
+ * fkv_attn_kernel.h) of the last launches to out, then zeroes them when
+ * clear is set.  Synchronous. */
+int fkv_phase_stamps(uint64_t* out, int32_t n_wgs, int32_t clear);
 
 /* fkv_attn_call with the decode-buffer length in device memory, for callers
  * that capture decode steps in a HIP graph (no counterpart in the

@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -157,29 +158,72 @@ def test_far_plan_balances_c3_16k():
         _lib.check(lib.fkv_far_plan(0, 1, 1, NB, FB, 0, None, None, None), "fkv_far_plan")
 
 
+@pytest.mark.parametrize("fmt", [0, 1, 2])
 @pytest.mark.parametrize("B,Hkv,D,S,Hq", [
     (8, 8, 128, 16384, 32), (8, 8, 128, 32768, 32), (1, 8, 128, 65536, 64), (1, 2, 64, 512, 14),
     (1, 8, 128, 4096, 32), (1, 2, 64, 600, 12), (4, 2, 128, 4096, 40), (1, 4, 128, 40, 24), (3, 4, 64, 333, 12),
-    (1, 1, 64, 100, 1), (2, 2, 128, 9000, 96),
+    (1, 1, 64, 100, 1), (2, 2, 128, 9000, 96), (4, 8, 128, 8192, 32),
 ])
-def test_launch_plan_never_outgrows_the_first_call_workspace(orc, B, Hkv, D, S, Hq):
+def test_launch_plan_never_outgrows_the_first_call_workspace(orc, B, Hkv, D, S, Hq, fmt):
     """A handle's workspace is allocated once, by its first call, and never
     re-allocated (a captured HIP graph keeps its pointers): every decode
-    length and split target must plan within it."""
+    length and split target must plan within it, for every far format
+    (TurboQuant rows of one head quad at D = 128 run 8 waves, so up to 32
+    wave records per row)."""
     from foveated_kv_amd import _lib
 
     lib = _lib.load()
     tb = orc.tier_boundaries(S)
     Na, F = tb["N_near_padded"], tb["far_count"]
-    out = (ctypes.c_int64 * 6)()
-    worst = 0
+    out = (ctypes.c_int64 * 8)()
+    worst, eight = 0, False
     for n_dec in list(range(0, 130)) + [255, 256, 257, 1000, 4096, 70000]:
         for target in (1, 64, 256, 1024, 4096):
-            assert lib.fkv_attn_plan(B, Hkv, D, Na, F, Hq, n_dec, target, out) == _lib.FKV_OK
-            hpg, rows, splits, need, have, rows_have = list(out)
+            assert lib.fkv_attn_plan(B, Hkv, D, Na, F, Hq, n_dec, target, fmt, out) == _lib.FKV_OK
+            hpg, rows, splits, need, have, rows_have, waves, recs = list(out)
             assert hpg in (4, 16) and 1 <= splits <= 64
+            assert waves == (8 if fmt == 1 and D == 128 and min(hpg, Hq // Hkv) <= 4 else 4)
+            assert recs in (1, waves) and splits * recs <= 64  # the merge reads at most kMaxSplits records
             assert rows <= rows_have, (n_dec, target, rows, rows_have)
             assert need <= have, (n_dec, target, need, have)
             worst = max(worst, need)
+            eight |= waves == 8 and recs == 8
     assert worst > 0 or Na + F < 2 * 64 * 4
-    assert lib.fkv_attn_plan(B, Hkv, D, Na, F, Hq + 1 if Hkv > 1 else 0, 0, 256, out) == _lib.FKV_EINVAL
+    if fmt == 1 and D == 128 and Hq // Hkv <= 4 and Na + F > 8 * 64 * 16:
+        assert eight  # some plan keeps 8 wave records per split (32 per row)
+    assert lib.fkv_attn_plan(B, Hkv, D, Na, F, Hq + 1 if Hkv > 1 else 0, 0, 256, fmt, out) == _lib.FKV_EINVAL
+    assert lib.fkv_attn_plan(B, Hkv, D, Na, F, Hq, 0, 256, 3, out) == _lib.FKV_EINVAL
+
+
+def test_xcd_rule_fit_and_watch_words():
+    """The host logic of the XCD-local merge's two checks: the dispatch rule
+    fitted to a probe's XCD ids (workgroup i on lo + (c + i) mod X), and the
+    violations a watch-word array holds."""
+    from foveated_kv_amd import _lib
+
+    lib = _lib.load()
+
+    def fit(ids):
+        a = np.ascontiguousarray(ids, np.uint32)
+        X, c = _lib.I32(-1), _lib.I32(-1)
+        assert lib.fkv_xcd_rule_fit(a.ctypes.data_as(ctypes.c_void_p), a.size, ctypes.byref(X), ctypes.byref(c)) == 0
+        return X.value, c.value
+
+    n = 4096
+    assert fit([(7 + i) % 8 for i in range(n)]) == (8, 7)
+    assert fit([(i % 8) for i in range(n)]) == (8, 0)
+    assert fit([2 + (3 + i) % 4 for i in range(n)]) == (4, 3)   # ids 2..5
+    assert fit([5] * n) == (1, 0)
+    broken = [(7 + i) % 8 for i in range(n)]
+    broken[1000], broken[1001] = broken[1001], broken[1000]
+    assert fit(broken) == (0, 0)
+    assert fit([(i // 2) % 8 for i in range(n)]) == (0, 0)      # pairs per XCD: not round-robin
+
+    def viol(words):
+        a = np.ascontiguousarray(words, np.uint32)
+        return lib.fkv_xcd_watch_violations(a.ctypes.data_as(ctypes.c_void_p), a.size - 1)
+
+    assert viol([0] * 65) == 0
+    assert viol([1] + [0] * 64) == 1                 # a merge saw another XCD's record
+    assert viol([0, 0, 3, 0, 1]) == 2                # counters no merge re-armed
+    assert viol([1, 2]) == 2

@@ -6,6 +6,7 @@ reference dequant+SDPA formulation); spike flags/tokens equal except where
 the oracle itself shows a near tie.
 """
 
+import ctypes
 import os
 
 import numpy as np
@@ -125,8 +126,8 @@ def test_compress_exhaustive_fp16_patterns(fkv, orc):
     dict(B=1, Hq=32, Hkv=8, D=128, S=4096, n_dec=64, seed=2, heavy_tail=True),  # config 2
     dict(B=1, Hq=4, Hkv=4, D=64, S=256, n_dec=0, seed=3),        # no GQA
     dict(B=2, Hq=8, Hkv=2, D=128, S=512, n_dec=7, seed=4),
-    dict(B=1, Hq=64, Hkv=8, D=128, S=2048, n_dec=3, seed=5),     # G = 8
-    dict(B=1, Hq=32, Hkv=2, D=64, S=700, n_dec=5, seed=6),       # G = 16: two head groups
+    dict(B=1, Hq=64, Hkv=8, D=128, S=2048, n_dec=3, seed=5),     # G = 8, small grid: rows of 4 heads
+    dict(B=1, Hq=32, Hkv=2, D=64, S=700, n_dec=5, seed=6),       # G = 16, small grid: four rows of 4 heads
     dict(B=1, Hq=6, Hkv=2, D=128, S=36, n_dec=2, seed=7),        # no far tier
     dict(B=1, Hq=8, Hkv=2, D=64, S=40, n_dec=0, seed=8),         # 4 far tokens
     dict(B=3, Hq=12, Hkv=4, D=64, S=333, n_dec=70, seed=9),      # ragged tiles
@@ -139,6 +140,33 @@ def test_compress_exhaustive_fp16_patterns(fkv, orc):
 ])
 def test_attention_parity(fkv, orc, args):
     run_attention(fkv, orc, **args)
+
+
+# Rows of 16-head workgroups whose last head quad is only partly filled
+# (fkv_attn_plan gives 16 heads per row for each): G = 7 and 5 fill two
+# quads with 3 and 1 heads in the second, G = 14 four quads with 2 in the
+# last -- common model shapes (Hq 28 / Hkv 4, Hq 40 / Hkv 8, Hq 56 / Hkv 4).
+PARTIAL = [
+    dict(B=1, Hq=28, Hkv=4, D=128, S=32768, n_dec=5, seed=51),   # G = 7, 64 splits
+    dict(B=8, Hq=28, Hkv=4, D=128, S=8192, n_dec=0, seed=52, spikes=0.02),  # G = 7, 8 splits
+    dict(B=1, Hq=40, Hkv=8, D=128, S=32768, n_dec=3, seed=53),   # G = 5
+    dict(B=1, Hq=56, Hkv=4, D=128, S=16384, n_dec=2, seed=54),   # G = 14: four quads
+    dict(B=2, Hq=28, Hkv=4, D=64, S=8192, n_dec=0, seed=55),     # G = 7 at D = 64
+]
+
+
+@pytest.mark.parametrize("vg", [0, 32])
+@pytest.mark.parametrize("args", PARTIAL, ids=[f"B{a['B']}_Hq{a['Hq']}_Hkv{a['Hkv']}_D{a['D']}_S{a['S']}"
+                                               for a in PARTIAL])
+def test_attention_partial_quad_rows(fkv, orc, args, vg):
+    from foveated_kv_amd import _lib
+
+    out = (ctypes.c_int64 * 8)()
+    tb = orc.tier_boundaries(args["S"], promo_headroom_min=8)
+    assert _lib.load().fkv_attn_plan(args["B"], args["Hkv"], args["D"], tb["N_near_padded"], tb["far_count"],
+                                     args["Hq"], args["n_dec"], 256, 2 if vg else 0, out) == 0
+    assert out[0] == 16 and (args["Hq"] // args["Hkv"]) % 4 != 0  # 16-head rows, last quad partial
+    run_attention(fkv, orc, v_group=vg, **args)
 
 
 GROUP32 = [
@@ -305,6 +333,9 @@ def test_fused_split_merge_back_to_back(fkv, orc, B, Hq, Hkv, D, S, n_dec, vg):
     for a, b in zip(first, ref_mem):
         assert torch.equal(a, b)
     assert h.dispatch_info() > 0, "the workgroup -> XCD dispatch rule did not hold on this device"
+    # every one of the 200 dispatches kept each row on one XCD (the watch
+    # words the merging workgroups check and clear)
+    assert h.dispatch_check() == 0 and h.dispatch_info() > 0
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,S,n_dec", [(8, 32, 8, 128, 8192, 0), (4, 32, 8, 64, 4096, 5)])
@@ -344,3 +375,4 @@ def test_xcd_local_merge_across_concurrent_streams(fkv, orc, B, Hq, Hkv, D, S, n
     for o in outs:
         for a, b in zip(o, ref):
             assert torch.equal(a, b)
+    assert [h.dispatch_check() for h in hs] == [0, 0, 0]

@@ -86,6 +86,7 @@ CASES = [
     (2, 4, 4, 64, 129, 64, (64, 10, 0, 33), 3),
     (1, 8, 2, 128, 0, 64, (40, 64), 2),
     (2, 24, 2, 128, 8000, 896, (800, 750), 4),  # G = 12: rows of three head quads
+    (1, 28, 4, 128, 9000, 1000, (900, 850, 1000, 700), 3),  # G = 7: 16-head rows, second quad partial
 ]
 
 

@@ -3,8 +3,10 @@ workspace is a fixed device array per GPU), through the C ABI, against
 fkv_attn_call on the same handles -- same kernels, same launch plan, so the
 outputs must be the same bits -- and against the CPU oracle within the
 parity tolerance.  Two calls in a row, the second with a smaller input
-(another shape, a bf16 query), then the first again; a call whose plan
-does not fit the array is refused before any GPU work."""
+(another shape, a bf16 query), then the first again; the first call on a
+fresh handle leaves the device's free memory unchanged; a call whose plan
+does not fit the array (too many rows, or rows whose split records exceed
+it) is refused before any GPU work."""
 
 import ctypes
 
@@ -78,6 +80,61 @@ def test_noalloc_matches_allocating_call(orc):
     again = _check(orc, *big, torch.float16, "call 3 (call 1 again)")
     for x, y in zip(first, again):
         assert torch.equal(x, y)
+
+
+def test_noalloc_first_call_on_a_fresh_handle_allocates_nothing(orc):
+    """fkv_attn_call would size a ~35 MB split workspace on this handle's
+    first call; the no-alloc entry point must leave the device's free memory
+    as it was (the kernels and the scratch array are loaded by a call on
+    another handle first)."""
+    flush("no-alloc fresh handle: B=4 Hq=32 Hkv=8 D=128 S=8192")
+    warm = _case(1, 14, 2, 64, 512, 16, seed=503)
+    _check(orc, *warm, torch.float16, "warm-up call (another handle)")
+    h, q, dk, dv, c = _case(4, 32, 8, 128, 8192, 0, seed=504)
+    qt = torch.from_numpy(q).cuda()
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    got = _call("fkv_attn_call_noalloc", h, qt, None, None)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 == free0, f"free device memory changed by {free0 - free1} bytes"
+    ko = orc.attend_kernel(q, c["near_k"], c["near_v"], c["near_valid"], c["far_k"], c["far_v"],
+                           c["far_v_scale"], c["far_v_zero"], spike_margin=10.0)[0]
+    out = np_(got[0]).astype(np.float64)
+    assert float(np.abs(out - ko).max()) <= ATOL and orc.cosine(out, ko) >= COS
+
+
+def test_noalloc_refuses_records_beyond_its_scratch():
+    """Rows that fit the counter region (128) but whose split records do
+    not fit the array: B=64 x 2 KV heads of 16-head rows, 2 splits x 4 wave
+    records x 16 heads x 136 floats = 8.5 MiB of records (9.06 MiB with the
+    counters and the query copy, fkv_attn_plan): refused before any GPU
+    work."""
+    from foveated_kv_amd import _lib, ext
+
+    B, Hkv, Hq, D, S = 64, 2, 32, 128, 1024
+    cfg = tier_config()
+    tb = ext.tier_boundaries_c(cfg, S)
+    lib = _lib.load()
+    plan = (ctypes.c_int64 * 8)()
+    assert lib.fkv_attn_plan(B, Hkv, D, tb["N_near_padded"], tb["far_count"], Hq, 0, 256, 0, plan) == 0
+    assert plan[0] == 16 and plan[1] == 128 and plan[2] == 2
+    qbytes = (B * Hq * D * 2 + 255) // 256 * 256
+    assert 65536 + qbytes + plan[3] * 4 > 8 << 20 and plan[1] * 4 <= 65536
+    nk = torch.zeros((B, Hkv, tb["N_near_padded"], D), dtype=torch.float16, device="cuda")
+    F = tb["far_count"]
+    fk = torch.zeros((B, Hkv, F, D), dtype=torch.uint8, device="cuda")
+    fv = torch.zeros((B, Hkv, F, D // 2), dtype=torch.uint8, device="cuda")
+    sc = torch.ones((B, Hkv, F), dtype=torch.float16, device="cuda")
+    h = ext.FoveatedHandle(nk, nk, fk, fv, sc, sc, torch.full((Hkv,), tb["R_actual"], dtype=torch.int32,
+                                                              device="cuda"))
+    q = torch.zeros((B, Hq, D), dtype=torch.float16, device="cuda")
+    out = torch.empty((B, Hq, D), dtype=torch.float16, device="cuda")
+    fl = torch.empty((B, Hq), dtype=torch.int32, device="cuda")
+    rc = lib.fkv_attn_call_noalloc(h._h, _lib.ptr(q), _lib.FKV_F16, Hq, None, None, 0, _lib.ptr(out), _lib.ptr(fl),
+                                   _lib.ptr(fl), _lib.stream_ptr())
+    assert rc == _lib.FKV_EINVAL
+    assert b"no-alloc entry point holds" in lib.fkv_last_error()
 
 
 def test_noalloc_refuses_a_plan_beyond_its_scratch():
