@@ -74,18 +74,54 @@ def check_spikes(orc, far_k, q16, flags, tokens, kf, kt, mf, mn, margin):
     return ties
 
 
+def plant_sharp(k, v, q, dk, dv, tb, scores=(30.0, 30.4, 30.9), vmul=8.0, far_vmul=8.0):
+    """A sharp softmax with large values: for every query head, one near
+    token (in the recent window), one far token and one decode token get
+    keys along that head's query with scores ``scores`` (near, far, decode;
+    the far key's fp8 encoding moves its score a little), and their value
+    rows are multiplied by ``vmul`` (the far row by ``far_vmul``).  Nearly
+    all of each head's weight then sits on three tokens, two of them below
+    the maximum: the case where rounding the P.V weights matters most."""
+    B, Hkv, S, D = k.shape
+    G = q.shape[1] // Hkv
+    for b in range(B):
+        for h in range(Hkv):
+            for j in range(G):
+                qq = q[b, h * G + j].astype(np.float64)
+                u = qq * np.sqrt(D) / (qq @ qq)  # q.(s u) / sqrt(D) = s
+                rows = [(k, v, S - 1 - j, scores[0], vmul), (k, v, tb["mid_start"] + 3 + 5 * j, scores[1], far_vmul)]
+                if dk is not None:
+                    rows.append((dk, dv, j % dk.shape[2], scores[2], vmul))
+                for kk, vv, t, sc, mul in rows:
+                    kk[b, h, t] = (u * sc).astype(np.float16)
+                    vv[b, h, t] = (vv[b, h, t].astype(np.float32) * mul).astype(np.float16)
+
+
 def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16, spikes=0.0,
-                  margin=10.0, near_valid_delta=0, check_formulation=True, heavy_tail=False, v_group=0):
+                  margin=10.0, near_valid_delta=0, check_formulation=True, heavy_tail=False, v_group=0,
+                  sharp=None):
+    """sharp: None, "near" (plant_sharp with the far row's values unscaled)
+    or "all" (every planted row x8).  Sharp cases have outputs near 20,
+    where half an fp16 unit in the last place of the output (the output
+    dtype of the reference and of this kernel) is 3.9e-3 to 7.8e-3, above
+    the 2e-3 bar: their max-abs error is taken beyond that rounding of each
+    element (and the raw max-abs recorded).  With "all" the reference's
+    formulation dequantises the x8 far values in fp16 and leaves the
+    reference kernel's fp32 semantics by more than the bar: the formulation
+    check then allows the two oracles' own difference on top of it (and
+    records it)."""
     from foveated_kv_amd import ext, synthetic
 
     case = (f"B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} seed={seed} q={str(q_dtype).split('.')[-1]} "
-            f"spikes={spikes} nv_delta={near_valid_delta} v_group={v_group}")
+            f"spikes={spikes} nv_delta={near_valid_delta} v_group={v_group}" + (f" sharp={sharp}" if sharp else ""))
     flush("attention " + case)
     k, v = synthetic.make_kv(B, Hkv, S, D, seed, heavy_tail=heavy_tail)
     q = synthetic.make_query(B, Hq, D, seed)
     tb = orc.tier_boundaries(S)
     synthetic.inject_spikes(k, q, tb["mid_start"], tb["far_count"], spikes, seed)
     dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, seed)
+    if sharp:
+        plant_sharp(k, v, q, dk, dv, tb, far_vmul=8.0 if sharp == "all" else 1.0)
     cl = ext.CompressHandle(tier_config(v_group=v_group)).compress_layer(
         torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), with_archive=False)
     nv = cl.near_valid.clone()
@@ -117,6 +153,13 @@ def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16
     cos = orc.cosine(out, ko)
     flush(f"  vs kernel oracle: max-abs {err:.3e} cos {cos:.8f}")
     rec = {"maxabs_kernel": err, "cos_kernel": cos}
+    # half an fp16 ulp of each exact output: the rounding of the fp16 output itself
+    half_ulp = np.spacing(np.abs(ko).astype(np.float16)).astype(np.float64) / 2 if sharp else 0.0
+    if sharp:
+        beyond = (np.abs(out - ko) - half_ulp).max()
+        flush(f"  beyond the fp16 output rounding: {beyond:.3e}")
+        rec.update(beyond_output_rounding=beyond)
+        err = max(beyond, 0.0)
     assert err <= ATOL and cos >= COS
     if check_formulation and near_valid_delta == 0:
         fo = orc.attend_formulation(q16, c["near_k"], c["near_v"], np_(nv), c["far_k"], c["far_v"],
@@ -125,7 +168,14 @@ def run_attention(fkv, orc, B, Hq, Hkv, D, S, n_dec, seed, q_dtype=torch.float16
         cos_f = orc.cosine(out, fo)
         flush(f"  vs formulation:   max-abs {err_f:.3e} cos {cos_f:.8f}")
         rec.update(maxabs_formulation=err_f, cos_formulation=cos_f)
-        assert err_f <= ATOL and cos_f >= COS
+        if sharp:
+            err_f = max((np.abs(out - fo) - half_ulp).max(), 0.0)
+        slack = 0.0
+        if sharp == "all":
+            slack = np.abs(ko - fo).max()
+            flush(f"  kernel oracle vs formulation: max-abs {slack:.3e}")
+            rec.update(oracle_gap=slack)
+        assert err_f <= ATOL + slack and cos_f >= COS
     flags, tokens = np_(flags), np_(tokens)
     ties = check_spikes(orc, c["far_k"], q16, flags, tokens, kf, kt, mf, mn, margin)
     record(case, flagged=int(flags.sum()), spike_ties=ties, **rec)

@@ -142,6 +142,24 @@ def test_attention_parity(fkv, orc, args):
     run_attention(fkv, orc, **args)
 
 
+@pytest.mark.parametrize("sharp", ["near", "all"])
+@pytest.mark.parametrize("args", [dict(B=1, Hq=14, Hkv=2, D=64, S=512, n_dec=16, seed=61),     # C1 shape
+                                  dict(B=1, Hq=32, Hkv=8, D=128, S=4096, n_dec=64, seed=62)],  # C2 shape
+                         ids=["c1", "c2"])
+def test_attention_sharp_softmax_value_outliers(fkv, orc, args, sharp):
+    """Every head's weight on three tokens (near, far, decode) at scores
+    30-31 with value rows x8 (plant_sharp): the P.V weights of such tokens
+    are the large ones, so their rounding to fp16 matrix-core operands shows
+    most here.  The outputs reach ~20, where the fp16 output's own rounding
+    (half an ulp: 3.9e-3 to 7.8e-3) exceeds 2e-3, so the bar applies beyond
+    that rounding (run_attention).  Checked against the kernel restatement,
+    and against the formulation: at the bar when the far row keeps its
+    values ("near"); with the far row x8 too ("all") the formulation's fp16
+    dequantisation of far values alone moves it 5e-3 from the kernel
+    semantics, which the check allows on top of the bar."""
+    run_attention(fkv, orc, sharp=sharp, **args)
+
+
 # Rows of 16-head workgroups whose last head quad is only partly filled
 # (fkv_attn_plan gives 16 heads per row for each): G = 7 and 5 fill two
 # quads with 3 and 1 heads in the second, G = 14 four quads with 2 in the

@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 import torch
 
+from _parity import record
 from oracle import turbo as T
 
 pytestmark = pytest.mark.gpu
@@ -159,11 +160,17 @@ def test_turbo_compress_keys_matches_restatement():
         gi, gs, gn, gg = turbo_compress_keys(_t(k), get_turbo_constants(D))
         gcodes = T.unpack_2bit(gi.cpu().numpy())
         gbits = (T.unpack_1bit(gs.cpu().numpy()) > 0).astype(np.uint8)
-        loose_c = ymarg < 1e-5
+        # a code may differ only where the fp64 rotated coordinate lies within
+        # 1e-6 of a boundary: the fp32 rotation of a unit vector (|y| <= 1,
+        # sum_j |k_j Pi_ij| / |k| <= 1) is off by ~sqrt(D) * 2^-24 << 1e-6
+        loose_c = ymarg < 1e-6
         loose_s = pmarg < 1e-4
         assert np.array_equal(gcodes[~loose_c], codes[~loose_c]), D
         assert np.array_equal(gbits[~loose_s], bits[~loose_s]), D
         assert loose_c.mean() < 5e-3 and loose_s.mean() < 5e-3  # the zero key alone is 1/900 of the codes
+        record(f"TurboQuant key compression D={D} (2x3x150 keys)", codes=int(loose_c.size),
+               loose_codes=int(loose_c.sum()), differing_codes=int((gcodes != codes).sum()),
+               loose_signs=int(loose_s.sum()), differing_signs=int((gbits != bits).sum()))
         n32, g32 = gn.float().cpu().numpy(), gg.float().cpu().numpy()
         assert np.allclose(n32, nrm.astype(np.float32), rtol=1e-3, atol=0)
         assert np.allclose(g32, gam.astype(np.float32), rtol=2e-3, atol=1e-3)
