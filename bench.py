@@ -181,6 +181,9 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c3_7b_16k_b8")
+    ap.add_argument("--context", type=int, default=0,
+                    help="run --config at this context length instead of its own (profiling: the same "
+                         "kernel over another number of tiles)")
     ap.add_argument("--layers", type=int, default=0, help="distinct layer blobs (0: enough for > 1 GB)")
     ap.add_argument("--spikes", type=float, default=0.02)
     ap.add_argument("--e2e", action="store_true",
@@ -255,6 +258,7 @@ def main():
         run_phase_stamps(args, torch, dev)
         return
     B, Hq, Hkv, D, S, n_dec = synthetic.CONFIGS[args.config]
+    S = args.context or S
     cfg = ext.TierConfig()
     cfg.promo_headroom_min = 8
     turbo = args.config.startswith("c4_turbo")
