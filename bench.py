@@ -210,6 +210,9 @@ def main():
     ap.add_argument("--v-group", type=int, default=0, choices=(0, 32),
                     help="fp8 far tier V: INT4 scale/zero per token (0) or per 32-dim group (32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stamps-spike-k", type=int, default=1,
+                    help="--phase-stamps: spike_k of the handle; above 1 the top-K candidates kernel's phases "
+                         "are reported too")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="per-workgroup phase timeline of --config's kernel from the phase-stamp build "
                          "(make -C foveated_kv_amd/csrc STAMPS=1)")
@@ -738,6 +741,8 @@ def run_phase_stamps(args, torch, dev):
     B, Hq, Hkv, D, S, n_dec = __import__("foveated_kv_amd.synthetic", fromlist=["CONFIGS"]).CONFIGS[name]
     make_handle, qt, dkt, dvt, _ = config_handles(torch, dev, ext, name, args.seed, args.spikes)
     h = make_handle()
+    if args.stamps_spike_k > 1:
+        h.set_spike_k(args.stamps_spike_k)
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < SETTLE_MS / 1e3:
         for _ in range(20):
@@ -781,6 +786,28 @@ def run_phase_stamps(args, torch, dev):
         "last_output": round(float(us(merged[:, 22].max() - t_first)), 3) if len(merged) else None,
         "last_stream_end": round(float(us(wave_end.max() - t_first)), 3),
     }
+    if args.stamps_spike_k > 1:
+        # the top-K candidates kernel's workgroups (slots 32..): entry, maxima
+        # staged, cuts known, each wave's candidates done
+        # slots 32 entry, 33 staged, 34 cuts, 35+w wave done, 39+w query operands, 43+w last batch begun
+        sel = np.frombuffer(raw, dtype=np.uint64).reshape(n_wgs, 64).astype(np.int64)[:, 32:47]
+        sel = sel[(sel[:, 0] > 0) & (sel[:, 3] > 0)]
+        if len(sel):
+            t0s = sel[:, 0].min()
+            done = sel[:, 3:7].max(axis=1)
+            out["topk_candidates"] = {
+                "workgroups": int(len(sel)), "spike_k": args.stamps_spike_k,
+                "entry_spread": pq(us(sel[:, 0] - t0s)),
+                "stage_maxima": pq(us(sel[:, 1] - sel[:, 0])),
+                "cut_search": pq(us(sel[:, 2] - sel[:, 1])),
+                "query_operands": pq(us((sel[:, 7:11] - sel[:, 2:3]).ravel())),
+                "deal_and_full_batches": pq(us((sel[:, 11:15] - sel[:, 7:11]).ravel())),
+                "last_batch": pq(us((sel[:, 3:7] - sel[:, 11:15]).ravel())),
+                "rescore_and_append": pq(us(done - sel[:, 2])),
+                "last_done": round(float(us(done.max() - t0s)), 3),
+                "start_after_attention_output": (round(float(us(t0s - merged[:, 22].max())), 3)
+                                                 if len(merged) else None),
+            }
     print(json.dumps(out), flush=True)
 
 

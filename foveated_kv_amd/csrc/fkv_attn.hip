@@ -313,7 +313,27 @@ struct SelectArgs {
     float* cand_s;              // (B*Hq, cap)
     int* cand_t;                // (B*Hq, cap)
     int cap;                    // 64 * K
+#ifdef FKV_PHASE_STAMPS
+    unsigned long long* stamps;  // the attention kernel's stamp array; slots 32.. of each workgroup
+#endif
 };
+
+// Phase stamps of the candidates kernel (the -DFKV_PHASE_STAMPS build):
+// slots 32 entry, 33 tile maxima staged, 34 cuts known, 35 + w wave w done,
+// 39 + w wave w's query operands loaded, 43 + w wave w's last batch begun.
+#ifdef FKV_PHASE_STAMPS
+#define FKV_SEL_STAMP(cond, slot)                                                                            \
+    do {                                                                                                    \
+        if (cond) {                                                                                         \
+            const int wg_ = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;                 \
+            if (wg_ < kStampWGs) a.stamps[kStampSlots * wg_ + 32 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+        }                                                                                                   \
+    } while (0)
+#else
+#define FKV_SEL_STAMP(cond, slot) \
+    do {                          \
+    } while (0)
+#endif
 
 // Workgroups per (batch, KV head, head quad) of the first selection
 // kernel, and the far tiles per head whose maxima a workgroup stages in
@@ -321,6 +341,26 @@ struct SelectArgs {
 constexpr int kSelParts = 8;
 constexpr int kSelStage = 4096;
 constexpr int kSelWaves = 4;
+// Far tiles per head whose maxima the cut search holds in registers (per
+// lane 32; beyond that it reads the staged copy on every step), and the low
+// key bits the register search leaves zero (its cut is then at most 2^-11
+// relative below the exact K-th tile maximum: a few more candidates, the
+// same selection).
+constexpr int kSelRegs = 32;
+constexpr int kCutLowBits = 12;
+
+// Sum of v over the wave, in every lane (DPP row rotations and lane-half
+// swaps, no LDS).
+__device__ inline int wave_sum_i32(int v) {
+    v += (int)row_ror<1>((uint32_t)v);
+    v += (int)row_ror<2>((uint32_t)v);
+    v += (int)row_ror<4>((uint32_t)v);
+    v += (int)row_ror<8>((uint32_t)v);
+    LanePair p = swap16((uint32_t)v);
+    v = (int)p.a + (int)p.b;
+    p = swap32((uint32_t)v);
+    return (int)p.a + (int)p.b;
+}
 
 // fp32 -> uint32 with the same order (no NaN among scores) and back.
 __device__ inline uint32_t fkey(float f) {
@@ -358,6 +398,15 @@ __device__ inline void rescore_tiles(const SelectArgs& a, int64_t bkv, const int
 #pragma unroll
         for (int c = 0; c < D / 16; c++) kc[n][c] = *(const uint4*)(rec + c * 1024 + lane * 16);
     }
+    // one round trip for the batch: every load is issued before the first
+    // use (the compiler would otherwise hoist the first conversions and
+    // MFMAs between the loads and wait for the first ones early); the empty
+    // asm statements tie each value's uses to a point after all loads
+#pragma unroll
+    for (int n = 0; n < N; n++)
+#pragma unroll
+        for (int c = 0; c < D / 16; c++)
+            asm volatile("" : "+v"(kc[n][c].x), "+v"(kc[n][c].y), "+v"(kc[n][c].z), "+v"(kc[n][c].w)::"memory");
     fkv_f4 acc[N];
 #pragma unroll
     for (int n = 0; n < N; n++) acc[n] = fkv_f4{0.f, 0.f, 0.f, 0.f};
@@ -410,6 +459,38 @@ __device__ inline void wave_sort(float& s, int& t, int lane) {
         }
 }
 
+// The cut of one head from its NSL x 64 tile maxima (tm, ntf of them; the
+// wave of the head): the largest key x with its low kCutLowBits bits zero
+// that at least K maxima above th reach (at most the K-th largest), or
+// -inf when at most K maxima clear th.  The maxima are held as keys in
+// registers (0 for those at or below th, or past the far tier: below every
+// trial), all loads in flight, and copied to the LDS row `lds` for the
+// rescoring; counts are per-lane compares and one wave sum, no branches.
+template <int NSL>
+__device__ inline float cut_search(const float* tm, int ntf, float th, int K, int lane, float* lds) {
+    uint32_t kv[NSL];
+#pragma unroll
+    for (int r = 0; r < NSL; r++) {
+        const int t = r * kWave + lane;
+        const float v = t < ntf ? tm[t] : -INFINITY;
+        if (t < ntf) lds[t] = v;
+        kv[r] = v > th ? fkey(v) : 0u;
+    }
+    int n_above = 0;
+#pragma unroll
+    for (int r = 0; r < NSL; r++) n_above += kv[r] != 0u;
+    if (__builtin_amdgcn_readfirstlane(wave_sum_i32(n_above)) <= K) return -INFINITY;
+    uint32_t x = 0;
+    for (int bit = 31; bit >= kCutLowBits; bit--) {
+        const uint32_t trial = x | (1u << bit);
+        int c = 0;
+#pragma unroll
+        for (int r = 0; r < NSL; r++) c += kv[r] >= trial;
+        if (__builtin_amdgcn_readfirstlane(wave_sum_i32(c)) >= K) x = trial;
+    }
+    return unfkey(x);  // x >= the key of -FLT_MAX: a finite cut
+}
+
 // Top-K spike selection, part 1: kSelParts workgroups per (batch, KV head,
 // head quad).  A far token spikes when its score exceeds its head's
 // threshold min_near + margin (the attention kernel's flag rule); each head
@@ -443,6 +524,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     const int64_t o0 = (int64_t)b * a.Hq + (int64_t)kvh * a.G + 4 * quad;  // head 0 of the quad
     const int K = a.K, ntf = a.ntf;
     const bool staged = ntf <= kSelStage;
+    FKV_SEL_STAMP(threadIdx.x == 0, 0);
     if (threadIdx.x < 4) {
         const int jj = threadIdx.x;
         const bool live = 4 * quad + jj < a.G;
@@ -452,8 +534,11 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     }
     __syncthreads();
     if (!(fl_s[0] | fl_s[1] | fl_s[2] | fl_s[3])) return;  // nothing spikes: part 2 writes the outputs
-    // the tile maxima of the quad's flagged heads -> LDS, eight loads in flight per thread
-    if (staged) {
+    // the register path: each flagged head's wave loads its own maxima (and
+    // writes the LDS copy the rescoring reads) in the cut search below
+    const bool regs = ntf <= kWave * kSelRegs;
+    // otherwise the tile maxima of the quad's flagged heads -> LDS, eight loads in flight per thread
+    if (staged && !regs) {
         constexpr int U = 8;
         for (int i0 = threadIdx.x; i0 < 4 * ntf; i0 += U * (int)blockDim.x) {
             float v[U];
@@ -470,28 +555,35 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         }
     }
     __syncthreads();
+    FKV_SEL_STAMP(threadIdx.x == 0, 1);
     auto tmv = [&](int jj, int t) -> float { return staged ? tm_s[jj][t] : a.tmax[(o0 + jj) * ntf + t]; };
     // ---- A: head `wave`'s cut ----
     if (wave < 4 && fl_s[wave]) {
         const float th = thr_s[wave];
-        int above = 0;
-        for (int t = lane; t < ntf; t += kWave) above += tmv(wave, t) > th;
-        for (int o = 32; o >= 1; o >>= 1) above += __shfl_xor(above, o);
         float cut = -INFINITY;
-        if (above > K) {
-            // the largest key x with at least K maxima (above th) at or above it
-            uint32_t x = 0;
-            for (int bit = 31; bit >= 0; bit--) {
-                const uint32_t trial = x | (1u << bit);
-                int c = 0;
-                for (int t = lane; t < ntf; t += kWave) {
-                    const float v = tmv(wave, t);
-                    c += v > th && fkey(v) >= trial;
+        if (regs) {
+            const float* tm = a.tmax + (o0 + wave) * ntf;
+            if (ntf <= 8 * kWave) cut = cut_search<8>(tm, ntf, th, K, lane, tm_s[wave]);
+            else if (ntf <= 16 * kWave) cut = cut_search<16>(tm, ntf, th, K, lane, tm_s[wave]);
+            else cut = cut_search<kSelRegs>(tm, ntf, th, K, lane, tm_s[wave]);
+        } else {
+            int above = 0;
+            for (int t = lane; t < ntf; t += kWave) above += tmv(wave, t) > th;
+            for (int o = 32; o >= 1; o >>= 1) above += __shfl_xor(above, o);
+            if (above > K) {
+                uint32_t x = 0;
+                for (int bit = 31; bit >= 0; bit--) {
+                    const uint32_t trial = x | (1u << bit);
+                    int c = 0;
+                    for (int t = lane; t < ntf; t += kWave) {
+                        const float v = tmv(wave, t);
+                        c += v > th && fkey(v) >= trial;
+                    }
+                    for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o);
+                    if (c >= K) x = trial;
                 }
-                for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o);
-                if (c >= K) x = trial;
+                cut = unfkey(x);
             }
-            cut = unfkey(x);
         }
         if (lane == 0) {
             cut_s[wave] = cut;
@@ -499,6 +591,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         }
     }
     __syncthreads();
+    FKV_SEL_STAMP(threadIdx.x == 0, 2);
     float th[4], ct[4];
     int fl[4];
 #pragma unroll
@@ -510,6 +603,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     fkv_h4 qv[NS];
     load_qv<D>(a, o0, quad, lane, qv);
     const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
+    FKV_SEL_STAMP(lane == 0, 7 + wave);
     // ---- B: this wave's candidate tiles (every kSelParts * kSelWaves-th), NR at a time ----
     const int gw = part * kSelWaves + wave, nw = kSelParts * kSelWaves;
     int r = 0, np = 0;  // candidates seen (the same in every wave of the quad); tiles pending
@@ -522,39 +616,77 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         for (int n = 0; n < NR; n++) tl[n] = n < count ? pend[n] : pend[0];
         float sv[NR][4];
         rescore_tiles<D, NR>(a, bkv, tl, qv, far_scale, lane, sv);
+        // the lane's candidates of the batch
+        uint32_t pm = 0;
 #pragma unroll
         for (int n = 0; n < NR; n++) {
             if (n >= count) break;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int t = tl[n] * kTile + 4 * blk + e;
-                if (fl[j] && t < a.L.F && sv[n][e] > th[j] && sv[n][e] >= ct[j]) {
-                    const int64_t oj = o0 + j;
-                    const int slot = atomicAdd(a.cand_n + oj, 1);
-                    if (slot < a.cap) {
-                        a.cand_s[oj * a.cap + slot] = sv[n][e];
-                        a.cand_t[oj * a.cap + slot] = t;
-                    }
-                }
+                if (fl[j] && t < a.L.F && sv[n][e] > th[j] && sv[n][e] >= ct[j]) pm |= 1u << (4 * n + e);
             }
         }
+        // one atomic per head and batch: a lane's slots follow those of the
+        // lanes of its head (lane % 4 == j) below it; its offset and the
+        // head's total come from bit-sliced ballots of the counts (0..16)
+        const int cnt = __builtin_popcount(pm);
+        const uint64_t head_lanes = 0x1111111111111111ull << j;
+        const uint64_t below = lane ? ~0ull >> (64 - lane) : 0ull;
+        int pre = 0, tot = 0;
+#pragma unroll
+        for (int b = 0; b < 5; b++) {
+            const uint64_t m = __builtin_amdgcn_ballot_w64((cnt >> b) & 1) & head_lanes;
+            pre += __builtin_popcountll(m & below) << b;
+            tot += __builtin_popcountll(m) << b;
+        }
+        int base = 0;
+        if (lane < 4 && tot > 0) base = atomicAdd(a.cand_n + o0 + lane, tot);  // lane j < 4: head j
+        const int b0 = __builtin_amdgcn_readlane(base, 0), b1 = __builtin_amdgcn_readlane(base, 1);
+        const int b2 = __builtin_amdgcn_readlane(base, 2), b3 = __builtin_amdgcn_readlane(base, 3);
+        if (pm == 0) return;
+        const int64_t oj = o0 + j;
+        int slot = (j == 0 ? b0 : j == 1 ? b1 : j == 2 ? b2 : b3) + pre;
+#pragma unroll
+        for (int n = 0; n < NR; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if ((pm >> (4 * n + e)) & 1u) {
+                    if (slot < a.cap) {
+                        a.cand_s[oj * a.cap + slot] = sv[n][e];
+                        a.cand_t[oj * a.cap + slot] = tl[n] * kTile + 4 * blk + e;
+                    }
+                    slot++;
+                }
     };
     for (int c0 = 0; c0 < ntf; c0 += kWave) {
         const int tl = c0 + lane;
+        // the four heads' maxima of the lane's tile: LDS reads issued together
+        // when staged (a run-time choice of address space inside one load
+        // would make it a generic load waiting on both counters)
+        float v[4];
+        if (staged) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) v[jj] = tm_s[jj][tl < ntf ? tl : 0];
+        } else {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                v[jj] = fl[jj] && tl < ntf ? a.tmax[(o0 + jj) * ntf + tl] : -INFINITY;
+        }
         bool cand = false;
         if (tl < ntf) {
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++)
-                if (fl[jj]) {
-                    const float v = tmv(jj, tl);
-                    cand |= v > th[jj] && v >= ct[jj];
-                }
+            for (int jj = 0; jj < 4; jj++) cand |= fl[jj] && v[jj] > th[jj] && v[jj] >= ct[jj];
         }
-        uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
-        while (mask) {
-            const int bit = (int)__builtin_ctzll(mask);
-            mask &= mask - 1;
-            if (r++ % nw != gw) continue;
+        const uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
+        // this wave's candidates of the chunk: rank r + (candidates in lower lanes) = gw mod nw
+        const int rank = r + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+        uint64_t mine = __builtin_amdgcn_ballot_w64(cand && rank % nw == gw);
+        r += (int)__builtin_popcountll(mask);
+        while (mine) {
+            const int bit = (int)__builtin_ctzll(mine);
+            mine &= mine - 1;
 #pragma unroll
             for (int n = 0; n < NR; n++)
                 if (n == np) pend[n] = c0 + bit;
@@ -564,7 +696,9 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
             }
         }
     }
+    FKV_SEL_STAMP(lane == 0, 11 + wave);
     if (np > 0) flush(np);
+    FKV_SEL_STAMP(lane == 0, 3 + wave);
 }
 
 // Top-K spike selection, part 2: one workgroup of 4 waves per (batch, KV
@@ -1266,6 +1400,9 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         sa.cand_s = h->spk_cand_s;
         sa.cand_t = h->spk_cand_t;
         sa.cap = fkv::kTile * h->spike_k;
+#ifdef FKV_PHASE_STAMPS
+        sa.stamps = a.stamps;
+#endif
         const unsigned quads = (unsigned)fkv::cdiv(G, 4);
         const dim3 cgrid(quads * fkv::kSelParts, L.Hkv, L.B), sgrid(quads, L.Hkv, L.B);
         const dim3 sblock(fkv::kWave * fkv::kSelWaves);
