@@ -427,6 +427,54 @@ def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroo
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B,K,cooldown,budget", [(1, 4, 0, 8), (2, 32, 2, 40), (1, 32, 1, 5), (2, 6, 3, 64)])
+def test_device_drain_top_k_matches_host_restatement(orc, B, K, cooldown, budget):
+    """The device drain with spike_k = K > 1 (each KV head's first flagged
+    query head hands up to K tokens through the filter, the budget checked
+    before each token) against the CPU restatement on random streams: spike
+    counts 0..K+2 (clamped to K), token lists with repeated positions and -1
+    entries, budgets that stop a head's list part way.  Same near tiers,
+    near_valid and statistics."""
+    import torch
+
+    from foveated_kv_amd.promotion import PromotionPipeline
+    from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
+
+    Hkv, Hq, D, S = 4, 16, 128, 1200
+    print(f"device drain top-K B={B} K={K} cooldown={cooldown} budget={budget}", flush=True)
+    k, v, cl, h = _layer(B, Hkv, D, S, 43, headroom_min=48)
+    tb = TierConfig(promo_headroom_min=48).tier_boundaries(S)
+    _, far_idx = tier_index_tensors(tb, S, B, Hkv, "cpu")
+    far_idx = far_idx.numpy()
+    fdev = torch.from_numpy(far_idx).cuda().contiguous()
+    pipe = PromotionPipeline(1, cooldown_steps=cooldown, max_per_drain=budget, spike_k=K)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_blob(0, h)
+    ref = opromo.Pipeline(1, cooldown, budget, K)
+    ref.register_archive(0, cl.archive_k.cpu().numpy(), cl.archive_v.cpu().numpy(), far_idx[0])
+    near_k = {0: cl.near_k.cpu().numpy().copy()}
+    near_v = {0: cl.near_v.cpu().numpy().copy()}
+    nv = {0: cl.near_valid.cpu().numpy().copy()}
+    rng = np.random.default_rng(B * 100 + K + budget)
+    n_far = far_idx.shape[2]
+    for step in range(24):
+        flags = np.where(rng.random((B, Hq)) < 0.4, rng.integers(1, K + 3, size=(B, Hq)), 0).astype(np.int32)
+        tokens = rng.integers(0, min(n_far, 3 * K + 20), size=(B, Hq, K)).astype(np.int32)  # repeats
+        tokens[rng.random((B, Hq, K)) < 0.05] = -1
+        fl, tk = torch.from_numpy(flags).cuda(), torch.from_numpy(tokens).cuda()
+        pipe.drain_spikes_device(0, fl, tk, fdev, step)
+        ref.drain(0, flags, tokens, far_idx, step)
+        ref.commit(near_k, near_v, nv, {0: cl.near_k.shape[2]})
+    torch.cuda.synchronize()
+    gk, gv = h.export_near()
+    assert h.read_near_valid() == [int(x) for x in nv[0]]
+    assert np.array_equal(gk.cpu().numpy().view(np.uint16), near_k[0].view(np.uint16))
+    assert np.array_equal(gv.cpu().numpy().view(np.uint16), near_v[0].view(np.uint16))
+    assert pipe.get_stats() == ref.stats and ref.stats["promotions_completed"] > 0
+    assert ref.stats["spikes_deduplicated"] > 0
+
+
+@pytest.mark.gpu
 def test_device_drain_step_advance_without_work():
     """advance_step advances the device step on every successful call, also
     where the drain has nothing to launch (a layer with no archive or blob
