@@ -705,8 +705,10 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
 // head, head quad), wave j for head j.  Keeps the best K of the head's
 // candidates in lanes 0..K-1 (the first 64 sorted across the wave, the
 // rest inserted), writes the outputs and re-arms the head's candidate
-// count.  A buffer overflows only when more than K tiles tie exactly at the
-// cut; that head then re-scans its tiles itself.  Output: flags = the spike
+// count.  A buffer (64 K pairs) overflows only when more than K tiles reach
+// the cut: ties at the K-th largest maximum, or, after the register cut
+// search, maxima less than 2^-11 relative below it; that head then re-scans
+// its tiles itself.  Output: flags = the spike
 // count (at most K), tokens[0..count) the list; entry 0 is the attention
 // kernel's first-index argmax when nothing spikes (the reference's single
 // token), the rest -1.
@@ -746,7 +748,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_select_kernel(SelectArgs
                 }
             }
         } else {
-            // more than K tiles tie at the cut: this head re-scans its tiles
+            // more than K tiles reached the cut: this head re-scans its tiles
             fkv_h4 qv[D / 4];
             load_qv<D>(a, o0, quad, lane, qv);
             const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
@@ -1370,8 +1372,8 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     const int nq = (ng_max + 3) / 4;
     const bool ext = topk || h->has_kscale;  // the kernels that carry the extensions
     fkv::AttnKernel k = L.fmt == 1 ? (L.D == 128 ? fkv::pick_attn_turbo<128>(nq) : fkv::pick_attn_turbo<64>(nq))
-                        : nq == 1  ? fkv::attn_kernel_one_quad(L.D, L.fmt, ext)
-                                   : fkv::attn_kernel_quads(L.D, L.fmt, nq, ext);
+                        : nq == 1  ? fkv::attn_kernel_one_quad(L.D, L.fmt, ext, topk)
+                                   : fkv::attn_kernel_quads(L.D, L.fmt, nq, ext, topk);
     hipLaunchKernelGGL(k, grid, block, 0, st, a);
     if (splits > 1 && !fused_merge) {
         const dim3 mgrid(rows, ng_max);

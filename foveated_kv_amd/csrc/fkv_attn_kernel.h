@@ -710,9 +710,10 @@ __device__ inline void pv_all(Lane<D, NQ>& st, const fkv_h4 (&w4)[NQ], VOp vop) 
 // weight of the lane is non-zero.
 template <int D, int NQ, bool FAR>
 __device__ inline bool softmax_w(Lane<D, NQ>& st, int qd, const float (&s)[4], const uint32_t (&sz)[4],
-                                 fkv_h4& w4) {
+                                 fkv_h4& w4, float* tile_max = nullptr) {
     float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     cmax = head_max(cmax);
+    if (tile_max) *tile_max = cmax;
     const float m_new = fmaxf(st.m[qd], cmax);
     if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
         rescale<D, NQ>(st, qd, m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f);
@@ -756,14 +757,12 @@ struct SpikeTiles {
     int stride, ng;
 };
 
-// The far tile's maximum score of each head of quad qd (sc: the lane's 4
-// scores, -inf past the far tier), stored by lanes 0-3.  The far-tile
-// functions take SPK as a template argument and the stream picks the
-// instantiation once per tile, so the spike_k = 1 path carries no branch.
+// The far tile's maximum score of each head of quad qd (c: the softmax's
+// tile maximum, lane % 4 = head of the quad, -inf past the far tier),
+// stored by lanes 0-3.  Only the top-K kernels (SPK) store.
 template <bool SPK>
-__device__ inline void store_tile_max(const SpikeTiles& sp, int qd, int tile, const float (&sc)[4]) {
+__device__ inline void store_tile_max(const SpikeTiles& sp, int qd, int tile, float c) {
     if (!SPK) return;
-    const float c = head_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
     const int lane = (int)threadIdx.x % kWave, h = 4 * qd + lane;
     if (lane < 4 && h < sp.ng) sp.p[(int64_t)h * sp.stride + tile] = c;
 }
@@ -822,8 +821,9 @@ __device__ inline void far_compute(Lane<D, NQ>& st, const FarTile<D>& r, int til
             sc[e] = ok ? sv : -INFINITY;
             if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
         }
-        store_tile_max<SPK>(sp, qd, tile, sc);
-        any |= softmax_w<D, NQ, true>(st, qd, sc, sz, w4[qd]);
+        float cmax = -INFINITY;  // set by the softmax where SPK
+        any |= softmax_w<D, NQ, true>(st, qd, sc, sz, w4[qd], SPK ? &cmax : nullptr);
+        store_tile_max<SPK>(sp, qd, tile, cmax);
     }
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
     // dword u = 8 dh + g / 2 of the section holds group g of half dh.  One
@@ -1063,9 +1063,11 @@ __device__ inline void QOperand<NS>::readn(int qd, int s0, fkv_h4 (&o)[N]) const
 // maximum, then the gated weights p (the reference skips V of far tokens
 // with s < m - 16, foveated_attn.metal:713).  Returns whether any p > 0.
 template <int D, int NQ>
-__device__ inline bool tq_softmax(Lane<D, NQ>& st, int qd, const float (&s)[4], float (&p)[4]) {
+__device__ inline bool tq_softmax(Lane<D, NQ>& st, int qd, const float (&s)[4], float (&p)[4],
+                                  float* tile_max = nullptr) {
     float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     cmax = head_max(cmax);
+    if (tile_max) *tile_max = cmax;
     const float m_new = fmaxf(st.m[qd], cmax);
     if (__builtin_amdgcn_ballot_w64(m_new > st.m[qd])) {
         rescale<D, NQ>(st, qd, m_new > st.m[qd] ? __expf(st.m[qd] - m_new) : 1.0f);
@@ -1403,8 +1405,9 @@ __device__ inline void g32_far_compute(Lane<D, NQ>& st, const FarTileG<D>& r, in
             sc[e] = ok ? sv : -INFINITY;
             if (ok && sv > st.mx[qd]) { st.mx[qd] = sv; st.arg[qd] = t; }  // first index of the max
         }
-        store_tile_max<SPK>(sp, qd, tile, sc);
-        any |= tq_softmax<D, NQ>(st, qd, sc, p[qd]);
+        float cmax = -INFINITY;  // set by the softmax where SPK
+        any |= tq_softmax<D, NQ>(st, qd, sc, p[qd], SPK ? &cmax : nullptr);
+        store_tile_max<SPK>(sp, qd, tile, cmax);
     }
     if (__builtin_amdgcn_ballot_w64(any) == 0) return;  // whole tile gated away
     // weights: [dh] own-half group (w1) and other-half group before the swap (w2)
@@ -2179,12 +2182,16 @@ __device__ inline void tq_rotate_query(const AttnArgs& a, const TqRotation<D>& r
 // the current one is computed.  The ring takes most of the CU's LDS (one
 // workgroup per CU).
 // EXT: the kernel of handles that use an extension beyond the reference --
-// per-head-scaled fp8 keys (a.kscale) or top-K spike tokens (a.tmax,
-// a.thr) -- both chosen at run time; without EXT neither exists and the
-// reference's path keeps its registers (the extensions' pointers and the
-// second far-tile body raised the register pressure of every kernel).
-template <int D, int NQ, int FMT, bool EXT = false>
+// per-head-scaled fp8 keys (a.kscale, chosen at run time) or top-K spike
+// tokens; SPK (top-K handles only, implies EXT): the far tiles also store
+// their per-head maxima (a.tmax) and the merge the heads' thresholds
+// (a.thr).  Without EXT none of it exists and the reference's path keeps
+// its registers; each kernel has one far-tile body (a run-time choice
+// between two bodies in the stream loop had cost the extension kernels
+// ~1.2 us at C5 even where they took the plain one).
+template <int D, int NQ, int FMT, bool EXT = false, bool SPK = false>
 __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnArgs a) {
+    static_assert(EXT || !SPK, "the top-K kernels are extension kernels");
     constexpr int WPG = attn_waves(D, NQ, FMT);  // waves of the workgroup
     constexpr int NS = D / 4;   // 4-dim k-steps of QK
     constexpr int NH = D / 64;  // 64-dim halves of P.V
@@ -2337,8 +2344,7 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
     const float far_scale = !EXT || TQ || !a.kscale
                                 ? a.inv_sqrt_d
                                 : a.inv_sqrt_d * *(const FKV_CONST float*)(uintptr_t)(a.kscale + bkv);
-    const SpikeTiles spk{EXT && a.tmax ? a.tmax + ((int64_t)b * a.Hq + head0) * a.tmax_stride : nullptr,
-                         a.tmax_stride, ng};
+    const SpikeTiles spk{SPK ? a.tmax + ((int64_t)b * a.Hq + head0) * a.tmax_stride : nullptr, a.tmax_stride, ng};
     const int nd_raw = a.n_dec_dev ? *(const FKV_CONST int32_t*)(uintptr_t)a.n_dec_dev : a.n_dec;
     float asum[NQ];
 #pragma unroll
@@ -2445,13 +2451,11 @@ __global__ __launch_bounds__(64 * attn_waves(D, NQ, FMT)) void attn_kernel(AttnA
             } else if constexpr (G32) {
                 FarTileG<D> r;
                 lds_g32(r, slot, lane);
-                if (EXT && spk.p) g32_far_compute<D, NQ, true>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
-                else g32_far_compute<D, NQ, false>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
+                g32_far_compute<D, NQ, SPK>(st, r, tile, a.L.F, lane, far_scale, qx, spk);
             } else {
                 FarTile<D> r;
                 lds_far(r, slot, lane);
-                if (EXT && spk.p) far_compute<D, NQ, true>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
-                else far_compute<D, NQ, false>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
+                far_compute<D, NQ, SPK>(st, r, tile, a.L.F, blk, far_scale, qx, spk);
             }
         } else if (kd == kNearK) {
             // near tiles: the unrotated query
@@ -2694,8 +2698,8 @@ typedef void (*AttnKernel)(AttnArgs);
 
 // The fp8 and group-32 attention kernels (fmt 0, 2) of rows of one head
 // quad (fkv_attn_q1.hip; EXT: fkv_attn_q1x.hip) and of nq = 2..4 quads
-// (fkv_attn_qn.hip, fkv_attn_qnx.hip).
-AttnKernel attn_kernel_one_quad(int D, int fmt, bool ext);
-AttnKernel attn_kernel_quads(int D, int fmt, int nq, bool ext);
+// (fkv_attn_qn.hip, fkv_attn_qnx.hip); spk picks the top-K kernels.
+AttnKernel attn_kernel_one_quad(int D, int fmt, bool ext, bool spk);
+AttnKernel attn_kernel_quads(int D, int fmt, int nq, bool ext, bool spk);
 
 }  // namespace fkv

@@ -9,10 +9,10 @@
 
 namespace fkv {
 
-AttnKernel attn_kernel_one_quad_ext(int D, int fmt);
+AttnKernel attn_kernel_one_quad_ext(int D, int fmt, bool spk);
 
-AttnKernel attn_kernel_one_quad(int D, int fmt, bool ext) {
-    if (ext) return attn_kernel_one_quad_ext(D, fmt);
+AttnKernel attn_kernel_one_quad(int D, int fmt, bool ext, bool spk) {
+    if (ext) return attn_kernel_one_quad_ext(D, fmt, spk);
     if (D == 128) return fmt == 2 ? attn_kernel<128, 1, 2> : attn_kernel<128, 1, 0>;
     return fmt == 2 ? attn_kernel<64, 1, 2> : attn_kernel<64, 1, 0>;
 }

@@ -21,10 +21,10 @@ AttnKernel pick(int nq) {
 
 }  // namespace
 
-AttnKernel attn_kernel_quads_ext(int D, int fmt, int nq);
+AttnKernel attn_kernel_quads_ext(int D, int fmt, int nq, bool spk);
 
-AttnKernel attn_kernel_quads(int D, int fmt, int nq, bool ext) {
-    if (ext) return attn_kernel_quads_ext(D, fmt, nq);
+AttnKernel attn_kernel_quads(int D, int fmt, int nq, bool ext, bool spk) {
+    if (ext) return attn_kernel_quads_ext(D, fmt, nq, spk);
     if (D == 128) return fmt == 2 ? pick<128, 2>(nq) : pick<128, 0>(nq);
     return fmt == 2 ? pick<64, 2>(nq) : pick<64, 0>(nq);
 }

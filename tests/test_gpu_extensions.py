@@ -195,11 +195,30 @@ TOPK = [  # B, Hq, Hkv, D, S, n_dec, spikes, margin, K, v_group
     (1, 80, 4, 64, 3000, 0, 0.02, 10.0, 16, 0),       # G = 20: two workgroup rows per KV head
     (1, 16, 4, 128, 2048, 8, 0.0, 0.5, 32, 0),        # dense: every far token clears the threshold
     (2, 8, 2, 64, 1000, 3, 0.0, 1e4, 4, 32),          # no spikes at all
+    # long contexts: the cut search over 1,407 tile maxima per head (32 per
+    # lane in registers), 2,813 (staged in LDS) and 4,219 (read from memory)
+    (1, 8, 1, 64, 100_000, 0, 0.005, 10.0, 32, 0),
+    (1, 8, 1, 64, 200_000, 0, 0.005, 10.0, 32, 0),
+    (1, 8, 1, 64, 300_000, 2, 0.005, 10.0, 32, 0),
 ]
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,S,n_dec,spikes,margin,K,vg", TOPK)
 def test_spike_topk_matches_oracle(fkv, orc, B, Hq, Hkv, D, S, n_dec, spikes, margin, K, vg):
+    _topk_case(orc, B, Hq, Hkv, D, S, n_dec, spikes, margin, K, vg)
+
+
+@pytest.mark.parametrize("Hq,vg", [(4, 0), (8, 0), (4, 32)])
+def test_spike_topk_long_wave_ranges(fkv, orc, monkeypatch, Hq, vg):
+    """One split per row (FKV_TARGET_WGS=1, read at handle creation): each
+    wave streams ~70 far tiles, so the tile maxima of its first 64 far tiles
+    are held in registers until the stream ends and the rest are stored as
+    they are computed."""
+    monkeypatch.setenv("FKV_TARGET_WGS", "1")
+    _topk_case(orc, 1, Hq, 1, 128, 20000, 3, 0.005, 10.0, 32, vg)
+
+
+def _topk_case(orc, B, Hq, Hkv, D, S, n_dec, spikes, margin, K, vg):
     from foveated_kv_amd import ext, synthetic
 
     case = f"top-K B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} spikes={spikes} margin={margin} K={K} vg={vg}"
@@ -243,6 +262,51 @@ def test_spike_topk_matches_oracle(fkv, orc, B, Hq, Hkv, D, S, n_dec, spikes, ma
     elif margin > 100:
         assert total == 0 and (tk[..., 1:] == -1).all()
     record(case, flagged=int((fk > 0).sum()), spike_ties=ties, spike_tokens=total)
+
+
+@pytest.mark.parametrize("K", [4, 32])
+def test_spike_topk_tied_tiles_overflow(fkv, orc, K):
+    """Every far key equal and spiking: every far tile ties at the cut, so
+    all 4,500 far tokens are candidates, more than a head's buffer holds
+    (64 x 32 pairs), and each head re-scans its tiles.  Equal scores go to
+    the smaller index: the list is far tokens 0..K-1."""
+    from foveated_kv_amd import ext, synthetic
+
+    B, Hq, Hkv, D, S = 1, 8, 1, 64, 5000
+    k, v = synthetic.make_kv(B, Hkv, S, D, 91)
+    q = synthetic.make_query(B, Hq, D, 91)
+    tb = orc.tier_boundaries(S)
+    f0, F = tb["mid_start"], tb["far_count"]
+    assert F > 64 * 32
+    u = q[0].astype(np.float32).mean(0)
+    u /= np.linalg.norm(u)
+    s = q[0].astype(np.float32) @ u
+    assert s.min() > 0
+    k[0, 0, f0:f0 + F] = (20.0 * np.sqrt(D) / s.min() * u).astype(np.float16)  # every head's score >= ~20
+    cl = ext.CompressHandle(_cfg(0, 0)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                                        with_archive=False)
+    assert bool((cl.far_k == cl.far_k[:, :, :1]).all())  # one code row for the whole far tier
+    mk = lambda kk: ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                                       cl.near_valid, spike_margin=10.0, spike_k=kk)
+    qt = torch.from_numpy(q).cuda()[:, :, None]
+    o1, f1, t1 = mk(1)(qt)
+    hk = mk(K)
+    for call in range(2):  # the second call: counts re-armed by the first
+        ok, fk, tk = hk(qt)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, ok)
+        fk, tk = np_(fk), np_(tk)
+        assert (fk == K).all(), fk
+        assert (tk == np.arange(K)[None, None]).all(), tk
+    c = {n: np_(getattr(cl, n)) for n in ("near_k", "near_v", "far_k", "far_v", "far_v_scale", "far_v_zero",
+                                          "near_valid")}
+    _, _, _, mf, mn, fs = orc.attend_kernel(q, c["near_k"], c["near_v"], c["near_valid"], c["far_k"], c["far_v"],
+                                            c["far_v_scale"], c["far_v_zero"], None, None, spike_margin=10.0,
+                                            return_far_scores=True)
+    for hq in range(Hq):
+        assert np.ptp(fs[0, hq]) == 0.0  # the exact scores tie too
+        check_topk(fs[0, hq], mn[0, hq] + 10.0, K, int(fk[0, hq]), tk[0, hq])
+    record(f"tied tiles K={K}", flagged=int((fk > 0).sum()), spike_tokens=int(fk.sum()))
 
 
 def test_spike_k_setter(fkv):
