@@ -349,19 +349,6 @@ constexpr int kSelWaves = 4;
 constexpr int kSelRegs = 32;
 constexpr int kCutLowBits = 12;
 
-// Sum of v over the wave, in every lane (DPP row rotations and lane-half
-// swaps, no LDS).
-__device__ inline int wave_sum_i32(int v) {
-    v += (int)row_ror<1>((uint32_t)v);
-    v += (int)row_ror<2>((uint32_t)v);
-    v += (int)row_ror<4>((uint32_t)v);
-    v += (int)row_ror<8>((uint32_t)v);
-    LanePair p = swap16((uint32_t)v);
-    v = (int)p.a + (int)p.b;
-    p = swap32((uint32_t)v);
-    return (int)p.a + (int)p.b;
-}
-
 // fp32 -> uint32 with the same order (no NaN among scores) and back.
 __device__ inline uint32_t fkey(float f) {
     const uint32_t b = __float_as_uint(f);
@@ -464,29 +451,38 @@ __device__ inline void wave_sort(float& s, int& t, int lane) {
 // that at least K maxima above th reach (at most the K-th largest), or
 // -inf when at most K maxima clear th.  The maxima are held as keys in
 // registers (0 for those at or below th, or past the far tier: below every
-// trial), all loads in flight, and copied to the LDS row `lds` for the
-// rescoring; counts are per-lane compares and one wave sum, no branches.
+// trial) and copied to the LDS row `lds` (NSL x 64 entries, -inf past the
+// far tier) for the rescoring.  The loads are buffer loads bounded by the
+// far tier (past it they read 0 without touching memory), so none sits
+// behind a branch and all are in flight at once: guarded loads had been
+// compiled as one branch, load and wait each, a round trip per 64 tiles.
+// A count is one compare per register, its ballot's population count and a
+// scalar sum: no cross-lane data movement, no branches.
 template <int NSL>
 __device__ inline float cut_search(const float* tm, int ntf, float th, int K, int lane, float* lds) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)tm, (short)0, ntf * 4, 0x00020000);
+    uint32_t raw[NSL];
+#pragma unroll
+    for (int r = 0; r < NSL; r++) raw[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, (r * kWave + lane) * 4, 0, 0);
     uint32_t kv[NSL];
 #pragma unroll
     for (int r = 0; r < NSL; r++) {
         const int t = r * kWave + lane;
-        const float v = t < ntf ? tm[t] : -INFINITY;
-        if (t < ntf) lds[t] = v;
+        const float v = t < ntf ? __uint_as_float(raw[r]) : -INFINITY;
+        lds[t] = v;
         kv[r] = v > th ? fkey(v) : 0u;
     }
-    int n_above = 0;
+    auto count_at_least = [&](uint32_t trial) {
+        int c = 0;
 #pragma unroll
-    for (int r = 0; r < NSL; r++) n_above += kv[r] != 0u;
-    if (__builtin_amdgcn_readfirstlane(wave_sum_i32(n_above)) <= K) return -INFINITY;
+        for (int r = 0; r < NSL; r++) c += (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(kv[r] >= trial));
+        return c;
+    };
+    if (count_at_least(1u) <= K) return -INFINITY;
     uint32_t x = 0;
     for (int bit = 31; bit >= kCutLowBits; bit--) {
         const uint32_t trial = x | (1u << bit);
-        int c = 0;
-#pragma unroll
-        for (int r = 0; r < NSL; r++) c += kv[r] >= trial;
-        if (__builtin_amdgcn_readfirstlane(wave_sum_i32(c)) >= K) x = trial;
+        if (count_at_least(trial) >= K) x = trial;
     }
     return unfkey(x);  // x >= the key of -FLT_MAX: a finite cut
 }
@@ -538,19 +534,24 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     // writes the LDS copy the rescoring reads) in the cut search below
     const bool regs = ntf <= kWave * kSelRegs;
     // otherwise the tile maxima of the quad's flagged heads -> LDS, eight loads in flight per thread
+    // the tile maxima of the quad's heads that exist (4 quad + jj < G) as one
+    // bounded buffer: loads past them read 0 without touching memory, so
+    // none needs a branch (a guarded load compiles to a branch, the load and
+    // a wait of its own)
+    const int live = min(4, a.G - 4 * quad);
+    const __amdgpu_buffer_rsrc_t qrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.tmax + o0 * ntf), (short)0, live * ntf * 4, 0x00020000);
     if (staged && !regs) {
         constexpr int U = 8;
         for (int i0 = threadIdx.x; i0 < 4 * ntf; i0 += U * (int)blockDim.x) {
-            float v[U];
+            uint32_t raw[U];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                raw[u] = __builtin_amdgcn_raw_buffer_load_b32(qrs, (i0 + u * (int)blockDim.x) * 4, 0, 0);
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int i = i0 + u * (int)blockDim.x, jj = i / ntf;
-                v[u] = i < 4 * ntf && fl_s[jj] ? a.tmax[(o0 + jj) * ntf + i % ntf] : -INFINITY;
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int i = i0 + u * (int)blockDim.x;
-                if (i < 4 * ntf) tm_s[i / ntf][i % ntf] = v[u];
+                if (i < 4 * ntf) tm_s[jj][i % ntf] = fl_s[jj] ? __uint_as_float(raw[u]) : -INFINITY;
             }
         }
     }
@@ -670,8 +671,10 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
             for (int jj = 0; jj < 4; jj++) v[jj] = tm_s[jj][tl < ntf ? tl : 0];
         } else {
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++)
-                v[jj] = fl[jj] && tl < ntf ? a.tmax[(o0 + jj) * ntf + tl] : -INFINITY;
+            for (int jj = 0; jj < 4; jj++) {
+                const uint32_t raw = __builtin_amdgcn_raw_buffer_load_b32(qrs, (jj * ntf + tl) * 4, 0, 0);
+                v[jj] = fl[jj] && tl < ntf ? __uint_as_float(raw) : -INFINITY;
+            }
         }
         bool cand = false;
         if (tl < ntf) {
