@@ -788,13 +788,17 @@ def run_phase_stamps(args, torch, dev):
     }
     if args.stamps_spike_k > 1:
         # the top-K candidates kernel's workgroups (slots 32..): entry, maxima
-        # staged, cuts known, each wave's candidates done
-        # slots 32 entry, 33 staged, 34 cuts, 35+w wave done, 39+w query operands, 43+w last batch begun
-        sel = np.frombuffer(raw, dtype=np.uint64).reshape(n_wgs, 64).astype(np.int64)[:, 32:47]
+        # staged, cuts known, each wave's candidates done, the selection
+        # slots 32 entry, 33 staged, 34 cuts, 35+w wave done, 39+w query
+        # operands, 43+w last batch begun, 47 the quad's selection done (its
+        # last workgroup; an older launch's stamp is earlier than this one's)
+        sel = np.frombuffer(raw, dtype=np.uint64).reshape(n_wgs, 64).astype(np.int64)[:, 32:48]
         sel = sel[(sel[:, 0] > 0) & (sel[:, 3] > 0)]
         if len(sel):
             t0s = sel[:, 0].min()
             done = sel[:, 3:7].max(axis=1)
+            selected = sel[:, 15] > done
+            end = max(done.max(), sel[selected, 15].max()) if selected.any() else done.max()
             out["topk_candidates"] = {
                 "workgroups": int(len(sel)), "spike_k": args.stamps_spike_k,
                 "entry_spread": pq(us(sel[:, 0] - t0s)),
@@ -804,7 +808,8 @@ def run_phase_stamps(args, torch, dev):
                 "deal_and_full_batches": pq(us((sel[:, 11:15] - sel[:, 7:11]).ravel())),
                 "last_batch": pq(us((sel[:, 3:7] - sel[:, 11:15]).ravel())),
                 "rescore_and_append": pq(us(done - sel[:, 2])),
-                "last_done": round(float(us(done.max() - t0s)), 3),
+                "arrival_and_selection": pq(us(sel[selected, 15] - done[selected])) if selected.any() else None,
+                "last_done": round(float(us(end - t0s)), 3),
                 "start_after_attention_output": (round(float(us(t0s - merged[:, 22].max())), 3)
                                                  if len(merged) else None),
             }

@@ -172,7 +172,7 @@ struct fkv_attn_impl {
     int32_t* spk_flags = nullptr;
     int32_t* spk_tokens = nullptr;
     int* spk_cand_n = nullptr;   // per head: candidates found (zero between calls)
-    float* spk_cut = nullptr;    // per head: the cut of the last call
+    int* spk_arrive = nullptr;   // per (batch, KV head, head quad): workgroups done (zero between calls)
     float* spk_cand_s = nullptr; // per head: up to 64 * FKV_MAX_SPIKE_K candidate scores
     int* spk_cand_t = nullptr;   // ... and their tokens
 };

@@ -306,10 +306,11 @@ struct SelectArgs {
     int32_t* flags;             // (B*Hq) number of spiking tokens, at most K
     int32_t* tokens;            // (B*Hq, K)
     const float* kscale;        // (B*Hkv) per-head fp8 key scales, or NULL (1)
-    // candidate buffers of the two selection kernels: per head a count
-    // (zero between calls), its cut, and up to cap (score, token) pairs
+    // candidate buffers: per head a count (zero between calls) and up to
+    // cap (score, token) pairs; per (batch, KV head, head quad) the
+    // workgroups that have finished (zero between calls)
     int* cand_n;                // (B*Hq)
-    float* cut;                 // (B*Hq)
+    int* arrive;                // (B*Hkv*quads)
     float* cand_s;              // (B*Hq, cap)
     int* cand_t;                // (B*Hq, cap)
     int cap;                    // 64 * K
@@ -487,6 +488,103 @@ __device__ inline float cut_search(const float* tm, int ntf, float th, int K, in
     return unfkey(x);  // x >= the key of -FLT_MAX: a finite cut
 }
 
+// Top-K spike selection, part 2, for head `wave` of a quad, run by the
+// last workgroup of the quad to finish part 1 (spike_candidates_kernel):
+// keeps the best K of the head's candidates in lanes 0..K-1 (the first 64
+// sorted across the wave, the rest inserted), writes the outputs and
+// re-arms the head's candidate count.  The candidates of the other
+// workgroups are read with sc1 loads (coherent across XCDs), the count
+// with an agent-scope atomic load.  A buffer (64 K pairs) overflows only
+// when more than K tiles reach the cut: ties at the K-th largest maximum,
+// or, after the register cut search, maxima less than 2^-11 relative below
+// it; that head then re-scans its tiles itself.  Output: flags = the spike
+// count (at most K), tokens[0..count) the list; entry 0 is the attention
+// kernel's first-index argmax when nothing spikes (the reference's single
+// token), the rest -1.
+template <int D>
+__device__ inline void select_head(const SelectArgs& a, int quad, int kvh, int b, int wave, int lane, float cut) {
+    const int j = lane & 3, blk = lane >> 2;
+    if (4 * quad + wave >= a.G) return;
+    const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
+    const int64_t o0 = (int64_t)b * a.Hq + (int64_t)kvh * a.G + 4 * quad, oj = o0 + wave;
+    const int K = a.K;
+    float ls = -INFINITY;
+    int li = INT_MAX, n = 0;
+    if (a.flags_in[oj] != 0) {
+        const int nb = __hip_atomic_load(a.cand_n + oj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (nb <= a.cap) {
+            // the head's pairs as bounded buffers: past nb they read 0
+            const __amdgpu_buffer_rsrc_t rs_s =
+                __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_s + oj * a.cap), (short)0, nb * 4, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rs_t =
+                __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_t + oj * a.cap), (short)0, nb * 4, 0x00020000);
+            for (int c0 = 0; c0 < nb; c0 += kWave) {
+                const int i = c0 + lane;
+                const uint32_t rsv = __builtin_amdgcn_raw_buffer_load_b32(rs_s, i * 4, 0, kCpolSc1);
+                const uint32_t rtv = __builtin_amdgcn_raw_buffer_load_b32(rs_t, i * 4, 0, kCpolSc1);
+                float s = i < nb ? __uint_as_float(rsv) : -INFINITY;
+                int t = i < nb ? (int)rtv : INT_MAX;
+                if (c0 == 0) {  // the first 64: one sort, the best K become the list
+                    wave_sort(s, t, lane);
+                    ls = s;
+                    li = t;
+                    n = nb < K ? nb : K;
+                    continue;
+                }
+                const float ks = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls), K - 1));
+                const int kt = __builtin_amdgcn_readlane(li, K - 1);
+                uint64_t m = __builtin_amdgcn_ballot_w64(i < nb && (n < K || ahead_of(s, t, ks, kt)));
+                while (m) {
+                    const int src = (int)__builtin_ctzll(m);
+                    m &= m - 1;
+                    list_insert(ls, li, n, K, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), src)),
+                                __builtin_amdgcn_readlane(t, src), lane);
+                }
+            }
+        } else {
+            // more than K tiles reached the cut: this head re-scans its tiles
+            fkv_h4 qv[D / 4];
+            load_qv<D>(a, o0, quad, lane, qv);
+            const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
+            const float thj = a.thr[oj], ctj = cut;
+            const float* tm = a.tmax + oj * a.ntf;
+            for (int c0 = 0; c0 < a.ntf; c0 += kWave) {
+                const int tl = c0 + lane;
+                const bool cand = tl < a.ntf && tm[tl] > thj && tm[tl] >= ctj;
+                uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
+                while (mask) {
+                    const int tile[1] = {c0 + (int)__builtin_ctzll(mask)};
+                    mask &= mask - 1;
+                    float sv[1][4];
+                    rescore_tiles<D, 1>(a, bkv, tile, qv, far_scale, lane, sv);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int t0 = tile[0] * kTile + e;
+                        uint64_t m = __builtin_amdgcn_ballot_w64(j == wave && t0 + 4 * blk < a.L.F &&
+                                                                  sv[0][e] > thj && sv[0][e] >= ctj);
+                        while (m) {
+                            const int src = (int)__builtin_ctzll(m);
+                            m &= m - 1;
+                            list_insert(ls, li, n, K,
+                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0][e]), src)),
+                                        t0 + 4 * (src >> 2), lane);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (lane < K) {
+        int t = lane < n ? li : -1;
+        if (lane == 0 && n == 0) t = a.tokens_in[oj];
+        a.tokens[oj * K + lane] = t;
+    }
+    if (lane == 0) {
+        a.flags[oj] = n;
+        __hip_atomic_store(a.cand_n + oj, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed for the next call
+    }
+}
+
 // Top-K spike selection, part 1: kSelParts workgroups per (batch, KV head,
 // head quad).  A far token spikes when its score exceeds its head's
 // threshold min_near + margin (the attention kernel's flag rule); each head
@@ -506,12 +604,18 @@ __device__ inline float cut_search(const float* tm, int ntf, float th, int K, in
 //     above its head's threshold and at or above its cut to the head's
 //     candidate buffer in memory -- at least K tokens when the cut is set
 //     (each of the K tiles contributes its maximum), all of them
-//     otherwise, at most 64 per tile at or above the cut.
+//     otherwise, at most 64 per tile at or above the cut;
+//  C. the last workgroup of the quad to finish B (an arrival count per
+//     quad, re-armed by that workgroup) runs part 2, select_head, for the
+//     quad's heads.  Candidate pairs are written with sc1 stores (coherent
+//     across XCDs) and a workgroup's arrival is counted once its stores are
+//     complete.  A quad where nothing spikes skips B and C: its first
+//     workgroup writes the outputs.
 template <int D>
 __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(SelectArgs a) {
     constexpr int NS = D / 4, NR = 4;  // tiles rescored together
     __shared__ float thr_s[4], cut_s[4];
-    __shared__ int fl_s[4];
+    __shared__ int fl_s[4], last_s;
     __shared__ float tm_s[4][kSelStage];
     const int quad = blockIdx.x / kSelParts, part = blockIdx.x % kSelParts, kvh = blockIdx.y, b = blockIdx.z;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = threadIdx.x % kWave;
@@ -529,11 +633,13 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         cut_s[jj] = INFINITY;
     }
     __syncthreads();
-    if (!(fl_s[0] | fl_s[1] | fl_s[2] | fl_s[3])) return;  // nothing spikes: part 2 writes the outputs
+    if (!(fl_s[0] | fl_s[1] | fl_s[2] | fl_s[3])) {  // nothing spikes: the outputs only
+        if (part == 0) select_head<D>(a, quad, kvh, b, wave, lane, INFINITY);
+        return;
+    }
     // the register path: each flagged head's wave loads its own maxima (and
     // writes the LDS copy the rescoring reads) in the cut search below
     const bool regs = ntf <= kWave * kSelRegs;
-    // otherwise the tile maxima of the quad's flagged heads -> LDS, eight loads in flight per thread
     // the tile maxima of the quad's heads that exist (4 quad + jj < G) as one
     // bounded buffer: loads past them read 0 without touching memory, so
     // none needs a branch (a guarded load compiles to a branch, the load and
@@ -541,6 +647,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     const int live = min(4, a.G - 4 * quad);
     const __amdgpu_buffer_rsrc_t qrs =
         __builtin_amdgcn_make_buffer_rsrc((void*)(a.tmax + o0 * ntf), (short)0, live * ntf * 4, 0x00020000);
+    // otherwise the tile maxima of the quad's flagged heads -> LDS, eight loads in flight per thread
     if (staged && !regs) {
         constexpr int U = 8;
         for (int i0 = threadIdx.x; i0 < 4 * ntf; i0 += U * (int)blockDim.x) {
@@ -586,10 +693,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
                 cut = unfkey(x);
             }
         }
-        if (lane == 0) {
-            cut_s[wave] = cut;
-            if (part == 0) a.cut[o0 + wave] = cut;
-        }
+        if (lane == 0) cut_s[wave] = cut;
     }
     __syncthreads();
     FKV_SEL_STAMP(threadIdx.x == 0, 2);
@@ -605,6 +709,11 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     load_qv<D>(a, o0, quad, lane, qv);
     const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
     FKV_SEL_STAMP(lane == 0, 7 + wave);
+    // the quad's candidate pairs (heads that exist) as bounded buffers
+    const __amdgpu_buffer_rsrc_t cs_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_s + o0 * a.cap), (short)0, live * a.cap * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ct_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_t + o0 * a.cap), (short)0, live * a.cap * 4, 0x00020000);
     // ---- B: this wave's candidate tiles (every kSelParts * kSelWaves-th), NR at a time ----
     const int gw = part * kSelWaves + wave, nw = kSelParts * kSelWaves;
     int r = 0, np = 0;  // candidates seen (the same in every wave of the quad); tiles pending
@@ -646,7 +755,6 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         const int b0 = __builtin_amdgcn_readlane(base, 0), b1 = __builtin_amdgcn_readlane(base, 1);
         const int b2 = __builtin_amdgcn_readlane(base, 2), b3 = __builtin_amdgcn_readlane(base, 3);
         if (pm == 0) return;
-        const int64_t oj = o0 + j;
         int slot = (j == 0 ? b0 : j == 1 ? b1 : j == 2 ? b2 : b3) + pre;
 #pragma unroll
         for (int n = 0; n < NR; n++)
@@ -654,8 +762,10 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
             for (int e = 0; e < 4; e++)
                 if ((pm >> (4 * n + e)) & 1u) {
                     if (slot < a.cap) {
-                        a.cand_s[oj * a.cap + slot] = sv[n][e];
-                        a.cand_t[oj * a.cap + slot] = tl[n] * kTile + 4 * blk + e;
+                        const int off = (j * a.cap + slot) * 4;
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sv[n][e]), cs_rs, off, 0, kCpolSc1);
+                        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(tl[n] * kTile + 4 * blk + e), ct_rs, off, 0,
+                                                              kCpolSc1);
                     }
                     slot++;
                 }
@@ -702,96 +812,18 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     FKV_SEL_STAMP(lane == 0, 11 + wave);
     if (np > 0) flush(np);
     FKV_SEL_STAMP(lane == 0, 3 + wave);
-}
-
-// Top-K spike selection, part 2: one workgroup of 4 waves per (batch, KV
-// head, head quad), wave j for head j.  Keeps the best K of the head's
-// candidates in lanes 0..K-1 (the first 64 sorted across the wave, the
-// rest inserted), writes the outputs and re-arms the head's candidate
-// count.  A buffer (64 K pairs) overflows only when more than K tiles reach
-// the cut: ties at the K-th largest maximum, or, after the register cut
-// search, maxima less than 2^-11 relative below it; that head then re-scans
-// its tiles itself.  Output: flags = the spike
-// count (at most K), tokens[0..count) the list; entry 0 is the attention
-// kernel's first-index argmax when nothing spikes (the reference's single
-// token), the rest -1.
-template <int D>
-__global__ __launch_bounds__(64 * kSelWaves) void spike_select_kernel(SelectArgs a) {
-    const int quad = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = threadIdx.x % kWave;
-    const int j = lane & 3, blk = lane >> 2;
-    if (4 * quad + wave >= a.G) return;
-    const int64_t bkv = (int64_t)b * a.L.Hkv + kvh;
-    const int64_t o0 = (int64_t)b * a.Hq + (int64_t)kvh * a.G + 4 * quad, oj = o0 + wave;
-    const int K = a.K;
-    float ls = -INFINITY;
-    int li = INT_MAX, n = 0;
-    if (a.flags_in[oj] != 0) {
-        const int nb = a.cand_n[oj];
-        if (nb <= a.cap) {
-            for (int c0 = 0; c0 < nb; c0 += kWave) {
-                const int i = c0 + lane;
-                float s = i < nb ? a.cand_s[oj * a.cap + i] : -INFINITY;
-                int t = i < nb ? a.cand_t[oj * a.cap + i] : INT_MAX;
-                if (c0 == 0) {  // the first 64: one sort, the best K become the list
-                    wave_sort(s, t, lane);
-                    ls = s;
-                    li = t;
-                    n = nb < K ? nb : K;
-                    continue;
-                }
-                const float ks = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls), K - 1));
-                const int kt = __builtin_amdgcn_readlane(li, K - 1);
-                uint64_t m = __builtin_amdgcn_ballot_w64(i < nb && (n < K || ahead_of(s, t, ks, kt)));
-                while (m) {
-                    const int src = (int)__builtin_ctzll(m);
-                    m &= m - 1;
-                    list_insert(ls, li, n, K, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), src)),
-                                __builtin_amdgcn_readlane(t, src), lane);
-                }
-            }
-        } else {
-            // more than K tiles reached the cut: this head re-scans its tiles
-            fkv_h4 qv[D / 4];
-            load_qv<D>(a, o0, quad, lane, qv);
-            const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
-            const float thj = a.thr[oj], ctj = a.cut[oj];
-            const float* tm = a.tmax + oj * a.ntf;
-            for (int c0 = 0; c0 < a.ntf; c0 += kWave) {
-                const int tl = c0 + lane;
-                const bool cand = tl < a.ntf && tm[tl] > thj && tm[tl] >= ctj;
-                uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
-                while (mask) {
-                    const int tile[1] = {c0 + (int)__builtin_ctzll(mask)};
-                    mask &= mask - 1;
-                    float sv[1][4];
-                    rescore_tiles<D, 1>(a, bkv, tile, qv, far_scale, lane, sv);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int t0 = tile[0] * kTile + e;
-                        uint64_t m = __builtin_amdgcn_ballot_w64(j == wave && t0 + 4 * blk < a.L.F &&
-                                                                  sv[0][e] > thj && sv[0][e] >= ctj);
-                        while (m) {
-                            const int src = (int)__builtin_ctzll(m);
-                            m &= m - 1;
-                            list_insert(ls, li, n, K,
-                                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0][e]), src)),
-                                        t0 + 4 * (src >> 2), lane);
-                        }
-                    }
-                }
-            }
-        }
-    }
-    if (lane < K) {
-        int t = lane < n ? li : -1;
-        if (lane == 0 && n == 0) t = a.tokens_in[oj];
-        a.tokens[oj * K + lane] = t;
-    }
-    if (lane == 0) {
-        a.flags[oj] = n;
-        a.cand_n[oj] = 0;  // re-armed for the next call
-    }
+    // ---- C: the quad's last workgroup selects ----
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's pairs are stored
+    __syncthreads();
+    const int64_t qrow = bkv * (int64_t)(gridDim.x / kSelParts) + quad;
+    if (threadIdx.x == 0)
+        last_s = __hip_atomic_fetch_add(a.arrive + qrow, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 kSelParts - 1;
+    __syncthreads();
+    if (!last_s) return;
+    select_head<D>(a, quad, kvh, b, wave, lane, cut_s[wave]);
+    if (threadIdx.x == 0) __hip_atomic_store(a.arrive + qrow, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    FKV_SEL_STAMP(lane == 0, 15);
 }
 
 // ---------------------------------------------------------------------------
@@ -1164,13 +1196,13 @@ int scratch_base(const std::string& name, int dev, hipStream_t st, uint8_t** out
 namespace {
 
 void free_spike_buffers(fkv_attn* h) {
-    void* bufs[] = {h->spk_tmax, h->spk_thr, h->spk_flags, h->spk_tokens, h->spk_cand_n, h->spk_cut, h->spk_cand_s,
+    void* bufs[] = {h->spk_tmax, h->spk_thr, h->spk_flags, h->spk_tokens, h->spk_cand_n, h->spk_arrive, h->spk_cand_s,
                     h->spk_cand_t};
     for (void* p : bufs)
         if (p) (void)hipFree(p);
-    h->spk_tmax = h->spk_thr = h->spk_cut = h->spk_cand_s = nullptr;
+    h->spk_tmax = h->spk_thr = h->spk_cand_s = nullptr;
     h->spk_flags = h->spk_tokens = nullptr;
-    h->spk_cand_n = h->spk_cand_t = nullptr;
+    h->spk_cand_n = h->spk_arrive = h->spk_cand_t = nullptr;
 }
 
 // The top-K spike selection's buffers for Hq query heads (spike_k > 1).
@@ -1187,10 +1219,12 @@ int ensure_spike_buffers(fkv_attn* h, int Hq) {
     if (!rc) rc = check_hip(hipMalloc(&h->spk_flags, heads * sizeof(int32_t)), "hipMalloc(flags)");
     if (!rc) rc = check_hip(hipMalloc(&h->spk_tokens, heads * sizeof(int32_t)), "hipMalloc(tokens)");
     if (!rc) rc = check_hip(hipMalloc(&h->spk_cand_n, heads * sizeof(int)), "hipMalloc(cand_n)");
-    if (!rc) rc = check_hip(hipMalloc(&h->spk_cut, heads * sizeof(float)), "hipMalloc(cut)");
+    // arrival counters of the (batch, KV head, head quad) rows: at most one per query head
+    if (!rc) rc = check_hip(hipMalloc(&h->spk_arrive, heads * sizeof(int)), "hipMalloc(arrive)");
     if (!rc) rc = check_hip(hipMalloc(&h->spk_cand_s, heads * cap * sizeof(float)), "hipMalloc(cand_s)");
     if (!rc) rc = check_hip(hipMalloc(&h->spk_cand_t, heads * cap * sizeof(int)), "hipMalloc(cand_t)");
     if (!rc) rc = check_hip(hipMemset(h->spk_cand_n, 0, heads * sizeof(int)), "hipMemset(cand_n)");
+    if (!rc) rc = check_hip(hipMemset(h->spk_arrive, 0, heads * sizeof(int)), "hipMemset(arrive)");
     if (rc) {
         free_spike_buffers(h);
         return rc;
@@ -1314,7 +1348,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     a.inv_sqrt_d = (float)(1.0 / sqrt((double)L.D));
     a.out = (uint16_t*)out;
     // spike_k > 1: the attention kernel's flag / argmax, tile maxima and
-    // thresholds go to the selection's buffers; spike_select_kernel writes
+    // thresholds go to the selection's buffers; the selection writes
     // the caller's spike outputs
     a.flags = topk ? h->spk_flags : spike_flags;
     a.tokens = topk ? h->spk_tokens : spike_tokens;
@@ -1401,7 +1435,7 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         sa.tokens = spike_tokens;
         sa.kscale = a.kscale;
         sa.cand_n = h->spk_cand_n;
-        sa.cut = h->spk_cut;
+        sa.arrive = h->spk_arrive;
         sa.cand_s = h->spk_cand_s;
         sa.cand_t = h->spk_cand_t;
         sa.cap = fkv::kTile * h->spike_k;
@@ -1409,15 +1443,10 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         sa.stamps = a.stamps;
 #endif
         const unsigned quads = (unsigned)fkv::cdiv(G, 4);
-        const dim3 cgrid(quads * fkv::kSelParts, L.Hkv, L.B), sgrid(quads, L.Hkv, L.B);
+        const dim3 cgrid(quads * fkv::kSelParts, L.Hkv, L.B);
         const dim3 sblock(fkv::kWave * fkv::kSelWaves);
-        if (L.D == 128) {
-            hipLaunchKernelGGL(fkv::spike_candidates_kernel<128>, cgrid, sblock, 0, st, sa);
-            hipLaunchKernelGGL(fkv::spike_select_kernel<128>, sgrid, sblock, 0, st, sa);
-        } else {
-            hipLaunchKernelGGL(fkv::spike_candidates_kernel<64>, cgrid, sblock, 0, st, sa);
-            hipLaunchKernelGGL(fkv::spike_select_kernel<64>, sgrid, sblock, 0, st, sa);
-        }
+        if (L.D == 128) hipLaunchKernelGGL(fkv::spike_candidates_kernel<128>, cgrid, sblock, 0, st, sa);
+        else hipLaunchKernelGGL(fkv::spike_candidates_kernel<64>, cgrid, sblock, 0, st, sa);
     }
     return check_hip(hipGetLastError(), "attn_kernel launch");
 }
