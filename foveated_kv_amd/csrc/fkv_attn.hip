@@ -511,24 +511,44 @@ __device__ inline void select_head(const SelectArgs& a, int quad, int kvh, int b
     float ls = -INFINITY;
     int li = INT_MAX, n = 0;
     if (a.flags_in[oj] != 0) {
-        const int nb = __hip_atomic_load(a.cand_n + oj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (nb <= a.cap) {
-            // the head's pairs as bounded buffers: past nb they read 0
-            const __amdgpu_buffer_rsrc_t rs_s =
-                __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_s + oj * a.cap), (short)0, nb * 4, 0x00020000);
-            const __amdgpu_buffer_rsrc_t rs_t =
-                __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_t + oj * a.cap), (short)0, nb * 4, 0x00020000);
+        // the first 64 pairs are loaded together with the count (one round
+        // trip); loads past the head's buffer read 0
+        const __amdgpu_buffer_rsrc_t rs_s =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_s + oj * a.cap), (short)0, a.cap * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rs_t =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_t + oj * a.cap), (short)0, a.cap * 4, 0x00020000);
+        const uint32_t rs0 = __builtin_amdgcn_raw_buffer_load_b32(rs_s, lane * 4, 0, kCpolSc1);
+        const uint32_t rt0 = __builtin_amdgcn_raw_buffer_load_b32(rs_t, lane * 4, 0, kCpolSc1);
+        const int nb = __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(a.cand_n + oj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (nb <= kWave) {
+            // each pair's place in the list = the pairs ahead of it (distinct
+            // tokens: a strict order); a forward permute puts rank p in lane
+            // p (lanes past nb keep their own place)
+            const float s = lane < nb ? __uint_as_float(rs0) : -INFINITY;
+            const int t = lane < nb ? (int)rt0 : INT_MAX;
+            int r = 0;
+            for (int src = 0; src < nb; src++) {
+                const float ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), src));
+                const int ts = __builtin_amdgcn_readlane(t, src);
+                r += ahead_of(ss, ts, s, t) ? 1 : 0;
+            }
+            if (lane >= nb) r = lane;
+            ls = __int_as_float(__builtin_amdgcn_ds_permute(r * 4, __float_as_int(s)));
+            li = __builtin_amdgcn_ds_permute(r * 4, t);
+            n = nb < K ? nb : K;
+        } else if (nb <= a.cap) {
             for (int c0 = 0; c0 < nb; c0 += kWave) {
                 const int i = c0 + lane;
-                const uint32_t rsv = __builtin_amdgcn_raw_buffer_load_b32(rs_s, i * 4, 0, kCpolSc1);
-                const uint32_t rtv = __builtin_amdgcn_raw_buffer_load_b32(rs_t, i * 4, 0, kCpolSc1);
+                const uint32_t rsv = c0 == 0 ? rs0 : __builtin_amdgcn_raw_buffer_load_b32(rs_s, i * 4, 0, kCpolSc1);
+                const uint32_t rtv = c0 == 0 ? rt0 : __builtin_amdgcn_raw_buffer_load_b32(rs_t, i * 4, 0, kCpolSc1);
                 float s = i < nb ? __uint_as_float(rsv) : -INFINITY;
                 int t = i < nb ? (int)rtv : INT_MAX;
                 if (c0 == 0) {  // the first 64: one sort, the best K become the list
                     wave_sort(s, t, lane);
                     ls = s;
                     li = t;
-                    n = nb < K ? nb : K;
+                    n = K;
                     continue;
                 }
                 const float ks = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls), K - 1));
