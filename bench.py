@@ -792,7 +792,7 @@ def run_phase_stamps(args, torch, dev):
         # slots 32 entry, 33 staged, 34 cuts, 35+w wave done, 39+w query
         # operands, 43+w last batch begun, 47 the quad's selection done (its
         # last workgroup; an older launch's stamp is earlier than this one's)
-        sel = np.frombuffer(raw, dtype=np.uint64).reshape(n_wgs, 64).astype(np.int64)[:, 32:48]
+        sel = np.frombuffer(raw, dtype=np.uint64).reshape(n_wgs, 64).astype(np.int64)[:, 32:60]
         sel = sel[(sel[:, 0] > 0) & (sel[:, 3] > 0)]
         if len(sel):
             t0s = sel[:, 0].min()
@@ -809,11 +809,30 @@ def run_phase_stamps(args, torch, dev):
                 "last_batch": pq(us((sel[:, 3:7] - sel[:, 11:15]).ravel())),
                 "rescore_and_append": pq(us(done - sel[:, 2])),
                 "arrival_and_selection": pq(us(sel[selected, 15] - done[selected])) if selected.any() else None,
+                # each wave's first batch (slots 48+w begun, 52+w rescored, 56+w slots reserved), where
+                # it ran in this launch (its stamps after the wave's query operands)
+                **first_batch_phases(sel, us, pq),
                 "last_done": round(float(us(end - t0s)), 3),
                 "start_after_attention_output": (round(float(us(t0s - merged[:, 22].max())), 3)
                                                  if len(merged) else None),
             }
     print(json.dumps(out), flush=True)
+
+
+def first_batch_phases(sel, us, pq):
+    """The top-K candidates kernel's first rescoring batch per wave, from
+    its phase stamps (columns relative to slot 32): 16+w begun, 20+w
+    rescored (loads and matrix instructions), 24+w slots reserved (one
+    atomic per head); a wave's stamps count only where they follow its
+    query-operand stamp (7+w) of this launch."""
+    begun, resc, resv, qop = sel[:, 16:20], sel[:, 20:24], sel[:, 24:28], sel[:, 7:11]
+    ok = (begun > qop) & (resc > begun) & (resv > resc)
+    if not ok.any():
+        return {}
+    return {"first_batch_waves": int(ok.sum()),
+            "first_batch_rescore": pq(us((resc - begun)[ok])),
+            "first_batch_slot_reservation": pq(us((resv - resc)[ok])),
+            "first_batch_begun_after_query": pq(us((begun - qop)[ok]))}
 
 
 def config_handles(torch, dev, ext, name, seed, spikes):

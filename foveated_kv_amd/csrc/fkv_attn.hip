@@ -321,7 +321,9 @@ struct SelectArgs {
 
 // Phase stamps of the candidates kernel (the -DFKV_PHASE_STAMPS build):
 // slots 32 entry, 33 tile maxima staged, 34 cuts known, 35 + w wave w done,
-// 39 + w wave w's query operands loaded, 43 + w wave w's last batch begun.
+// 39 + w wave w's query operands loaded, 43 + w wave w's last batch begun,
+// 47 the quad's selection done (its last workgroup), and of wave w's first
+// batch: 48 + w begun, 52 + w rescored, 56 + w its slots reserved.
 #ifdef FKV_PHASE_STAMPS
 #define FKV_SEL_STAMP(cond, slot)                                                                            \
     do {                                                                                                    \
@@ -349,6 +351,32 @@ constexpr int kSelWaves = 4;
 // same selection).
 constexpr int kSelRegs = 32;
 constexpr int kCutLowBits = 12;
+
+// Sum of v over the wave, in every lane (DPP row rotations and lane-half
+// swaps, no LDS).
+__device__ inline int wave_sum_i32(int v) {
+    v += (int)row_ror<1>((uint32_t)v);
+    v += (int)row_ror<2>((uint32_t)v);
+    v += (int)row_ror<4>((uint32_t)v);
+    v += (int)row_ror<8>((uint32_t)v);
+    LanePair p = swap16((uint32_t)v);
+    v = (int)p.a + (int)p.b;
+    p = swap32((uint32_t)v);
+    return (int)p.a + (int)p.b;
+}
+
+// Largest uint32 over the wave, in every lane (DPP row rotations and
+// lane-half swaps, no LDS).
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, row_ror<1>(v));
+    v = max(v, row_ror<2>(v));
+    v = max(v, row_ror<4>(v));
+    v = max(v, row_ror<8>(v));
+    LanePair p = swap16(v);
+    v = max(p.a, p.b);
+    p = swap32(v);
+    return max(p.a, p.b);
+}
 
 // fp32 -> uint32 with the same order (no NaN among scores) and back.
 __device__ inline uint32_t fkey(float f) {
@@ -388,13 +416,9 @@ __device__ inline void rescore_tiles(const SelectArgs& a, int64_t bkv, const int
     }
     // one round trip for the batch: every load is issued before the first
     // use (the compiler would otherwise hoist the first conversions and
-    // MFMAs between the loads and wait for the first ones early); the empty
-    // asm statements tie each value's uses to a point after all loads
-#pragma unroll
-    for (int n = 0; n < N; n++)
-#pragma unroll
-        for (int c = 0; c < D / 16; c++)
-            asm volatile("" : "+v"(kc[n][c].x), "+v"(kc[n][c].y), "+v"(kc[n][c].z), "+v"(kc[n][c].w)::"memory");
+    // MFMAs between the loads and wait for the first ones early); nothing
+    // is scheduled across the barrier
+    __builtin_amdgcn_sched_barrier(0);
     fkv_f4 acc[N];
 #pragma unroll
     for (int n = 0; n < N; n++) acc[n] = fkv_f4{0.f, 0.f, 0.f, 0.f};
@@ -453,18 +477,16 @@ __device__ inline void wave_sort(float& s, int& t, int lane) {
 // -inf when at most K maxima clear th.  The maxima are held as keys in
 // registers (0 for those at or below th, or past the far tier: below every
 // trial) and copied to the LDS row `lds` (NSL x 64 entries, -inf past the
-// far tier) for the rescoring.  The loads are buffer loads bounded by the
-// far tier (past it they read 0 without touching memory), so none sits
-// behind a branch and all are in flight at once: guarded loads had been
-// compiled as one branch, load and wait each, a round trip per 64 tiles.
-// A count is one compare per register, its ballot's population count and a
-// scalar sum: no cross-lane data movement, no branches.
+// far tier) for the rescoring.  raw: the lane's maxima r * 64 + lane, loaded
+// at the kernel's entry by buffer loads bounded by the far tier (past it
+// they read 0 without touching memory), so none sits behind a branch and
+// all are in flight at once (guarded loads had been compiled as one
+// branch, load and wait each, a round trip per 64 tiles).
+// A count is one compare and add per register and one wave sum on DPP
+// (per-register ballots, each a vector-to-scalar round trip through VCC,
+// were twice as slow per step).
 template <int NSL>
-__device__ inline float cut_search(const float* tm, int ntf, float th, int K, int lane, float* lds) {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)tm, (short)0, ntf * 4, 0x00020000);
-    uint32_t raw[NSL];
-#pragma unroll
-    for (int r = 0; r < NSL; r++) raw[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, (r * kWave + lane) * 4, 0, 0);
+__device__ inline float cut_search(const uint32_t (&raw)[kSelRegs], int ntf, float th, int K, int lane, float* lds) {
     uint32_t kv[NSL];
 #pragma unroll
     for (int r = 0; r < NSL; r++) {
@@ -476,12 +498,23 @@ __device__ inline float cut_search(const float* tm, int ntf, float th, int K, in
     auto count_at_least = [&](uint32_t trial) {
         int c = 0;
 #pragma unroll
-        for (int r = 0; r < NSL; r++) c += (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(kv[r] >= trial));
-        return c;
+        for (int r = 0; r < NSL; r++) c += kv[r] >= trial ? 1 : 0;
+        return __builtin_amdgcn_readfirstlane(wave_sum_i32(c));
     };
     if (count_at_least(1u) <= K) return -INFINITY;
-    uint32_t x = 0;
-    for (int bit = 31; bit >= kCutLowBits; bit--) {
+    // every key above th lies in [fkey(th) + 1, the largest key]: the bits
+    // above the highest one where the two bounds differ are the cut's too
+    // (a trial with such a bit set counts every key or none), so the
+    // search starts below them
+    uint32_t kmax = 0;
+#pragma unroll
+    for (int r = 0; r < NSL; r++) kmax = kv[r] > kmax ? kv[r] : kmax;
+    kmax = __builtin_amdgcn_readfirstlane(wave_max_u32(kmax));
+    const uint32_t diff = (fkey(th) + 1u) ^ kmax;
+    const int top = diff ? 31 - __builtin_clz(diff) : -1;  // the highest differing bit
+    uint32_t x = top < 0 ? kmax : top >= 31 ? 0u : kmax & ~((2u << top) - 1u);
+    x &= ~((1u << kCutLowBits) - 1u);
+    for (int bit = top < 31 ? top : 31; bit >= kCutLowBits; bit--) {
         const uint32_t trial = x | (1u << bit);
         if (count_at_least(trial) >= K) x = trial;
     }
@@ -636,6 +669,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     constexpr int NS = D / 4, NR = 4;  // tiles rescored together
     __shared__ float thr_s[4], cut_s[4];
     __shared__ int fl_s[4], last_s;
+    __shared__ uint64_t cmask_s[kSelStage / kWave];  // candidate tiles per 64-tile chunk (staged tiers)
     __shared__ float tm_s[4][kSelStage];
     const int quad = blockIdx.x / kSelParts, part = blockIdx.x % kSelParts, kvh = blockIdx.y, b = blockIdx.z;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = threadIdx.x % kWave;
@@ -645,6 +679,20 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
     const int K = a.K, ntf = a.ntf;
     const bool staged = ntf <= kSelStage;
     FKV_SEL_STAMP(threadIdx.x == 0, 0);
+    // the rescoring's query operands and (tiers of at most kSelRegs x 64
+    // tiles) the cut search's tile maxima, head `wave`'s, in flight with the
+    // thresholds' and flags' loads
+    fkv_h4 qv[NS];
+    load_qv<D>(a, o0, quad, lane, qv);
+    const bool regs = ntf <= kWave * kSelRegs;
+    uint32_t tmr[kSelRegs];
+    {
+        const bool own = regs && 4 * quad + wave < a.G;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.tmax + (o0 + wave) * ntf), (short)0, own ? ntf * 4 : 0, 0x00020000);
+#pragma unroll
+        for (int r = 0; r < kSelRegs; r++) tmr[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, (r * kWave + lane) * 4, 0, 0);
+    }
     if (threadIdx.x < 4) {
         const int jj = threadIdx.x;
         const bool live = 4 * quad + jj < a.G;
@@ -657,9 +705,8 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         if (part == 0) select_head<D>(a, quad, kvh, b, wave, lane, INFINITY);
         return;
     }
-    // the register path: each flagged head's wave loads its own maxima (and
-    // writes the LDS copy the rescoring reads) in the cut search below
-    const bool regs = ntf <= kWave * kSelRegs;
+    // the register path: each flagged head's wave writes the LDS copy of its
+    // maxima that the rescoring reads in the cut search below
     // the tile maxima of the quad's heads that exist (4 quad + jj < G) as one
     // bounded buffer: loads past them read 0 without touching memory, so
     // none needs a branch (a guarded load compiles to a branch, the load and
@@ -690,10 +737,9 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         const float th = thr_s[wave];
         float cut = -INFINITY;
         if (regs) {
-            const float* tm = a.tmax + (o0 + wave) * ntf;
-            if (ntf <= 8 * kWave) cut = cut_search<8>(tm, ntf, th, K, lane, tm_s[wave]);
-            else if (ntf <= 16 * kWave) cut = cut_search<16>(tm, ntf, th, K, lane, tm_s[wave]);
-            else cut = cut_search<kSelRegs>(tm, ntf, th, K, lane, tm_s[wave]);
+            if (ntf <= 8 * kWave) cut = cut_search<8>(tmr, ntf, th, K, lane, tm_s[wave]);
+            else if (ntf <= 16 * kWave) cut = cut_search<16>(tmr, ntf, th, K, lane, tm_s[wave]);
+            else cut = cut_search<kSelRegs>(tmr, ntf, th, K, lane, tm_s[wave]);
         } else {
             int above = 0;
             for (int t = lane; t < ntf; t += kWave) above += tmv(wave, t) > th;
@@ -725,8 +771,6 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         ct[jj] = cut_s[jj];
         fl[jj] = fl_s[jj];
     }
-    fkv_h4 qv[NS];
-    load_qv<D>(a, o0, quad, lane, qv);
     const float far_scale = a.inv_sqrt_d * (a.kscale ? a.kscale[bkv] : 1.0f);
     FKV_SEL_STAMP(lane == 0, 7 + wave);
     // the quad's candidate pairs (heads that exist) as bounded buffers
@@ -736,16 +780,20 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         __builtin_amdgcn_make_buffer_rsrc((void*)(a.cand_t + o0 * a.cap), (short)0, live * a.cap * 4, 0x00020000);
     // ---- B: this wave's candidate tiles (every kSelParts * kSelWaves-th), NR at a time ----
     const int gw = part * kSelWaves + wave, nw = kSelParts * kSelWaves;
-    int r = 0, np = 0;  // candidates seen (the same in every wave of the quad); tiles pending
+    int np = 0;  // tiles pending
+    int nfl = 0;        // batches flushed (the phase stamps time the first)
+    (void)nfl;
     int pend[NR];
 #pragma unroll
     for (int n = 0; n < NR; n++) pend[n] = -1;
-    auto flush = [&](int count) {
+    auto flush = [&](int count) __attribute__((always_inline)) {
         int tl[NR];
 #pragma unroll
         for (int n = 0; n < NR; n++) tl[n] = n < count ? pend[n] : pend[0];
         float sv[NR][4];
+        FKV_SEL_STAMP(lane == 0 && nfl == 0, 16 + wave);
         rescore_tiles<D, NR>(a, bkv, tl, qv, far_scale, lane, sv);
+        FKV_SEL_STAMP(lane == 0 && nfl == 0, 20 + wave);
         // the lane's candidates of the batch
         uint32_t pm = 0;
 #pragma unroll
@@ -774,6 +822,8 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
         if (lane < 4 && tot > 0) base = atomicAdd(a.cand_n + o0 + lane, tot);  // lane j < 4: head j
         const int b0 = __builtin_amdgcn_readlane(base, 0), b1 = __builtin_amdgcn_readlane(base, 1);
         const int b2 = __builtin_amdgcn_readlane(base, 2), b3 = __builtin_amdgcn_readlane(base, 3);
+        FKV_SEL_STAMP(lane == 0 && nfl == 0, 24 + wave);
+        nfl++;
         if (pm == 0) return;
         int slot = (j == 0 ? b0 : j == 1 ? b1 : j == 2 ? b2 : b3) + pre;
 #pragma unroll
@@ -790,42 +840,85 @@ __global__ __launch_bounds__(64 * kSelWaves) void spike_candidates_kernel(Select
                     slot++;
                 }
     };
-    for (int c0 = 0; c0 < ntf; c0 += kWave) {
-        const int tl = c0 + lane;
-        // the four heads' maxima of the lane's tile: LDS reads issued together
-        // when staged (a run-time choice of address space inside one load
-        // would make it a generic load waiting on both counters)
-        float v[4];
-        if (staged) {
+    // queue one of this wave's tiles; a full batch is rescored at once
+    auto take = [&](int tile) __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < NR; n++)
+            if (n == np) pend[n] = tile;
+        if (++np == NR) {
+            flush(NR);
+            np = 0;
+        }
+    };
+    if (staged) {
+        // B1: each 64-tile chunk's candidate tiles as a mask, the chunks
+        // shared among the workgroup's waves (at most 64 chunks)
+        const int nch = (ntf + kWave - 1) / kWave;
+        for (int c = wave; c < nch; c += kSelWaves) {
+            const int tl = c * kWave + lane;
+            float v[4];
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) v[jj] = tm_s[jj][tl < ntf ? tl : 0];
-        } else {
+            bool cand = false;
+            if (tl < ntf) {
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) cand |= fl[jj] && v[jj] > th[jj] && v[jj] >= ct[jj];
+            }
+            const uint64_t m = __builtin_amdgcn_ballot_w64(cand);
+            if (lane == 0) cmask_s[c] = m;
+        }
+        __syncthreads();
+        // B2: lane c holds chunk c's mask and the candidates of the chunks
+        // before it (a bit-sliced prefix count: one ballot per count bit);
+        // candidate rho (in tile order) is the nth set bit of its chunk's
+        // mask, found by the lane whose bit it is
+        const uint64_t mc = lane < nch ? cmask_s[lane] : 0ull;
+        const int cnt = (int)__builtin_popcountll(mc);
+        int excl = 0;
+#pragma unroll
+        for (int bb = 0; bb < 7; bb++) {
+            const uint64_t bm = __builtin_amdgcn_ballot_w64((cnt >> bb) & 1);
+            excl += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u))
+                    << bb;
+        }
+        const int total = __builtin_amdgcn_readlane(excl + cnt, kWave - 1);
+        for (int rho = gw; rho < total; rho += nw) {
+            const int c = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(excl + cnt > rho));
+            const int nth = rho - __builtin_amdgcn_readlane(excl, c);
+            const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)mc, c);
+            const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(mc >> 32), c);
+            const uint64_t m = ((uint64_t)hi << 32) | lo;
+            const bool hit = ((m >> lane) & 1ull) &&
+                             (int)__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u)) == nth;
+            take(c * kWave + (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(hit)));
+        }
+    } else {
+        // far tiers past the LDS stage: one chunk at a time, the maxima read
+        // from memory; the wave takes the candidates whose rank (in tile
+        // order) is gw mod nw
+        int r = 0;  // candidates seen (the same in every wave of the quad)
+        for (int c0 = 0; c0 < ntf; c0 += kWave) {
+            const int tl = c0 + lane;
+            float v[4];
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {
                 const uint32_t raw = __builtin_amdgcn_raw_buffer_load_b32(qrs, (jj * ntf + tl) * 4, 0, 0);
                 v[jj] = fl[jj] && tl < ntf ? __uint_as_float(raw) : -INFINITY;
             }
-        }
-        bool cand = false;
-        if (tl < ntf) {
+            bool cand = false;
+            if (tl < ntf) {
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) cand |= fl[jj] && v[jj] > th[jj] && v[jj] >= ct[jj];
-        }
-        const uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
-        // this wave's candidates of the chunk: rank r + (candidates in lower lanes) = gw mod nw
-        const int rank = r + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-        uint64_t mine = __builtin_amdgcn_ballot_w64(cand && rank % nw == gw);
-        r += (int)__builtin_popcountll(mask);
-        while (mine) {
-            const int bit = (int)__builtin_ctzll(mine);
-            mine &= mine - 1;
-#pragma unroll
-            for (int n = 0; n < NR; n++)
-                if (n == np) pend[n] = c0 + bit;
-            if (++np == NR) {
-                flush(NR);
-                np = 0;
+                for (int jj = 0; jj < 4; jj++) cand |= fl[jj] && v[jj] > th[jj] && v[jj] >= ct[jj];
+            }
+            const uint64_t mask = __builtin_amdgcn_ballot_w64(cand);
+            const int rank = r + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+            uint64_t mine = __builtin_amdgcn_ballot_w64(cand && rank % nw == gw);
+            r += (int)__builtin_popcountll(mask);
+            while (mine) {
+                const int bit = (int)__builtin_ctzll(mine);
+                mine &= mine - 1;
+                take(c0 + bit);
             }
         }
     }
