@@ -554,6 +554,7 @@ def run_e2e(args, torch, dev):
     promotion of exact fp16 rows from the pinned host archive -- on the
     device, and again with a host-side drain for comparison.  Prints one JSON
     line: us per decode step of the graph-replayed device-drain loop, with
+    the same loop reading the archive from HBM instead of pinned host memory,
     the eager device-drain loop, the host-drain loop and the reference's
     single-token drain (spike_k 1, budget 8) beside it, and the promotions
     per step of each."""
@@ -629,20 +630,22 @@ def run_e2e(args, torch, dev):
                 "host_call_us": t_call / steps * 1e6, "host_drain_us": t_drain / steps * 1e6,
                 "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
 
-    def loop_graph(kk, bud):
+    def loop_graph(kk, bud, hbm_archive=False):
         """The device-drain loop with the decode step captured once in a HIP
         graph: with n (a device int32) the step's decode-row count, gather the
         query of step n - 1, attention over the fixed-capacity decode buffer,
         the drain kernel with n as its step (the filter only compares steps,
         so the +1 offset changes nothing), which then advances n.  Step 0
         runs eagerly (it sizes the workspaces), steps 1.. are graph replays
-        with nothing read back."""
+        with nothing read back.  hbm_archive: the archive rows stay in device
+        memory (register_archive_tensors(device=True)) instead of pinned host
+        memory."""
         t0 = time.perf_counter()
         cl, h = compress(kk)
         torch.cuda.synchronize()
         compress_ms = (time.perf_counter() - t0) * 1e3
         pipe = PromotionPipeline(1, cooldown_steps=5, max_per_drain=bud, spike_k=kk)
-        pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+        pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx, device=hbm_archive)
         pipe.register_blob(0, h)
         n_d = torch.ones(1, dtype=torch.int32, device=dev)
         q1 = torch.cat([qs[:1], qs])  # row n holds the query of step n - 1
@@ -672,6 +675,7 @@ def run_e2e(args, torch, dev):
     dres = loop(True, spike_k, budget)
     hres = loop(False, spike_k, budget)
     gres = loop_graph(spike_k, budget)
+    hbres = loop_graph(spike_k, budget, hbm_archive=True)
     g1res = loop_graph(1, 8) if spike_k != 1 or budget != 8 else gres
     cl, h = dres["cl"], dres["h"]
     # device time of the attention call on the final state (queued back to back)
@@ -707,6 +711,9 @@ def run_e2e(args, torch, dev):
                                                     "drain_launch": round(dres["host_drain_us"], 2)},
                                "same_promotions": gres["stats"] == dres["stats"]
                                and gres["near_valid_end"] == dres["near_valid_end"]},
+        "archive_in_hbm": {"us_per_step": round(hbres["us_per_step"], 2),
+                           "same_promotions": hbres["stats"] == gres["stats"]
+                           and hbres["near_valid_end"] == gres["near_valid_end"]},
         "reference_single_token": {"spike_k": 1, "budget_per_drain": 8,
                                    "us_per_step": round(g1res["us_per_step"], 2),
                                    "promotions_per_step": round(g1res["stats"]["promotions_completed"] / steps, 3),

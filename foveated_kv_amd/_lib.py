@@ -118,6 +118,7 @@ SIGNATURES = {
     "fkv_promoter_create": (ctypes.c_int, [I32, I32, I32, ctypes.POINTER(P)]),
     "fkv_promoter_set_spike_k": (ctypes.c_int, [P, I32]),
     "fkv_promoter_register_archive": (ctypes.c_int, [P, I32, P, P, I32, I32, I32, I32, P, I32]),
+    "fkv_promoter_register_archive_device": (ctypes.c_int, [P, I32, P, P, I32, I32, I32, I32, P]),
     "fkv_promoter_register_archive_files": (ctypes.c_int, [P, I32, ctypes.c_char_p, ctypes.c_char_p, I32, I32,
                                                            I32, P]),
     "fkv_promoter_register_handle": (ctypes.c_int, [P, I32, P, P]),

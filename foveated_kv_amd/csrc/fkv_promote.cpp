@@ -37,10 +37,11 @@ using fkv::set_error;
 namespace {
 
 struct Archive {
-    const uint16_t* k = nullptr;  // [B_arc][Hkv][S_arc][D] fp16 (host)
+    const uint16_t* k = nullptr;  // [B_arc][Hkv][S_arc][D] fp16 (host, or device memory when `device`)
     const uint16_t* v = nullptr;
     void* owned_k = nullptr;  // pinned copies owned by the pipeline
     void* owned_v = nullptr;
+    bool device = false;      // rows in device memory, borrowed (fkv_promoter_register_archive_device)
     int B = 0, Hkv = 0, S = 0, D = 0;
     std::vector<std::unordered_map<int32_t, int32_t>> pos_to_local;  // [Hkv]: position -> archive row
 };
@@ -463,8 +464,9 @@ int ensure_dev_drain(fkv_promoter* p, int layer, hipStream_t st) {
     DevDrain& d = p->dev[layer];
     if (d.last_step) return FKV_OK;
     const Archive& a = p->arch[layer];
-    if (!a.owned_k || !a.owned_v)
-        return set_error("fkv_promoter_drain_device: the layer's archive is not in pipeline-owned pinned memory");
+    if (!a.device && (!a.owned_k || !a.owned_v))
+        return set_error("fkv_promoter_drain_device: the layer's archive is neither in pipeline-owned pinned memory "
+                         "nor in device memory");
     int maxpos = -1;
     for (const auto& m : a.pos_to_local)
         for (const auto& kv : m) maxpos = kv.first > maxpos ? kv.first : maxpos;
@@ -482,10 +484,10 @@ int ensure_dev_drain(fkv_promoter* p, int layer, hipStream_t st) {
     if (!rc) rc = check_hip(hipMemcpy(d.last_step, ls.data(), ls.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
     if (!rc) rc = check_hip(hipMemset(d.promoted, 0, (size_t)a.Hkv * (d.words > 0 ? d.words : 1) * 4), "hipMemset");
     if (!rc) rc = check_hip(hipMemcpy(d.pos_to_local, p2l.data(), p2l.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
-    void* dk = nullptr;
-    void* dv = nullptr;
-    if (!rc) rc = check_hip(hipHostGetDevicePointer(&dk, a.owned_k, 0), "hipHostGetDevicePointer");
-    if (!rc) rc = check_hip(hipHostGetDevicePointer(&dv, a.owned_v, 0), "hipHostGetDevicePointer");
+    void* dk = (void*)a.k;  // a device archive is read in place
+    void* dv = (void*)a.v;
+    if (!rc && !a.device) rc = check_hip(hipHostGetDevicePointer(&dk, a.owned_k, 0), "hipHostGetDevicePointer");
+    if (!rc && !a.device) rc = check_hip(hipHostGetDevicePointer(&dv, a.owned_v, 0), "hipHostGetDevicePointer");
     if (rc) {
         if (d.last_step) (void)hipFree(d.last_step);
         if (d.promoted) (void)hipFree(d.promoted);
@@ -555,6 +557,34 @@ int fkv_promoter_register_archive(fkv_promoter* p, int32_t layer, const void* k,
     return FKV_OK;
 }
 
+int fkv_promoter_register_archive_device(fkv_promoter* p, int32_t layer, const void* k, const void* v, int32_t B,
+                                         int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx) {
+    if (!p) return set_error("fkv_promoter_register_archive_device: NULL pipeline");
+    if (layer < 0 || layer >= p->n_layers)
+        return set_error("fkv_promoter_register_archive_device: layer out of range");
+    if (B <= 0 || Hkv <= 0 || S_arc < 0 || D <= 0 || D % 8 != 0 || (S_arc > 0 && (!k || !v)))
+        return set_error("fkv_promoter_register_archive_device: bad shape or NULL rows");
+    hipPointerAttribute_t attr{};
+    if (S_arc > 0 && (hipPointerGetAttributes(&attr, k) != hipSuccess || attr.type != hipMemoryTypeDevice ||
+                      hipPointerGetAttributes(&attr, v) != hipSuccess || attr.type != hipMemoryTypeDevice)) {
+        (void)hipGetLastError();
+        return set_error("fkv_promoter_register_archive_device: the rows are not in device memory");
+    }
+    Archive a;
+    a.B = B;
+    a.Hkv = Hkv;
+    a.S = S_arc;
+    a.D = D;
+    a.k = (const uint16_t*)k;
+    a.v = (const uint16_t*)v;
+    a.device = true;
+    build_positions(a, archive_idx);
+    free_dev_drain(p, layer);
+    free_archive(p->arch[layer]);
+    p->arch[layer] = std::move(a);
+    return FKV_OK;
+}
+
 int fkv_promoter_register_archive_files(fkv_promoter* p, int32_t layer, const char* path_k, const char* path_v,
                                         int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx) {
     if (!p || !path_k || !path_v) return set_error("fkv_promoter_register_archive_files: NULL argument");
@@ -581,6 +611,7 @@ int fkv_promoter_register_archive_files(fkv_promoter* p, int32_t layer, const ch
             if (fp) fclose(fp);
             if (got != bytes) {  // the layer is left without an archive, as in the reference
                 free_archive(a);
+                free_dev_drain(p, layer);  // a queued device drain may still read the old rows
                 free_archive(p->arch[layer]);
                 return set_error(std::string("fkv_promoter_register_archive_files: cannot read ") +
                                  std::to_string(bytes) + " bytes from " + paths[f]);
@@ -795,6 +826,7 @@ int fkv_promoter_flush(fkv_promoter* p) {
             const Item& it = per[l][i];
             hs[2 * i] = it.head;
             hs[2 * i + 1] = it.slot;
+            if (a.device) continue;  // copied device to device below
             for (int b = 0; b < a.B; b++) {
                 const size_t src = (((size_t)b * a.Hkv + it.head) * a.S + it.arc_local) * row;
                 memcpy(rk + (i * a.B + b) * row, a.k + src, row * 2);
@@ -804,6 +836,25 @@ int fkv_promoter_flush(fkv_promoter* p) {
     }
     int rc = check_hip(hipMemcpyAsync(p->stage_d, p->stage_h, total, hipMemcpyHostToDevice, p->side),
                        "hipMemcpyAsync(promotion rows)");
+    // rows of device-resident archives: device-to-device into the device
+    // staging, after (on the same stream) the copy of the host staging
+    for (int l = 0; l < p->n_layers && !rc; l++) {
+        const Archive& a = p->arch[l];
+        if (per[l].empty() || !a.device) continue;
+        const size_t n = per[l].size(), row = (size_t)a.D;
+        uint16_t* rk = (uint16_t*)(p->stage_d + off[l] + align16(n * 8));
+        uint16_t* rv = (uint16_t*)((uint8_t*)rk + align16(n * a.B * row * 2));
+        for (size_t i = 0; i < n && !rc; i++)
+            for (int b = 0; b < a.B && !rc; b++) {
+                const size_t src = (((size_t)b * a.Hkv + per[l][i].head) * a.S + per[l][i].arc_local) * row;
+                rc = check_hip(hipMemcpyAsync(rk + (i * a.B + b) * row, a.k + src, row * 2, hipMemcpyDeviceToDevice,
+                                              p->side), "hipMemcpyAsync(device archive row)");
+                if (!rc)
+                    rc = check_hip(hipMemcpyAsync(rv + (i * a.B + b) * row, a.v + src, row * 2,
+                                                  hipMemcpyDeviceToDevice, p->side),
+                                   "hipMemcpyAsync(device archive row)");
+            }
+    }
     if (!rc) rc = check_hip(hipEventRecord(p->staged, p->side), "hipEventRecord");
     if (rc) return rc;
     p->staged_pending = true;

@@ -55,6 +55,7 @@ class PromotionPipeline:
         self.spike_k = int(spike_k)
         self.n_layers = int(n_layers)
         self._keep = {}  # layer -> host arrays the C side borrows
+        self._device_archives = {}  # layer -> GPU archive rows the C side borrows
         self._handles = {}
         self._stopped = False
 
@@ -70,26 +71,48 @@ class PromotionPipeline:
         disk_archive.py:127-185).  Like the reference, an unusable archive is
         not an error: the layer is left without one and its drains are no-ops."""
         idx = _host_i32(archive_idx).reshape(-1)
+        self._device_archives.pop(int(layer_idx), None)
         rc = self._lib.fkv_promoter_register_archive_files(self._h, int(layer_idx), str(path_k).encode(),
                                                            str(path_v).encode(), int(H_kv), int(S_arc), int(D),
                                                            _np_ptr(idx))
         return rc == _lib.FKV_OK
 
-    def register_archive_tensors(self, layer_idx, archive_k, archive_v, archive_idx):
+    def register_archive_tensors(self, layer_idx, archive_k, archive_v, archive_idx, device=False):
         """From archive rows (B, H_kv, S_arc, D) fp16 on any device (e.g. a
         compressed layer's ``archive_k/v``) and ``archive_idx`` (B, H_kv, S_arc)
-        or (H_kv, S_arc); the rows are copied into pinned host memory."""
-        k = archive_k.detach().to("cpu", torch.float16).contiguous()
-        v = archive_v.detach().to("cpu", torch.float16).contiguous()
+        or (H_kv, S_arc).  By default the rows are copied into pinned host
+        memory, the reference's placement.  device=True keeps them in GPU
+        memory (fp16, contiguous; the pipeline holds a reference), so the
+        device drain reads promoted rows from HBM instead of over PCIe
+        (fkv_promoter_register_archive_device; no counterpart in the
+        reference)."""
+        if device:
+            if not (archive_k.is_cuda and archive_v.is_cuda):
+                raise ValueError("register_archive_tensors(device=True): the rows must be GPU tensors")
+            k = archive_k.detach().to(torch.float16).contiguous()
+            v = archive_v.detach().to(torch.float16).contiguous()
+        else:
+            k = archive_k.detach().to("cpu", torch.float16).contiguous()
+            v = archive_v.detach().to("cpu", torch.float16).contiguous()
         if k.dim() == 3:
             k, v = k[None], v[None]
         B, H, S, D = k.shape
         idx = _host_i32(archive_idx)
         if idx.ndim == 3:
             idx = np.ascontiguousarray(idx[0])
-        check(self._lib.fkv_promoter_register_archive(self._h, int(layer_idx), ctypes.c_void_p(k.data_ptr()),
-                                                      ctypes.c_void_p(v.data_ptr()), B, H, S, D, _np_ptr(idx), 1),
-              "fkv_promoter_register_archive")
+        if device:
+            check(self._lib.fkv_promoter_register_archive_device(self._h, int(layer_idx),
+                                                                 ctypes.c_void_p(k.data_ptr()),
+                                                                 ctypes.c_void_p(v.data_ptr()), B, H, S, D,
+                                                                 _np_ptr(idx)),
+                  "fkv_promoter_register_archive_device")
+            self._device_archives[int(layer_idx)] = (k, v)  # borrowed by the pipeline: kept alive here
+        else:
+            check(self._lib.fkv_promoter_register_archive(self._h, int(layer_idx), ctypes.c_void_p(k.data_ptr()),
+                                                          ctypes.c_void_p(v.data_ptr()), B, H, S, D, _np_ptr(idx),
+                                                          1),
+                  "fkv_promoter_register_archive")
+            self._device_archives.pop(int(layer_idx), None)
 
     def register_blob(self, layer_idx, info):
         """``info``: a FoveatedHandle or the BlobWriteInfo of one."""

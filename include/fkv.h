@@ -438,6 +438,18 @@ int fkv_promoter_register_archive(fkv_promoter* p, int32_t layer, const void* k,
                                   int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx,
                                   int32_t copy_to_pinned);
 
+/* register_archive with the rows [B_arc][Hkv][S_arc][D] fp16 already in
+ * device memory (e.g. the compress kernel's archive output), borrowed: they
+ * must stay valid while the layer is registered.  No counterpart in the
+ * reference, whose archive is host (on its platform, unified) memory: on
+ * MI355X the device drain reads a pinned host archive over PCIe, while HBM
+ * holds a model's whole archive (C5: 241 MB per layer); at C5 with 32
+ * tokens per head the drain kernel takes 7.6 us instead of 8.6.  The device
+ * drain reads the rows in place; the host drain copies them device to
+ * device.  D must be a multiple of 8. */
+int fkv_promoter_register_archive_device(fkv_promoter* p, int32_t layer, const void* k, const void* v, int32_t B_arc,
+                                         int32_t Hkv, int32_t S_arc, int32_t D, const int32_t* archive_idx);
+
 /* register_archive from the reference's on-disk archive files
  * (disk_archive.py:127-185: (Hkv, S_arc, D) fp16 raw, batch 0), read into
  * pinned host memory.  An unreadable file leaves the layer without an

@@ -264,21 +264,26 @@ def _layer(B, Hkv, D, S, seed, headroom_min=8):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("arc", ["pinned", "device"])
 @pytest.mark.parametrize("B", [1, 2])
-def test_promotion_rows_bit_exact_and_near_valid(orc, B):
+def test_promotion_rows_bit_exact_and_near_valid(orc, B, arc):
+    """The host drain + flush against the CPU restatement: promoted rows
+    bit-exact, near_valid and statistics equal, with the archive in pinned
+    host memory (the reference's placement) or in device memory (rows
+    copied device to device)."""
     import torch
 
     from foveated_kv_amd.promotion import PromotionPipeline
     from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
 
     Hkv, Hq, D, S = 2, 8, 128, 1000
-    print(f"promotion B={B} Hkv={Hkv} D={D} S={S}", flush=True)
+    print(f"promotion B={B} Hkv={Hkv} D={D} S={S} archive={arc}", flush=True)
     k, v, cl, h = _layer(B, Hkv, D, S, 31)
     tb = TierConfig(promo_headroom_min=8).tier_boundaries(S)
     _, far_idx = tier_index_tensors(tb, S, B, Hkv, "cpu")
     far_idx = far_idx.numpy()
     pipe = PromotionPipeline(1, cooldown_steps=0, max_per_drain=8)
-    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx, device=arc == "device")
     pipe.register_blob(0, h.get_blob_info())
     ref = opromo.Pipeline(1, 0, 8)
     ref.register_archive(0, cl.archive_k.cpu().numpy(), cl.archive_v.cpu().numpy(), far_idx[0])
@@ -375,27 +380,31 @@ def test_promotion_from_archive_files(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,cooldown,budget,headroom_min", [(1, 0, 8, 8), (2, 3, 2, 8), (1, 1, 8, 2), (3, 2, 3, 8)])
-def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroom_min):
+@pytest.mark.parametrize("B,cooldown,budget,headroom_min,arc", [(1, 0, 8, 8, "pinned"), (2, 3, 2, 8, "pinned"),
+                                                                (1, 1, 8, 2, "pinned"), (3, 2, 3, 8, "pinned"),
+                                                                (1, 0, 8, 8, "device"), (3, 2, 3, 8, "device")])
+def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroom_min, arc):
     """drain_spikes_device (filter + promotion in one kernel, spike outputs
     and far_idx in device memory) against the CPU restatement of the host
     drain + flush on random flag streams: same near tiers, near_valid and
     statistics.  Batches above 1 keep the step on the device and let the
-    drain advance it."""
+    drain advance it.  The archive rows come from pinned host memory or,
+    registered with device=True, from device memory."""
     import torch
 
     from foveated_kv_amd.promotion import PromotionPipeline
     from foveated_kv_amd.tier_cache import TierConfig, tier_index_tensors
 
     Hkv, Hq, D, S = 4, 16, 128, 900
-    print(f"device drain B={B} cooldown={cooldown} budget={budget} headroom_min={headroom_min}", flush=True)
+    print(f"device drain B={B} cooldown={cooldown} budget={budget} headroom_min={headroom_min} archive={arc}",
+          flush=True)
     k, v, cl, h = _layer(B, Hkv, D, S, 41, headroom_min=headroom_min)
     tb = TierConfig(promo_headroom_min=headroom_min).tier_boundaries(S)
     _, far_idx = tier_index_tensors(tb, S, B, Hkv, "cpu")
     far_idx = far_idx.numpy()
     fdev = torch.from_numpy(far_idx).cuda().contiguous()
     pipe = PromotionPipeline(1, cooldown_steps=cooldown, max_per_drain=budget)
-    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx, device=arc == "device")
     pipe.register_blob(0, h)
     ref = opromo.Pipeline(1, cooldown, budget)
     ref.register_archive(0, cl.archive_k.cpu().numpy(), cl.archive_v.cpu().numpy(), far_idx[0])
@@ -427,8 +436,10 @@ def test_device_drain_matches_host_restatement(orc, B, cooldown, budget, headroo
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,K,cooldown,budget", [(1, 4, 0, 8), (2, 32, 2, 40), (1, 32, 1, 5), (2, 6, 3, 64)])
-def test_device_drain_top_k_matches_host_restatement(orc, B, K, cooldown, budget):
+@pytest.mark.parametrize("B,K,cooldown,budget,arc", [(1, 4, 0, 8, "pinned"), (2, 32, 2, 40, "pinned"),
+                                                     (1, 32, 1, 5, "pinned"), (2, 6, 3, 64, "pinned"),
+                                                     (2, 32, 2, 40, "device")])
+def test_device_drain_top_k_matches_host_restatement(orc, B, K, cooldown, budget, arc):
     """The device drain with spike_k = K > 1 (each KV head's first flagged
     query head hands up to K tokens through the filter, the budget checked
     before each token) against the CPU restatement on random streams: spike
@@ -448,7 +459,7 @@ def test_device_drain_top_k_matches_host_restatement(orc, B, K, cooldown, budget
     far_idx = far_idx.numpy()
     fdev = torch.from_numpy(far_idx).cuda().contiguous()
     pipe = PromotionPipeline(1, cooldown_steps=cooldown, max_per_drain=budget, spike_k=K)
-    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx)
+    pipe.register_archive_tensors(0, cl.archive_k, cl.archive_v, far_idx, device=arc == "device")
     pipe.register_blob(0, h)
     ref = opromo.Pipeline(1, cooldown, budget, K)
     ref.register_archive(0, cl.archive_k.cpu().numpy(), cl.archive_v.cpu().numpy(), far_idx[0])
@@ -472,6 +483,29 @@ def test_device_drain_top_k_matches_host_restatement(orc, B, K, cooldown, budget
     assert np.array_equal(gv.cpu().numpy().view(np.uint16), near_v[0].view(np.uint16))
     assert pipe.get_stats() == ref.stats and ref.stats["promotions_completed"] > 0
     assert ref.stats["spikes_deduplicated"] > 0
+
+
+@pytest.mark.gpu
+def test_device_archive_rejects_host_rows():
+    """register_archive_tensors(device=True) takes GPU tensors only, and the
+    C entry point refuses rows that are not in device memory."""
+    import torch
+
+    from foveated_kv_amd.promotion import PromotionPipeline
+
+    pipe = PromotionPipeline(1)
+    k = torch.zeros((1, 2, 10, 64), dtype=torch.float16)
+    idx = np.arange(20, dtype=np.int32).reshape(2, 10)
+    with pytest.raises(ValueError):
+        pipe.register_archive_tensors(0, k, k, idx, device=True)
+    rc = pipe._lib.fkv_promoter_register_archive_device(pipe._h, 0, ctypes.c_void_p(k.data_ptr()),
+                                                        ctypes.c_void_p(k.data_ptr()), 1, 2, 10, 64,
+                                                        idx.ctypes.data_as(ctypes.c_void_p))
+    assert rc != 0
+    kd = k.cuda()
+    assert pipe._lib.fkv_promoter_register_archive_device(pipe._h, 0, ctypes.c_void_p(kd.data_ptr()),
+                                                          ctypes.c_void_p(kd.data_ptr()), 1, 2, 10, 64,
+                                                          idx.ctypes.data_as(ctypes.c_void_p)) == 0
 
 
 @pytest.mark.gpu
