@@ -121,17 +121,15 @@ __device__ inline uint16_t load_as_f16(const void* p, int64_t i, int dtype) {
 // sketch MFMAs (tq_rot_index).
 struct TurboConsts {
     float alpha = 0.f, beta = 0.f, gamma = 0.f, delta = 0.f, lvh = 0.f, lvl = 0.f;
-    uint16_t* rot = nullptr;  // 8 * D * D bytes of fp16 operands
+    uint16_t* rot = nullptr;  // 4 * D * D bytes of fp16 operands
 };
 
-// Pi (mat 0) and S (mat 1) as fp16 pairs hi + lo / 1024 with hi = fp16(M)
-// and lo = fp16((M - hi) * 1024) (together ~22 significant bits; the 1024
-// keeps lo out of the fp16 subnormal range), laid out so that lane l of a
-// wave reads row i = 64 * rg + l of M, k-steps 2 * s2 and 2 * s2 + 1
-// (columns 8 * s2 .. 8 * s2 + 7), as one 16-byte load:
-//   [mat][part: 0 hi, 1 lo][s2 < D/8][i < D][8 halves]
-__host__ __device__ inline int64_t tq_rot_index(int D, int mat, int part, int i, int j) {
-    return ((((int64_t)mat * 2 + part) * (D / 8) + j / 8) * D + i) * 8 + j % 8;
+// Pi (mat 0) and S (mat 1) as fp16, laid out so that lane l of a wave
+// reads row i = 64 * rg + l of M, k-steps 2 * s2 and 2 * s2 + 1 (columns
+// 8 * s2 .. 8 * s2 + 7), as one 16-byte load:
+//   [mat][s2 < D/8][i < D][8 halves]
+__host__ __device__ inline int64_t tq_rot_index(int D, int mat, int i, int j) {
+    return (((int64_t)mat * (D / 8) + j / 8) * D + i) * 8 + j % 8;
 }
 
 }  // namespace fkv

@@ -2100,16 +2100,20 @@ __host__ __device__ inline FarPlan plan_far(int w, int n_waves, int nt_far, int 
 // q.Pi^T and q.S^T (foveated_attn.cpp:415-421) for the workgroup's heads on
 // the matrix cores.  Wave w < D/32 takes matrix mat and the 64 output dims
 // 64 * rg .. + 63 (lane l: output dim 64 * rg + l as the A row of
-// v_mfma_f32_4x4x4f16, the head quad's fp16 query as B); M = hi + lo / 1024
-// (tq_rot_index), two accumulator chains over the D/4 k-steps.  The
-// products of fp16 values are exact and summed in fp32.  Lane l ends with
+// v_mfma_f32_4x4x4f16, the head quad's fp16 query as B) with M in fp16
+// (tq_rot_index), one accumulator chain over the D/4 k-steps.  The products
+// of fp16 values are exact and summed in fp32; M's own fp16 rounding adds
+// at most about as much as the final rounding of the rotated query to fp16
+// (a lo correction, M - fp16(M), in a second chain had cost C4 1.1 us of
+// operand loads and matrix instructions for no visible parity change: C4
+// max-abs 1.6e-4 either way).  Lane l ends with
 // dims 64 * rg + 4 * (l / 4) .. + 3 of head l % 4, rounded to fp16 into the
 // qt operand layout; mat 0 also leaves q.Pi^T in fp32 in `qf` and alpha *
 // sum(q.Pi^T) per head in `rsum`.  Waves past D/32 only take part in the
 // barriers.  Must be entered by every thread of the workgroup.
 template <int D>
 struct TqRotation {
-    fkv_v4u hl[2][D / 8];  // [hi, lo][s2]: k-steps 2 * s2, 2 * s2 + 1 of the lane's row
+    fkv_v4u h[D / 8];  // [s2]: k-steps 2 * s2, 2 * s2 + 1 of the lane's row
 };
 
 // The wave's A operands, loaded together with the query (before any use);
@@ -2120,10 +2124,8 @@ __device__ inline void tq_rotation_load(const AttnArgs& a, TqRotation<D>& r, int
     if (wave >= WR) return;
     const int wr = wave % WR, mat = wr / RG, rg = wr % RG;
 #pragma unroll
-    for (int part = 0; part < 2; part++)
-#pragma unroll
-        for (int s2 = 0; s2 < D / 8; s2++)
-            r.hl[part][s2] = *(const fkv_v4u*)(a.tq_rot + tq_rot_index(D, mat, part, 64 * rg + lane, 8 * s2));
+    for (int s2 = 0; s2 < D / 8; s2++)
+        r.h[s2] = *(const fkv_v4u*)(a.tq_rot + tq_rot_index(D, mat, 64 * rg + lane, 8 * s2));
 }
 
 template <int D, int NQ, int WPG>
@@ -2135,25 +2137,22 @@ __device__ inline void tq_rotate_query(const AttnArgs& a, const TqRotation<D>& r
     const bool idle = wave >= WR;  // no operands loaded
 #pragma unroll 1
     for (int qd = 0; qd < NQ && !idle; qd++) {
-        fkv_f4 ch = fkv_f4{0.f, 0.f, 0.f, 0.f}, cl = fkv_f4{0.f, 0.f, 0.f, 0.f};
+        fkv_f4 ch = fkv_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s0 = 0; s0 < NS; s0 += 8) {
             fkv_h4 q8[8];
             qop.template readn<8>(qd, s0, q8);
 #pragma unroll
             for (int s = s0; s < s0 + 8; s++) {
-                const fkv_v4u& h = rot.hl[0][s / 2];
-                const fkv_v4u& l = rot.hl[1][s / 2];
+                const fkv_v4u& h = rot.h[s / 2];
                 const fkv_h4 ah = __builtin_bit_cast(fkv_h4, (s & 1) ? fkv_v2u{h.z, h.w} : fkv_v2u{h.x, h.y});
-                const fkv_h4 al = __builtin_bit_cast(fkv_h4, (s & 1) ? fkv_v2u{l.z, l.w} : fkv_v2u{l.x, l.y});
                 ch = mfma4_local(ah, q8[s - s0], ch);
-                cl = mfma4_local(al, q8[s - s0], cl);
             }
         }
         if (wave < WR) {
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[e] = fmaf(cl[e], 1.f / 1024.f, ch[e]);
+            for (int e = 0; e < 4; e++) v[e] = ch[e];
             const int sq = 16 * rg + blk;  // k-step of output dims 4 * sq .. 4 * sq + 3
             const uint32_t w0 = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
             const uint32_t w1 = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);

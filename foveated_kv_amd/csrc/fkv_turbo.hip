@@ -115,17 +115,14 @@ __global__ void tq_pack_sn_kernel(const void* __restrict__ vscale, const void* _
 }
 
 // out[j][i] = in[i][j] for a (D, D) fp32 matrix.
-// Pi and S -> the rotation MFMAs' fp16 hi / lo operands (tq_rot_index).
+// Pi and S -> the rotation MFMAs' fp16 operands (tq_rot_index).
 __global__ void rot_operand_kernel(const float* __restrict__ Pi, const float* __restrict__ S,
                                    uint16_t* __restrict__ rot, int D) {
     const int64_t n = 2 * (int64_t)D * D;
     for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
          e += (int64_t)gridDim.x * blockDim.x) {
         const int mat = (int)(e / ((int64_t)D * D)), i = (int)(e / D % D), j = (int)(e % D);
-        const float m = (mat ? S : Pi)[(int64_t)i * D + j];
-        const uint16_t hi = f2h(m);
-        rot[tq_rot_index(D, mat, 0, i, j)] = hi;
-        rot[tq_rot_index(D, mat, 1, i, j)] = f2h((m - h2f(hi)) * 1024.f);
+        rot[tq_rot_index(D, mat, i, j)] = f2h((mat ? S : Pi)[(int64_t)i * D + j]);
     }
 }
 
@@ -306,7 +303,7 @@ int fkv_turbo_create(fkv_attn** out, int32_t B, int32_t Hkv, int32_t D, int32_t 
     hipStream_t st = (hipStream_t)stream;
     fkv_attn* h = new fkv_attn();
     int rc = fkv::attn_begin(h, B, Hkv, D, Na, F, 1, near_k, near_v, near_dtype, near_valid, spike_margin, st);
-    if (!rc) rc = check_hip(hipMalloc(&h->tq.rot, (size_t)8 * D * D), "hipMalloc(rotation operands)");
+    if (!rc) rc = check_hip(hipMalloc(&h->tq.rot, (size_t)4 * D * D), "hipMalloc(rotation operands)");
     float cb[4] = {0.f, 0.f, 0.f, 0.f};
     if (!rc) {
         const int blk = 256;
