@@ -173,6 +173,14 @@ struct fkv_attn_impl {
     int* spk_arrive = nullptr;   // per (batch, KV head, head quad): workgroups done (zero between calls)
     float* spk_cand_s = nullptr; // per head: up to 64 * FKV_MAX_SPIKE_K candidate scores
     int* spk_cand_t = nullptr;   // ... and their tokens
+    // Every call reuses the workspace and the selection's buffers, so a call
+    // on another stream than the handle's last eager call first waits for
+    // that call's work (an event recorded after each eager call's launches;
+    // calls under graph capture neither wait nor record: a captured graph's
+    // replays are ordered by whoever launches them)
+    hipEvent_t order_ev = nullptr;
+    hipStream_t order_st = nullptr;
+    bool order_pending = false;
 };
 
 struct fkv_attn : fkv_attn_impl {};

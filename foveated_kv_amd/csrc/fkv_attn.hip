@@ -1413,6 +1413,13 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
     if (q_dtype == FKV_F16 && ((uintptr_t)query & 7) != 0)
         return set_error(name + ": an fp16 query must be 8-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    // order this call after the handle's last eager call when that ran on
+    // another stream (fkv_attn_impl::order_ev)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (int rc = check_hip(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing")) return rc;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (!capturing && h->order_pending && h->order_st != st)
+        if (int rc = check_hip(hipStreamWaitEvent(st, h->order_ev, 0), "hipStreamWaitEvent(order)")) return rc;
     const int G = Hq / L.Hkv;
     const bool topk = h->spike_k > 1;
     if (topk && no_alloc && h->spk_hq != Hq)
@@ -1561,7 +1568,15 @@ int attn_call(const char* fn, fkv_attn* h, const void* query, int32_t q_dtype, i
         if (L.D == 128) hipLaunchKernelGGL(fkv::spike_candidates_kernel<128>, cgrid, sblock, 0, st, sa);
         else hipLaunchKernelGGL(fkv::spike_candidates_kernel<64>, cgrid, sblock, 0, st, sa);
     }
-    return check_hip(hipGetLastError(), "attn_kernel launch");
+    if (int rc = check_hip(hipGetLastError(), "attn_kernel launch")) return rc;
+    if (capturing) return FKV_OK;
+    if (!h->order_ev)
+        if (int rc = check_hip(hipEventCreateWithFlags(&h->order_ev, hipEventDisableTiming), "hipEventCreate(order)"))
+            return rc;
+    if (int rc = check_hip(hipEventRecord(h->order_ev, st), "hipEventRecord(order)")) return rc;
+    h->order_st = st;
+    h->order_pending = true;
+    return FKV_OK;
 }
 
 int scratch_workspace(const std::string& name, fkv_attn* h, const fkv::LaunchPlan& p, int Hq, hipStream_t st,
@@ -1851,6 +1866,7 @@ void fkv_attn_destroy(fkv_attn* h) {
     if (h->qbuf) (void)hipFree(h->qbuf);
     if (h->arrive) (void)hipFree(h->arrive);
     if (h->tq.rot) (void)hipFree(h->tq.rot);
+    if (h->order_ev) (void)hipEventDestroy(h->order_ev);
     delete h;
 }
 

@@ -220,8 +220,11 @@ int fkv_turbo_compress_values(const void* values, int32_t dtype, int64_t n_token
  * Later calls with a different Hq return FKV_EINVAL (one handle serves one
  * query-head count, as a model layer does).  The first call is therefore
  * not capturable.  One handle owns one workspace and one set of split
- * arrival counters: calls on one handle must not overlap on two streams
- * (queue them on one stream, or order the streams). */
+ * arrival counters, which every call reuses: an eager call on another
+ * stream than the handle's last eager call first waits (hipStreamWaitEvent)
+ * for that call's work, so calls on one handle never overlap.  Calls under
+ * graph capture neither wait nor record: the replays of a captured graph,
+ * and eager calls beside them, are ordered by the caller. */
 int fkv_attn_call(fkv_attn* h, const void* query, int32_t q_dtype, int32_t Hq,
                   const void* decode_k, const void* decode_v, int32_t n_decode, void* out,
                   int32_t* spike_flags, int32_t* spike_tokens, void* stream);

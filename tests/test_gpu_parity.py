@@ -394,3 +394,41 @@ def test_xcd_local_merge_across_concurrent_streams(fkv, orc, B, Hq, Hkv, D, S, n
         for a, b in zip(o, ref):
             assert torch.equal(a, b)
     assert [h.dispatch_check() for h in hs] == [0, 0, 0]
+
+
+@pytest.mark.parametrize("K", [1, 8])
+def test_one_handle_called_from_three_streams(fkv, orc, K):
+    """One handle called from three streams, back to back without host
+    synchronisation: every call reuses the handle's split records, arrival
+    counters and (K > 1) selection buffers, so the library orders a call
+    after the handle's previous eager call when that ran on another stream;
+    every output equals the single-stream one bit for bit."""
+    from foveated_kv_amd import ext, synthetic
+
+    B, Hq, Hkv, D, S, n_dec = 1, 32, 8, 128, 4096, 64
+    _flush(f"one handle, 3 streams B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} n_dec={n_dec} spike_k={K}")
+    k, v = synthetic.make_kv(B, Hkv, S, D, 29)
+    q0 = synthetic.make_query(B, Hq, D, 29)
+    tb = orc.tier_boundaries(S)
+    synthetic.inject_spikes(k, q0, tb["mid_start"], tb["far_count"], 0.02, 29)
+    q = torch.from_numpy(q0).cuda()[:, :, None]
+    dk, dv = synthetic.make_decode(B, Hkv, n_dec, D, 29)
+    dkt, dvt = torch.from_numpy(dk).cuda(), torch.from_numpy(dv).cuda()
+    cl = ext.CompressHandle(_cfg(fkv)).compress_layer(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                                      with_archive=False)
+    h = ext.FoveatedHandle(cl.near_k, cl.near_v, cl.far_k, cl.far_v, cl.far_v_scale, cl.far_v_zero,
+                           cl.near_valid, spike_margin=10.0, spike_k=K)
+    ref = [t.clone() for t in h(q, dkt, dvt)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    outs = []
+    for _ in range(30):
+        for st in streams:
+            with torch.cuda.stream(st):
+                outs.append(h(q, dkt, dvt))
+    torch.cuda.synchronize()
+    for o in outs:
+        for a, b in zip(o, ref):
+            assert torch.equal(a, b)
+    if K > 1:
+        assert int(ref[1].sum()) > 0
