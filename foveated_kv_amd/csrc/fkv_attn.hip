@@ -646,14 +646,17 @@ __device__ inline void select_head(const SelectArgs& a, int quad, int kvh, int b
 // (among the tiles whose maximum clears the threshold): a tile holding one
 // of them has a maximum at least that token's score, and at most K - 1
 // tokens -- so at most K - 1 tiles -- score higher.  So, from the tile
-// maxima the attention kernel stored (staged in LDS):
+// maxima the attention kernel stored:
 //  A. wave j finds head j's cut, the K-th largest tile maximum above the
 //     threshold (a bitwise binary search on order-preserving keys), or -inf
 //     when at most K tiles clear the threshold (every workgroup of the
 //     quad computes the same cuts);
 //  B. the quad's kSelParts x 4 waves share out the tiles whose maximum
-//     clears some head's threshold and cut, rescore them four at a time
-//     (rescore_tiles: the attention kernel's bits) and append every token
+//     clears some head's threshold and cut by their rank in tile order
+//     (each 64-tile chunk's candidate mask computed once per workgroup,
+//     in LDS; wave gw takes ranks gw, gw + kSelParts * 4, ...), rescore
+//     them four at a time (rescore_tiles: the attention kernel's bits) and
+//     append every token
 //     above its head's threshold and at or above its cut to the head's
 //     candidate buffer in memory -- at least K tokens when the cut is set
 //     (each of the K tiles contributes its maximum), all of them
