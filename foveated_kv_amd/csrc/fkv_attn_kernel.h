@@ -107,8 +107,8 @@ struct AttnArgs {
     // keep their kernel-argument offsets).  Top-K spike selection (spike_k >
     // 1, else NULL): every far tile's maximum score per query head, (B*Hq,
     // tmax_stride = far tiles) fp32, and each head's spike threshold
-    // min_near + margin, (B*Hq) fp32; spike_select_kernel reads both after
-    // the launch
+    // min_near + margin, (B*Hq) fp32; the top-K candidates kernel reads
+    // both after the launch
     float* tmax;
     int tmax_stride;
     float* thr;
