@@ -216,6 +216,8 @@ def main():
     ap.add_argument("--phase-stamps", action="store_true",
                     help="per-workgroup phase timeline of --config's kernel from the phase-stamp build "
                          "(make -C foveated_kv_amd/csrc STAMPS=1)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the C5 end-to-end step of the default run (e2e_c5)")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip timing the other benchmark configurations (reported under other_configs)")
     ap.add_argument("--other-steps", type=int, default=30, help="timed steps per other configuration")
@@ -405,6 +407,14 @@ def main():
             print(f"[bench] {key}: {others[key]['us_per_layer']} us/layer, {others[key]['gbs']} GB/s",
                   file=sys.stderr, flush=True)
         result["other_configs"] = others
+    if not args.no_e2e and not args.no_other_configs:
+        # the C5 decode step end to end (attention, spike drain, promotion),
+        # graph-replayed, with C5's up to 32 tokens per head and with the
+        # reference's single token (bench.py --e2e: the full comparison)
+        result["e2e_c5"] = run_e2e(args, torch, dev, brief=True)
+        print(f"[bench] e2e_c5: {result['e2e_c5']['us_per_step']} us/step (spike_k {args.spike_k}), "
+              f"{result['e2e_c5']['reference_single_token']['us_per_step']} us/step (spike_k 1)",
+              file=sys.stderr, flush=True)
     if args.copy_mib:
         result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)
         result["read_ceiling_gbs"], result["read_ceiling_launch"] = read_ceiling(torch, dev, args.copy_mib,
@@ -544,7 +554,7 @@ def time_layers(torch, dev, make_handle, layers, qt, dkt, dvt, steps, warmup, ea
     return len(handles), blob_bytes, ms_step
 
 
-def run_e2e(args, torch, dev):
+def run_e2e(args, torch, dev, brief=False):
     """Workload C5: compress + decode + promote on one 70B-like layer (Hq=64,
     Hkv=8, D=128, 64K context, B=1).  Seeded importance partition, 2 % of
     far tokens aligned with the group query, per-step query drift, one
@@ -557,7 +567,9 @@ def run_e2e(args, torch, dev):
     the same loop reading the archive from HBM instead of pinned host memory,
     the eager device-drain loop, the host-drain loop and the reference's
     single-token drain (spike_k 1, budget 8) beside it, and the promotions
-    per step of each."""
+    per step of each.  brief: the two graph-replayed loops only (--spike-k
+    tokens, and the reference's single token), returned as a dict for the
+    default run's line instead of printed."""
     from foveated_kv_amd import ext, synthetic
     from foveated_kv_amd.promotion import PromotionPipeline
 
@@ -672,6 +684,19 @@ def run_e2e(args, torch, dev):
         return {"us_per_step": loop_s / max(steps - 1, 1) * 1e6, "compress_ms": compress_ms,
                 "stats": pipe.get_stats(), "near_valid_end": h.read_near_valid()}
 
+    if brief:
+        gres = loop_graph(spike_k, budget)
+        g1res = loop_graph(1, 8) if spike_k != 1 or budget != 8 else gres
+        return {"workload": "c5_70b_64k_e2e", "steps": steps - 1,
+                "launch": "one HIP graph replay per step (query gather, attention, drain + step advance)",
+                "spike_k": spike_k, "budget_per_drain": budget,
+                "us_per_step": round(gres["us_per_step"], 2),
+                "promotions_per_step": round(gres["stats"]["promotions_completed"] / steps, 3),
+                "near_valid_end": gres["near_valid_end"],
+                "reference_single_token": {"spike_k": 1, "budget_per_drain": 8,
+                                           "us_per_step": round(g1res["us_per_step"], 2),
+                                           "promotions_per_step":
+                                               round(g1res["stats"]["promotions_completed"] / steps, 3)}}
     dres = loop(True, spike_k, budget)
     hres = loop(False, spike_k, budget)
     gres = loop_graph(spike_k, budget)
