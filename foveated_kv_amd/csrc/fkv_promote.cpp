@@ -419,25 +419,41 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
     const int nb = a.arc_B < a.L.B ? a.arc_B : a.L.B;
     uint16_t* nk = (uint16_t*)(a.blob + a.L.near_k);
     uint16_t* nv = (uint16_t*)(a.blob + a.L.near_v);
-    // 16-byte reads of the pinned archive (8 dims of a row: few, wide bus
+    // 16-byte reads of the archive (8 dims of a row: few, wide bus
     // transactions); the 8 K dims are contiguous in the near tile, the V
-    // dims are 8 elements apart
+    // dims are 8 elements apart.  Every head's rows in one loop (item e:
+    // record row r of all heads' records, batch, chunk), so the reads of
+    // different heads are in flight together: roff[h] = the records of the
+    // heads before h.
+    __shared__ int roff[kMaxDrainHeads + 1];
+    if (tid < a.Hkv) {
+        int sum = 0;
+        for (int g = 0; g <= tid; g++) sum += n_rec[g];
+        roff[tid + 1] = sum;
+    }
+    if (tid == 0) roff[0] = 0;
+    __syncthreads();
     const int D = a.L.D, DC = D / 8;
-    for (int h = 0; h < a.Hkv; h++) {
-        const int n = n_rec[h];
-        for (int e = tid; e < n * nb * DC; e += blockDim.x) {
-            const int c = e % DC, b = (e / DC) % nb, i = e / (DC * nb);
-            const int slot = slot0[h] + i;
-            const int64_t base = ((int64_t)b * a.L.Hkv + h) * a.L.Na_pad * D;
-            const int64_t src = (((int64_t)b * a.Hkv + h) * a.arc_S + rec_arc[h][i]) * D + 8 * c;
-            const uint4 kw = *(const uint4*)(a.ark + src);
-            const uint4 vw = *(const uint4*)(a.arv + src);
-            *(uint4*)(nk + base + fkv::near_k_index(slot, 8 * c, D)) = kw;
-            const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-                nv[base + fkv::near_v_index(slot, 8 * c + k, D)] = (uint16_t)(vv[k >> 1] >> (16 * (k & 1)));
+    const int nrows = roff[a.Hkv];
+    for (int e = tid; e < nrows * nb * DC; e += blockDim.x) {
+        const int c = e % DC, b = (e / DC) % nb, r = e / (DC * nb);
+        int h = 0, hi = a.Hkv - 1;  // the last head with roff[h] <= r: the head of row r
+        while (h < hi) {
+            const int mid = (h + hi + 1) >> 1;
+            if (roff[mid] <= r) h = mid;
+            else hi = mid - 1;
         }
+        const int i = r - roff[h];
+        const int slot = slot0[h] + i;
+        const int64_t base = ((int64_t)b * a.L.Hkv + h) * a.L.Na_pad * D;
+        const int64_t src = (((int64_t)b * a.Hkv + h) * a.arc_S + rec_arc[h][i]) * D + 8 * c;
+        const uint4 kw = *(const uint4*)(a.ark + src);
+        const uint4 vw = *(const uint4*)(a.arv + src);
+        *(uint4*)(nk + base + fkv::near_k_index(slot, 8 * c, D)) = kw;
+        const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            nv[base + fkv::near_v_index(slot, 8 * c + k, D)] = (uint16_t)(vv[k >> 1] >> (16 * (k & 1)));
     }
     __syncthreads();
     for (int h = tid; h < a.Hkv; h += blockDim.x)
