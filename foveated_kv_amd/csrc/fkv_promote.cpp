@@ -286,25 +286,37 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
         // a position repeated in one head's list: the scan marks it at its first
         // occurrence, so every later occurrence is a duplicate (spike lists of
         // the attention kernel never repeat a token; other callers' may)
+        // (the loops over a head's tokens run over all FKV_MAX_SPIKE_K entries
+        // with the bound as a mask: their LDS reads issue together)
         if (K > 1) {
-            uint8_t dup_of_earlier[(kMaxDrainHeads * FKV_MAX_SPIKE_K + 255) / 256];
+            uint32_t dup_bits = 0;  // bit n: this thread's n-th (KV head, token); at most 32 of them
             int n_mine = 0;
             for (int u = tid; u < a.Hkv * K; u += blockDim.x, n_mine++) {
                 const int h = u / K, j = u % K, kind = tok_kind[h][j];
-                bool dup = false;
-                if (kind == kTokMarked || kind == kTokQueued)
-                    for (int i = 0; i < j; i++) dup |= tok_kind[h][i] != kTokSkip && tok_pos[h][i] == tok_pos[h][j];
-                dup_of_earlier[n_mine] = dup;
+                if (kind == kTokMarked || kind == kTokQueued) {
+                    const int pj = tok_pos[h][j];
+                    bool dup = false;
+#pragma unroll
+                    for (int i = 0; i < FKV_MAX_SPIKE_K; i++) {
+                        const int ki = tok_kind[h][i], pi = tok_pos[h][i];
+                        dup |= (i < j) & (ki != kTokSkip) & (pi == pj);
+                    }
+                    if (dup) dup_bits |= 1u << n_mine;
+                }
             }
             __syncthreads();
             n_mine = 0;
             for (int u = tid; u < a.Hkv * K; u += blockDim.x, n_mine++)
-                if (dup_of_earlier[n_mine]) tok_kind[u / K][u % K] = kTokDup;
+                if ((dup_bits >> n_mine) & 1u) tok_kind[u / K][u % K] = kTokDup;
             __syncthreads();
         }
         for (int h = tid; h < a.Hkv; h += blockDim.x) {
             int q = 0;
-            for (int j = 0; j < K; j++) q += tok_kind[h][j] == kTokQueued;
+#pragma unroll
+            for (int j = 0; j < FKV_MAX_SPIKE_K; j++) {
+                const int kj = tok_kind[h][j];
+                q += (j < K) & (kj == kTokQueued);
+            }
             nq[h] = q;
         }
         __syncthreads();
@@ -341,7 +353,11 @@ __global__ __launch_bounds__(256) void drain_promote_kernel(DrainArgs a) {
             const int kind = tok_kind[h][j];
             if (allow == 0 || kind == kTokSkip) continue;
             int qb = 0;
-            for (int i = 0; i < j; i++) qb += tok_kind[h][i] == kTokQueued;
+#pragma unroll
+            for (int i = 0; i < FKV_MAX_SPIKE_K; i++) {
+                const int ki = tok_kind[h][i];
+                qb += (i < j) & (ki == kTokQueued);
+            }
             if (qb >= allow) continue;
             if (kind == kTokDup) {
                 atomicAdd(&cnt[2], 1u);
