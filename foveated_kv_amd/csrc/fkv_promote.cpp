@@ -209,11 +209,12 @@ struct DrainArgs {
 // token) for the token's outcome, one per KV head for the budget prefix, its
 // cooldown and its counts, one per (KV head, token) again to mark the
 // reached tokens' positions and record the queued ones' archive rows; with
-// spike_k = 1 one per KV head for all of it; then all threads copy
-// the exact fp16 rows of every archive batch from pinned host memory into
-// the assigned headroom slots; the near_valid bumps are written last (the
-// next launch on the stream sees rows and counts together).  A head's
-// records take the slots from its near_valid on, in token order.
+// spike_k = 1 one per KV head for all of it; then all threads copy the
+// exact fp16 rows of every archive batch (pinned host or device memory)
+// into the assigned headroom slots, all heads' rows in one loop; the
+// near_valid bumps are written last (the next launch on the stream sees
+// rows and counts together).  A head's records take the slots from its
+// near_valid on, in token order.
 enum : int { kTokSkip = 0, kTokDup, kTokMarked, kTokQueued };
 
 // The outcome of one token of KV head hkv's first spike (f: its flat
