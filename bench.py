@@ -218,6 +218,10 @@ def main():
                          "(make -C foveated_kv_amd/csrc STAMPS=1)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the C5 end-to-end step of the default run (e2e_c5)")
+    ap.add_argument("--no-generate", action="store_true",
+                    help="skip the whole-model decode of the default run (generate)")
+    ap.add_argument("--no-crossover", action="store_true",
+                    help="skip the kernel crossover of the default run (crossover)")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip timing the other benchmark configurations (reported under other_configs)")
     ap.add_argument("--other-steps", type=int, default=30, help="timed steps per other configuration")
@@ -420,6 +424,19 @@ def main():
         except Exception as e:  # noqa: BLE001
             result["e2e_c5"] = {"error": f"{type(e).__name__}: {e}"}
             print(f"[bench] e2e_c5 failed: {e!r}", file=sys.stderr, flush=True)
+    # the whole-model decode (a tiny LM through the patched closure, one HIP
+    # graph per token) and the kernel crossover against exact fp16 attention,
+    # in the default run too (bench.py --generate / --crossover print them alone)
+    for key, flag, fn in (("generate", args.no_generate, run_generate),
+                          ("crossover", args.no_crossover, run_crossover)):
+        if flag or args.no_other_configs:
+            continue
+        try:
+            result[key] = fn(args, torch, dev, brief=True)
+            print(f"[bench] {key} done", file=sys.stderr, flush=True)
+        except Exception as e:  # noqa: BLE001
+            result[key] = {"error": f"{type(e).__name__}: {e}"}
+            print(f"[bench] {key} failed: {e!r}", file=sys.stderr, flush=True)
     if args.copy_mib:
         result["copy_gbs"] = copy_bandwidth(torch, dev, args.copy_mib)
         result["read_ceiling_gbs"], result["read_ceiling_launch"] = read_ceiling(torch, dev, args.copy_mib,
@@ -940,7 +957,7 @@ def time_graph(torch, dev, fns, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def run_crossover(args, torch, dev):
+def run_crossover(args, torch, dev, brief=False):
     """Kernel crossover (benchmark_crossover.py:45-82 of the reference, on
     one GPU): one decode attention call at 7B shapes (Hq=32, Hkv=8, D=128),
     exact fp16 attention over all S tokens against the fused kernel over the
@@ -1039,10 +1056,12 @@ def run_crossover(args, torch, dev):
                    "far_format": "fp8-e4m3 K + int4 per-token V", "launch": "hip-graph, distinct layer copies"},
         "rows": rows,
     }
+    if brief:
+        return result
     print(json.dumps(result), flush=True)
 
 
-def run_generate(args, torch, dev):
+def run_generate(args, torch, dev, brief=False):
     """The closure's host overhead against one HIP graph per model decode
     step: a seeded tiny LM (fp32 weights, --gen-layers layers of Hq=32,
     Hkv=8, D=128 attention, model dim 1024) prefills a --gen-context byte
@@ -1093,6 +1112,8 @@ def run_generate(args, torch, dev):
         "same_tokens": len({text for text, _ in runs.values()}) == 1,
         "same_promotions": len({tuple(st.get(k) for k in keys) for _, st in runs.values()}) == 1,
     }
+    if brief:
+        return result
     print(json.dumps(result), flush=True)
 
 
