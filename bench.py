@@ -23,6 +23,10 @@ faster of the C oracle's dequant+SDPA formulation and the reference's
 formulation in torch ops (dequant -> cat -> repeat_interleave -> SDPA), each
 timed over 100 calls or 20 s.
 
+Every other benchmark configuration is timed the same way in the same run
+(``other_configs``), and the default run also carries ``e2e_c5``,
+``generate`` and ``crossover``: brief forms of the modes below.
+
 Other modes (each prints its own JSON line): ``--e2e`` (the C5 decode +
 promotion loop), ``--generate`` (a tiny LM decoding through the closure,
 eager against one HIP graph per decode step), ``--crossover`` (the fused
